@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark: fwd+bwd ms/frame of the holographic hot path on one MI355X.
+
+A step (frame) = rasterizer forward (projection, binning, complex tile
+render) + multi-plane band-limited ASM to the (C,S,S) hologram, then the ASM
+adjoint of a CN(0,1) hologram gradient + rasterizer backward to the 8
+Gaussian gradients.  Default workload: the BASELINE.json headline, 1M
+Gaussians at 800x800, 3 planes, 3 wavelengths, synthetic seeded scene.
+
+Prints ONE JSON line (see the repository contract).  Per-stage times are
+measured live with hipEvents recorded by the library on the stream each
+stage runs on (hrf_trace_*), over the same timed steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "fwd+bwd ms/frame, 1M Gaussians @800x800, 3 planes; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+STAGES = ["project", "depth_sort", "scan", "emit", "tile_sort", "ranges", "render_fwd",
+          "render_bwd", "geom_bwd", "asm_pad", "asm_fft", "asm_mac_fwd", "asm_mac_adj",
+          "asm_crop"]
+
+
+def algorithmic_bytes(N, K, P, C, W, H, S, T):
+    """Compulsory-dataflow byte model per frame and per stage launch.
+
+    Each tensor crosses HBM once per producer and once per consumer; index
+    maps (shift, pad, crop) are free; a 2-D FFT is one read + one write of
+    its M x M complex64 grid.  g_in = 48+4P+8C bytes of Gaussian inputs,
+    g_rec = 32+4P+8C bytes of per-Gaussian render record.
+    """
+    M = 2 * S
+    g_in = 48 + 4 * P + 8 * C
+    g_rec = 32 + 4 * P + 8 * C
+    RF = N * g_in + 64 * N + 48 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H
+    RB = (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec + N * (28 + 4 * P + 8 * C) +
+          104 * N)
+    AF = P * C * (8 * W * H + 32 * M * M) + C * (16 * M * M + 8 * S * S)
+    AB = C * (8 * S * S + 16 * M * M) + P * C * (32 * M * M + 8 * W * H)
+    per_launch = {
+        "render_fwd": 4 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H + 8 * T,
+        "render_bwd": (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec +
+                       N * (28 + 4 * P + 8 * C) + 8 * T),
+        "project": N * g_in + N * (g_rec + 24),
+        "geom_bwd": N * g_in + N * (20 + 4 * P + 8 * C) + N * (40 + 4 * P + 8 * C),
+        "asm_mac_fwd": 8 * P * C * M * M + 8 * C * M * M,
+        "asm_mac_adj": 8 * C * M * M + 8 * P * C * M * M,
+        # FFT launches alternate batch P*C and C; the average per launch:
+        "asm_fft": 16 * M * M * (P * C + C) / 2,
+        "tile_sort": 2 * 16 * K,
+        "depth_sort": 4 * 16 * N,
+    }
+    return dict(RF=RF, RB=RB, AF=AF, AB=AB, total=RF + RB + AF + AB, per_launch=per_launch)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="headline")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; --gpus/WORLD_SIZE above 1 is not "
+              "supported (the hot path has no multi-GPU leg in this build).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import _lib, scenes
+    from complex_valued_holographic_radiance_fields_amd.frame import Frame
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    spec = scenes.config(args.config)
+    t_gen = time.perf_counter()
+    sc = scenes.generate(spec)
+    print(f"[bench] generated {spec.name}: N={sc.cam_means.shape[0]} in "
+          f"{time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+    t = scenes.to_torch(sc, dev)
+    fr = Frame(t, spec, sc.fx, sc.fy, sc.px, sc.py)
+    grad = t["grad_holo"]
+
+    def step():
+        fr.forward()
+        if spec.backward:
+            fr.backward(grad)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    _lib.trace_reset()
+    _lib.trace_enable(True)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    fwd_ms = []
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fr.forward()
+        b.record()
+        if spec.backward:
+            fr.backward(grad)
+        fwd_ms.append((a, b))
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - wall0
+    _lib.trace_enable(False)
+    total_ms = ev0.elapsed_time(ev1)
+    ms_per_step = total_ms / args.steps
+    fwd = float(np.median([a.elapsed_time(b) for a, b in fwd_ms]))
+    stages = {}
+    for s in STAGES:
+        n, ms = _lib.trace_read(s)
+        if n:
+            stages[s] = {"launches": n, "ms_per_frame": ms / args.steps,
+                         "avg_launch_ms": ms / n}
+    _lib.trace_reset()
+
+    N = int(sc.cam_means.shape[0])
+    K = fr.num_pairs
+    P, C, W, H, S = spec.planes, len(spec.wavelengths), spec.width, spec.height, spec.size
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    B = algorithmic_bytes(N, K, P, C, W, H, S, T)
+    frame_bytes = B["total"] if spec.backward else B["RF"] + B["AF"]
+    frame_gbs = frame_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Dominant kernel stage and its roofline.
+    dom = max((s for s in stages if s in B["per_launch"]),
+              key=lambda s: stages[s]["ms_per_frame"], default=None)
+    roof = None
+    if dom is not None:
+        ach = B["per_launch"][dom] / (stages[dom]["avg_launch_ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "avg_launch_ms": round(stages[dom]["avg_launch_ms"], 4),
+                "bytes_per_launch": int(B["per_launch"][dom])}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            from oracle import cpu_baseline
+
+            cores = len(os.sched_getaffinity(0))
+            torch.set_num_threads(cores)
+            ms, desc = cpu_baseline.time_frame(sc, budget_s=args.cpu_budget)
+            cpu = {"value": round(ms, 1), "unit": "ms/frame", "cores": cores, "kind": "port",
+                   "sample": desc}
+        except Exception as e:  # reported, never fatal to the GPU measurement
+            cpu = {"value": None, "unit": "ms/frame", "cores": None, "kind": "port",
+                   "sample": f"failed: {e!r}"}
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 4),
+        "unit": "ms/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{spec.name}: {N} Gaussians @{W}x{H}, P={P}, C={C}, "
+                               f"{'fwd+bwd' if spec.backward else 'fwd'}",
+                   "gaussians": N, "width": W, "height": H, "planes": P, "channels": C,
+                   "pairs_K": K, "fft_grid": 2 * S, "parallelism": "single-gpu"},
+        "fwd_ms": round(fwd, 4),
+        "bwd_ms": round(ms_per_step - fwd, 4) if spec.backward else None,
+        "gaussians_per_s": round(N / (ms_per_step * 1e-3), 1),
+        "frame_alg_bytes": int(frame_bytes),
+        "frame_achieved_GBs": round(frame_gbs, 1),
+        "frame_hbm_frac": round(frame_gbs / HBM_PEAK_GBS, 4),
+        "wall_s": round(wall_s, 3),
+        "stages_ms_per_frame": {s: round(v["ms_per_frame"], 4) for s, v in stages.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

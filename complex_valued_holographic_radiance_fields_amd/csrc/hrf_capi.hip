@@ -1,0 +1,680 @@
+// hrf_capi.cpp — extern "C" entry points declared in include/hrf.h.
+//
+// Host-side orchestration only: argument validation, workspace carving,
+// launch sequencing on the caller's stream, hipFFT calls.  No allocation is
+// done here except hipFFT's own plan work areas (cached per device/size).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "hrf_internal.h"
+
+namespace hrf {
+
+namespace {
+thread_local std::string g_err;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+
+const char* get_error() { return g_err.c_str(); }
+
+namespace {
+
+// ------------------------------------------------------------ validation --
+int check_raster_args(const hrf_gaussians* g, const hrf_camera* cam) {
+  if (!g || !cam) {
+    set_error("null gaussians/camera descriptor");
+    return HRF_ERR_INVALID;
+  }
+  if (g->n < 0 || g->n > 0x7FFFFFFFLL) {
+    set_error("number of Gaussians must be in [0, 2^31) (got %lld)",
+              static_cast<long long>(g->n));
+    return HRF_ERR_INVALID;
+  }
+  if (g->channels < 1 || g->channels > kMaxChannels) {
+    set_error("number of channels must be 1..%d (got %d); the reference supports at most "
+              "MAX_CHANNELS=3",
+              kMaxChannels, g->channels);
+    return HRF_ERR_INVALID;
+  }
+  if (g->planes < 1 || g->planes > kMaxPlanes) {
+    set_error("number of planes must be 1..%d (got %d)", kMaxPlanes, g->planes);
+    return HRF_ERR_INVALID;
+  }
+  if (cam->width <= 0 || cam->height <= 0) {
+    set_error("image size must be positive (got %dx%d)", cam->width, cam->height);
+    return HRF_ERR_INVALID;
+  }
+  const int gx = (cam->width + kTile - 1) / kTile, gy = (cam->height + kTile - 1) / kTile;
+  if (gx > 65535 || gy > 65535 || static_cast<int64_t>(gx) * gy * g->planes > 0x7FFFFFFFLL) {
+    set_error("image too large (%dx%d)", cam->width, cam->height);
+    return HRF_ERR_INVALID;
+  }
+  if (g->n > 0 && (!g->cam_means || !g->z_vals || !g->quats || !g->scales || !g->colours ||
+                   !g->phase || !g->opacities || !g->plane_probs || !cam->view_matrix)) {
+    set_error("null input pointer");
+    return HRF_ERR_INVALID;
+  }
+  return HRF_OK;
+}
+
+struct Frame {
+  int gx, gy, ntiles;
+  float lim_x, lim_y;
+};
+
+Frame frame_of(const hrf_camera* cam) {
+  Frame f;
+  f.gx = (cam->width + kTile - 1) / kTile;
+  f.gy = (cam->height + kTile - 1) / kTile;
+  f.ntiles = f.gx * f.gy;
+  // half_tan_fov = 0.5f * width / fx (forward.cu:199-200), lim = 1.3f * it.
+  const float htx = 0.5f * static_cast<float>(cam->width) / cam->fx;
+  const float hty = 0.5f * static_cast<float>(cam->height) / cam->fy;
+  f.lim_x = 1.3f * htx;
+  f.lim_y = 1.3f * hty;
+  return f;
+}
+
+// ------------------------------------------------------ geometry workspace --
+struct GeomWs {
+  float* rec;
+  uint32_t* pmask;
+  uint2* rect;
+  uint32_t* tiles;
+  uint32_t* dkey;
+  uint32_t* dkey_b;
+  uint32_t* order;
+  uint32_t* order_b;
+  uint32_t* cnt;
+  uint64_t* off;  // n + 1
+  uint32_t* vis;
+  uint32_t* vis_off;
+  uint64_t* scan64;
+  uint32_t* scan32;
+  uint32_t* radix;
+  uint64_t* totals;  // [K, V]
+};
+
+GeomWs carve_geom(Carver& cv, int64_t n, int C) {
+  GeomWs w;
+  const int64_t m = n > 0 ? n : 1;
+  w.rec = cv.take<float>(static_cast<size_t>(m) * rec_stride(C));
+  w.pmask = cv.take<uint32_t>(m);
+  w.rect = cv.take<uint2>(m);
+  w.tiles = cv.take<uint32_t>(m);
+  w.dkey = cv.take<uint32_t>(m);
+  w.dkey_b = cv.take<uint32_t>(m);
+  w.order = cv.take<uint32_t>(m);
+  w.order_b = cv.take<uint32_t>(m);
+  w.cnt = cv.take<uint32_t>(m);
+  w.off = cv.take<uint64_t>(m + 1);
+  w.vis = cv.take<uint32_t>(m);
+  w.vis_off = cv.take<uint32_t>(m);
+  w.scan64 = cv.take<uint64_t>(scan_scratch_elems(m));
+  w.scan32 = cv.take<uint32_t>(scan_scratch_elems(m));
+  w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
+  w.totals = cv.take<uint64_t>(4);
+  return w;
+}
+
+struct BinWs {
+  uint32_t* keys_a;
+  uint32_t* keys_b;
+  uint32_t* vals_s;
+  uint32_t* radix;
+};
+
+BinWs carve_bin(Carver& cv, int64_t k) {
+  BinWs w;
+  const int64_t m = k > 0 ? k : 1;
+  w.keys_a = cv.take<uint32_t>(m);
+  w.keys_b = cv.take<uint32_t>(m);
+  w.vals_s = cv.take<uint32_t>(m);
+  w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
+  return w;
+}
+
+struct BwdWs {
+  float* rec;
+  uint32_t* pmask;
+  uint2* rect;
+  uint32_t* tiles;
+  uint32_t* dkey;
+  uint32_t* vis;
+  float* acc;
+};
+
+BwdWs carve_bwd(Carver& cv, int64_t n, int C, int P) {
+  BwdWs w;
+  const int64_t m = n > 0 ? n : 1;
+  w.rec = cv.take<float>(static_cast<size_t>(m) * rec_stride(C));
+  w.pmask = cv.take<uint32_t>(m);
+  w.rect = cv.take<uint2>(m);
+  w.tiles = cv.take<uint32_t>(m);
+  w.dkey = cv.take<uint32_t>(m);
+  w.vis = cv.take<uint32_t>(m);
+  w.acc = cv.take<float>(static_cast<size_t>(m) * acc_stride(C, P));
+  return w;
+}
+
+ProjectParams project_params(const hrf_gaussians* g, const hrf_camera* cam, const Frame& f) {
+  ProjectParams p{};
+  p.cam = g->cam_means;
+  p.z = g->z_vals;
+  p.quats = g->quats;
+  p.scales = g->scales;
+  p.colours = g->colours;
+  p.phase = g->phase;
+  p.opac = g->opacities;
+  p.pprobs = g->plane_probs;
+  p.view = cam->view_matrix;
+  p.n = g->n;
+  p.C = g->channels;
+  p.P = g->planes;
+  p.fx = cam->fx;
+  p.fy = cam->fy;
+  p.px = cam->px;
+  p.py = cam->py;
+  p.lim_x = f.lim_x;
+  p.lim_y = f.lim_y;
+  p.W = cam->width;
+  p.H = cam->height;
+  p.gx = f.gx;
+  p.gy = f.gy;
+  p.near_plane = cam->near_plane;
+  p.far_plane = cam->far_plane;
+  return p;
+}
+
+__global__ void k_totals(const uint64_t* off, const uint32_t* cnt, const uint32_t* vis_off,
+                         const uint32_t* vis, int64_t n, uint64_t* off_end,
+                         uint64_t* totals) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const uint64_t k = off[n - 1] + cnt[n - 1];
+    off_end[0] = k;
+    totals[0] = k;
+    totals[1] = static_cast<uint64_t>(vis_off[n - 1]) + vis[n - 1];
+  }
+}
+
+int bits_for(int ntiles) {
+  int b = 0;
+  while (b < 31 && (1u << b) < static_cast<uint32_t>(ntiles)) ++b;
+  return b;
+}
+
+int check_ws(void* ws, size_t have, size_t need, const char* what) {
+  if (need > 0 && (!ws || have < need)) {
+    set_error("%s workspace too small: %zu bytes given, %zu needed", what, have, need);
+    return HRF_ERR_WORKSPACE;
+  }
+  return HRF_OK;
+}
+
+int check_asm(int P, int C, int H, int W, int S) {
+  if (P < 1 || P > kMaxPlanes || C < 1 || C > kMaxChannels) {
+    set_error("asm: planes must be 1..%d and channels 1..%d (got %d, %d)", kMaxPlanes,
+              kMaxChannels, P, C);
+    return HRF_ERR_INVALID;
+  }
+  if (S <= 0 || H <= 0 || W <= 0 || H > 2 * S || W > 2 * S) {
+    set_error("asm: field %dx%d does not fit the padded grid 2*%d", H, W, S);
+    return HRF_ERR_INVALID;
+  }
+  if ((H & 1) || (W & 1) || (S & 1)) {
+    set_error("asm: sizes must be even (field %dx%d, size %d): centred pad/crop of odd sizes "
+              "is ill-defined in the reference (odak crop_center returns size-1)",
+              H, W, S);
+    return HRF_ERR_INVALID;
+  }
+  if (static_cast<int64_t>(2 * S) * (2 * S) > 0x7FFFFFFFLL) {
+    set_error("asm: grid too large (size %d)", S);
+    return HRF_ERR_INVALID;
+  }
+  return HRF_OK;
+}
+
+}  // namespace
+}  // namespace hrf
+
+using namespace hrf;
+
+extern "C" {
+
+const char* hrf_last_error(void) { return hrf::get_error(); }
+
+const char* hrf_version(void) { return "hrf 0.1 gfx950"; }
+
+size_t hrf_raster_geom_workspace_size(int64_t n, int32_t channels, int32_t planes) {
+  (void)planes;
+  Carver cv(nullptr);
+  carve_geom(cv, n, channels < 1 ? 1 : (channels > 3 ? 3 : channels));
+  return cv.bytes();
+}
+
+size_t hrf_raster_binning_workspace_size(int64_t num_pairs, int32_t width, int32_t height) {
+  (void)width;
+  (void)height;
+  Carver cv(nullptr);
+  carve_bin(cv, num_pairs);
+  return cv.bytes();
+}
+
+size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t planes) {
+  Carver cv(nullptr);
+  carve_bwd(cv, n, channels < 1 ? 1 : (channels > 3 ? 3 : channels),
+            planes < 1 ? 1 : planes);
+  return cv.bytes();
+}
+
+int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, void* geom_ws,
+                               size_t geom_ws_bytes, void* stream, int64_t* num_pairs,
+                               int64_t* num_visible) {
+  HRF_TRY(check_raster_args(g, cam));
+  if (!num_pairs || !num_visible) {
+    set_error("null count outputs");
+    return HRF_ERR_INVALID;
+  }
+  *num_pairs = 0;
+  *num_visible = 0;
+  const int64_t n = g->n;
+  if (n == 0) return HRF_OK;
+  HRF_TRY(check_ws(geom_ws, geom_ws_bytes,
+                   hrf_raster_geom_workspace_size(n, g->channels, g->planes), "geometry"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Frame f = frame_of(cam);
+  Carver cv(geom_ws);
+  GeomWs w = carve_geom(cv, n, g->channels);
+
+  ProjectParams pp = project_params(g, cam, f);
+  pp.rec = w.rec;
+  pp.pmask = w.pmask;
+  pp.rect = w.rect;
+  pp.tiles = w.tiles;
+  pp.dkey = w.dkey;
+  pp.vis = w.vis;
+  {
+    HRF_STAGE("project", s);
+    HRF_TRY(launch_project(pp, s));
+  }
+
+  // Stable depth ordering of the Gaussians (32-bit keys, 4 passes: the
+  // sorted order ends in the first buffer pair).
+  {
+    HRF_STAGE("depth_sort", s);
+    HRF_TRY(launch_iota(w.order, n, s));
+    bool in_b = false;
+    HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s));
+    if (in_b) HRF_HIP(hipMemcpyAsync(w.order, w.order_b, n * sizeof(uint32_t),
+                                     hipMemcpyDeviceToDevice, s));
+  }
+  {
+    HRF_STAGE("scan", s);
+    HRF_TRY(launch_gather_counts(w.order, w.tiles, w.cnt, n, s));
+    HRF_TRY(scan_exclusive_u64(w.cnt, w.off, n, w.scan64, s));
+    HRF_TRY(scan_exclusive_u32(w.vis, w.vis_off, n, w.scan32, s));
+    hipLaunchKernelGGL(k_totals, dim3(1), dim3(64), 0, s, w.off, w.cnt, w.vis_off, w.vis, n,
+                       w.off + n, w.totals);
+    HRF_LAUNCH_CHECK();
+  }
+  uint64_t host_tot[2] = {0, 0};
+  HRF_HIP(hipMemcpyAsync(host_tot, w.totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
+  HRF_HIP(hipStreamSynchronize(s));
+  if (host_tot[0] > 0x7FFFFFFFull) {
+    set_error("pair count %llu exceeds the int32 point_list/ranges format",
+              static_cast<unsigned long long>(host_tot[0]));
+    return HRF_ERR_OVERFLOW;
+  }
+  *num_pairs = static_cast<int64_t>(host_tot[0]);
+  *num_visible = static_cast<int64_t>(host_tot[1]);
+  return HRF_OK;
+}
+
+int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, void* geom_ws,
+                              size_t geom_ws_bytes, void* bin_ws, size_t bin_ws_bytes,
+                              int64_t num_pairs, int64_t num_visible, void* field,
+                              float* final_T, int32_t* n_contrib, int32_t* point_list,
+                              int32_t* ranges, int64_t* visible, void* stream) {
+  HRF_TRY(check_raster_args(g, cam));
+  if (num_pairs < 0 || num_pairs > 0x7FFFFFFFLL || num_visible < 0 || num_visible > g->n) {
+    set_error("invalid pair/visible counts (%lld, %lld)", static_cast<long long>(num_pairs),
+              static_cast<long long>(num_visible));
+    return HRF_ERR_INVALID;
+  }
+  if (!field || !final_T || !n_contrib || !ranges) {
+    set_error("null output pointer");
+    return HRF_ERR_INVALID;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Frame f = frame_of(cam);
+  RenderParams rp{};
+  rp.C = g->channels;
+  rp.P = g->planes;
+  rp.W = cam->width;
+  rp.H = cam->height;
+  rp.gx = f.gx;
+  rp.gy = f.gy;
+  rp.field = static_cast<float2*>(field);
+  rp.final_T = final_T;
+  rp.n_contrib = n_contrib;
+  if (num_pairs == 0) {
+    HRF_TRY(launch_render_empty(rp, s));
+    HRF_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2 * int64_t(f.ntiles), s));
+    return HRF_OK;
+  }
+  if (!point_list || (num_visible > 0 && !visible)) {
+    set_error("null point_list/visible output");
+    return HRF_ERR_INVALID;
+  }
+  const int64_t n = g->n;
+  HRF_TRY(check_ws(geom_ws, geom_ws_bytes,
+                   hrf_raster_geom_workspace_size(n, g->channels, g->planes), "geometry"));
+  HRF_TRY(check_ws(bin_ws, bin_ws_bytes,
+                   hrf_raster_binning_workspace_size(num_pairs, cam->width, cam->height),
+                   "binning"));
+  Carver cg(geom_ws);
+  GeomWs w = carve_geom(cg, n, g->channels);
+  Carver cb(bin_ws);
+  BinWs b = carve_bin(cb, num_pairs);
+
+  // Pair emission in depth-rank order, then a stable sort on the tile id.
+  const int end_bit = bits_for(f.ntiles);
+  const bool odd = (radix_passes(end_bit) % 2) == 1;
+  uint32_t* vals_a = odd ? b.vals_s : reinterpret_cast<uint32_t*>(point_list);
+  uint32_t* vals_b = odd ? reinterpret_cast<uint32_t*>(point_list) : b.vals_s;
+  {
+    HRF_STAGE("emit", s);
+    HRF_TRY(launch_emit_pairs(w.off, w.order, w.rect, n, num_pairs, f.gx, b.keys_a, vals_a, s));
+  }
+  bool in_b = false;
+  {
+    HRF_STAGE("tile_sort", s);
+    HRF_TRY(radix_sort_pairs(b.keys_a, vals_a, b.keys_b, vals_b, num_pairs, end_bit, b.radix,
+                             &in_b, s));
+  }
+  const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
+  {
+    HRF_STAGE("ranges", s);
+    HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
+  }
+
+  rp.ranges = ranges;
+  rp.plist = point_list;
+  rp.pmask = w.pmask;
+  rp.rec = w.rec;
+  rp.pprobs = g->plane_probs;
+  {
+    HRF_STAGE("render_fwd", s);
+    HRF_TRY(launch_render_forward(rp, s));
+  }
+  if (num_visible > 0) HRF_TRY(launch_compact_visible(w.vis, w.vis_off, n, visible, s));
+  return HRF_OK;
+}
+
+int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const void* grad_field,
+                        const float* final_T, const int32_t* n_contrib,
+                        const int32_t* point_list, const int32_t* ranges, int64_t num_pairs,
+                        void* ws, size_t ws_bytes, float* grad_cam, float* grad_z,
+                        float* grad_quats, float* grad_scales, float* grad_colours,
+                        float* grad_phase, float* grad_opacities, float* grad_plane_probs,
+                        void* stream) {
+  HRF_TRY(check_raster_args(g, cam));
+  const int64_t n = g->n;
+  if (n == 0) return HRF_OK;
+  if (!grad_cam || !grad_z || !grad_quats || !grad_scales || !grad_colours || !grad_phase ||
+      !grad_opacities || !grad_plane_probs) {
+    set_error("null gradient output pointer");
+    return HRF_ERR_INVALID;
+  }
+  if (num_pairs < 0 || num_pairs > 0x7FFFFFFFLL) {
+    set_error("invalid pair count %lld", static_cast<long long>(num_pairs));
+    return HRF_ERR_INVALID;
+  }
+  if (num_pairs > 0 && (!grad_field || !final_T || !n_contrib || !point_list || !ranges)) {
+    set_error("null forward-state pointer");
+    return HRF_ERR_INVALID;
+  }
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_raster_backward_workspace_size(n, g->channels, g->planes),
+                   "backward"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Frame f = frame_of(cam);
+  Carver cv(ws);
+  BwdWs w = carve_bwd(cv, n, g->channels, g->planes);
+
+  ProjectParams pp = project_params(g, cam, f);
+  pp.rec = w.rec;
+  pp.pmask = w.pmask;
+  pp.rect = w.rect;
+  pp.tiles = w.tiles;
+  pp.dkey = w.dkey;
+  pp.vis = w.vis;
+  {
+    HRF_STAGE("project", s);
+    HRF_TRY(launch_project(pp, s));
+    HRF_TRY(launch_fill_f32(w.acc, 0.0f, n * acc_stride(g->channels, g->planes), s));
+  }
+
+  if (num_pairs > 0) {
+    RenderParams rp{};
+    rp.ranges = ranges;
+    rp.plist = point_list;
+    rp.pmask = w.pmask;
+    rp.rec = w.rec;
+    rp.pprobs = g->plane_probs;
+    rp.C = g->channels;
+    rp.P = g->planes;
+    rp.W = cam->width;
+    rp.H = cam->height;
+    rp.gx = f.gx;
+    rp.gy = f.gy;
+    rp.grad_field = static_cast<const float2*>(grad_field);
+    rp.final_T_in = final_T;
+    rp.n_contrib_in = n_contrib;
+    rp.acc = w.acc;
+    HRF_STAGE("render_bwd", s);
+    HRF_TRY(launch_render_backward(rp, s));
+  }
+
+  GeomBwdParams gb{};
+  gb.cam = g->cam_means;
+  gb.z = g->z_vals;
+  gb.quats = g->quats;
+  gb.scales = g->scales;
+  gb.colours = g->colours;
+  gb.phase = g->phase;
+  gb.opac = g->opacities;
+  gb.pprobs = g->plane_probs;
+  gb.view = cam->view_matrix;
+  gb.acc = w.acc;
+  gb.n = n;
+  gb.C = g->channels;
+  gb.P = g->planes;
+  gb.fx = cam->fx;
+  gb.fy = cam->fy;
+  gb.lim_x = f.lim_x;
+  gb.lim_y = f.lim_y;
+  gb.near_plane = cam->near_plane;
+  gb.far_plane = cam->far_plane;
+  gb.g_cam = grad_cam;
+  gb.g_z = grad_z;
+  gb.g_quat = grad_quats;
+  gb.g_scale = grad_scales;
+  gb.g_col = grad_colours;
+  gb.g_phase = grad_phase;
+  gb.g_opac = grad_opacities;
+  gb.g_plane = grad_plane_probs;
+  {
+    HRF_STAGE("geom_bwd", s);
+    HRF_TRY(launch_geom_backward(gb, s));
+  }
+  return HRF_OK;
+}
+
+// ------------------------------------------------------------------ ASM --
+
+int hrf_asm_spectral_forward(const float* re, const float* im, const float* fx_grid,
+                             const float* fy_grid, float* out_re, float* out_im, int32_t nx,
+                             int32_t ny, float wavelength, float distance, float aperture,
+                             float pixel_pitch, void* stream) {
+  if (nx <= 0 || ny <= 0 || nx != ny) {
+    set_error("asm spectral: only square grids are defined (got %dx%d)", nx, ny);
+    return HRF_ERR_INVALID;
+  }
+  if (!re || !im || !fx_grid || !fy_grid || !out_re || !out_im) {
+    set_error("asm spectral: null pointer");
+    return HRF_ERR_INVALID;
+  }
+  return launch_asm_spectral_grid(re, im, fx_grid, fy_grid, out_re, out_im, nx, ny,
+                                  wavelength, distance, aperture, pixel_pitch, false,
+                                  static_cast<hipStream_t>(stream));
+}
+
+int hrf_asm_spectral_backward(const float* grad_re, const float* grad_im,
+                              const float* field_re, const float* field_im,
+                              const float* fx_grid, const float* fy_grid, float* out_re,
+                              float* out_im, int32_t nx, int32_t ny, float wavelength,
+                              float distance, float aperture, float pixel_pitch,
+                              void* stream) {
+  (void)field_re;
+  (void)field_im;
+  if (nx <= 0 || ny <= 0 || nx != ny) {
+    set_error("asm spectral: only square grids are defined (got %dx%d)", nx, ny);
+    return HRF_ERR_INVALID;
+  }
+  if (!grad_re || !grad_im || !fx_grid || !fy_grid || !out_re || !out_im) {
+    set_error("asm spectral: null pointer");
+    return HRF_ERR_INVALID;
+  }
+  return launch_asm_spectral_grid(grad_re, grad_im, fx_grid, fy_grid, out_re, out_im, nx, ny,
+                                  wavelength, distance, aperture, pixel_pitch, true,
+                                  static_cast<hipStream_t>(stream));
+}
+
+size_t hrf_asm_workspace_size(int32_t planes, int32_t channels, int32_t size) {
+  if (planes < 1 || channels < 1 || size < 1) return 0;
+  const int64_t M = 2 * static_cast<int64_t>(size);
+  Carver cv(nullptr);
+  cv.take<float2>(static_cast<size_t>(planes) * channels * M * M);
+  cv.take<float2>(static_cast<size_t>(channels) * M * M);
+  return cv.bytes();
+}
+
+int hrf_asm_multiplane_forward(const void* fields, int32_t planes, int32_t channels,
+                               int32_t height, int32_t width, int32_t size,
+                               const float* wavelengths, const float* distances,
+                               double pixel_pitch, float aperture, void* hologram, void* ws,
+                               size_t ws_bytes, void* stream) {
+  HRF_TRY(check_asm(planes, channels, height, width, size));
+  if (!fields || !wavelengths || !distances || !hologram) {
+    set_error("asm: null pointer");
+    return HRF_ERR_INVALID;
+  }
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_asm_workspace_size(planes, channels, size), "asm"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = 2 * size;
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  Carver cv(ws);
+  float2* spec = cv.take<float2>(static_cast<size_t>(planes) * channels * MM);
+  float2* outs = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  const int PC = planes * channels;
+  {
+    HRF_STAGE("asm_pad", s);
+    HRF_TRY(launch_asm_pad(static_cast<const float2*>(fields), PC, height, width, spec, M, s));
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(spec, M, PC, false, s));
+  }
+  {
+    HRF_STAGE("asm_mac_fwd", s);
+    HRF_TRY(launch_asm_mac_forward(spec, planes, channels, M, pixel_pitch, wavelengths,
+                                   distances, aperture, outs, s));
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(outs, M, channels, true, s));
+  }
+  {
+    HRF_STAGE("asm_crop", s);
+    HRF_TRY(launch_asm_crop(outs, channels, M, size, size,
+                            static_cast<float>(1.0 / static_cast<double>(MM)),
+                            static_cast<float2*>(hologram), s));
+  }
+  return HRF_OK;
+}
+
+int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes, int32_t channels,
+                               int32_t height, int32_t width, int32_t size,
+                               const float* wavelengths, const float* distances,
+                               double pixel_pitch, float aperture, void* grad_fields, void* ws,
+                               size_t ws_bytes, void* stream) {
+  HRF_TRY(check_asm(planes, channels, height, width, size));
+  if (!grad_hologram || !wavelengths || !distances || !grad_fields) {
+    set_error("asm: null pointer");
+    return HRF_ERR_INVALID;
+  }
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_asm_workspace_size(planes, channels, size), "asm"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = 2 * size;
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  Carver cv(ws);
+  float2* spec = cv.take<float2>(static_cast<size_t>(planes) * channels * MM);
+  float2* gsp = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  const int PC = planes * channels;
+  {
+    HRF_STAGE("asm_pad", s);
+    HRF_TRY(launch_asm_pad(static_cast<const float2*>(grad_hologram), channels, size, size,
+                           gsp, M, s));
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(gsp, M, channels, false, s));
+  }
+  {
+    HRF_STAGE("asm_mac_adj", s);
+    HRF_TRY(launch_asm_mac_adjoint(gsp, planes, channels, M, pixel_pitch, wavelengths,
+                                   distances, aperture, spec, s));
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(spec, M, PC, true, s));
+  }
+  {
+    HRF_STAGE("asm_crop", s);
+    HRF_TRY(launch_asm_crop(spec, PC, M, height, width,
+                            static_cast<float>(1.0 / static_cast<double>(MM)),
+                            static_cast<float2*>(grad_fields), s));
+  }
+  return HRF_OK;
+}
+
+int hrf_asm_forward(const void* field, int32_t height, int32_t width, int32_t size,
+                    float wavelength, double pixel_pitch, float distance, float aperture,
+                    void* out, void* ws, size_t ws_bytes, void* stream) {
+  return hrf_asm_multiplane_forward(field, 1, 1, height, width, size, &wavelength, &distance,
+                                    pixel_pitch, aperture, out, ws, ws_bytes, stream);
+}
+
+int hrf_asm_adjoint(const void* grad_out, int32_t height, int32_t width, int32_t size,
+                    float wavelength, double pixel_pitch, float distance, float aperture,
+                    void* grad_field, void* ws, size_t ws_bytes, void* stream) {
+  return hrf_asm_multiplane_adjoint(grad_out, 1, 1, height, width, size, &wavelength,
+                                    &distance, pixel_pitch, aperture, grad_field, ws, ws_bytes,
+                                    stream);
+}
+
+void hrf_release_caches(void) { hrf::fft_release_all(); }
+
+}  // extern "C"

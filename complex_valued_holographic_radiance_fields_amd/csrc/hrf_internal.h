@@ -1,0 +1,248 @@
+// hrf_internal.h — shared constants, error plumbing, workspace carving and
+// device helpers for the gfx950 rasterizer / ASM library.
+//
+// The whole library is compiled with -ffp-contract=off: every floating-point
+// expression that must reproduce the reference bit-for-bit (projection,
+// culling, radius, tile rectangles, transfer-function phase) is evaluated in
+// source order, and fused multiply-adds are written out with fmaf() only
+// where the reference's own arithmetic is a dot product (the cuBLAS matmul
+// chain of forward.cu:265-268 / backward.cu:426-439).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "hrf.h"
+
+namespace hrf {
+
+// Compile-time constants of the reference (wave_rasterizer/config.h:15-23).
+constexpr int kTile = 16;                     // BLOCK_X == BLOCK_Y
+constexpr int kBlock = kTile * kTile;         // threads per render block
+constexpr float kPlaneCutoff = 1e-6f;         // PLANE_PROBABILITY_CUTOFF
+constexpr float kMaxAlpha = 0.99f;            // MAX_ALPHA_VALUE
+constexpr float kMinAlphaBwd = 1.0f / 255.0f; // backward_splat.cu:218
+constexpr float kTermT = 0.0001f;             // forward_splat.cu:243
+constexpr int kMaxChannels = 3;               // MAX_CHANNELS
+constexpr int kMaxPlanes = 32;                // plane membership is a u32 bitmask
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+const char* get_error();
+
+#define HRF_HIP(expr)                                                         \
+  do {                                                                        \
+    hipError_t e_ = (expr);                                                   \
+    if (e_ != hipSuccess) {                                                   \
+      ::hrf::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                       __FILE__, __LINE__);                                   \
+      return HRF_ERR_HIP;                                                     \
+    }                                                                         \
+  } while (0)
+
+#define HRF_LAUNCH_CHECK()                                                    \
+  do {                                                                        \
+    hipError_t e_ = hipGetLastError();                                        \
+    if (e_ != hipSuccess) {                                                   \
+      ::hrf::set_error("kernel launch failed: %s (%s:%d)",                    \
+                       hipGetErrorString(e_), __FILE__, __LINE__);            \
+      return HRF_ERR_HIP;                                                     \
+    }                                                                         \
+  } while (0)
+
+#define HRF_TRY(expr)             \
+  do {                            \
+    int s_ = (expr);              \
+    if (s_ != HRF_OK) return s_;  \
+  } while (0)
+
+// ------------------------------------------------------- workspace carving --
+// A bump allocator over a caller-provided buffer.  Run once with base ==
+// nullptr to size a workspace, then with the real buffer to carve it; both
+// runs take the same sequence of requests, so sizes always agree.
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off += count * sizeof(T);
+    return p;
+  }
+  size_t bytes() const { return (off + 255) & ~size_t(255); }
+};
+
+// Scope that brackets a stage with hipEvents on its stream while tracing is
+// enabled (hrf_trace_enable); a no-op otherwise.
+class StageTimer {
+ public:
+  StageTimer(const char* stage, hipStream_t s);
+  ~StageTimer();
+  StageTimer(const StageTimer&) = delete;
+  StageTimer& operator=(const StageTimer&) = delete;
+
+ private:
+  const char* stage_;
+  hipStream_t s_;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+  bool active_ = false;
+};
+#define HRF_CAT2(a, b) a##b
+#define HRF_CAT(a, b) HRF_CAT2(a, b)
+#define HRF_STAGE(name, s) ::hrf::StageTimer HRF_CAT(hrf_stage_, __LINE__)(name, s)
+
+inline int blocks_for(int64_t n, int per_block) {
+  return static_cast<int>((n + per_block - 1) / per_block);
+}
+
+// Render record layout, floats: [mx, my, i00, i01, i10, i11, opacity, w,
+// amp_re0, amp_im0, ...] padded to a multiple of 4 floats.  Slot 7 is 0 in
+// the per-Gaussian array and receives the plane weight when a render block
+// stages the record in LDS.
+__host__ __device__ constexpr int rec_quads(int channels) {
+  return (8 + 2 * channels + 3) / 4;
+}
+__host__ __device__ constexpr int rec_stride(int channels) {
+  return 4 * rec_quads(channels);
+}
+// Per-Gaussian backward accumulator: [dmx, dmy, dconic_x, dconic_y,
+// dconic_z, A_0..A_{C-1}, B_0..B_{C-1}, Q_0..Q_{P-1}].
+__host__ __device__ constexpr int acc_stride(int channels, int planes) {
+  return 5 + 2 * channels + planes;
+}
+
+// ------------------------------------------------------ launch interfaces --
+struct ProjectParams {
+  const float* cam;
+  const float* z;
+  const float* quats;
+  const float* scales;
+  const float* colours;
+  const float* phase;
+  const float* opac;
+  const float* pprobs;
+  const float* view;
+  int64_t n;
+  int C, P;
+  float fx, fy, px, py;
+  float lim_x, lim_y;  // 1.3 * half tan fov (host-evaluated as the reference)
+  int W, H, gx, gy;
+  float near_plane, far_plane;
+  // outputs
+  float* rec;       // n * rec_stride(C)
+  uint32_t* pmask;  // n
+  uint2* rect;      // n: x = minx | miny << 16, y = maxx | maxy << 16
+  uint32_t* tiles;  // n
+  uint32_t* dkey;   // n: depth sort key
+  uint32_t* vis;    // n: 0/1
+};
+int launch_project(const ProjectParams& p, hipStream_t s);
+
+struct GeomBwdParams {
+  const float* cam;
+  const float* z;
+  const float* quats;
+  const float* scales;
+  const float* colours;
+  const float* phase;
+  const float* opac;
+  const float* pprobs;
+  const float* view;
+  const float* acc;  // n * acc_stride(C,P)
+  int64_t n;
+  int C, P;
+  float fx, fy;
+  float lim_x, lim_y;
+  float near_plane, far_plane;
+  float* g_cam;
+  float* g_z;
+  float* g_quat;
+  float* g_scale;
+  float* g_col;
+  float* g_phase;
+  float* g_opac;
+  float* g_plane;
+};
+int launch_geom_backward(const GeomBwdParams& p, hipStream_t s);
+
+// Scans (exclusive).  Scratch sizing: scan_scratch_elems(n).
+size_t scan_scratch_elems(int64_t n);
+int scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n,
+                       uint32_t* scratch, hipStream_t s);
+int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n,
+                       uint64_t* scratch, hipStream_t s);
+
+// Stable LSD radix sort of (u32 key, u32 value) pairs over bits
+// [0, end_bit).  Ping-pongs between (ka,va) and (kb,vb); returns in
+// *result_in_b whether the sorted data ended in (kb,vb).
+size_t radix_scratch_elems(int64_t n);
+int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
+                     int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
+                     hipStream_t s);
+int radix_passes(int end_bit);
+
+int launch_gather_counts(const uint32_t* order, const uint32_t* tiles,
+                         uint32_t* cnt, int64_t n, hipStream_t s);
+int launch_iota(uint32_t* v, int64_t n, hipStream_t s);
+int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* rect,
+                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
+                      hipStream_t s);
+int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
+                       int ntiles, hipStream_t s);
+int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,
+                           int64_t* visible, hipStream_t s);
+int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s);
+int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
+
+struct RenderParams {
+  const int32_t* ranges;
+  const int32_t* plist;
+  const uint32_t* pmask;
+  const float* rec;
+  const float* pprobs;
+  int C, P, W, H, gx, gy;
+  // forward outputs
+  float2* field;
+  float* final_T;
+  int32_t* n_contrib;
+  // backward inputs / outputs
+  const float2* grad_field;
+  const float* final_T_in;
+  const int32_t* n_contrib_in;
+  float* acc;
+};
+int launch_render_forward(const RenderParams& p, hipStream_t s);
+int launch_render_empty(const RenderParams& p, hipStream_t s);
+int launch_render_backward(const RenderParams& p, hipStream_t s);
+
+// ASM (band-limited angular spectrum).
+struct AsmConsts {
+  float k;        // (float)(2*pi/(double)lambda)
+  float fx_max;   // band limit along rows
+  float fy_max;   // band limit along cols
+  float dist;     // signed distance used in the phase
+  int pass;       // fx_max/fy_max computed; always 1
+};
+AsmConsts asm_consts(float wavelength, float distance, float pixel_pitch, int nx, int ny);
+
+int launch_asm_spectral_grid(const float* re, const float* im, const float* fxg,
+                             const float* fyg, float* ore, float* oim, int nx, int ny,
+                             float wavelength, float distance, float aperture,
+                             float pitch, bool adjoint, hipStream_t s);
+int launch_asm_pad(const float2* in, int batch, int h, int w, float2* out, int M,
+                   hipStream_t s);
+int launch_asm_crop(const float2* in, int batch, int M, int h, int w, float scale,
+                    float2* out, hipStream_t s);
+int launch_asm_mac_forward(const float2* spec, int P, int C, int M, double pitch,
+                           const float* wavelengths, const float* distances,
+                           float aperture, float2* out, hipStream_t s);
+int launch_asm_mac_adjoint(const float2* spec, int P, int C, int M, double pitch,
+                           const float* wavelengths, const float* distances,
+                           float aperture, float2* out, hipStream_t s);
+int fft_c2c(float2* buf, int M, int batch, bool inverse, hipStream_t s);
+void fft_release_all();
+
+}  // namespace hrf

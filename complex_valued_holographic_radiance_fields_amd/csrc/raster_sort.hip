@@ -1,0 +1,384 @@
+// raster_sort.hip — stage 2: device scans, the stable LSD radix sort, pair
+// emission in depth-rank order and tile ranges.
+//
+// Binning order.  The reference emits (tile<<32 | depth') keys in Gaussian
+// index order and stable-sorts all K pairs over 32+ceil(log2 T) bits
+// (rasterizer_splat.cu:114-174,473-480): ~6 passes over 12-byte pairs.  The
+// resulting order is (tile, depth', gaussian index).  Here the N Gaussians are
+// stable-sorted once by depth' (4 passes over N), pairs are emitted in that
+// rank order, and a stable sort by tile id alone (ceil(log2 T / 8) passes,
+// 2 for T <= 65536) finishes the job: same order, far fewer bytes moved.
+#include "hrf_internal.h"
+
+namespace hrf {
+namespace {
+
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kScanThreads * kScanItems;  // elements per block
+
+constexpr int kRadixThreads = 256;
+constexpr int kRadixWaves = kRadixThreads / 64;
+constexpr int kRadixItems = 8;  // per thread
+constexpr int kRadixTile = kRadixThreads * kRadixItems;
+constexpr int kRadixBins = 256;
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Exclusive block scan of one value per thread (wave64 shuffles + LDS).
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  T x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    T y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) s_wave[wave] = x;
+  __syncthreads();
+  T wave_off = 0, tot = 0;
+  const int nw = blockDim.x >> 6;
+  for (int w = 0; w < nw; ++w) {
+    T t = s_wave[w];
+    if (w < wave) wave_off += t;
+    tot += t;
+  }
+  *total = tot;
+  return wave_off + x - v;
+}
+
+// Phase 1: per-block exclusive scan of kScanTile elements, block totals out.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kScanThreads) void k_scan_local(const Tin* __restrict__ in,
+                                                             Tout* __restrict__ out,
+                                                             Tout* __restrict__ sums,
+                                                             int64_t n) {
+  __shared__ Tout s_wave[kScanThreads / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+                       static_cast<int64_t>(threadIdx.x) * kScanItems;
+  Tout vals[kScanItems];
+  Tout run = 0;
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    const int64_t idx = base + i;
+    const Tout v = idx < n ? static_cast<Tout>(in[idx]) : Tout(0);
+    vals[i] = run;
+    run += v;
+  }
+  Tout total;
+  const Tout off = block_exclusive_scan<Tout>(run, &total, s_wave);
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    const int64_t idx = base + i;
+    if (idx < n) out[idx] = vals[i] + off;
+  }
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kScanThreads) void k_scan_add(T* __restrict__ out,
+                                                           const T* __restrict__ sums,
+                                                           int64_t n) {
+  const T add = sums[blockIdx.x];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  for (int i = threadIdx.x; i < kScanTile; i += kScanThreads) {
+    const int64_t idx = base + i;
+    if (idx < n) out[idx] += add;
+  }
+}
+
+// Recursive exclusive scan.  Scratch holds the block-sum pyramid.
+template <typename Tin, typename Tout>
+int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  const int64_t nb = (n + kScanTile - 1) / kScanTile;
+  Tout* sums = scratch;
+  hipLaunchKernelGGL((k_scan_local<Tin, Tout>), dim3(static_cast<unsigned>(nb)),
+                     dim3(kScanThreads), 0, s, in, out, sums, n);
+  HRF_LAUNCH_CHECK();
+  if (nb > 1) {
+    HRF_TRY((scan_exclusive<Tout, Tout>(sums, sums, nb, scratch + nb, s)));
+    hipLaunchKernelGGL((k_scan_add<Tout>), dim3(static_cast<unsigned>(nb)),
+                       dim3(kScanThreads), 0, s, out, sums, n);
+    HRF_LAUNCH_CHECK();
+  }
+  return HRF_OK;
+}
+
+// ----------------------------------------------------------- radix sort --
+
+__global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
+                                                              int64_t n, int shift,
+                                                              uint32_t* __restrict__ hist,
+                                                              int nblocks) {
+  __shared__ uint32_t s_hist[kRadixBins];
+  s_hist[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kRadixTile;
+#pragma unroll
+  for (int i = 0; i < kRadixItems; ++i) {
+    const int64_t idx = base + i * kRadixThreads + threadIdx.x;
+    if (idx < n) atomicAdd(&s_hist[(keys[idx] >> shift) & 0xFF], 1u);
+  }
+  __syncthreads();
+  hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = s_hist[threadIdx.x];
+}
+
+// Stable scatter.  Wave w owns the contiguous sub-range
+// [base + w*512, base + (w+1)*512) processed as 8 iterations of 64 keys;
+// the rank of a key among equal digits before it is found with a ballot
+// match (8 ballots) plus per-wave LDS digit counters, then offset by the
+// counts of the lower waves and the global digit/block offset.
+__global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
+    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
+    const uint32_t* __restrict__ hist_scan, int nblocks) {
+  __shared__ uint32_t s_cnt[kRadixWaves][kRadixBins];
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int w = 0; w < kRadixWaves; ++w) s_cnt[w][threadIdx.x] = 0;
+  __syncthreads();
+
+  const int64_t wbase = static_cast<int64_t>(blockIdx.x) * kRadixTile +
+                        static_cast<int64_t>(wave) * (kRadixItems * 64);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
+  int dig[kRadixItems];
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    const int64_t idx = wbase + it * 64 + lane;
+    const bool valid = idx < n;
+    key[it] = valid ? kin[idx] : 0u;
+    val[it] = valid ? vin[idx] : 0u;
+    const int d = valid ? static_cast<int>((key[it] >> shift) & 0xFF) : 0;
+    dig[it] = valid ? d : -1;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
+    uint32_t prev = 0;
+    if (valid) prev = s_cnt[wave][d];
+    rank[it] = prev + before;
+    if (valid && before == 0) s_cnt[wave][d] = prev + static_cast<uint32_t>(__popcll(peers));
+  }
+  __syncthreads();
+  // Per-digit prefix over waves plus the global offset of (digit, block).
+  {
+    const int d = threadIdx.x;
+    uint32_t run = hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kRadixWaves; ++w) {
+      const uint32_t c = s_cnt[w][d];
+      s_cnt[w][d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    if (dig[it] >= 0) {
+      const uint32_t pos = s_cnt[wave][dig[it]] + rank[it];
+      kout[pos] = key[it];
+      vout[pos] = val[it];
+    }
+  }
+}
+
+__global__ void k_iota(uint32_t* v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) v[i] = static_cast<uint32_t>(i);
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void k_fill_f32(float* p, float v, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void k_gather_counts(const uint32_t* __restrict__ order,
+                                const uint32_t* __restrict__ tiles,
+                                uint32_t* __restrict__ cnt, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) cnt[i] = tiles[order[i]];
+}
+
+// One thread per pair e: the owning rank r is the last r with off[r] <= e
+// (binary search over the exclusive offsets); tile order inside a Gaussian
+// is y outer, x inner (rasterizer_splat.cu:162-173).
+__global__ void k_emit(const uint64_t* __restrict__ off, const uint32_t* __restrict__ order,
+                       const uint2* __restrict__ rect, int64_t n, int64_t k, int gx,
+                       uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= k) return;
+  int64_t lo = 0, hi = n;  // invariant: off[lo] <= e < off[hi] (off[n] == k)
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (off[mid] <= static_cast<uint64_t>(e))
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const uint32_t g = order[lo];
+  const uint2 rc = rect[g];
+  const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
+  const uint32_t w = maxx - minx;
+  const uint32_t i = static_cast<uint32_t>(static_cast<uint64_t>(e) - off[lo]);
+  const uint32_t ty = miny + i / w, tx = minx + i % w;
+  keys[e] = ty * static_cast<uint32_t>(gx) + tx;
+  vals[e] = g;
+}
+
+__global__ void k_tile_ranges(const uint32_t* __restrict__ keys, int64_t k,
+                              int32_t* __restrict__ ranges) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= k) return;
+  const uint32_t t = keys[i];
+  if (i == 0 || keys[i - 1] != t) ranges[2 * static_cast<int64_t>(t)] = static_cast<int32_t>(i);
+  if (i == k - 1 || keys[i + 1] != t)
+    ranges[2 * static_cast<int64_t>(t) + 1] = static_cast<int32_t>(i + 1);
+}
+
+__global__ void k_compact_visible(const uint32_t* __restrict__ vis,
+                                  const uint32_t* __restrict__ vis_off, int64_t n,
+                                  int64_t* __restrict__ visible) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n && vis[i]) visible[vis_off[i]] = i;
+}
+
+}  // namespace
+
+size_t scan_scratch_elems(int64_t n) {
+  size_t total = 0;
+  int64_t m = n;
+  while (m > 1) {
+    m = (m + kScanTile - 1) / kScanTile;
+    total += static_cast<size_t>(m);
+  }
+  return total + 4;
+}
+
+int scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, uint32_t* scratch,
+                       hipStream_t s) {
+  return scan_exclusive<uint32_t, uint32_t>(in, out, n, scratch, s);
+}
+
+int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n, uint64_t* scratch,
+                       hipStream_t s) {
+  return scan_exclusive<uint32_t, uint64_t>(in, out, n, scratch, s);
+}
+
+int radix_passes(int end_bit) { return (end_bit + 7) / 8; }
+
+size_t radix_scratch_elems(int64_t n) {
+  const int64_t nb = (n + kRadixTile - 1) / kRadixTile;
+  const size_t hist = static_cast<size_t>(nb) * kRadixBins;
+  return 2 * hist + scan_scratch_elems(static_cast<int64_t>(hist)) + 4;
+}
+
+int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
+                     int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s) {
+  *result_in_b = false;
+  if (n <= 1) return HRF_OK;
+  const int passes = radix_passes(end_bit);
+  const int64_t nb64 = (n + kRadixTile - 1) / kRadixTile;
+  if (nb64 > 0x7FFFFFFF) {
+    set_error("radix sort: too many keys (%lld)", static_cast<long long>(n));
+    return HRF_ERR_INVALID;
+  }
+  const int nb = static_cast<int>(nb64);
+  const int64_t hist_n = static_cast<int64_t>(nb) * kRadixBins;
+  uint32_t* hist = scratch;
+  uint32_t* hist_scan = scratch + hist_n;
+  uint32_t* scan_tmp = scratch + 2 * hist_n;
+  uint32_t *src_k = ka, *src_v = va, *dst_k = kb, *dst_v = vb;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = pass * 8;
+    hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
+                       hist, nb);
+    HRF_LAUNCH_CHECK();
+    HRF_TRY(scan_exclusive_u32(hist, hist_scan, hist_n, scan_tmp, s));
+    hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(kRadixThreads), 0, s, src_k, src_v,
+                       dst_k, dst_v, n, shift, hist_scan, nb);
+    HRF_LAUNCH_CHECK();
+    uint32_t* tk = src_k;
+    uint32_t* tv = src_v;
+    src_k = dst_k;
+    src_v = dst_v;
+    dst_k = tk;
+    dst_v = tv;
+  }
+  *result_in_b = (passes % 2) == 1;
+  return HRF_OK;
+}
+
+int launch_iota(uint32_t* v, int64_t n, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_iota, dim3(blocks_for(n, 256)), dim3(256), 0, s, v, n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_fill_u32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_fill_f32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_gather_counts(const uint32_t* order, const uint32_t* tiles, uint32_t* cnt,
+                         int64_t n, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_gather_counts, dim3(blocks_for(n, 256)), dim3(256), 0, s, order,
+                     tiles, cnt, n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* rect,
+                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
+                      hipStream_t s) {
+  if (k <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_emit, dim3(blocks_for(k, 256)), dim3(256), 0, s, off, order, rect, n,
+                     k, gx, keys, vals);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges, int ntiles,
+                       hipStream_t s) {
+  HRF_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2 * int64_t(ntiles), s));
+  if (k <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_tile_ranges, dim3(blocks_for(k, 256)), dim3(256), 0, s, keys, k,
+                     ranges);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,
+                           int64_t* visible, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_compact_visible, dim3(blocks_for(n, 256)), dim3(256), 0, s, vis,
+                     vis_off, n, visible);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+}  // namespace hrf

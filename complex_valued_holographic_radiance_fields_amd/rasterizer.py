@@ -1,0 +1,179 @@
+"""Host side of the rasterizer: torch tensors in, C-ABI calls, torch tensors out.
+
+Mirrors ``CudaRasterizer::Rasterizer::forward/backward``
+(cuda_prop/cov3d_cuda/wave_rasterizer/rasterizer_splat.h:255-293,
+rasterizer_splat.cu:324-684): same arguments, same outputs, same empty-scene
+behaviour, with errors raised as RuntimeError instead of printed.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+
+def _f32c(t: torch.Tensor, name: str, shape_tail: Tuple[int, ...] | None = None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (the HIP rasterizer has no CPU path)")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32 (got {t.dtype})")
+    if shape_tail is not None and tuple(t.shape[1:]) != shape_tail:
+        raise RuntimeError(f"{name} must have shape (N, {', '.join(map(str, shape_tail))}), "
+                           f"got {tuple(t.shape)}")
+    return t.contiguous()
+
+
+def _as_float(x) -> float:
+    if isinstance(x, torch.Tensor):
+        return float(x.detach().reshape(-1)[0].item())
+    return float(x)
+
+
+class _Inputs:
+    """Validated, contiguous inputs plus the C descriptors pointing at them."""
+
+    def __init__(self, cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
+                 plane_probs, fx, fy, px, py, view_matrix, img_size, near_plane, far_plane):
+        self.cam = _f32c(cam_means_3D, "cam_means_3D", (3,))
+        n = self.cam.shape[0]
+        self.z = _f32c(z_vals, "z_vals").reshape(-1)
+        self.quats = _f32c(quats, "quats", (4,))
+        self.scales = _f32c(scales, "scales", (3,))
+        if colours.dim() != 2 or phase.dim() != 2 or plane_probs.dim() != 2:
+            raise RuntimeError("colours/phase must be (N,C) and plane_probs (N,P)")
+        self.colours = _f32c(colours, "colours")
+        self.phase = _f32c(phase, "phase", (self.colours.shape[1],))
+        self.opac = _f32c(opacities, "opacities").reshape(-1)
+        self.pprobs = _f32c(plane_probs, "plane_probs")
+        for name, t in (("z_vals", self.z), ("quats", self.quats), ("scales", self.scales),
+                        ("colours", self.colours), ("phase", self.phase),
+                        ("opacities", self.opac), ("plane_probs", self.pprobs)):
+            if t.shape[0] != n:
+                raise RuntimeError(f"{name} has {t.shape[0]} rows, expected {n}")
+        vm = view_matrix
+        if vm.dim() == 3:
+            vm = vm[0]
+        self.view = _f32c(vm, "view_matrix")
+        if tuple(self.view.shape) != (3, 3):
+            raise RuntimeError("view_matrix must have shape (3, 3)")
+        self.device = self.cam.device
+        for t in (self.z, self.quats, self.scales, self.colours, self.phase, self.opac,
+                  self.pprobs, self.view):
+            if t.device != self.device:
+                raise RuntimeError("all inputs must be on the same device")
+        self.n = n
+        self.C = int(self.colours.shape[1])
+        self.P = int(self.pprobs.shape[1])
+        self.W, self.H = int(img_size[0]), int(img_size[1])
+        self.g = _lib.HrfGaussians(
+            self.cam.data_ptr(), self.z.data_ptr(), self.quats.data_ptr(),
+            self.scales.data_ptr(), self.colours.data_ptr(), self.phase.data_ptr(),
+            self.opac.data_ptr(), self.pprobs.data_ptr(), n, self.C, self.P)
+        self.c = _lib.HrfCamera(_as_float(fx), _as_float(fy), _as_float(px), _as_float(py),
+                                self.view.data_ptr(), self.W, self.H, _as_float(near_plane),
+                                _as_float(far_plane))
+
+    @property
+    def ntiles(self) -> int:
+        return ((self.W + 15) // 16) * ((self.H + 15) // 16)
+
+
+def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
+            fx, fy, px, py, view_matrix, img_size: Sequence[int], tile_size=(16, 16),
+            near_plane=1.0, far_plane=1000.0):
+    """Rasterizer::forward -> (field (P,C,H,W) complex64,
+    (final_Ts, n_contrib, point_list, ranges, visible_indices))."""
+    if tuple(int(t) for t in tile_size) != (16, 16):
+        # The reference ignores tile_size and always uses 16x16 tiles
+        # (config.h:16-17); any other request is accepted and ignored the same way.
+        pass
+    inp = _Inputs(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
+                  fx, fy, px, py, view_matrix, img_size, near_plane, far_plane)
+    lib = _lib.load()
+    dev = inp.device
+    P, C, H, W = inp.P, inp.C, inp.H, inp.W
+    with torch.cuda.device(dev):
+        stream = _lib.stream_ptr(dev)
+        gbytes = lib.hrf_raster_geom_workspace_size(inp.n, C, P)
+        geom_ws = torch.empty(max(gbytes, 1), dtype=torch.uint8, device=dev)
+        K = ctypes.c_int64(0)
+        V = ctypes.c_int64(0)
+        _lib.check(lib.hrf_raster_forward_prepare(ctypes.byref(inp.g), ctypes.byref(inp.c),
+                                                  geom_ws.data_ptr(), gbytes, stream,
+                                                  ctypes.byref(K), ctypes.byref(V)))
+        K, V = int(K.value), int(V.value)
+        field = torch.empty((P, C, H, W), dtype=torch.complex64, device=dev)
+        final_T = torch.empty((P, H, W), dtype=torch.float32, device=dev)
+        n_contrib = torch.empty((P, H, W), dtype=torch.int32, device=dev)
+        ranges = torch.empty((inp.ntiles, 2), dtype=torch.int32, device=dev)
+        if K == 0:
+            point_list = torch.zeros(1, dtype=torch.int32, device=dev)
+            visible = torch.zeros(0, dtype=torch.int64, device=dev)
+            bbytes = 0
+            bin_ws = None
+        else:
+            point_list = torch.empty(K, dtype=torch.int32, device=dev)
+            visible = torch.empty(V, dtype=torch.int64, device=dev)
+            bbytes = lib.hrf_raster_binning_workspace_size(K, W, H)
+            bin_ws = torch.empty(bbytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.hrf_raster_forward_render(
+            ctypes.byref(inp.g), ctypes.byref(inp.c), geom_ws.data_ptr(), gbytes,
+            _lib.ptr(bin_ws), bbytes, K, V if K > 0 else 0, field.data_ptr(),
+            final_T.data_ptr(), n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
+            visible.data_ptr() if visible.numel() else None, stream))
+    return field, (final_T, n_contrib, point_list, ranges, visible)
+
+
+def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
+             plane_probs, fx, fy, px, py, view_matrix, img_size, tile_size, final_Ts,
+             n_contrib, point_list, ranges, near_plane=1.0, far_plane=1000.0):
+    """Rasterizer::backward -> [grad_cam_means_3D, grad_z_vals, grad_quats, grad_scales,
+    grad_colours, grad_phase, grad_opacities, grad_plane_probs]."""
+    inp = _Inputs(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
+                  fx, fy, px, py, view_matrix, img_size, near_plane, far_plane)
+    lib = _lib.load()
+    dev = inp.device
+    n, C, P, H, W = inp.n, inp.C, inp.P, inp.H, inp.W
+    go = grad_output
+    if go.dtype != torch.complex64:
+        go = go.to(torch.complex64)
+    if tuple(go.shape) != (P, C, H, W):
+        raise RuntimeError(f"grad_output must have shape {(P, C, H, W)}, got {tuple(go.shape)}")
+    go = go.contiguous()
+    final_Ts = final_Ts.contiguous()
+    n_contrib = n_contrib.contiguous()
+    point_list = point_list.contiguous()
+    ranges = ranges.contiguous()
+    if tuple(final_Ts.shape) != (P, H, W) or tuple(n_contrib.shape) != (P, H, W):
+        raise RuntimeError("final_Ts / n_contrib must have shape (P, H, W)")
+    if tuple(ranges.shape) != (inp.ntiles, 2) or ranges.dtype != torch.int32:
+        raise RuntimeError(f"ranges must be int32 of shape ({inp.ntiles}, 2)")
+    if point_list.dtype != torch.int32 or n_contrib.dtype != torch.int32:
+        raise RuntimeError("point_list and n_contrib must be int32")
+    opts = dict(dtype=torch.float32, device=dev)
+    g_cam = torch.empty((n, 3), **opts)
+    g_z = torch.empty((n,), **opts)
+    g_q = torch.empty((n, 4), **opts)
+    g_s = torch.empty((n, 3), **opts)
+    g_col = torch.empty((n, C), **opts)
+    g_ph = torch.empty((n, C), **opts)
+    g_o = torch.empty((n,), **opts)
+    g_pl = torch.empty((n, P), **opts)
+    if n == 0:
+        return [g_cam, g_z, g_q, g_s, g_col, g_ph, g_o, g_pl]
+    with torch.cuda.device(dev):
+        stream = _lib.stream_ptr(dev)
+        wbytes = lib.hrf_raster_backward_workspace_size(n, C, P)
+        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.hrf_raster_backward(
+            ctypes.byref(inp.g), ctypes.byref(inp.c), go.data_ptr(), final_Ts.data_ptr(),
+            n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
+            int(point_list.numel()), ws.data_ptr(), wbytes, g_cam.data_ptr(), g_z.data_ptr(),
+            g_q.data_ptr(), g_s.data_ptr(), g_col.data_ptr(), g_ph.data_ptr(), g_o.data_ptr(),
+            g_pl.data_ptr(), stream))
+    return [g_cam, g_z, g_q, g_s, g_col, g_ph, g_o, g_pl]

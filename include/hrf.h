@@ -1,0 +1,206 @@
+/*
+ * hrf.h — C ABI of the MI355X-native complex-valued wave rasterizer and
+ * band-limited angular-spectrum (ASM) propagator.
+ *
+ * Every entry point takes raw device pointers, plain sizes and a hipStream_t
+ * (passed as void*), returns an int status (HRF_OK == 0) and never throws.
+ * On failure hrf_last_error() returns a message for the calling thread.
+ * All kernels are enqueued on the given stream; the only host synchronisation
+ * in the whole library is the pair/visible count read-back at the end of
+ * hrf_raster_forward_prepare (the reference reads the same count back,
+ * rasterizer_splat.cu:430-432).
+ *
+ * Layouts (all row-major, fp32 unless stated):
+ *   cam_means (N,3), z_vals (N), quats (N,4) (r,x,y,z), scales (N,3),
+ *   colours (N,C), phase (N,C), opacities (N), plane_probs (N,P),
+ *   view_matrix (3,3) device memory, field (P,C,H,W) complex64 interleaved,
+ *   final_T (P,H,W) f32, n_contrib (P,H,W) i32, point_list (K) i32,
+ *   ranges (T,2) i32, visible (V) i64.  T = ceil(W/16)*ceil(H/16).
+ */
+#ifndef HRF_H
+#define HRF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HRF_OK 0
+#define HRF_ERR_INVALID 1   /* bad shape / argument */
+#define HRF_ERR_HIP 2       /* a HIP / hipFFT call failed */
+#define HRF_ERR_WORKSPACE 3 /* workspace too small */
+#define HRF_ERR_OVERFLOW 4  /* pair count does not fit the int32 outputs */
+
+/* Gaussians as passed to the rasterizer (post-activation values, device
+ * pointers).  Mirrors the tensor arguments of Rasterizer::forward
+ * (cuda_prop/cov3d_cuda/wave_rasterizer/rasterizer_splat.h:255-270). */
+typedef struct hrf_gaussians {
+  const float* cam_means;   /* (N,3) camera-space means */
+  const float* z_vals;      /* (N)   depth used for culling and sorting */
+  const float* quats;       /* (N,4) */
+  const float* scales;      /* (N,3) */
+  const float* colours;     /* (N,C) amplitudes */
+  const float* phase;       /* (N,C) */
+  const float* opacities;   /* (N) */
+  const float* plane_probs; /* (N,P) */
+  int64_t n;
+  int32_t channels; /* C in 1..3 */
+  int32_t planes;   /* P in 1..32 */
+} hrf_gaussians;
+
+/* Camera and image.  Mirrors the scalar arguments of Rasterizer::forward
+ * (fx, fy, px, py, view_matrix, img_size=(W,H), near, far). */
+typedef struct hrf_camera {
+  float fx, fy, px, py;
+  const float* view_matrix; /* (3,3) device pointer, used as W in cov2D */
+  int32_t width, height;
+  float near_plane, far_plane;
+} hrf_camera;
+
+const char* hrf_last_error(void);
+/* Library version string ("hrf <major>.<minor> gfx950"). */
+const char* hrf_version(void);
+
+/* ---------------- rasterizer (replaces CudaRasterizer::Rasterizer) -------- */
+
+/* Bytes of the per-Gaussian workspace ("geometry state") that must persist
+ * from hrf_raster_forward_prepare to hrf_raster_forward_render.
+ * Replaces GeometryState/CudaMemoryManager (rasterizer_splat.h:9-39,192-248). */
+size_t hrf_raster_geom_workspace_size(int64_t n, int32_t channels, int32_t planes);
+
+/* Bytes of the per-pair workspace ("binning state") for K pairs.
+ * Replaces BinningState/ImageState (rasterizer_splat.h:64-94). */
+size_t hrf_raster_binning_workspace_size(int64_t num_pairs, int32_t width, int32_t height);
+
+/* Forward, phase 1: projection (means2D, J, Sigma, cov2D), culling, radius,
+ * tile counts, depth ordering, offsets, visibility; reads back the pair
+ * count K and the visible count V (one host sync).
+ * Replaces Rasterizer::forward up to the K read-back
+ * (rasterizer_splat.cu:324-432). */
+int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam,
+                               void* geom_ws, size_t geom_ws_bytes, void* stream,
+                               int64_t* num_pairs, int64_t* num_visible);
+
+/* Forward, phase 2: pair emission, stable tile sort, tile ranges and the
+ * complex tile render.  Writes field, final_T, n_contrib, point_list (K),
+ * ranges (T,2) and visible (V).  With K == 0 it writes the reference's
+ * empty-scene outputs (rasterizer_splat.cu:434-449): zero field, final_T=1,
+ * n_contrib=0, ranges=0; point_list and visible are not touched.
+ * Replaces rasterizer_splat.cu:451-547 and forward_splat.cu:101-289. */
+int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
+                              void* geom_ws, size_t geom_ws_bytes,
+                              void* bin_ws, size_t bin_ws_bytes,
+                              int64_t num_pairs, int64_t num_visible,
+                              void* field, float* final_T, int32_t* n_contrib,
+                              int32_t* point_list, int32_t* ranges, int64_t* visible,
+                              void* stream);
+
+/* Bytes of workspace hrf_raster_backward needs. */
+size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t planes);
+
+/* Backward: render backward (back-to-front recurrence) and the fused
+ * geometry backward (means2D, cov2D, Jacobian, Sigma chains).
+ * Outputs, all fully overwritten: grad_cam (N,3), grad_z (N) (always 0),
+ * grad_quats (N,4), grad_scales (N,3), grad_colours (N,C), grad_phase (N,C),
+ * grad_opacities (N), grad_plane_probs (N,P).
+ * Replaces Rasterizer::backward (rasterizer_splat.cu:551-684),
+ * backward_splat.cu:78-417 and backward.cu. */
+int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
+                        const void* grad_field, const float* final_T,
+                        const int32_t* n_contrib, const int32_t* point_list,
+                        const int32_t* ranges, int64_t num_pairs,
+                        void* ws, size_t ws_bytes,
+                        float* grad_cam, float* grad_z, float* grad_quats,
+                        float* grad_scales, float* grad_colours, float* grad_phase,
+                        float* grad_opacities, float* grad_plane_probs,
+                        void* stream);
+
+/* ---------------- band-limited ASM (replaces cuda_modules) ---------------- */
+
+/* Spectral multiply on a pre-shifted (fftshift) spectrum, reading the
+ * frequency grids, exactly as bound by cuda_modules.bandlimited_propagation_
+ * forward(re, im, FX, FY, wavelength, distance, aperture, pitch)
+ * (cuda_prop/cpp/module_def.cpp:4-13,55-56; cuda_prop/cpp/bandlimited_
+ * propagation.cpp:34-54).  nx = rows, ny = cols; only nx == ny is defined. */
+int hrf_asm_spectral_forward(const float* re, const float* im,
+                             const float* fx_grid, const float* fy_grid,
+                             float* out_re, float* out_im, int32_t nx, int32_t ny,
+                             float wavelength, float distance, float aperture,
+                             float pixel_pitch, void* stream);
+
+/* Adjoint spectral multiply (conjugate transfer function).  field_re/im are
+ * accepted for signature parity and unused, as in the reference
+ * (cuda_prop/cpp/bandlimited_propagation.cpp:57-80). */
+int hrf_asm_spectral_backward(const float* grad_re, const float* grad_im,
+                              const float* field_re, const float* field_im,
+                              const float* fx_grid, const float* fy_grid,
+                              float* out_re, float* out_im, int32_t nx, int32_t ny,
+                              float wavelength, float distance, float aperture,
+                              float pixel_pitch, void* stream);
+
+/* Workspace for the whole-propagation entry points below: M = 2*S. */
+size_t hrf_asm_workspace_size(int32_t planes, int32_t channels, int32_t size);
+
+/* One field (H,W) c64 -> (S,S) c64: centred zero pad to (2S,2S), FFT,
+ * transfer function x band-limit x aperture, inverse FFT (1/M^2), centred
+ * crop.  Replaces BandlimitedPropagationFunction.forward
+ * (cuda_prop/python_function.py:111-163).  pixel_pitch is double because the
+ * reference builds its frequency grid with torch.fft.fftfreq(d=pitch) from a
+ * Python float. */
+int hrf_asm_forward(const void* field, int32_t height, int32_t width, int32_t size,
+                    float wavelength, double pixel_pitch, float distance,
+                    float aperture, void* out, void* ws, size_t ws_bytes, void* stream);
+
+/* Exact adjoint of hrf_asm_forward: (S,S) c64 -> (H,W) c64.  Replaces
+ * BandlimitedPropagationFunction.backward (python_function.py:166-218). */
+int hrf_asm_adjoint(const void* grad_out, int32_t height, int32_t width, int32_t size,
+                    float wavelength, double pixel_pitch, float distance,
+                    float aperture, void* grad_field, void* ws, size_t ws_bytes,
+                    void* stream);
+
+/* All planes and wavelengths at once: fields (P,C,H,W) c64 ->
+ * hologram (C,S,S) c64 with hologram[c] = sum_p propagate(fields[p,c],
+ * wavelengths[c], distances[p]).  wavelengths (C) and distances (P) are host
+ * arrays of the per-call propagation distances.  Replaces the per-(p,c) loop
+ * and the Python sum in Scene.splat (model.py:1251-1272). */
+int hrf_asm_multiplane_forward(const void* fields, int32_t planes, int32_t channels,
+                               int32_t height, int32_t width, int32_t size,
+                               const float* wavelengths, const float* distances,
+                               double pixel_pitch, float aperture, void* hologram,
+                               void* ws, size_t ws_bytes, void* stream);
+
+/* Adjoint of hrf_asm_multiplane_forward: grad hologram (C,S,S) ->
+ * grad fields (P,C,H,W). */
+int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes,
+                               int32_t channels, int32_t height, int32_t width,
+                               int32_t size, const float* wavelengths,
+                               const float* distances, double pixel_pitch,
+                               float aperture, void* grad_fields, void* ws,
+                               size_t ws_bytes, void* stream);
+
+/* Releases cached hipFFT plans (optional; also released at unload). */
+void hrf_release_caches(void);
+
+/* ---------------- stage tracing (no counterpart in the reference, which
+ * prints per-phase CUDA event times from train.py:263-344) ---------------- */
+
+/* Enables (1) or disables (0) stage tracing.  While enabled, every kernel
+ * stage of the calls above is bracketed by a pair of hipEvents recorded on
+ * the caller's stream. */
+int hrf_trace_enable(int on);
+/* Clears all recorded stage events. */
+void hrf_trace_reset(void);
+/* Waits for the recorded events of `stage` and returns the number of
+ * launches and their summed duration in milliseconds since the last reset.
+ * Stages: project, depth_sort, scan, emit, tile_sort, ranges, render_fwd,
+ * render_bwd, geom_bwd, asm_pad, asm_fft, asm_mac_fwd, asm_mac_adj,
+ * asm_crop. */
+int hrf_trace_read(const char* stage, int64_t* launches, double* total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HRF_H */

@@ -1,0 +1,204 @@
+"""The reference's CPU PyTorch path, restated — TEST INFRASTRUCTURE / BASELINE ONLY.
+
+Used only by bench.py's cpu_baseline leg (and tests).  It restates, with
+torch ops on the CPU, the path a user of the reference gets without the CUDA
+extension:
+
+* ``Scene.splat(render_using_python=True)`` (model.py:1194-1228): 64x64
+  tiles, per tile the Gaussians whose 3-sigma diagonal box (clamped to the
+  image) overlaps it (``calculate_gaussian_bounds``, model.py:553-592);
+* ``splat_tile_python`` (model.py:1276-1363) with the geometry fallbacks
+  ``compute_means_2D`` / ``compute_cov_2D`` / ``_compute_jacobian`` /
+  ``compute_cov_3D`` / ``invert_cov_2D`` (model.py:406-551), the cumprod
+  transmittance (model.py:1090-1103), and the CUDA-only helper ops
+  (batch_matrix_mult_cuda.cu:48-49, sum_last_dim_cuda.cu:39,
+  element_wise_mult_cuda.cu:34-35) replaced by the equivalent torch ops;
+* the pure-torch band-limited ASM (python_function.py:35-78) per (plane,
+  wavelength) with ``distance = -distances[p]``, summed over planes.
+
+Backward is torch autograd through the same graph.  pytorch3d's
+quaternion_to_matrix and odak's pad/crop/circular mask are restated from
+their published definitions (centred pad/crop; a disc of radius r about the
+grid centre).  Semantics differ slightly from the CUDA rasterizer (no 0.99
+alpha clamp, 3-sigma boxes, float32 kz) — this path is for timing, parity is
+measured against hrf_oracle.c.
+"""
+from __future__ import annotations
+
+import math
+import time
+
+import torch
+
+
+def quaternion_to_matrix(q):
+    r, i, j, k = torch.unbind(q, -1)
+    two_s = 2.0 / (q * q).sum(-1)
+    o = torch.stack((
+        1 - two_s * (j * j + k * k), two_s * (i * j - k * r), two_s * (i * k + j * r),
+        two_s * (i * j + k * r), 1 - two_s * (i * i + k * k), two_s * (j * k - i * r),
+        two_s * (i * k - j * r), two_s * (j * k + i * r), 1 - two_s * (i * i + j * j)), -1)
+    return o.reshape(q.shape[:-1] + (3, 3))
+
+
+def means_2d(cam, fx, fy, px, py, near=1.0, far=1000.0):
+    mask = (cam[:, 2] > near) & (cam[:, 2] < far)
+    inv_z = 1.0 / cam[:, 2].unsqueeze(1)
+    xy = -cam[:, :2] * inv_z
+    m = torch.stack([fx * xy[:, 0] + px, fy * xy[:, 1] + py], 1)
+    return torch.where(mask[:, None], m, torch.full_like(m, 1e6))
+
+
+def jacobian(cam, fx, fy, W, H, near=1.0, far=1000.0):
+    lim_x = 1.3 * (0.5 * W / fx)
+    lim_y = 1.3 * (0.5 * H / fy)
+    tx, ty, tz = cam[:, 0], cam[:, 1], cam[:, 2]
+    mask = ((tz > near) & (tz < far)).float()
+    tx = torch.clamp(tx / tz, -lim_x, lim_x) * tz
+    ty = torch.clamp(ty / tz, -lim_y, lim_y) * tz
+    z = torch.zeros_like(tz)
+    J = torch.stack([fx / tz, z, -(fx * tx) / (tz * tz), z, fy / tz, -(fy * ty) / (tz * tz)], 1)
+    return J.reshape(-1, 2, 3) * mask[:, None, None]
+
+
+def cov_2d(cam, quats, scales, fx, fy, R, W, H):
+    J = jacobian(cam, fx, fy, W, H)
+    n = J.shape[0]
+    Wm = R.expand(n, 3, 3)
+    S = torch.diag_embed(scales)
+    rots = quaternion_to_matrix(quats)
+    cov3 = rots @ S @ S.transpose(1, 2) @ rots.transpose(1, 2)
+    c = J @ Wm @ cov3 @ Wm.transpose(1, 2) @ J.transpose(1, 2)
+    return c + 0.3 * torch.eye(2)
+
+
+def invert_cov_2d(c):
+    det = (c[:, 0, 0] * c[:, 1, 1] - c[:, 1, 0] * c[:, 0, 1])[:, None, None]
+    inv = torch.stack([c[:, 1, 1], -c[:, 0, 1], -c[:, 1, 0], c[:, 0, 0]], 1).reshape(-1, 2, 2)
+    return inv / det
+
+
+def gaussian_bounds(m, c, W, H, conf=3.0):
+    rx = conf * torch.sqrt(c[:, 0, 0])
+    ry = conf * torch.sqrt(c[:, 1, 1])
+    return torch.stack([torch.clamp(m[:, 0] - rx, 0, W - 1), torch.clamp(m[:, 1] - ry, 0, H - 1),
+                        torch.clamp(m[:, 0] + rx, 0, W - 1), torch.clamp(m[:, 1] + ry, 0, H - 1)], 1)
+
+
+def splat_tile(params, idx, x0, y0, tw, th, fx, fy, px, py, R, W, H, nplanes, nch):
+    cam, quats, scales, colours, phase, opac, pprobs = params
+    if idx.numel() == 0:
+        return torch.zeros((nplanes, nch, th, tw), dtype=torch.complex64)
+    xs, ys = torch.meshgrid(torch.arange(x0, x0 + tw), torch.arange(y0, y0 + th), indexing="xy")
+    pts = torch.stack([xs.flatten(), ys.flatten()], 1).float()
+    tc = cam[idx]
+    valid = (tc[:, 2] > 1.0) & (tc[:, 2] < 1000.0)
+    idx = idx[valid]
+    tc = tc[valid]
+    tm = means_2d(tc, fx, fy, px, py).unsqueeze(1)
+    diff = pts.unsqueeze(0) - tm
+    c2 = cov_2d(tc, quats[idx], scales[idx], fx, fy, R, W, H)
+    ci = invert_cov_2d(c2)
+    term = torch.matmul(diff, ci)                 # compute_bmm_cuda
+    term = (term * diff)                          # element_wise_multiplication_cuda
+    term = term[..., 0] + term[..., 1]            # sum_last_dim_cuda
+    term = term.view(-1, th, tw)
+    gexp = torch.exp(-0.5 * term)
+    base = opac[idx].view(-1, 1, 1) * gexp
+    tp = pprobs[idx]
+    out = []
+    for p in range(nplanes):
+        a = base * tp[:, p].view(-1, 1, 1)
+        one = torch.ones((1, th, tw))
+        T = torch.cumprod(torch.cat((one, 1.0 - a), 0), 0)[:-1]
+        T = torch.where(T < 1e-4, torch.zeros_like(T), T)
+        chans = []
+        for c in range(nch):
+            col = colours[idx, c].view(-1, 1, 1)
+            ph = phase[idx, c].view(-1, 1, 1)
+            chans.append(torch.sum(col * a * T * torch.exp(1j * ph), 0))
+        out.append(torch.stack(chans, 0))
+    return torch.stack(out, 0)
+
+
+def asm_torch(field, wavelength, pitch, distance, S, aperture):
+    M = 2 * S
+    H, W = field.shape
+    pad = torch.zeros((M, M), dtype=torch.complex64)
+    r0, c0 = M // 2 - H // 2, M // 2 - W // 2
+    pad = pad.index_put((torch.arange(r0, r0 + H)[:, None], torch.arange(c0, c0 + W)[None, :]),
+                        field)
+    yy, xx = torch.meshgrid(torch.arange(M), torch.arange(M), indexing="ij")
+    ap = (((xx - M / 2) ** 2 + (yy - M / 2) ** 2) < aperture ** 2).float()
+    ff = torch.fft.fftshift(torch.fft.fft2(pad))
+    fx = torch.fft.fftshift(torch.fft.fftfreq(M, d=pitch))
+    FX, FY = torch.meshgrid(fx, fx, indexing="ij")
+    L = torch.tensor(pitch * M)
+    d = torch.tensor(distance)
+    lam = torch.tensor(wavelength)
+    fxmax = 1 / torch.sqrt((2 * d * (1 / L)) ** 2 + 1) / lam
+    mask = (torch.abs(FX) < fxmax) & (torch.abs(FY) < fxmax)
+    k = 2 * torch.pi / lam
+    kz = torch.sqrt(k ** 2 - (2 * torch.pi * FX) ** 2 - (2 * torch.pi * FY) ** 2)
+    kz = torch.where(torch.isnan(kz), torch.zeros_like(kz), kz)
+    Hf = torch.exp(1j * d * kz) * mask
+    out = torch.fft.ifft2(torch.fft.ifftshift(ff * Hf * ap))
+    s0 = M // 2 - S // 2
+    return out[s0:s0 + S, s0:s0 + S]
+
+
+def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
+    """Time the CPU path on a bounded sample of one frame of scene ``sc``
+    (package Scene).  Returns (ms_per_frame_estimate, sample description)."""
+    torch.manual_seed(seed)
+    spec = sc.spec
+    W, H, P, C = spec.width, spec.height, spec.planes, len(spec.wavelengths)
+    t = lambda a: torch.from_numpy(a.copy())  # noqa: E731
+    params = [t(sc.cam_means).requires_grad_(True), t(sc.quats).requires_grad_(True),
+              t(sc.scales).requires_grad_(True), t(sc.colours).requires_grad_(True),
+              t(sc.phase).requires_grad_(True), t(sc.opac).requires_grad_(True),
+              t(sc.pprobs).requires_grad_(True)]
+    R = t(sc.view)
+    fx, fy, px, py = sc.fx, sc.fy, sc.px, sc.py
+    tile = 64
+    xt, yt = math.ceil(W / tile), math.ceil(H / tile)
+    order = torch.randperm(xt * yt).tolist()
+    # Per-frame setup the reference runs once: means/cov/bounds for all Gaussians.
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        m = means_2d(params[0], fx, fy, px, py)
+        c2 = cov_2d(params[0], params[1], params[2], fx, fy, R, W, H)
+        bounds = gaussian_bounds(m, c2, W, H)
+    setup_s = time.perf_counter() - t0
+    done = 0
+    raster_s = 0.0
+    for ti in order:
+        yi, xi = divmod(ti, xt)
+        x, y = xi * tile, yi * tile
+        tw, th = min(tile, W - x), min(tile, H - y)
+        sel = ((bounds[:, 0] <= x + tw - 1) & (bounds[:, 2] >= x) & (bounds[:, 1] <= y + th - 1) &
+               (bounds[:, 3] >= y))
+        idx = torch.where(sel)[0]
+        t1 = time.perf_counter()
+        out = splat_tile(params, idx, x, y, tw, th, fx, fy, px, py, R, W, H, P, C)
+        if out.requires_grad:
+            g = torch.randn(out.shape, dtype=torch.complex64)
+            (out.real * g.real + out.imag * g.imag).sum().backward()
+        raster_s += time.perf_counter() - t1
+        done += 1
+        if raster_s > budget_s * 0.7:
+            break
+    raster_frame_s = raster_s * (xt * yt) / done
+    # ASM: one (plane, wavelength) propagation forward+backward, times P*C.
+    f = torch.randn((H, W), dtype=torch.complex64).requires_grad_(True)
+    S = spec.size
+    t2 = time.perf_counter()
+    o = asm_torch(f, spec.wavelengths[0], 3.74e-6, -spec.distances[0], S, float(S))
+    g = torch.randn(o.shape, dtype=torch.complex64)
+    (o.real * g.real + o.imag * g.imag).sum().backward()
+    asm_one_s = time.perf_counter() - t2
+    total_s = setup_s + raster_frame_s + asm_one_s * P * C
+    desc = (f"reference CPU PyTorch path restated (oracle/cpu_baseline.py): {done} of {xt * yt} "
+            f"64x64 tiles fwd+bwd (random sample, scaled by tile count) + 1 of {P * C} ASM "
+            f"fwd+bwd (scaled by P*C) + projection setup; {spec.name} N={sc.cam_means.shape[0]}")
+    return total_s * 1000.0, desc

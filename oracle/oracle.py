@@ -1,0 +1,344 @@
+"""Python face of the CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this module, and only as the checker.  The product package
+never imports it.
+
+It wraps ``liboracle_hrf.so`` (``hrf_oracle.c``, a literal C restatement of
+the reference CUDA code) and composes the reference's ASM propagation
+(``cuda_prop/python_function.py:111-218``) from that spectral kernel and
+numpy's FFT (pocketfft, computed in double precision).
+
+Pinning status (what independently checks each function) is recorded in
+``tests/test_oracle_pinning.py`` and listed in DESIGN.md.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_hrf.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    src = os.path.join(_HERE, "hrf_oracle.c")
+    if not os.path.exists(_LIB_PATH) or (
+        os.path.exists(src) and os.path.getmtime(src) > os.path.getmtime(_LIB_PATH)
+    ):
+        build()
+    L = ctypes.CDLL(_LIB_PATH)
+    L.oracle_cov3d.argtypes = [_f32p, _f32p, _f32p]
+    L.oracle_project.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _flt, _flt, _flt, _flt,
+                                 _int, _int, _flt, _flt, _f32p, _f32p, _f32p, _f32p, _f32p]
+    L.oracle_preprocess.argtypes = [_i64, _f32p, _f32p, _f32p, _int, _int, _flt, _flt,
+                                    _i32p, _u32p, _u32p]
+    L.oracle_count_pairs.argtypes = [_i64, _u32p]
+    L.oracle_count_pairs.restype = _i64
+    L.oracle_bin.argtypes = [_i64, _f32p, _u32p, _u32p, _int, _int, _i64, _i32p, _i32p]
+    L.oracle_render_forward.argtypes = [_int, _int, _int, _int, _i32p, _i32p, _f32p, _f32p,
+                                        _f32p, _f32p, _f32p, _f32p, _f32p, _flt, _flt,
+                                        _f32p, _f32p, _i32p]
+    L.oracle_render_backward.argtypes = [_i64, _int, _int, _int, _int, _i32p, _i32p, _f32p,
+                                         _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p,
+                                         _f32p, _f64p, _f64p, _f64p, _f64p, _f64p, _f64p]
+    L.oracle_geom_backward.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _flt, _flt, _int,
+                                       _int, _flt, _flt, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                       _f32p, _f32p]
+    L.oracle_asm_spectral.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _int, _int,
+                                      _flt, _flt, _flt, _flt, _int]
+    L.oracle_asm_consts.argtypes = [_flt, _flt, _flt, _int, _f32p]
+    _lib = L
+    return L
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+@dataclass
+class Camera:
+    fx: float
+    fy: float
+    px: float
+    py: float
+    view: np.ndarray  # (3,3) float32
+    width: int
+    height: int
+    near: float = 1.0
+    far: float = 1000.0
+
+
+@dataclass
+class Gaussians:
+    cam_means: np.ndarray  # (N,3)
+    z: np.ndarray  # (N,)
+    quats: np.ndarray  # (N,4)
+    scales: np.ndarray  # (N,3)
+    colours: np.ndarray  # (N,C)
+    phase: np.ndarray  # (N,C)
+    opac: np.ndarray  # (N,)
+    pprobs: np.ndarray  # (N,P)
+
+    @property
+    def n(self):
+        return int(self.cam_means.shape[0])
+
+    @property
+    def C(self):
+        return int(self.colours.shape[1])
+
+    @property
+    def P(self):
+        return int(self.pprobs.shape[1])
+
+
+def cov3d(quats, scales):
+    L = lib()
+    n = quats.shape[0]
+    out = np.zeros((n, 9), np.float32)
+    q = _f32(quats)
+    s = _f32(scales)
+    for g in range(n):
+        o = np.zeros(9, np.float32)
+        L.oracle_cov3d(q[g], s[g], o)
+        out[g] = o
+    return out.reshape(n, 3, 3)
+
+
+def project(g: Gaussians, cam: Camera):
+    """means2D (N,2), J (N,2,3), Sigma (N,3,3), JW (N,2,3), cov2D (N,4)."""
+    L = lib()
+    n = g.n
+    m = np.zeros((n, 2), np.float32)
+    J = np.zeros((n, 6), np.float32)
+    S = np.zeros((n, 9), np.float32)
+    JW = np.zeros((n, 6), np.float32)
+    c2 = np.zeros((n, 4), np.float32)
+    L.oracle_project(n, _f32(g.cam_means), _f32(g.quats), _f32(g.scales), _f32(cam.view),
+                     cam.fx, cam.fy, cam.px, cam.py, cam.width, cam.height, cam.near, cam.far,
+                     m, J, S, JW, c2)
+    return dict(means2d=m, J=J.reshape(n, 2, 3), sigma=S.reshape(n, 3, 3),
+                JW=JW.reshape(n, 2, 3), cov2d=c2)
+
+
+def preprocess(means2d, cov2d, z, cam: Camera):
+    L = lib()
+    n = means2d.shape[0]
+    radii = np.zeros(n, np.int32)
+    tiles = np.zeros(n, np.uint32)
+    rect = np.zeros((n, 4), np.uint32)
+    L.oracle_preprocess(n, _f32(means2d), _f32(cov2d), _f32(z), cam.width, cam.height,
+                        cam.near, cam.far, radii, tiles, rect)
+    return radii, tiles, rect
+
+
+def bin_pairs(z, tiles, rect, cam: Camera):
+    L = lib()
+    n = z.shape[0]
+    k = int(L.oracle_count_pairs(n, np.ascontiguousarray(tiles, np.uint32)))
+    gx = (cam.width + 15) // 16
+    gy = (cam.height + 15) // 16
+    pl = np.zeros(max(k, 1), np.int32)
+    ranges = np.zeros((gx * gy, 2), np.int32)
+    L.oracle_bin(n, _f32(z), np.ascontiguousarray(tiles, np.uint32),
+                 np.ascontiguousarray(rect, np.uint32), cam.width, cam.height, k, pl, ranges)
+    return pl[:k], ranges
+
+
+def render_forward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges):
+    L = lib()
+    P, C, H, W = g.P, g.C, cam.height, cam.width
+    field = np.zeros((P, C, H, W, 2), np.float32)
+    fT = np.zeros((P, H, W), np.float32)
+    nc = np.zeros((P, H, W), np.int32)
+    pl = np.ascontiguousarray(point_list if len(point_list) else np.zeros(1), np.int32)
+    L.oracle_render_forward(W, H, P, C, np.ascontiguousarray(ranges, np.int32), pl,
+                            _f32(means2d), _f32(cov2d), _f32(g.z), _f32(g.colours),
+                            _f32(g.phase), _f32(g.opac), _f32(g.pprobs), cam.near, cam.far,
+                            field, fT, nc)
+    return field[..., 0] + 1j * field[..., 1], fT, nc
+
+
+def render_backward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges, final_T,
+                    n_contrib, grad_field):
+    L = lib()
+    n, P, C, H, W = g.n, g.P, g.C, cam.height, cam.width
+    gf = np.ascontiguousarray(
+        np.stack([grad_field.real, grad_field.imag], axis=-1), dtype=np.float32)
+    out = dict(means2d=np.zeros((n, 2)), cov2d=np.zeros((n, 4)), colours=np.zeros((n, C)),
+               phase=np.zeros((n, C)), opac=np.zeros(n), plane=np.zeros((n, P)))
+    pl = np.ascontiguousarray(point_list if len(point_list) else np.zeros(1), np.int32)
+    L.oracle_render_backward(n, W, H, P, C, np.ascontiguousarray(ranges, np.int32), pl,
+                             _f32(means2d), _f32(cov2d), _f32(g.colours), _f32(g.phase),
+                             _f32(g.opac), _f32(g.pprobs), _f32(final_T),
+                             np.ascontiguousarray(n_contrib, np.int32), gf, out["means2d"],
+                             out["cov2d"], out["colours"], out["phase"], out["opac"],
+                             out["plane"])
+    return out
+
+
+def geom_backward(g: Gaussians, cam: Camera, grad_means2d, grad_cov2d, want_links=False):
+    L = lib()
+    n = g.n
+    gc = np.zeros((n, 3), np.float32)
+    gq = np.zeros((n, 4), np.float32)
+    gs = np.zeros((n, 3), np.float32)
+    dsig = np.zeros((n, 9), np.float32)
+    dJ = np.zeros((n, 6), np.float32)
+    L.oracle_geom_backward(n, _f32(g.cam_means), _f32(g.quats), _f32(g.scales), _f32(cam.view),
+                           cam.fx, cam.fy, cam.width, cam.height, cam.near, cam.far,
+                           _f32(grad_means2d), _f32(grad_cov2d), gc, gq, gs, dsig, dJ)
+    if want_links:
+        return gc, gq, gs, dsig.reshape(n, 3, 3), dJ.reshape(n, 2, 3)
+    return gc, gq, gs
+
+
+def visible_indices(g: Gaussians, cam: Camera):
+    z = g.cam_means[:, 2]
+    return np.nonzero((z > 0.2) & (z > cam.near) & (z < cam.far))[0].astype(np.int64)
+
+
+def rasterize_forward(g: Gaussians, cam: Camera):
+    """Full SplatTileCuda forward: field (P,C,H,W) c64 + forward_info."""
+    pr = project(g, cam)
+    radii, tiles, rect = preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
+    pl, ranges = bin_pairs(g.z, tiles, rect, cam)
+    K = len(pl)
+    if K == 0:
+        P, C, H, W = g.P, g.C, cam.height, cam.width
+        return dict(field=np.zeros((P, C, H, W), np.complex64), final_T=np.ones((P, H, W), np.float32),
+                    n_contrib=np.zeros((P, H, W), np.int32), point_list=np.zeros(1, np.int32),
+                    ranges=ranges, visible=np.zeros(0, np.int64), K=0, proj=pr, radii=radii,
+                    tiles=tiles, rect=rect)
+    field, fT, nc = render_forward(g, cam, pr["means2d"], pr["cov2d"], pl, ranges)
+    return dict(field=field.astype(np.complex64), final_T=fT, n_contrib=nc, point_list=pl,
+                ranges=ranges, visible=visible_indices(g, cam), K=K, proj=pr, radii=radii,
+                tiles=tiles, rect=rect)
+
+
+def rasterize_backward(g: Gaussians, cam: Camera, fwd, grad_field):
+    """Full Rasterizer::backward: the 8 gradients (float32)."""
+    pr = fwd["proj"]
+    rb = render_backward(g, cam, pr["means2d"], pr["cov2d"], fwd["point_list"], fwd["ranges"],
+                         fwd["final_T"], fwd["n_contrib"], grad_field)
+    gc, gq, gs = geom_backward(g, cam, rb["means2d"].astype(np.float32),
+                               rb["cov2d"].astype(np.float32))
+    return dict(cam=gc, z=np.zeros(g.n, np.float32), quats=gq, scales=gs,
+                colours=rb["colours"].astype(np.float32), phase=rb["phase"].astype(np.float32),
+                opac=rb["opac"].astype(np.float32), plane=rb["plane"].astype(np.float32),
+                render=rb)
+
+
+# ------------------------------------------------------------------ ASM ---
+
+def fftfreq_f32(n: int, d: float) -> np.ndarray:
+    """torch.fft.fftfreq(n, d) in float32: float32(bin) * float32(1/(n*d))."""
+    k = np.fft.fftfreq(n, d=1.0 / n)
+    return (k.astype(np.float32) * np.float32(1.0 / (n * d))).astype(np.float32)
+
+
+def freq_grids(M: int, pitch: float):
+    """FX, FY = meshgrid(fftshift(fftfreq)), indexing='ij' (python_function.py:137-142)."""
+    f = np.fft.fftshift(fftfreq_f32(M, pitch))
+    FX, FY = np.meshgrid(f, f, indexing="ij")
+    return np.ascontiguousarray(FX, np.float32), np.ascontiguousarray(FY, np.float32)
+
+
+def asm_spectral(re, im, FX, FY, wavelength, distance, aperture, pitch, adjoint=False):
+    L = lib()
+    nx, ny = re.shape
+    ore = np.zeros_like(_f32(re))
+    oim = np.zeros_like(_f32(im))
+    L.oracle_asm_spectral(_f32(re), _f32(im), _f32(FX), _f32(FY), ore, oim, nx, ny,
+                          np.float32(wavelength), np.float32(distance), np.float32(aperture),
+                          np.float32(pitch), 1 if adjoint else 0)
+    return ore, oim
+
+
+def asm_consts(wavelength, distance, pitch, n):
+    out = np.zeros(4, np.float32)
+    lib().oracle_asm_consts(np.float32(wavelength), np.float32(distance), np.float32(pitch), n, out)
+    return out
+
+
+def zero_pad(field, size):
+    """Centred zero pad, start = size//2 - n//2 (odak zero_pad, 'center')."""
+    H, W = field.shape[-2:]
+    out = np.zeros(field.shape[:-2] + tuple(size), dtype=np.complex128)
+    r0, c0 = size[0] // 2 - H // 2, size[1] // 2 - W // 2
+    out[..., r0:r0 + H, c0:c0 + W] = field
+    return out
+
+
+def crop_center(field, size):
+    """Centred crop, start = M//2 - s//2 (odak crop_center with size)."""
+    M0, M1 = field.shape[-2:]
+    r0, c0 = M0 // 2 - size[0] // 2, M1 // 2 - size[1] // 2
+    return field[..., r0:r0 + size[0], c0:c0 + size[1]]
+
+
+def asm_forward(field, wavelength, pitch, distance, S, aperture):
+    """BandlimitedPropagationFunction.forward (python_function.py:111-163)."""
+    M = 2 * S
+    padded = zero_pad(field, (M, M))
+    ff = np.fft.fftshift(np.fft.fft2(padded))
+    FX, FY = freq_grids(M, pitch)
+    ore, oim = asm_spectral(ff.real, ff.imag, FX, FY, wavelength, distance, aperture, pitch)
+    out = np.fft.ifft2(np.fft.ifftshift(ore.astype(np.float64) + 1j * oim.astype(np.float64)))
+    return crop_center(out, (S, S))
+
+
+def asm_adjoint(grad, H, W, wavelength, pitch, distance, S, aperture):
+    """BandlimitedPropagationFunction.backward (python_function.py:166-218)."""
+    M = 2 * S
+    padded = zero_pad(grad, (M, M))
+    gf = np.fft.fftshift(np.fft.fft2(padded))
+    FX, FY = freq_grids(M, pitch)
+    ore, oim = asm_spectral(gf.real, gf.imag, FX, FY, wavelength, distance, aperture, pitch,
+                            adjoint=True)
+    out = np.fft.ifft2(np.fft.ifftshift(ore.astype(np.float64) + 1j * oim.astype(np.float64)))
+    return crop_center(out, (H, W))
+
+
+def multiplane_forward(fields, wavelengths, distances, pitch, S, aperture):
+    """Scene.splat's per-(p,c) loop and Python sum (model.py:1251-1272)."""
+    P, C = fields.shape[:2]
+    holo = np.zeros((C, S, S), np.complex128)
+    for p in range(P):
+        for c in range(C):
+            holo[c] += asm_forward(fields[p, c], wavelengths[c], pitch, distances[p], S, aperture)
+    return holo
+
+
+def multiplane_adjoint(grad_holo, H, W, wavelengths, distances, pitch, S, aperture):
+    C = grad_holo.shape[0]
+    P = len(distances)
+    out = np.zeros((P, C, H, W), np.complex128)
+    for p in range(P):
+        for c in range(C):
+            out[p, c] = asm_adjoint(grad_holo[c], H, W, wavelengths[c], pitch, distances[p], S,
+                                    aperture)
+    return out
