@@ -405,6 +405,12 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
                              &in_b, s));
   }
   const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
+  // The sorted values must end in point_list whatever the pass count did
+  // (a single pair is never moved by the sort).
+  const uint32_t* sorted_vals = in_b ? vals_b : vals_a;
+  if (sorted_vals != reinterpret_cast<uint32_t*>(point_list))
+    HRF_HIP(hipMemcpyAsync(point_list, sorted_vals, num_pairs * sizeof(uint32_t),
+                           hipMemcpyDeviceToDevice, s));
   {
     HRF_STAGE("ranges", s);
     HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
@@ -415,6 +421,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.pmask = w.pmask;
   rp.rec = w.rec;
   rp.pprobs = g->plane_probs;
+  rp.n = n;
+  rp.num_pairs = num_pairs;
   {
     HRF_STAGE("render_fwd", s);
     HRF_TRY(launch_render_forward(rp, s));
@@ -473,6 +481,8 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     rp.pmask = w.pmask;
     rp.rec = w.rec;
     rp.pprobs = g->plane_probs;
+    rp.n = n;
+    rp.num_pairs = num_pairs;
     rp.C = g->channels;
     rp.P = g->planes;
     rp.W = cam->width;

@@ -203,6 +203,8 @@ struct RenderParams {
   const uint32_t* pmask;
   const float* rec;
   const float* pprobs;
+  int64_t n;          // Gaussians: list entries outside [0, n) are skipped
+  int64_t num_pairs;  // list length: ranges are clamped to [0, num_pairs]
   int C, P, W, H, gx, gy;
   // forward outputs
   float2* field;

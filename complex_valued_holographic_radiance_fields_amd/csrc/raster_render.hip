@@ -32,6 +32,17 @@ __device__ __forceinline__ void map_block(int b, int nb, int P, int* tile, int* 
   *plane = logical - (*tile) * P;
 }
 
+// Tile range [r0, r0+n), clamped to the pair list so malformed caller input
+// (the backward takes ranges from the caller) cannot index out of bounds.
+__device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int* r0, int* n) {
+  const int64_t K = p.num_pairs;
+  int64_t a = p.ranges[2 * tile], b = p.ranges[2 * tile + 1];
+  a = a < 0 ? 0 : (a > K ? K : a);
+  b = b < a ? a : (b > K ? K : b);
+  *r0 = static_cast<int>(a);
+  *n = static_cast<int>(b - a);
+}
+
 // exp(x) through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
@@ -87,8 +98,8 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   const int pxi = tx * kTile + (threadIdx.x & 15);
   const int pyi = ty * kTile + (threadIdx.x >> 4);
   const bool inside = pxi < p.W && pyi < p.H;
-  const int r0 = p.ranges[2 * tile];
-  const int n = p.ranges[2 * tile + 1] - r0;
+  int r0, n;
+  tile_range(p, tile, &r0, &n);
   const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
 
   float T = 1.0f;
@@ -105,7 +116,8 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     int g = 0;
     if (k < n) {
       g = p.plist[r0 + k];
-      mem = (p.pmask[g] >> plane) & 1u;
+      mem = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+            ((p.pmask[g] >> plane) & 1u);
     }
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
@@ -186,8 +198,8 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   const int pxi = tx * kTile + (threadIdx.x & 15);
   const int pyi = ty * kTile + (threadIdx.x >> 4);
   const bool inside = pxi < p.W && pyi < p.H;
-  const int r0 = p.ranges[2 * tile];
-  const int n = p.ranges[2 * tile + 1] - r0;
+  int r0, n;
+  tile_range(p, tile, &r0, &n);
   const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
   const int64_t HW = static_cast<int64_t>(p.W) * p.H;
   const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
@@ -230,7 +242,8 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     int g = 0;
     if (k < end) {
       g = p.plist[r0 + k];
-      mem = (p.pmask[g] >> plane) & 1u;
+      mem = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+            ((p.pmask[g] >> plane) & 1u);
     }
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
