@@ -69,6 +69,9 @@ def main():
     ap.add_argument("--config", default="headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run 3 elementwise copies of 256 MiB (x*2 -> y), a kernel of "
+                         "known HBM traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -86,6 +89,12 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        for _ in range(3):
+            dst = src * 2.0
+        torch.cuda.synchronize()
+        del src, dst
     spec = scenes.config(args.config)
     t_gen = time.perf_counter()
     sc = scenes.generate(spec)

@@ -88,5 +88,22 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> str:
     return LIB_PATH
 
 
+TEST_SRC = os.path.join(REPO_DIR, "tests", "hip", "wave_reduce_test.hip")
+TEST_LIB = os.path.join(REPO_DIR, "tests", "hip", "libwave_test.so")
+
+
+def build_test_library(verbose: bool = False) -> str:
+    """Compile the GPU unit-test kernels of tests/hip (wave reductions)."""
+    cmd = [_hipcc(), *COMMON_FLAGS, "-shared", TEST_SRC, "-o", TEST_LIB + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {TEST_SRC}:\n{res.stdout}\n{res.stderr}")
+    os.replace(TEST_LIB + ".tmp", TEST_LIB)
+    return TEST_LIB
+
+
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv))
+    print(build_test_library(verbose="-v" in sys.argv))

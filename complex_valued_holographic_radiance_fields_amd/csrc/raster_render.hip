@@ -14,12 +14,16 @@
 // blocks round-robin, so consecutive logical ids are given to one XCD and the
 // P planes of a tile (and neighbouring tiles) share that XCD's L2.
 //
-// Backward gradients: per staged Gaussian each wave reduces its 6+2C partial
-// sums with DPP (quad_perm, row mirrors, row_bcast15/31), accumulates the
-// four wave totals with LDS float atomics, and one global atomic per
-// (block, Gaussian, value) lands in a per-Gaussian accumulator.  The
-// reference issues 8+2C global atomics per contributing (pixel, Gaussian).
+// Backward gradients: waves own 8x8 quadrants; each batch stages records
+// with a per-quadrant cull mask (exact: alpha >= 1/255 box and n_contrib
+// bound), each wave walks its own compacted list back to front and reduces
+// the 6+2C per-lane partial sums of G members at once with a 64-value
+// transpose-reduce (v_permlane32/16_swap + DPP), lands the totals in LDS
+// with one ds_add per lane, and flushes one global atomic per (block,
+// Gaussian, value) into a per-Gaussian accumulator.  The reference issues
+// 8+2C global atomics per contributing (pixel, Gaussian).
 #include "hrf_internal.h"
+#include "wave_reduce.h"
 
 namespace hrf {
 namespace {
@@ -46,23 +50,6 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
 // exp(x) through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-}
-
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, true));
-}
-
-// Wave64 sum; the total lands in lane 63.
-__device__ __forceinline__ float wave_sum_to_lane63(float v) {
-  v += dpp_f<0xB1>(v);        // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E>(v);        // quad_perm [2,3,0,1]
-  v += dpp_f<0x141>(v);       // row_half_mirror
-  v += dpp_f<0x140>(v);       // row_mirror
-  v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-  v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
-  return v;
 }
 
 // Ballot compaction of one flag per thread across the block.  Returns the
@@ -180,31 +167,62 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   }
 }
 
+// Conservative screen-space box of the region where a Gaussian can reach
+// alpha >= 1/255 in the backward (power = -q/2 with q = d^T A d, A the conic):
+// alpha = min(.99, o*G*w) >= 1/255 needs q <= 2 ln(255 o w).  The box is
+// widened by 0.1% + 0.01 in q and again in extent, far beyond the rounding of
+// the exp/power evaluation, so culling with it never drops a contribution.
+// Returns false when no pixel can qualify (o*w below 1/255).  A non-positive
+// definite conic or NaN yields an infinite box (never culled).
+__device__ __forceinline__ bool alpha_box(float cxx, float cxy, float czz, float ow,
+                                          float* ex, float* ey) {
+  if (ow * 255.0f < 0.999f) return false;
+  const float q = 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
+  const float det = cxx * czz - cxy * cxy;
+  if (!(det > 0.0f) || !(cxx > 0.0f) || !(czz > 0.0f)) {
+    *ex = *ey = INFINITY;
+    return true;
+  }
+  *ex = sqrtf(q * czz / det) * 1.0001f + 1e-3f;
+  *ey = sqrtf(q * cxx / det) * 1.0001f + 1e-3f;
+  return true;
+}
+
+// Backward.  Waves own 8x8 quadrants of the tile.  Per batch, every staged
+// Gaussian gets a 4-bit quadrant mask (its alpha >= 1/255 box intersects the
+// quadrant and its list position is below that quadrant's max n_contrib);
+// each wave walks only its own compacted list, back to front, in groups of
+// G members whose 6+2C partial sums per lane are reduced together with one
+// transpose_reduce64.  Skipping a member for a whole wave is exact: every
+// lane of that wave would skip it (alpha < 1/255 or position >= n_contrib).
 template <int C>
 __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   constexpr int NQ = rec_quads(C);
   constexpr int RS = rec_stride(C);
   constexpr int NV = 6 + 2 * C;
+  constexpr int G = 64 / NV;
   __shared__ float4 s_rec[kBlock * NQ];
   __shared__ int s_k[kBlock];
   __shared__ int s_g[kBlock];
   __shared__ float s_acc[kBlock * NV];
-  __shared__ int s_wt[kBlock / 64];
-  __shared__ int s_maxlast;
+  __shared__ unsigned short s_wl[4][kBlock];
+  __shared__ int s_cnt[4][5];
+  __shared__ int s_wmax[4];
 
   int tile, plane;
   map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
   const int tx = tile % p.gx, ty = tile / p.gx;
-  const int pxi = tx * kTile + (threadIdx.x & 15);
-  const int pyi = ty * kTile + (threadIdx.x >> 4);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pxi = tx * kTile + (wave & 1) * 8 + (lane & 7);
+  const int pyi = ty * kTile + (wave >> 1) * 8 + (lane >> 3);
   const bool inside = pxi < p.W && pyi < p.H;
   int r0, n;
   tile_range(p, tile, &r0, &n);
   const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
   const int64_t HW = static_cast<int64_t>(p.W) * p.H;
   const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
-  const int lane = threadIdx.x & 63;
   const int AS = acc_stride(C, p.P);
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
   float T = 0.0f;
   int last = 0;
@@ -221,11 +239,20 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       gim[c] = gv.y;
     }
   }
-  if (threadIdx.x == 0) s_maxlast = 0;
+  {
+    int m = inside ? last : 0;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = max(m, __shfl_xor(m, d, 64));
+    if (lane == 0) s_wmax[wave] = m < n ? m : n;
+  }
   __syncthreads();
-  if (inside && last > 0) atomicMax(&s_maxlast, last);
-  __syncthreads();
-  const int maxlast = s_maxlast < n ? s_maxlast : n;
+  int wmax[4];
+  int maxlast = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    wmax[w] = s_wmax[w];
+    maxlast = max(maxlast, wmax[w]);
+  }
 
   float accr[C], acci[C], lastr[C], lasti[C];
 #pragma unroll
@@ -233,93 +260,145 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   float last_alpha = 0.0f;
   const float half_w = 0.5f * static_cast<float>(p.W);
   const float half_h = 0.5f * static_cast<float>(p.H);
+  const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
 
   for (int end = maxlast; end > 0; end -= kBlock) {
     const int start = end > kBlock ? end - kBlock : 0;
     __syncthreads();
     const int k = start + static_cast<int>(threadIdx.x);
-    bool mem = false;
     int g = 0;
+    unsigned qm = 0;
+    float4 rq[NQ];
+    float wpl = 0.0f;
     if (k < end) {
       g = p.plist[r0 + k];
-      mem = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
-            ((p.pmask[g] >> plane) & 1u);
-    }
-    int cnt;
-    const int pos = block_compact(mem, s_wt, &cnt);
-    if (mem) {
-      const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
+      if (static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+          ((p.pmask[g] >> plane) & 1u)) {
+        const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) s_rec[pos * NQ + q] = src[q];
-      s_rec[pos * NQ + 1].w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
-      s_k[pos] = k;
-      s_g[pos] = g;
+        for (int q = 0; q < NQ; ++q) rq[q] = src[q];
+        wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
+        float ex, ey;
+        if (alpha_box(rq[0].z, rq[0].w, rq[1].y, rq[1].z * wpl, &ex, &ey)) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float x0 = tx0 + (w & 1) * 8, y0 = ty0 + (w >> 1) * 8;
+            const bool hit = k < wmax[w] && !(rq[0].x + ex < x0 || rq[0].x - ex > x0 + 7.0f ||
+                                              rq[0].y + ey < y0 || rq[0].y - ey > y0 + 7.0f);
+            qm |= hit ? (1u << w) : 0u;
+          }
+        }
+      }
+    }
+    uint64_t bal[5];
+    bal[0] = __ballot(qm != 0u);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) bal[1 + w] = __ballot((qm >> w) & 1u);
+    if (lane == 0) {
+#pragma unroll
+      for (int f = 0; f < 5; ++f) s_cnt[wave][f] = __popcll(bal[f]);
+    }
+    __syncthreads();
+    int off[5], tot[5];
+#pragma unroll
+    for (int f = 0; f < 5; ++f) {
+      off[f] = 0;
+      tot[f] = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int c = s_cnt[w][f];
+        off[f] += (w < wave) ? c : 0;
+        tot[f] += c;
+      }
+      off[f] += __popcll(bal[f] & lt);
+    }
+    const int cnt = tot[0];
+    if (qm != 0u) {
+      const int slot = off[0];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) s_rec[slot * NQ + q] = rq[q];
+      s_rec[slot * NQ + 1].w = wpl;
+      s_k[slot] = k;
+      s_g[slot] = g;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        if ((qm >> w) & 1u) s_wl[w][off[1 + w]] = static_cast<unsigned short>(slot);
     }
     for (int e = threadIdx.x; e < cnt * NV; e += kBlock) s_acc[e] = 0.0f;
     __syncthreads();
 
-    for (int j = cnt - 1; j >= 0; --j) {
-      float v[NV];
+    int nl = 0;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) v[i] = 0.0f;
-      bool con = false;
-      if (inside && s_k[j] < last) {
-        const float4 a = s_rec[j * NQ];
-        const float4 b = s_rec[j * NQ + 1];
-        const float dx = a.x - pxf, dy = a.y - pyf;
-        const float cxx = a.z, cxy = a.w, czz = b.y;
-        const float power = -0.5f * (cxx * dx * dx + czz * dy * dy) - cxy * dx * dy;
-        if (power <= 0.0f) {
-          const float G = fast_exp(power);
-          const float alpha = fminf(kMaxAlpha, b.z * G * b.w);
-          if (alpha >= kMinAlphaBwd) {
-            T = T / (1.0f - alpha);
-            const float dcol = alpha * T;
-            float amp[8];
-            {
-              const float4 c0 = s_rec[j * NQ + 2];
-              amp[0] = c0.x;
-              amp[1] = c0.y;
-              amp[2] = c0.z;
-              amp[3] = c0.w;
-              const float4 c1 = s_rec[j * NQ + (NQ > 3 ? 3 : 2)];
-              amp[4] = c1.x;
-              amp[5] = c1.y;
-              amp[6] = c1.z;
-              amp[7] = c1.w;
-            }
-            float dLda = 0.0f;
+    for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] : nl;
+    for (int hi = nl - 1; hi >= 0; hi -= G) {
+      float buf[64];
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
-              const float cr = amp[2 * c], ci = amp[2 * c + 1];
-              accr[c] = last_alpha * lastr[c] + (1.0f - last_alpha) * accr[c];
-              acci[c] = last_alpha * lasti[c] + (1.0f - last_alpha) * acci[c];
-              lastr[c] = cr;
-              lasti[c] = ci;
-              dLda += (cr - accr[c]) * gre[c];
-              dLda += (ci - acci[c]) * gim[c];
-              v[6 + c] = dcol * gre[c];
-              v[6 + C + c] = dcol * gim[c];
+      for (int i = 0; i < 64; ++i) buf[i] = 0.0f;
+      bool any = false;
+#pragma unroll
+      for (int m = 0; m < G; ++m) {
+        const int li = hi - m;
+        if (li < 0) break;
+        const int slot = s_wl[wave][li];
+        const int kk = s_k[slot];
+        if (inside && kk < last) {
+          const float4 a = s_rec[slot * NQ];
+          const float4 b = s_rec[slot * NQ + 1];
+          const float dx = a.x - pxf, dy = a.y - pyf;
+          const float cxx = a.z, cxy = a.w, czz = b.y;
+          const float power = -0.5f * (cxx * dx * dx + czz * dy * dy) - cxy * dx * dy;
+          if (power <= 0.0f) {
+            const float Gv = fast_exp(power);
+            const float alpha = fminf(kMaxAlpha, b.z * Gv * b.w);
+            if (alpha >= kMinAlphaBwd) {
+              T = T / (1.0f - alpha);
+              const float dcol = alpha * T;
+              float amp[8];
+              {
+                const float4 c0 = s_rec[slot * NQ + 2];
+                const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
+                amp[0] = c0.x;
+                amp[1] = c0.y;
+                amp[2] = c0.z;
+                amp[3] = c0.w;
+                amp[4] = c1.x;
+                amp[5] = c1.y;
+                amp[6] = c1.z;
+                amp[7] = c1.w;
+              }
+              float dLda = 0.0f;
+#pragma unroll
+              for (int c = 0; c < C; ++c) {
+                const float cr = amp[2 * c], ci = amp[2 * c + 1];
+                accr[c] = last_alpha * lastr[c] + (1.0f - last_alpha) * accr[c];
+                acci[c] = last_alpha * lasti[c] + (1.0f - last_alpha) * acci[c];
+                lastr[c] = cr;
+                lasti[c] = ci;
+                dLda += (cr - accr[c]) * gre[c];
+                dLda += (ci - acci[c]) * gim[c];
+                buf[m * NV + 6 + c] = dcol * gre[c];
+                buf[m * NV + 6 + C + c] = dcol * gim[c];
+              }
+              dLda *= T;
+              last_alpha = alpha;
+              const float Q = Gv * dLda;
+              buf[m * NV + 0] = Q * fmaf(dx, cxx, dy * cxy);
+              buf[m * NV + 1] = Q * fmaf(dy, czz, dx * cxy);
+              buf[m * NV + 2] = Q * dx * dx;
+              buf[m * NV + 3] = Q * dx * dy;
+              buf[m * NV + 4] = Q * dy * dy;
+              buf[m * NV + 5] = Q;
+              any = true;
             }
-            dLda *= T;
-            last_alpha = alpha;
-            const float Q = G * dLda;
-            v[0] = Q * fmaf(dx, cxx, dy * cxy);
-            v[1] = Q * fmaf(dy, czz, dx * cxy);
-            v[2] = Q * dx * dx;
-            v[3] = Q * dx * dy;
-            v[4] = Q * dy * dy;
-            v[5] = Q;
-            con = true;
           }
         }
       }
-      if (__ballot(con) != 0ull) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = wave_sum_to_lane63(v[i]);
-        if (lane == 63) {
-#pragma unroll
-          for (int i = 0; i < NV; ++i) atomicAdd(&s_acc[j * NV + i], v[i]);
+      if (__ballot(any) != 0ull) {
+        const float tot_v = transpose_reduce64(buf);
+        if (lane < G * NV) {
+          const int m = lane / NV, v = lane - m * NV;
+          const int li = hi - m;
+          if (li >= 0 && tot_v != 0.0f) atomicAdd(&s_acc[s_wl[wave][li] * NV + v], tot_v);
         }
       }
     }

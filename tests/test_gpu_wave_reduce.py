@@ -1,0 +1,42 @@
+"""Lane layout of the wave64 reductions used by the backward render kernel."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from conftest import REPO
+
+pytestmark = pytest.mark.gpu
+
+LIB = os.path.join(REPO, "tests", "hip", "libwave_test.so")
+
+
+@pytest.fixture(scope="module")
+def wlib(hrf):
+    lib = ctypes.CDLL(LIB)
+    for f in (lib.wave_test_transpose, lib.wave_test_sum):
+        f.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        f.restype = ctypes.c_int
+    return lib
+
+
+def test_transpose_reduce64(wlib):
+    import torch
+
+    rng = np.random.default_rng(0)
+    x = rng.integers(-1000, 1000, size=(64, 64)).astype(np.float32)  # exact sums
+    xin = torch.from_numpy(x).cuda()
+    out = torch.zeros(64, dtype=torch.float32, device="cuda")
+    assert wlib.wave_test_transpose(xin.data_ptr(), out.data_ptr()) == 0
+    np.testing.assert_array_equal(out.cpu().numpy(), x.sum(axis=0))
+
+
+def test_wave_sum_lane63(wlib):
+    import torch
+
+    x = np.arange(64, dtype=np.float32) * 3 - 50
+    xin = torch.from_numpy(x).cuda()
+    out = torch.zeros(64, dtype=torch.float32, device="cuda")
+    assert wlib.wave_test_sum(xin.data_ptr(), out.data_ptr()) == 0
+    assert out[63].item() == x.sum()
