@@ -105,6 +105,7 @@ struct GeomWs {
   uint32_t* scan32;
   uint32_t* radix;
   uint64_t* totals;  // [K, V]
+  uint32_t* sort_flag;
 };
 
 GeomWs carve_geom(Carver& cv, int64_t n, int C) {
@@ -126,6 +127,7 @@ GeomWs carve_geom(Carver& cv, int64_t n, int C) {
   w.scan32 = cv.take<uint32_t>(scan_scratch_elems(m));
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
   w.totals = cv.take<uint64_t>(4);
+  w.sort_flag = cv.take<uint32_t>(4);
   return w;
 }
 
@@ -313,12 +315,20 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // Stable depth ordering of the Gaussians (32-bit keys, 4 passes: the
   // sorted order ends in the first buffer pair).
   {
+    // The reference's caller hands Gaussians over already sorted by depth
+    // (Scene.render, model.py:1387); the device checks that and the four
+    // passes then skip themselves (a stable sort of sorted keys is the
+    // identity).
     HRF_STAGE("depth_sort", s);
     HRF_TRY(launch_iota(w.order, n, s));
+    HRF_TRY(launch_check_sorted(w.dkey, n, w.sort_flag, s));
     bool in_b = false;
-    HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s));
-    if (in_b) HRF_HIP(hipMemcpyAsync(w.order, w.order_b, n * sizeof(uint32_t),
-                                     hipMemcpyDeviceToDevice, s));
+    HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s,
+                             w.sort_flag));
+    if (in_b) {
+      set_error("internal: depth sort expected an even pass count");
+      return HRF_ERR_INVALID;
+    }
   }
   {
     HRF_STAGE("scan", s);

@@ -177,11 +177,14 @@ int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n,
 
 // Stable LSD radix sort of (u32 key, u32 value) pairs over bits
 // [0, end_bit).  Ping-pongs between (ka,va) and (kb,vb); returns in
-// *result_in_b whether the sorted data ended in (kb,vb).
+// *result_in_b whether the sorted data ended in (kb,vb).  With run_flag, the
+// passes do nothing on the device while *run_flag == 0 (callers use an even
+// pass count then, so the data stays in (ka,va) either way).
 size_t radix_scratch_elems(int64_t n);
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
-                     hipStream_t s);
+                     hipStream_t s, const uint32_t* run_flag = nullptr);
+int launch_check_sorted(const uint32_t* keys, int64_t n, uint32_t* flag, hipStream_t s);
 int radix_passes(int end_bit);
 
 int launch_gather_counts(const uint32_t* order, const uint32_t* tiles,

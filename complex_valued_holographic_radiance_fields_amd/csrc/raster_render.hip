@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
             const float Gv = fast_exp(power);
             const float alpha = fminf(kMaxAlpha, b.z * Gv * b.w);
             if (alpha >= kMinAlphaBwd) {
-              T = T / (1.0f - alpha);
+              T = T * __builtin_amdgcn_rcpf(1.0f - alpha);
               const float dcol = alpha * T;
               float amp[8];
               {
@@ -370,12 +370,13 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
               for (int c = 0; c < C; ++c) {
                 const float cr = amp[2 * c], ci = amp[2 * c + 1];
-                accr[c] = last_alpha * lastr[c] + (1.0f - last_alpha) * accr[c];
-                acci[c] = last_alpha * lasti[c] + (1.0f - last_alpha) * acci[c];
+                // last_alpha*last + (1-last_alpha)*acc, as acc + last_alpha*(last-acc)
+                accr[c] = fmaf(last_alpha, lastr[c] - accr[c], accr[c]);
+                acci[c] = fmaf(last_alpha, lasti[c] - acci[c], acci[c]);
                 lastr[c] = cr;
                 lasti[c] = ci;
-                dLda += (cr - accr[c]) * gre[c];
-                dLda += (ci - acci[c]) * gim[c];
+                dLda = fmaf(cr - accr[c], gre[c], dLda);
+                dLda = fmaf(ci - acci[c], gim[c], dLda);
                 buf[m * NV + 6 + c] = dcol * gre[c];
                 buf[m * NV + 6 + C + c] = dcol * gim[c];
               }

@@ -112,7 +112,9 @@ int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream
 __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
                                                               uint32_t* __restrict__ hist,
-                                                              int nblocks) {
+                                                              int nblocks,
+                                                              const uint32_t* __restrict__ run_flag) {
+  if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_hist[kRadixBins];
   s_hist[threadIdx.x] = 0;
   __syncthreads();
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __
 __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
-    const uint32_t* __restrict__ hist_scan, int nblocks) {
+    const uint32_t* __restrict__ hist_scan, int nblocks, const uint32_t* __restrict__ run_flag) {
+  if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_cnt[kRadixWaves][kRadixBins];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
@@ -206,6 +209,14 @@ __global__ void k_fill_f32(float* p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
+// flag = 1 when keys are not already non-decreasing (then the stable sort
+// must run; otherwise it is the identity and is skipped on the device).
+__global__ void k_check_sorted(const uint32_t* __restrict__ keys, int64_t n,
+                               uint32_t* __restrict__ flag) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i + 1 < n && keys[i] > keys[i + 1]) *flag = 1u;
+}
+
 __global__ void k_gather_counts(const uint32_t* __restrict__ order,
                                 const uint32_t* __restrict__ tiles,
                                 uint32_t* __restrict__ cnt, int64_t n) {
@@ -213,30 +224,50 @@ __global__ void k_gather_counts(const uint32_t* __restrict__ order,
   if (i < n) cnt[i] = tiles[order[i]];
 }
 
-// One thread per pair e: the owning rank r is the last r with off[r] <= e
-// (binary search over the exclusive offsets); tile order inside a Gaussian
-// is y outer, x inner (rasterizer_splat.cu:162-173).
-__global__ void k_emit(const uint64_t* __restrict__ off, const uint32_t* __restrict__ order,
-                       const uint2* __restrict__ rect, int64_t n, int64_t k, int gx,
-                       uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= k) return;
-  int64_t lo = 0, hi = n;  // invariant: off[lo] <= e < off[hi] (off[n] == k)
-  while (hi - lo > 1) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (off[mid] <= static_cast<uint64_t>(e))
-      lo = mid;
-    else
-      hi = mid;
+// Pair emission.  A block owns 256 consecutive ranks; it stages their
+// exclusive offsets in LDS and its threads walk the block's output range
+// [off[r_begin], off[r_end]) with a stride of 256, each finding its rank by
+// binary search in LDS, so consecutive threads write consecutive pairs
+// (coalesced).  Tile order inside a Gaussian is y outer, x inner
+// (rasterizer_splat.cu:162-173).
+constexpr int kEmitThreads = 256;
+__global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ off,
+                                                      const uint32_t* __restrict__ order,
+                                                      const uint2* __restrict__ rect, int64_t n,
+                                                      int gx, uint32_t* __restrict__ keys,
+                                                      uint32_t* __restrict__ vals) {
+  __shared__ uint64_t s_off[kEmitThreads + 1];
+  __shared__ uint32_t s_g[kEmitThreads];
+  __shared__ uint2 s_rect[kEmitThreads];
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
+  const int64_t r = rb + threadIdx.x;
+  const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
+  if (threadIdx.x < nr) {
+    s_off[threadIdx.x] = off[r];
+    const uint32_t g = order[r];
+    s_g[threadIdx.x] = g;
+    s_rect[threadIdx.x] = rect[g];
   }
-  const uint32_t g = order[lo];
-  const uint2 rc = rect[g];
-  const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
-  const uint32_t w = maxx - minx;
-  const uint32_t i = static_cast<uint32_t>(static_cast<uint64_t>(e) - off[lo]);
-  const uint32_t ty = miny + i / w, tx = minx + i % w;
-  keys[e] = ty * static_cast<uint32_t>(gx) + tx;
-  vals[e] = g;
+  if (threadIdx.x == 0) s_off[nr] = off[rb + nr];
+  __syncthreads();
+  const uint64_t e0 = s_off[0], e1 = s_off[nr];
+  for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
+    int lo = 0, hi = nr;  // s_off[lo] <= e < s_off[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= e)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const uint2 rc = s_rect[lo];
+    const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
+    const uint32_t w = maxx - minx;
+    const uint32_t i = static_cast<uint32_t>(e - s_off[lo]);
+    const uint32_t ty = miny + i / w, tx = minx + i % w;
+    keys[e] = ty * static_cast<uint32_t>(gx) + tx;
+    vals[e] = s_g[lo];
+  }
 }
 
 __global__ void k_tile_ranges(const uint32_t* __restrict__ keys, int64_t k,
@@ -287,7 +318,8 @@ size_t radix_scratch_elems(int64_t n) {
 }
 
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
-                     int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s) {
+                     int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s,
+                     const uint32_t* run_flag) {
   *result_in_b = false;
   if (n <= 1) return HRF_OK;
   const int passes = radix_passes(end_bit);
@@ -305,11 +337,11 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
   for (int pass = 0; pass < passes; ++pass) {
     const int shift = pass * 8;
     hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
-                       hist, nb);
+                       hist, nb, run_flag);
     HRF_LAUNCH_CHECK();
     HRF_TRY(scan_exclusive_u32(hist, hist_scan, hist_n, scan_tmp, s));
     hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(kRadixThreads), 0, s, src_k, src_v,
-                       dst_k, dst_v, n, shift, hist_scan, nb);
+                       dst_k, dst_v, n, shift, hist_scan, nb, run_flag);
     HRF_LAUNCH_CHECK();
     uint32_t* tk = src_k;
     uint32_t* tv = src_v;
@@ -325,6 +357,15 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
 int launch_iota(uint32_t* v, int64_t n, hipStream_t s) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_iota, dim3(blocks_for(n, 256)), dim3(256), 0, s, v, n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_check_sorted(const uint32_t* keys, int64_t n, uint32_t* flag, hipStream_t s) {
+  HRF_TRY(launch_fill_u32(flag, 0u, 1, s));
+  if (n <= 1) return HRF_OK;
+  hipLaunchKernelGGL(k_check_sorted, dim3(blocks_for(n - 1, 256)), dim3(256), 0, s, keys, n,
+                     flag);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -355,9 +396,9 @@ int launch_gather_counts(const uint32_t* order, const uint32_t* tiles, uint32_t*
 int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
                       hipStream_t s) {
-  if (k <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_emit, dim3(blocks_for(k, 256)), dim3(256), 0, s, off, order, rect, n,
-                     k, gx, keys, vals);
+  if (k <= 0 || n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, off,
+                     order, rect, n, gx, keys, vals);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

@@ -60,6 +60,25 @@ def test_forward_parity(hrf, oracle_mod, case):
     assert mism < 1e-3, mism
 
 
+def _shuffle(sc, seed=3):
+    perm = np.random.default_rng(seed).permutation(sc.cam_means.shape[0])
+    for name in ("cam_means", "z", "quats", "scales", "colours", "phase", "opac", "pprobs"):
+        setattr(sc, name, np.ascontiguousarray(getattr(sc, name)[perm]))
+    return sc
+
+
+@pytest.mark.parametrize("case", CASES[1:3], ids=[c[0] for c in CASES[1:3]])
+def test_forward_parity_unsorted_depth(hrf, oracle_mod, case):
+    """Gaussians not pre-sorted by depth: the device depth sort must run."""
+    sc = _shuffle(_scene(*case))
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_backward_parity(hrf, oracle_mod, case):
     import torch
