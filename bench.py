@@ -25,17 +25,23 @@ sys.path.insert(0, REPO)
 METRIC = "fwd+bwd ms/frame, 1M Gaussians @800x800, 3 planes; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
 STAGES = ["project", "depth_sort", "scan", "emit", "tile_sort", "ranges", "render_fwd",
-          "render_bwd", "geom_bwd", "asm_pad", "asm_fft", "asm_mac_fwd", "asm_mac_adj",
-          "asm_crop"]
+          "render_bwd", "geom_bwd", "asm_rows_in", "asm_col_fwd", "asm_col_adj",
+          "asm_rows_out", "asm_pad", "asm_fft", "asm_mac_fwd", "asm_mac_adj", "asm_crop"]
 
 
 def algorithmic_bytes(N, K, P, C, W, H, S, T):
     """Compulsory-dataflow byte model per frame and per stage launch.
 
     Each tensor crosses HBM once per producer and once per consumer; index
-    maps (shift, pad, crop) are free; a 2-D FFT is one read + one write of
-    its M x M complex64 grid.  g_in = 48+4P+8C bytes of Gaussian inputs,
-    g_rec = 32+4P+8C bytes of per-Gaussian render record.
+    maps (shift, pad, crop) are free.  g_in = 48+4P+8C bytes of Gaussian
+    inputs, g_rec = 32+4P+8C bytes of per-Gaussian render record.
+
+    Propagation: an M x M complex64 grid (M = 2S, 20 MB at M = 1600) does not
+    fit on chip, so a 2-D transform needs one intermediate that is written
+    and read once: rows of the zero-padded input (only its H nonzero rows
+    exist) -> (P*C, H, M) row spectra -> column pass (FFT, transfer multiply
+    summed over planes, inverse FFT, row crop) -> (C, S, M) -> inverse rows
+    with column crop -> (C, S, S); the adjoint is the mirror image.
     """
     M = 2 * S
     g_in = 48 + 4 * P + 8 * C
@@ -43,18 +49,21 @@ def algorithmic_bytes(N, K, P, C, W, H, S, T):
     RF = N * g_in + 64 * N + 48 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H
     RB = (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec + N * (28 + 4 * P + 8 * C) +
           104 * N)
-    AF = P * C * (8 * W * H + 32 * M * M) + C * (16 * M * M + 8 * S * S)
-    AB = C * (8 * S * S + 16 * M * M) + P * C * (32 * M * M + 8 * W * H)
+    pcx = 8 * P * C * H * M      # row spectra of the P*C fields
+    csz = 8 * C * S * M          # column-pass output / adjoint row spectra
+    AF = 8 * P * C * W * H + 2 * pcx + 2 * csz + 8 * C * S * S
+    AB = 8 * C * S * S + 2 * csz + 2 * pcx + 8 * P * C * W * H
     per_launch = {
         "render_fwd": 4 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H + 8 * T,
         "render_bwd": (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec +
                        N * (28 + 4 * P + 8 * C) + 8 * T),
         "project": N * g_in + N * (g_rec + 24),
         "geom_bwd": N * g_in + N * (20 + 4 * P + 8 * C) + N * (40 + 4 * P + 8 * C),
-        "asm_mac_fwd": 8 * P * C * M * M + 8 * C * M * M,
-        "asm_mac_adj": 8 * C * M * M + 8 * P * C * M * M,
-        # FFT launches alternate batch P*C and C; the average per launch:
-        "asm_fft": 16 * M * M * (P * C + C) / 2,
+        # row launches alternate forward (P*C fields) and adjoint (C holograms):
+        "asm_rows_in": (8 * P * C * W * H + pcx + 8 * C * S * S + csz) / 2,
+        "asm_rows_out": (csz + 8 * C * S * S + pcx + 8 * P * C * W * H) / 2,
+        "asm_col_fwd": pcx + csz,
+        "asm_col_adj": csz + pcx,
         "tile_sort": 2 * 16 * K,
         "depth_sort": 4 * 16 * N,
     }

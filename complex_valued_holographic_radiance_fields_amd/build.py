@@ -31,6 +31,7 @@ SOURCES = [
     "raster_sort.hip",
     "raster_render.hip",
     "asm_prop.hip",
+    "asm_fft.hip",
     "hrf_capi.hip",
     "hrf_trace.hip",
 ]

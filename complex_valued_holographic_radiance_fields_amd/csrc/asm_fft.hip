@@ -1,0 +1,701 @@
+// asm_fft.hip — fused band-limited ASM propagation with hand-written LDS
+// FFTs for gfx950 (the per-frame multi-plane forward and adjoint).
+//
+// A 2-D transform is two 1-D passes.  The zero padding, the transfer
+// function multiply-accumulate over planes and the centred crops are folded
+// into the passes, so every (plane, wavelength) grid crosses HBM about three
+// times instead of the ~12 M x M passes of pad -> FFT (with transposes) ->
+// shift -> multiply -> shift -> iFFT -> crop:
+//
+//   forward  (fields (P,C,H,W) -> hologram (C,S,S)), M = 2S:
+//     A  row FFT of the H nonzero rows of each padded field  -> X (PC,H,M)
+//     B  per channel and block of 4 columns: for each plane, column FFT of
+//        the implicitly padded column, times T[p,c] x aperture, summed over
+//        planes; inverse column FFT; keep the S cropped rows  -> Z (C,S,M)
+//     C  inverse row FFT of those rows, keep S columns, x 1/M^2 -> hologram
+//   adjoint (grad hologram (C,S,S) -> grad fields (P,C,H,W)): the mirror
+//     A' row FFT of the S rows -> X (C,S,M); B' column FFT once per channel,
+//     then per plane conj(T) x aperture and inverse column FFT, keep H rows
+//     -> Z (PC,H,M); C' inverse row FFT, keep W columns, x 1/M^2.
+//
+// The 1-D FFT is a radix-{2,4,8,3,5,7} Stockham autosort transform on a
+// batch of B rows or columns held in LDS: each stage reads all butterfly
+// inputs into registers, applies table twiddles (double-precision table,
+// rounded to float), does the R-point DFT, and writes the outputs back to
+// their Stockham positions between two barriers.  Transform lengths with
+// other prime factors (or longer than 2048) use the hipFFT path.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "hrf_internal.h"
+
+namespace hrf {
+namespace {
+
+constexpr int kFftThreads = 512;
+constexpr int kFftBatch = 4;  // rows / columns per block
+constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmulf(float2 a, float2 b) {
+  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+// multiply by -i (forward) or +i (inverse)
+template <bool INV>
+__device__ __forceinline__ float2 mul_mi(float2 a) {
+  return INV ? make_float2(-a.y, a.x) : make_float2(a.y, -a.x);
+}
+
+template <int R, bool INV>
+struct Dft;
+
+template <bool INV>
+struct Dft<2, INV> {
+  __device__ __forceinline__ static void run(float2 (&x)[2]) {
+    const float2 a = x[0], b = x[1];
+    x[0] = cadd(a, b);
+    x[1] = csub(a, b);
+  }
+};
+
+template <bool INV>
+struct Dft<4, INV> {
+  __device__ __forceinline__ static void run(float2 (&x)[4]) {
+    const float2 a0 = cadd(x[0], x[2]), a1 = csub(x[0], x[2]);
+    const float2 a2 = cadd(x[1], x[3]), a3 = mul_mi<INV>(csub(x[1], x[3]));
+    x[0] = cadd(a0, a2);
+    x[1] = cadd(a1, a3);
+    x[2] = csub(a0, a2);
+    x[3] = csub(a1, a3);
+  }
+};
+
+template <bool INV>
+struct Dft<8, INV> {
+  __device__ __forceinline__ static void run(float2 (&x)[8]) {
+    float2 e[4] = {x[0], x[2], x[4], x[6]};
+    float2 o[4] = {x[1], x[3], x[5], x[7]};
+    Dft<4, INV>::run(e);
+    Dft<4, INV>::run(o);
+    constexpr float c = 0.70710678118654752f;
+    const float sg = INV ? 1.0f : -1.0f;
+    const float2 w1 = make_float2(c, sg * c), w3 = make_float2(-c, sg * c);
+    const float2 o1 = cmulf(o[1], w1), o2 = mul_mi<INV>(o[2]), o3 = cmulf(o[3], w3);
+    x[0] = cadd(e[0], o[0]);
+    x[4] = csub(e[0], o[0]);
+    x[1] = cadd(e[1], o1);
+    x[5] = csub(e[1], o1);
+    x[2] = cadd(e[2], o2);
+    x[6] = csub(e[2], o2);
+    x[3] = cadd(e[3], o3);
+    x[7] = csub(e[3], o3);
+  }
+};
+
+// Odd radix by symmetric pairing: X_m = x0 + sum_j cos(2 pi jm/R)(x_j+x_{R-j})
+//   -/+ i sum_j sin(2 pi jm/R)(x_j-x_{R-j}),  X_{R-m} with the opposite sign.
+template <int R>
+struct OddConsts;
+template <>
+struct OddConsts<3> {
+  // only k = 1 occurs for R = 3 (j = m = 1)
+  __device__ static constexpr float c(int) { return -0.5f; }
+  __device__ static constexpr float s(int) { return 0.86602540378443865f; }
+};
+template <>
+struct OddConsts<5> {
+  // index (j*m) mod 5 in 1..4 -> cos/sin(2 pi k / 5)
+  __device__ static constexpr float c(int k) {
+    return (k == 1 || k == 4) ? 0.30901699437494742f : -0.80901699437494742f;
+  }
+  __device__ static constexpr float s(int k) {
+    return k == 1 ? 0.95105651629515357f
+                  : (k == 2 ? 0.58778525229247313f
+                            : (k == 3 ? -0.58778525229247313f : -0.95105651629515357f));
+  }
+};
+template <>
+struct OddConsts<7> {
+  __device__ static constexpr float c(int k) {
+    return (k == 1 || k == 6) ? 0.62348980185873353f
+                              : ((k == 2 || k == 5) ? -0.22252093395631440f : -0.90096886790241913f);
+  }
+  __device__ static constexpr float s(int k) {
+    return k == 1 ? 0.78183148246802981f
+                  : (k == 2 ? 0.97492791218182361f
+                            : (k == 3 ? 0.43388373911755812f
+                                      : (k == 4 ? -0.43388373911755812f
+                                                : (k == 5 ? -0.97492791218182361f
+                                                          : -0.78183148246802981f))));
+  }
+};
+
+template <int R, bool INV>
+struct DftOdd {
+  __device__ __forceinline__ static void run(float2 (&x)[R]) {
+    constexpr int H = (R - 1) / 2;
+    float2 sp[H + 1], dm[H + 1];
+    float2 x0 = x[0];
+    float2 X0 = x0;
+#pragma unroll
+    for (int j = 1; j <= H; ++j) {
+      sp[j] = cadd(x[j], x[R - j]);
+      dm[j] = csub(x[j], x[R - j]);
+      X0 = cadd(X0, sp[j]);
+    }
+    float2 out[R];
+    out[0] = X0;
+#pragma unroll
+    for (int m = 1; m <= H; ++m) {
+      float2 re = x0, im = make_float2(0.0f, 0.0f);
+#pragma unroll
+      for (int j = 1; j <= H; ++j) {
+        const int k = (j * m) % R;
+        re = make_float2(fmaf(OddConsts<R>::c(k), sp[j].x, re.x), fmaf(OddConsts<R>::c(k), sp[j].y, re.y));
+        im = make_float2(fmaf(OddConsts<R>::s(k), dm[j].x, im.x), fmaf(OddConsts<R>::s(k), dm[j].y, im.y));
+      }
+      // X_m = re - i*im (forward), X_{R-m} = re + i*im
+      const float2 mi = mul_mi<INV>(im);
+      out[m] = cadd(re, mi);
+      out[R - m] = csub(re, mi);
+    }
+#pragma unroll
+    for (int t = 0; t < R; ++t) x[t] = out[t];
+  }
+};
+template <bool INV>
+struct Dft<3, INV> : DftOdd<3, INV> {};
+template <bool INV>
+struct Dft<5, INV> : DftOdd<5, INV> {};
+template <bool INV>
+struct Dft<7, INV> : DftOdd<7, INV> {};
+
+// LDS address of element (i, b) of a batch of B transforms of length N.
+// Each 32-element (256 B) chunk is rotated by 4 * (chunk % 8) slots: the
+// strided butterfly stores of the first Stockham stages (stride R*B or R
+// elements) then fall on distinct bank pairs, and contiguous accesses stay
+// conflict-free because the rotation permutes within a chunk.
+__device__ __forceinline__ int swz(int a) { return (a & ~31) | ((a + ((a >> 3) & 28)) & 31); }
+
+template <int N, int B, bool ROWS>
+__device__ __forceinline__ int lidx(int i, int b) {
+  return swz(ROWS ? b * N + i : i * B + b);
+}
+
+template <int N, int B, int R, int NS, bool INV, bool ROWS>
+__device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw_in) {
+  constexpr int NR = N / R;
+  constexpr int NB = B * NR;
+  constexpr int BPT = (NB + kFftThreads - 1) / kFftThreads;
+  // The thread index and the twiddle table pointer pass through empty asm
+  // statements, so a caller that runs the transform inside a loop (the plane
+  // loop of the column passes) cannot hoist this stage's addresses and
+  // twiddle loads out of the loop and hold them in registers for its whole
+  // length.
+  int tid = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(tid));
+  const float2* tw = tw_in;
+  asm volatile("" : "+s"(tw));
+  float2 y[BPT][R];
+  int ob[BPT], bb[BPT];
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    const int q = tid + u * kFftThreads;
+    ob[u] = -1;
+    if (BPT * kFftThreads == NB || q < NB) {
+      const int j = ROWS ? q % NR : q / B;
+      const int b = ROWS ? q / NR : q % B;
+      const int k = j % NS;
+      float2 x[R];
+#pragma unroll
+      for (int t = 0; t < R; ++t) x[t] = lds[lidx<N, B, ROWS>(j + t * NR, b)];
+      if (NS > 1) {
+#pragma unroll
+        for (int t = 1; t < R; ++t) {
+          float2 w = tw[t * k * (N / (NS * R))];
+          if (INV) w.y = -w.y;
+          x[t] = cmulf(x[t], w);
+        }
+      }
+      Dft<R, INV>::run(x);
+#pragma unroll
+      for (int t = 0; t < R; ++t) y[u][t] = x[t];
+      ob[u] = (j / NS) * NS * R + k;
+      bb[u] = b;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    if (ob[u] >= 0) {
+#pragma unroll
+      for (int t = 0; t < R; ++t) lds[lidx<N, B, ROWS>(ob[u] + t * NS, bb[u])] = y[u][t];
+    }
+  }
+  __syncthreads();
+}
+
+template <int N, int B, bool INV, bool ROWS, int NS, int R, int... Rest>
+__device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
+  fft_stage<N, B, R, NS, INV, ROWS>(lds, tw);
+  if constexpr (sizeof...(Rest) > 0) run_stages<N, B, INV, ROWS, NS * R, Rest...>(lds, tw);
+}
+
+template <int N>
+struct Plan;
+#define HRF_FFT_PLAN(NN, ...)                                                       \
+  template <>                                                                       \
+  struct Plan<NN> {                                                                 \
+    template <int B, bool INV, bool ROWS>                                           \
+    __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
+      run_stages<NN, B, INV, ROWS, 1, __VA_ARGS__>(lds, tw);                        \
+    }                                                                               \
+  };
+HRF_FFT_PLAN(128, 8, 4, 4)
+HRF_FFT_PLAN(160, 8, 4, 5)
+HRF_FFT_PLAN(192, 8, 8, 3)
+HRF_FFT_PLAN(512, 8, 8, 8)
+HRF_FFT_PLAN(1024, 8, 8, 4, 4)
+HRF_FFT_PLAN(1600, 8, 8, 5, 5)
+HRF_FFT_PLAN(2016, 8, 4, 7, 3, 3)
+HRF_FFT_PLAN(2048, 8, 8, 8, 4)
+#undef HRF_FFT_PLAN
+
+// Transfer-function geometry of natural-order spectral element (row i,
+// column k): frequencies as torch.fft.fftfreq float32 values and the
+// aperture on the fftshifted grid (same mapping as asm_prop.hip).
+__device__ __forceinline__ void coords(int i, int kcol, int M, float sfreq, float ap,
+                                       float* fxv, float* fyv, bool* inap) {
+  const int h = M / 2;
+  int kr = i + h;
+  if (kr >= M) kr -= M;
+  int kc = kcol + h;
+  if (kc >= M) kc -= M;
+  *fxv = static_cast<float>(kr - h) * sfreq;
+  *fyv = static_cast<float>(kc - h) * sfreq;
+  bool a = true;
+  if (ap > 0.0f) {
+    const float off = static_cast<float>(M) / 2.0f - 0.5f;
+    const float x = static_cast<float>(kc) - off;
+    const float y = static_cast<float>(kr) - off;
+    a = x * x + y * y < ap * ap;
+  }
+  *inap = a;
+}
+
+// kz^2 and kz exactly as the reference kernel evaluates them
+// (bandlimited_propagation_cuda.cu:60,65-67); kz2 <= 0 -> evanescent.
+__device__ __forceinline__ float kz_of(float k, float fxv, float fyv, bool* prop) {
+  const double a = kTwoPiD * static_cast<double>(fxv);
+  const double b = kTwoPiD * static_cast<double>(fyv);
+  const float kz2 = static_cast<float>((static_cast<double>(k * k) - a * a) - b * b);
+  *prop = kz2 > 0.0f;
+  return *prop ? sqrtf(kz2) : 0.0f;
+}
+
+struct AsmFftConsts {
+  float k[kMaxChannels];
+  float d[kMaxPlanes];
+  float fxmax[kMaxPlanes * kMaxChannels];
+  float fymax[kMaxPlanes * kMaxChannels];
+};
+
+// Intermediate spectra are stored tile-major: image `img` (h rows of N
+// columns) as N/B column tiles, each h x B with the B columns innermost, at
+// ((img * N/B + tile) * h + row) * B + col.  A column pass then reads and
+// writes one contiguous h*B*8-byte run per tile, and a row pass touches
+// B*B*8 = 128-byte runs.
+__device__ __forceinline__ int64_t tile_off(int img, int ncb, int cb, int h, int r, int b, int B) {
+  return ((static_cast<int64_t>(img) * ncb + cb) * h + r) * B + b;
+}
+
+// A / A': forward FFT of B rows of a plain (nimg, h, w_in) image placed at
+// column c_in of the zero-padded N-length row -> tiled (nimg, h, N).
+template <int N>
+__global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restrict__ src,
+                                                         float2* __restrict__ dst, int nimg,
+                                                         int h, int w_in, int c_in,
+                                                         const float2* __restrict__ tw) {
+  constexpr int B = kFftBatch;
+  constexpr int ncb = N / B;
+  __shared__ float2 lds[B * N];
+  const int blocks_per_img = (h + B - 1) / B;
+  const int img = blockIdx.x / blocks_per_img;
+  const int r0 = (blockIdx.x - img * blocks_per_img) * B;
+  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+    const int rr = e / N, i = e - rr * N;
+    const int r = r0 + rr;
+    const int col = i - c_in;
+    float2 v = make_float2(0.0f, 0.0f);
+    if (r < h && col >= 0 && col < w_in)
+      v = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
+    lds[swz(e)] = v;
+  }
+  __syncthreads();
+  Plan<N>::template run<B, false, true>(lds, tw);
+  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+    const int cb = e / (B * B), rr = (e / B) % B, b = e % B;
+    const int r = r0 + rr;
+    if (r < h) dst[tile_off(img, ncb, cb, h, r, b, B)] = lds[swz(rr * N + cb * B + b)];
+  }
+}
+
+// C / C': inverse FFT of B rows of a tiled (nimg, h, N) spectrum; keeps
+// columns [c_out, c_out + w_out) times `scale` -> plain (nimg, h, w_out).
+template <int N>
+__global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restrict__ src,
+                                                          float2* __restrict__ dst, int nimg,
+                                                          int h, int w_out, int c_out,
+                                                          float scale,
+                                                          const float2* __restrict__ tw) {
+  constexpr int B = kFftBatch;
+  constexpr int ncb = N / B;
+  __shared__ float2 lds[B * N];
+  const int blocks_per_img = (h + B - 1) / B;
+  const int img = blockIdx.x / blocks_per_img;
+  const int r0 = (blockIdx.x - img * blocks_per_img) * B;
+  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+    const int cb = e / (B * B), rr = (e / B) % B, b = e % B;
+    const int r = r0 + rr;
+    float2 v = make_float2(0.0f, 0.0f);
+    if (r < h) v = src[tile_off(img, ncb, cb, h, r, b, B)];
+    lds[swz(rr * N + cb * B + b)] = v;
+  }
+  __syncthreads();
+  Plan<N>::template run<B, true, true>(lds, tw);
+  for (int e = threadIdx.x; e < B * w_out; e += kFftThreads) {
+    const int rr = e / w_out, i = e - rr * w_out;
+    const int r = r0 + rr;
+    if (r < h) {
+      const float2 v = lds[swz(rr * N + c_out + i)];
+      dst[(static_cast<int64_t>(img) * h + r) * w_out + i] = cscale(v, scale);
+    }
+  }
+}
+
+__device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb, int ncb) {
+  // XCD-aware: consecutive column tiles of a channel go to one XCD, so the
+  // tiles of neighbouring blocks stream through the same L2.
+  const int q = nblk >> 3, r = nblk & 7;
+  const int x = bid & 7, i = bid >> 3;
+  const int logical = (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+  *chan = logical / ncb;
+  *cb = logical - (*chan) * ncb;
+}
+
+// B: forward column pass for one channel and one column tile.  X tiled
+// (P*C, H, N) row spectra of the fields (rows r_pad..r_pad+H of the padded
+// grid; the other rows are zero); Z tiled (C, S, N) receives rows
+// [s_crop, s_crop+S) of iFFTcol(sum_p FFTcol(X[p,c]) * T[p,c] * A).
+template <int N>
+__global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(const float2* __restrict__ X,
+                                                         float2* __restrict__ Z, int P, int C,
+                                                         int H, int r_pad, int S, int s_crop,
+                                                         float sfreq, float ap, AsmFftConsts mc,
+                                                         const float2* __restrict__ tw) {
+  constexpr int B = kFftBatch;
+  constexpr int ncb = N / B;
+  constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
+  __shared__ float2 lds[B * N];
+  int c, cb;
+  map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
+  const int k0 = cb * B;
+
+  // kz of each owned element, or -1 where the aperture or the evanescent
+  // cut zeroes the transfer function for every plane.
+  float kz[EPT];
+  float2 acc[EPT];
+#pragma unroll
+  for (int u = 0; u < EPT; ++u) {
+    const int q = threadIdx.x + u * kFftThreads;
+    acc[u] = make_float2(0.0f, 0.0f);
+    kz[u] = -1.0f;
+    if (q < B * N) {
+      const int i = q / B, b = q % B;
+      float fxv, fyv;
+      bool inap, prop;
+      coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &inap);
+      const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
+      if (inap && prop) kz[u] = kk;
+    }
+  }
+  for (int p = 0; p < P; ++p) {
+    __syncthreads();
+    const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
+    for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+      const int r = e / B - r_pad;
+      float2 v = make_float2(0.0f, 0.0f);
+      if (r >= 0 && r < H) v = src[e - r_pad * B];
+      lds[swz(e)] = v;
+    }
+    __syncthreads();
+    Plan<N>::template run<B, false, false>(lds, tw);
+    const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
+    const float d = mc.d[p];
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int q = threadIdx.x + u * kFftThreads;
+      if (q < B * N && kz[u] >= 0.0f) {
+        const int i = q / B, b = q % B;
+        float fxv, fyv;
+        bool inap;
+        coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
+        if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
+          float sn, cs;
+          sincosf(d * kz[u], &sn, &cs);
+          const float2 x = lds[swz(q)];
+          acc[u].x += x.x * cs - x.y * sn;
+          acc[u].y += x.x * sn + x.y * cs;
+        }
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < EPT; ++u) {
+    const int q = threadIdx.x + u * kFftThreads;
+    if (q < B * N) lds[swz(q)] = acc[u];
+  }
+  __syncthreads();
+  Plan<N>::template run<B, true, false>(lds, tw);
+  float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, B);
+  for (int e = threadIdx.x; e < B * S; e += kFftThreads) dst[e] = lds[swz(e + s_crop * B)];
+}
+
+// B': adjoint column pass.  X tiled (C, S, N) row spectra of the padded
+// hologram gradient (rows s_pad..s_pad+S of the grid); Z tiled (P*C, H, N)
+// receives rows [r_crop, r_crop+H) of iFFTcol(FFTcol(X[c]) conj(T[p,c]) A).
+template <int N>
+__global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(const float2* __restrict__ X,
+                                                         float2* __restrict__ Z, int P, int C,
+                                                         int S, int s_pad, int H, int r_crop,
+                                                         float sfreq, float ap, AsmFftConsts mc,
+                                                         const float2* __restrict__ tw) {
+  constexpr int B = kFftBatch;
+  constexpr int ncb = N / B;
+  constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
+  __shared__ float2 lds[B * N];
+  int c, cb;
+  map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
+  const int k0 = cb * B;
+
+  const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, B);
+  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+    const int r = e / B - s_pad;
+    float2 v = make_float2(0.0f, 0.0f);
+    if (r >= 0 && r < S) v = src[e - s_pad * B];
+    lds[swz(e)] = v;
+  }
+  __syncthreads();
+  Plan<N>::template run<B, false, false>(lds, tw);
+  float kz[EPT];
+  float2 gs[EPT];
+#pragma unroll
+  for (int u = 0; u < EPT; ++u) {
+    const int q = threadIdx.x + u * kFftThreads;
+    kz[u] = -1.0f;
+    gs[u] = make_float2(0.0f, 0.0f);
+    if (q < B * N) {
+      const int i = q / B, b = q % B;
+      float fxv, fyv;
+      bool inap, prop;
+      coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &inap);
+      const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
+      if (inap && prop) kz[u] = kk;
+      gs[u] = lds[swz(q)];
+    }
+  }
+  for (int p = 0; p < P; ++p) {
+    __syncthreads();
+    const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
+    const float nd = -mc.d[p];
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int q = threadIdx.x + u * kFftThreads;
+      if (q < B * N) {
+        float2 r = make_float2(0.0f, 0.0f);
+        if (kz[u] >= 0.0f) {
+          const int i = q / B, b = q % B;
+          float fxv, fyv;
+          bool inap;
+          coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
+          if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
+            float sn, cs;
+            sincosf(nd * kz[u], &sn, &cs);
+            r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
+          }
+        }
+        lds[swz(q)] = r;
+      }
+    }
+    __syncthreads();
+    Plan<N>::template run<B, true, false>(lds, tw);
+    float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
+    for (int e = threadIdx.x; e < B * H; e += kFftThreads) dst[e] = lds[swz(e + r_crop * B)];
+  }
+}
+
+// ------------------------------------------------------------ host side --
+std::mutex g_tw_mu;
+std::map<std::pair<int, int>, float2*>& tw_tables() {
+  static std::map<std::pair<int, int>, float2*> m;
+  return m;
+}
+
+int twiddles(int N, const float2** out) {
+  int dev = 0;
+  HRF_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_tw_mu);
+  auto key = std::make_pair(dev, N);
+  auto it = tw_tables().find(key);
+  if (it != tw_tables().end()) {
+    *out = it->second;
+    return HRF_OK;
+  }
+  std::vector<float2> h(N);
+  for (int m = 0; m < N; ++m) {
+    const double a = -kTwoPiD * static_cast<double>(m) / static_cast<double>(N);
+    h[m] = make_float2(static_cast<float>(std::cos(a)), static_cast<float>(std::sin(a)));
+  }
+  float2* d = nullptr;
+  HRF_HIP(hipMalloc(&d, N * sizeof(float2)));
+  HRF_HIP(hipMemcpy(d, h.data(), N * sizeof(float2), hipMemcpyHostToDevice));
+  tw_tables()[key] = d;
+  *out = d;
+  return HRF_OK;
+}
+
+AsmFftConsts fft_consts(int P, int C, int M, double pitch, const float* wl, const float* dist) {
+  AsmFftConsts mc{};
+  for (int c = 0; c < C; ++c) mc.k[c] = asm_consts(wl[c], 0.0f, static_cast<float>(pitch), M, M).k;
+  for (int p = 0; p < P; ++p) {
+    mc.d[p] = dist[p];
+    for (int c = 0; c < C; ++c) {
+      const AsmConsts a = asm_consts(wl[c], dist[p], static_cast<float>(pitch), M, M);
+      mc.fxmax[p * kMaxChannels + c] = a.fx_max;
+      mc.fymax[p * kMaxChannels + c] = a.fy_max;
+    }
+  }
+  return mc;
+}
+
+template <int N>
+int run_forward(const float2* fields, int P, int C, int H, int W, int S, double pitch,
+                const float* wl, const float* dist, float ap, float2* holo, float2* X, float2* Z,
+                hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw));
+  const int B = kFftBatch;
+  const float sfreq = static_cast<float>(1.0 / (static_cast<double>(N) * pitch));
+  const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
+  {
+    HRF_STAGE("asm_rows_in", s);
+    const int nimg = P * C;
+    hipLaunchKernelGGL((k_rows_in<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kFftThreads), 0, s,
+                       fields, X, nimg, H, W, N / 2 - W / 2, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  {
+    HRF_STAGE("asm_col_fwd", s);
+    hipLaunchKernelGGL((k_col_fwd<N>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P, C, H,
+                       N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  {
+    HRF_STAGE("asm_rows_out", s);
+    const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
+    hipLaunchKernelGGL((k_rows_out<N>), dim3(C * ((S + B - 1) / B)), dim3(kFftThreads), 0, s, Z,
+                       holo, C, S, S, N / 2 - S / 2, scale, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  return HRF_OK;
+}
+
+template <int N>
+int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double pitch,
+                const float* wl, const float* dist, float ap, float2* gfields, float2* X,
+                float2* Z, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw));
+  const int B = kFftBatch;
+  const float sfreq = static_cast<float>(1.0 / (static_cast<double>(N) * pitch));
+  const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
+  {
+    HRF_STAGE("asm_rows_in", s);
+    hipLaunchKernelGGL((k_rows_in<N>), dim3(C * ((S + B - 1) / B)), dim3(kFftThreads), 0, s,
+                       gholo, X, C, S, S, N / 2 - S / 2, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  {
+    HRF_STAGE("asm_col_adj", s);
+    hipLaunchKernelGGL((k_col_adj<N>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P, C, S,
+                       N / 2 - S / 2, H, N / 2 - H / 2, sfreq, ap, mc, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  {
+    HRF_STAGE("asm_rows_out", s);
+    const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
+    const int nimg = P * C;
+    hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kFftThreads), 0, s,
+                       Z, gfields, nimg, H, W, N / 2 - W / 2, scale, tw);
+    HRF_LAUNCH_CHECK();
+  }
+  return HRF_OK;
+}
+
+}  // namespace
+
+bool fused_fft_supported(int M) {
+  return M == 128 || M == 160 || M == 192 || M == 512 || M == 1024 || M == 1600 ||
+         M == 2016 || M == 2048;
+}
+
+int fused_asm_forward(const float2* fields, int P, int C, int H, int W, int S, double pitch,
+                      const float* wl, const float* dist, float ap, float2* holo, float2* X,
+                      float2* Z, hipStream_t s) {
+  switch (2 * S) {
+    case 128: return run_forward<128>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 160: return run_forward<160>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 192: return run_forward<192>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 512: return run_forward<512>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 1024: return run_forward<1024>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 1600: return run_forward<1600>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 2016: return run_forward<2016>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    case 2048: return run_forward<2048>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    default:
+      set_error("fused ASM: unsupported grid %d", 2 * S);
+      return HRF_ERR_INVALID;
+  }
+}
+
+int fused_asm_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double pitch,
+                      const float* wl, const float* dist, float ap, float2* gfields, float2* X,
+                      float2* Z, hipStream_t s) {
+  switch (2 * S) {
+    case 128: return run_adjoint<128>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 160: return run_adjoint<160>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 192: return run_adjoint<192>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 512: return run_adjoint<512>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 1024: return run_adjoint<1024>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 1600: return run_adjoint<1600>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 2016: return run_adjoint<2016>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    case 2048: return run_adjoint<2048>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    default:
+      set_error("fused ASM: unsupported grid %d", 2 * S);
+      return HRF_ERR_INVALID;
+  }
+}
+
+void fused_fft_release_all() {
+  std::lock_guard<std::mutex> lock(g_tw_mu);
+  for (auto& kv : tw_tables()) hipFree(kv.second);
+  tw_tables().clear();
+}
+
+}  // namespace hrf

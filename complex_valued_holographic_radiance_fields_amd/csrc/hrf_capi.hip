@@ -609,6 +609,11 @@ int hrf_asm_multiplane_forward(const void* fields, int32_t planes, int32_t chann
   float2* spec = cv.take<float2>(static_cast<size_t>(planes) * channels * MM);
   float2* outs = cv.take<float2>(static_cast<size_t>(channels) * MM);
   const int PC = planes * channels;
+  if (fused_fft_supported(M)) {
+    return fused_asm_forward(static_cast<const float2*>(fields), planes, channels, height,
+                             width, size, pixel_pitch, wavelengths, distances, aperture,
+                             static_cast<float2*>(hologram), spec, outs, s);
+  }
   {
     HRF_STAGE("asm_pad", s);
     HRF_TRY(launch_asm_pad(static_cast<const float2*>(fields), PC, height, width, spec, M, s));
@@ -653,6 +658,11 @@ int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes, int32_
   float2* spec = cv.take<float2>(static_cast<size_t>(planes) * channels * MM);
   float2* gsp = cv.take<float2>(static_cast<size_t>(channels) * MM);
   const int PC = planes * channels;
+  if (fused_fft_supported(M)) {
+    return fused_asm_adjoint(static_cast<const float2*>(grad_hologram), planes, channels,
+                             height, width, size, pixel_pitch, wavelengths, distances, aperture,
+                             static_cast<float2*>(grad_fields), gsp, spec, s);
+  }
   {
     HRF_STAGE("asm_pad", s);
     HRF_TRY(launch_asm_pad(static_cast<const float2*>(grad_hologram), channels, size, size,
@@ -695,6 +705,9 @@ int hrf_asm_adjoint(const void* grad_out, int32_t height, int32_t width, int32_t
                                     stream);
 }
 
-void hrf_release_caches(void) { hrf::fft_release_all(); }
+void hrf_release_caches(void) {
+  hrf::fft_release_all();
+  hrf::fused_fft_release_all();
+}
 
 }  // extern "C"

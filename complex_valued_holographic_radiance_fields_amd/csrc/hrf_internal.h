@@ -250,4 +250,16 @@ int launch_asm_mac_adjoint(const float2* spec, int P, int C, int M, double pitch
 int fft_c2c(float2* buf, int M, int batch, bool inverse, hipStream_t s);
 void fft_release_all();
 
+// Fused LDS-FFT propagation (asm_fft.hip) for the grid sizes it has plans
+// for.  X needs P*C*H*M (forward) / C*S*M (adjoint) complex elements, Z
+// C*S*M / P*C*H*M.
+bool fused_fft_supported(int M);
+int fused_asm_forward(const float2* fields, int P, int C, int H, int W, int S, double pitch,
+                      const float* wl, const float* dist, float ap, float2* holo, float2* X,
+                      float2* Z, hipStream_t s);
+int fused_asm_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double pitch,
+                      const float* wl, const float* dist, float ap, float2* gfields, float2* X,
+                      float2* Z, hipStream_t s);
+void fused_fft_release_all();
+
 }  // namespace hrf

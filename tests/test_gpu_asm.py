@@ -115,3 +115,44 @@ def test_odd_size_rejected(hrf):
     f = torch.zeros((33, 32), dtype=torch.complex64, device="cuda")
     with pytest.raises(RuntimeError):
         propagation.propagate(f, 515e-9, PITCH, 1e-3, (64, 64), -1.0)
+
+
+# Grids with a hand-written LDS-FFT plan (M = 2S in 128, 160, 192, 512, 1024,
+# 1600, 2016, 2048) run the fused row/column kernels; other sizes (M = 96
+# above) run the hipFFT path.  The headline grid (800 -> 1600) and every
+# large plan are checked against the oracle, forward and adjoint.
+@pytest.mark.parametrize("P,C,H,W,S", [(3, 3, 800, 800, 800), (1, 2, 100, 60, 512),
+                                       (2, 1, 64, 64, 1008), (1, 1, 128, 96, 1024)],
+                         ids=["headline1600", "m1024", "m2016", "m2048"])
+def test_multiplane_fused_grids(hrf, oracle_mod, P, C, H, W, S):
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import propagation
+
+    rng = np.random.default_rng(S)
+    wl = [639e-9, 515e-9, 473e-9][:C]
+    dist = [-2e-3, -4e-3, -6e-3][:P]
+    f = _field(rng, (P, C, H, W))
+    print(f"fused grid M={2 * S} P={P} C={C}", flush=True)
+    ref = oracle_mod.multiplane_forward(f, wl, dist, PITCH, S, float(S))
+    got = propagation.multiplane(torch.from_numpy(f).cuda(), wl, PITCH, dist, (S, S), float(S))
+    assert rel_l2(got.cpu().numpy(), ref) < TOL
+    g = _field(rng, (C, S, S))
+    ref_adj = oracle_mod.multiplane_adjoint(g, H, W, wl, dist, PITCH, S, float(S))
+    got_adj = propagation.multiplane_adjoint(torch.from_numpy(g).cuda(), (H, W), wl, PITCH, dist,
+                                             (S, S), float(S))
+    assert rel_l2(got_adj.cpu().numpy(), ref_adj) < TOL
+
+
+def test_fused_matches_hipfft_path(hrf):
+    """At d = 0 with the aperture off, both transform paths reduce to
+    pad -> FFT -> iFFT -> crop: the hipFFT path (M = 96) and the fused path
+    (M = 128) must each give the input back."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import propagation
+
+    rng = np.random.default_rng(4)
+    f = torch.from_numpy(_field(rng, (48, 48))).cuda()
+    a = propagation.propagate(f, 515e-9, PITCH, 0.0, (48, 48), -1.0)   # M = 96, hipFFT
+    b = propagation.propagate(f, 515e-9, PITCH, 0.0, (64, 64), -1.0)   # M = 128, fused
+    assert rel_l2(a.cpu().numpy(), f.cpu().numpy()) < 1e-6
+    assert rel_l2(b[8:56, 8:56].cpu().numpy(), f.cpu().numpy()) < 1e-6
