@@ -29,19 +29,47 @@ STAGES = ["project", "depth_sort", "scan", "emit", "tile_sort", "ranges", "rende
           "asm_rows_out", "asm_pad", "asm_fft", "asm_mac_fwd", "asm_mac_adj", "asm_crop"]
 
 
+# Stage -> kernel name in the rocprofv3 summaries under profiles/.
+STAGE_KERNEL = {"render_bwd": "k_render_bwd<{C}>", "render_fwd": "k_render_fwd<{C}>",
+                "project": "k_project", "geom_bwd": "k_geom_backward",
+                "asm_col_fwd": "k_col_fwd<{M}>", "asm_col_adj": "k_col_adj<{M}>",
+                "asm_rows_in": "k_rows_in<{M}>", "asm_rows_out": "k_rows_out<{M}>",
+                "emit": "k_emit", "ranges": "k_tile_ranges"}
+
+
+def profiled_traffic(config, stage, C, M):
+    """HBM bytes per dispatch of `stage`'s kernel from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this workload (calibrated
+    against a copy kernel of known size), or None."""
+    path = os.path.join(REPO, "profiles", f"hbm_traffic_{config}.txt")
+    name = STAGE_KERNEL.get(stage, "").format(C=C, M=M)
+    if not name or not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
+                return int(parts[2]), os.path.relpath(path, REPO)
+    return None, None
+
+
 def algorithmic_bytes(N, K, P, C, W, H, S, T):
     """Compulsory-dataflow byte model per frame and per stage launch.
 
-    Each tensor crosses HBM once per producer and once per consumer; index
-    maps (shift, pad, crop) are free.  g_in = 48+4P+8C bytes of Gaussian
-    inputs, g_rec = 32+4P+8C bytes of per-Gaussian render record.
+    Frame model (the metric's definition): each tensor crosses HBM once per
+    producer and once per consumer; index maps (shift, pad, crop) are free; a
+    2-D FFT is one read + one write of its M x M complex64 grid.  g_in =
+    48+4P+8C bytes of Gaussian inputs, g_rec = 32+4P+8C bytes of per-Gaussian
+    render record.
 
-    Propagation: an M x M complex64 grid (M = 2S, 20 MB at M = 1600) does not
-    fit on chip, so a 2-D transform needs one intermediate that is written
-    and read once: rows of the zero-padded input (only its H nonzero rows
-    exist) -> (P*C, H, M) row spectra -> column pass (FFT, transfer multiply
-    summed over planes, inverse FFT, row crop) -> (C, S, M) -> inverse rows
-    with column crop -> (C, S, S); the adjoint is the mirror image.
+    The propagation kernels here move fewer bytes than that frame model
+    counts: an M x M grid (20 MB at M = 1600) does not fit on chip, so a 2-D
+    transform needs one intermediate written and read once, and only the H
+    nonzero rows of a padded field (the S kept rows of an output) exist.  The
+    rows pass writes (P*C, H, M) row spectra; the column pass (FFT, transfer
+    multiply summed over planes, inverse FFT, row crop) writes (C, S, M); the
+    inverse rows pass writes (C, S, S); the adjoint mirrors it.  The
+    per-launch figures of the asm_* kernels and `fused` use this dataflow.
     """
     M = 2 * S
     g_in = 48 + 4 * P + 8 * C
@@ -49,10 +77,12 @@ def algorithmic_bytes(N, K, P, C, W, H, S, T):
     RF = N * g_in + 64 * N + 48 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H
     RB = (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec + N * (28 + 4 * P + 8 * C) +
           104 * N)
+    AF = P * C * (8 * W * H + 32 * M * M) + C * (16 * M * M + 8 * S * S)
+    AB = C * (8 * S * S + 16 * M * M) + P * C * (32 * M * M + 8 * W * H)
     pcx = 8 * P * C * H * M      # row spectra of the P*C fields
     csz = 8 * C * S * M          # column-pass output / adjoint row spectra
-    AF = 8 * P * C * W * H + 2 * pcx + 2 * csz + 8 * C * S * S
-    AB = 8 * C * S * S + 2 * csz + 2 * pcx + 8 * P * C * W * H
+    AF_fused = 8 * P * C * W * H + 2 * pcx + 2 * csz + 8 * C * S * S
+    AB_fused = 8 * C * S * S + 2 * csz + 2 * pcx + 8 * P * C * W * H
     per_launch = {
         "render_fwd": 4 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H + 8 * T,
         "render_bwd": (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec +
@@ -67,7 +97,9 @@ def algorithmic_bytes(N, K, P, C, W, H, S, T):
         "tile_sort": 2 * 16 * K,
         "depth_sort": 4 * 16 * N,
     }
-    return dict(RF=RF, RB=RB, AF=AF, AB=AB, total=RF + RB + AF + AB, per_launch=per_launch)
+    return dict(RF=RF, RB=RB, AF=AF, AB=AB, total=RF + RB + AF + AB,
+                fused_fwd=RF + AF_fused, fused_total=RF + RB + AF_fused + AB_fused,
+                per_launch=per_launch)
 
 
 def main():
@@ -162,6 +194,8 @@ def main():
     B = algorithmic_bytes(N, K, P, C, W, H, S, T)
     frame_bytes = B["total"] if spec.backward else B["RF"] + B["AF"]
     frame_gbs = frame_bytes / (ms_per_step * 1e-3) / 1e9
+    fused_bytes = B["fused_total"] if spec.backward else B["fused_fwd"]
+    fused_gbs = fused_bytes / (ms_per_step * 1e-3) / 1e9
 
     # Dominant kernel stage and its roofline.
     dom = max((s for s in stages if s in B["per_launch"]),
@@ -169,10 +203,11 @@ def main():
     roof = None
     if dom is not None:
         ach = B["per_launch"][dom] / (stages[dom]["avg_launch_ms"] * 1e-3) / 1e9
+        traffic, src = profiled_traffic(spec.name, dom, C, 2 * S)
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "avg_launch_ms": round(stages[dom]["avg_launch_ms"], 4),
-                "bytes_per_launch": int(B["per_launch"][dom])}
+                "bytes_per_launch": int(B["per_launch"][dom]), "traffic_source": src}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -211,6 +246,8 @@ def main():
         "frame_alg_bytes": int(frame_bytes),
         "frame_achieved_GBs": round(frame_gbs, 1),
         "frame_hbm_frac": round(frame_gbs / HBM_PEAK_GBS, 4),
+        "frame_fused_dataflow_bytes": int(fused_bytes),
+        "frame_fused_dataflow_frac": round(fused_gbs / HBM_PEAK_GBS, 4),
         "wall_s": round(wall_s, 3),
         "stages_ms_per_frame": {s: round(v["ms_per_frame"], 4) for s, v in stages.items()},
         "roofline": roof,

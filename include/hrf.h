@@ -140,7 +140,12 @@ int hrf_asm_spectral_backward(const float* grad_re, const float* grad_im,
                               float wavelength, float distance, float aperture,
                               float pixel_pitch, void* stream);
 
-/* Workspace for the whole-propagation entry points below: M = 2*S. */
+/* Workspace for the whole-propagation entry points below: M = 2*S.
+ * Grids with M in {128, 160, 192, 512, 1024, 1600, 2016, 2048} run the
+ * fused hand-written LDS-FFT kernels (row pass with the zero pad, column
+ * pass with the transfer-function multiply summed over planes and the row
+ * crop, inverse row pass with the column crop and 1/M^2); other even sizes
+ * run the same arithmetic around hipFFT transforms. */
 size_t hrf_asm_workspace_size(int32_t planes, int32_t channels, int32_t size);
 
 /* One field (H,W) c64 -> (S,S) c64: centred zero pad to (2S,2S), FFT,
@@ -180,7 +185,7 @@ int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes,
                                float aperture, void* grad_fields, void* ws,
                                size_t ws_bytes, void* stream);
 
-/* Releases cached hipFFT plans (optional; also released at unload). */
+/* Releases cached hipFFT plans and FFT twiddle tables (optional). */
 void hrf_release_caches(void);
 
 /* ---------------- stage tracing (no counterpart in the reference, which
@@ -195,8 +200,9 @@ void hrf_trace_reset(void);
 /* Waits for the recorded events of `stage` and returns the number of
  * launches and their summed duration in milliseconds since the last reset.
  * Stages: project, depth_sort, scan, emit, tile_sort, ranges, render_fwd,
- * render_bwd, geom_bwd, asm_pad, asm_fft, asm_mac_fwd, asm_mac_adj,
- * asm_crop. */
+ * render_bwd, geom_bwd; fused propagation: asm_rows_in, asm_col_fwd,
+ * asm_col_adj, asm_rows_out; hipFFT propagation: asm_pad, asm_fft,
+ * asm_mac_fwd, asm_mac_adj, asm_crop. */
 int hrf_trace_read(const char* stage, int64_t* launches, double* total_ms);
 
 #ifdef __cplusplus

@@ -9,8 +9,9 @@ the reference CUDA code) and composes the reference's ASM propagation
 (``cuda_prop/python_function.py:111-218``) from that spectral kernel and
 numpy's FFT (pocketfft, computed in double precision).
 
-Pinning status (what independently checks each function) is recorded in
-``tests/test_oracle_pinning.py`` and listed in DESIGN.md.
+What independently checks each function (closed forms, brute force,
+float64 restatements, finite differences, a brute-force DFT, invariants) is
+in ``tests/test_oracle_pinning.py``.
 """
 from __future__ import annotations
 
