@@ -55,6 +55,23 @@ SIGNATURES = {
     "hrf_raster_backward": (ctypes.c_int, [
         _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz,
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hrf_cov3d_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "hrf_cov3d_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "hrf_jacobian_forward": (ctypes.c_int, [_vp, _i64, _f32, _f32, _i32, _i32, _f32, _f32,
+                                            _vp, _vp]),
+    "hrf_jacobian_backward": (ctypes.c_int, [_vp, _vp, _i64, _f32, _f32, _i32, _i32, _f32,
+                                             _f32, _vp, _vp]),
+    "hrf_cov2d_forward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _f32, _f32, _i32, _i32,
+                                         _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hrf_cov2d_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                          _f32, _f32, _i32, _i32, _f32, _f32, _vp, _vp, _vp,
+                                          _vp]),
+    "hrf_means2d_forward": (ctypes.c_int, [_vp, _i64, _f32, _f32, _f32, _f32, _f32, _f32, _vp,
+                                           _vp]),
+    "hrf_means2d_backward": (ctypes.c_int, [_vp, _vp, _i64, _f32, _f32, _f32, _f32, _f32, _f32,
+                                            _vp, _vp]),
+    "hrf_invert_cov2d_forward": (ctypes.c_int, [_vp, _i64, _vp, _vp]),
+    "hrf_invert_cov2d_backward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "hrf_asm_spectral_forward": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _f32, _f32, _f32, _vp]),
     "hrf_asm_spectral_backward": (ctypes.c_int, [

@@ -1,5 +1,9 @@
 """Build the gfx950 HIP library ``lib/libhrf.so`` in-tree with hipcc.
 
+Run as a script (``python complex_valued_holographic_radiance_fields_amd/build.py``)
+or through ``__graft_entry__.build()``; it imports nothing from the package,
+whose ``__init__`` loads the library this file builds.
+
 Every source under ``csrc/`` is compiled separately (in parallel) and linked
 into one shared library exposing the C ABI of ``include/hrf.h``.  Flags:
 
@@ -28,6 +32,7 @@ OBJ_DIR = os.path.join(REPO_DIR, "_build", "obj")
 
 SOURCES = [
     "raster_geom.hip",
+    "geom_ops.hip",
     "raster_sort.hip",
     "raster_render.hip",
     "asm_prop.hip",

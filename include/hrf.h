@@ -117,6 +117,66 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
                         float* grad_opacities, float* grad_plane_probs,
                         void* stream);
 
+/* ---------------- standalone geometry operators ----------------------------
+ * The reference's separate autograd operators (cov3d_cuda module,
+ * binding.cpp:14-25; python_import.py:53-281).  The rasterizer does not call
+ * them (its projection and geometry backward are fused); they exist for
+ * callers of compute_cov3d_cuda & co.  All tensors row-major fp32 on the
+ * device; n Gaussians; outputs fully overwritten. */
+
+/* Sigma = R S^2 R^T, cov3d (n,3,3).  Replaces compute_cov3d_forward
+ * (wave_rasterizer/forward.cu:138-181). */
+int hrf_cov3d_forward(const float* quats, const float* scales, int64_t n, float* cov3d,
+                      void* stream);
+/* grad_quats (n,4), grad_scales (n,3) from grad_cov3d (n,3,3).  Replaces
+ * compute_cov3d_backward (wave_rasterizer/backward.cu:274-320). */
+int hrf_cov3d_backward(const float* grad_cov3d, const float* quats, const float* scales,
+                       int64_t n, float* grad_quats, float* grad_scales, void* stream);
+/* Projection Jacobian (n,2,3), zero outside (near, far), clamp at
+ * 1.3 * 0.5 * width / fx.  Replaces compute_jacobian_forward
+ * (forward.cu:183-219). */
+int hrf_jacobian_forward(const float* cam_means, int64_t n, float fx, float fy, int32_t width,
+                         int32_t height, float near_plane, float far_plane, float* jacobian,
+                         void* stream);
+/* grad_cam (n,3) from grad_jacobian (n,2,3).  Replaces
+ * compute_jacobian_backward (backward.cu:322-361). */
+int hrf_jacobian_backward(const float* grad_jacobian, const float* cam_means, int64_t n,
+                          float fx, float fy, int32_t width, int32_t height, float near_plane,
+                          float far_plane, float* grad_cam, void* stream);
+/* cov2D (n,2,2) = ((J W) Sigma) W^T J^T + 0.3 I and the saved J (n,2,3),
+ * Sigma (n,3,3), W repeated (n,3,3), JW (n,2,3).  Replaces
+ * compute_cov2d_forward (forward.cu:221-294). */
+int hrf_cov2d_forward(const float* cam_means, const float* quats, const float* scales,
+                      const float* view_matrix, int64_t n, float fx, float fy, int32_t width,
+                      int32_t height, float near_plane, float far_plane, float* cov2d,
+                      float* jacobian, float* cov3d, float* view_rep, float* jw, void* stream);
+/* grad_cam (n,3), grad_quats (n,4), grad_scales (n,3) from grad_cov2d
+ * (n,2,2), using the saved J, Sigma, W, JW as given (view_matrix is unused,
+ * as in the reference).  Replaces compute_cov2d_backward
+ * (backward.cu:363-450). */
+int hrf_cov2d_backward(const float* grad_cov2d, const float* cam_means, const float* quats,
+                       const float* scales, const float* view_matrix, const float* jacobian,
+                       const float* cov3d, const float* view_rep, const float* jw, int64_t n,
+                       float fx, float fy, int32_t width, int32_t height, float near_plane,
+                       float far_plane, float* grad_cam, float* grad_quats, float* grad_scales,
+                       void* stream);
+/* means2D (n,2) = (fx*(-x/z)+px, fy*(-y/z)+py), (1e6, 1e6) outside (near,
+ * far).  Replaces compute_means2d_forward (forward.cu:358-394). */
+int hrf_means2d_forward(const float* cam_means, int64_t n, float fx, float fy, float px,
+                        float py, float near_plane, float far_plane, float* means2d,
+                        void* stream);
+/* grad_cam (n,3) from grad_means2d (n,2).  Replaces compute_means2d_backward
+ * (backward.cu:545-585). */
+int hrf_means2d_backward(const float* grad_means2d, const float* cam_means, int64_t n, float fx,
+                         float fy, float px, float py, float near_plane, float far_plane,
+                         float* grad_cam, void* stream);
+/* (n,2,2) inverse.  Replaces invert_cov2d_forward (forward.cu:396-432). */
+int hrf_invert_cov2d_forward(const float* cov2d, int64_t n, float* cov2d_inverse, void* stream);
+/* grad_cov2d = -(A^-1 G A^-1).  Replaces invert_cov2d_backward
+ * (backward.cu:587-627). */
+int hrf_invert_cov2d_backward(const float* grad_inverse, const float* cov2d, int64_t n,
+                              float* grad_cov2d, void* stream);
+
 /* ---------------- band-limited ASM (replaces cuda_modules) ---------------- */
 
 /* Spectral multiply on a pre-shifted (fftshift) spectrum, reading the

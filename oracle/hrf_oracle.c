@@ -497,6 +497,103 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
  * means2D (N,2) and cov2D (N,4); outputs grad_cam (N,3), grad_quat (N,4),
  * grad_scale (N,3).  Also exposes dL_dSigma (N,9) and dL_dJ (N,6) if
  * non-NULL (for the unit tests of each chain link). */
+/* means2D backward (backward.cu:453-497); zero when clipped. */
+static void means2d_bwd(float tx, float ty, float tz, float fx, float fy, float near_p,
+                        float far_p, float gx_, float gy_, float g[3]) {
+  g[0] = g[1] = g[2] = 0.f;
+  if (tz <= near_p || tz >= far_p) return;
+  const float z2 = tz * tz;
+  g[0] = -fx * gx_ / tz;
+  g[1] = -fy * gy_ / tz;
+  g[2] = (fx * tx * gx_ / z2) + (fy * ty * gy_ / z2);
+}
+
+/* cov2D chain backward (backward.cu:426-439): dL_dC = G2 J, dL_dB = dL_dC W,
+ * dL_dSigma = JW^T (G2 JW), dL_dA = dL_dB Sigma^T, dL_dJ = dL_dA W^T. */
+static void cov2d_chain_bwd(const float G2[2][2], const float J[2][3], const float Wm[3][3],
+                            const float sig[3][3], const float JW[2][3], float dSig[3][3],
+                            float dJ[2][3]) {
+  float dC[2][3], dB[2][3], X[2][3], dA[2][3];
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) dC[i][j] = dot2(G2[i][0], J[0][j], G2[i][1], J[1][j]);
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) dB[i][j] = dot3(dC[i][0], Wm[0][j], dC[i][1], Wm[1][j], dC[i][2], Wm[2][j]);
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) X[i][j] = dot2(G2[i][0], JW[0][j], G2[i][1], JW[1][j]);
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) dSig[i][j] = dot2(JW[0][i], X[0][j], JW[1][i], X[1][j]);
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) dA[i][j] = dot3(dB[i][0], sig[j][0], dB[i][1], sig[j][1], dB[i][2], sig[j][2]);
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 3; ++j) dJ[i][j] = dot3(dA[i][0], Wm[j][0], dA[i][1], Wm[j][1], dA[i][2], Wm[j][2]);
+}
+
+/* compute_jacobian_backward_kernel (backward.cu:201-272): clamp mask, but
+ * the unclamped tx/ty in dJ02/dtz, dJ12/dtz; zero when clipped. */
+static void jacobian_bwd(float tx, float ty, float tz, float fx, float fy, float lim_x,
+                         float lim_y, float near_p, float far_p, const float dJ[2][3], float g[3]) {
+  g[0] = g[1] = g[2] = 0.f;
+  if (tz <= near_p || tz >= far_p) return;
+  const float tz2 = tz * tz;
+  const float tz3 = tz2 * tz;
+  const float tx_tz = tx / tz;
+  const float ty_tz = ty / tz;
+  const float xm = (tx_tz < -lim_x || tx_tz > lim_x) ? 0.0f : 1.0f;
+  const float ym = (ty_tz < -lim_y || ty_tz > lim_y) ? 0.0f : 1.0f;
+  const float dJ00_dtz = -fx / tz2;
+  const float dJ02_dtx = xm * (-fx / tz2);
+  const float dJ02_dtz = xm * (2.0f * fx * tx / tz3);
+  const float dJ11_dtz = -fy / tz2;
+  const float dJ12_dty = ym * (-fy / tz2);
+  const float dJ12_dtz = ym * (2.0f * fy * ty / tz3);
+  g[0] = dJ[0][2] * dJ02_dtx;
+  g[1] = dJ[1][2] * dJ12_dty;
+  g[2] = dJ[0][0] * dJ00_dtz + dJ[0][2] * dJ02_dtz + dJ[1][1] * dJ11_dtz + dJ[1][2] * dJ12_dtz;
+}
+
+/* compute_cov3d_backward_cuda_kernel (backward.cu:76-198): Gm[i][j] =
+ * grad[i*3+j] read as GLM column i, row j; grad_s = (2 R^T G R)[k][k] s[k];
+ * grad_q = elementwise sums over S * dR/dq (backward.cu:31-73,161-187). */
+static void cov3d_bwd(const float Gm[3][3], const float* q, const float* s, float gq[4],
+                      float gs[3]) {
+  float R[3][3], S[3][3];
+  float r, x, y, z;
+  rotation(q, R, &r, &x, &y, &z);
+  diag3(s, S);
+  const float dRr[3][3] = {{0.f, -2.f * z, 2.f * y}, {2.f * z, 0.f, -2.f * x}, {-2.f * y, 2.f * x, 0.f}};
+  const float dRx[3][3] = {{0.f, 2.f * y, 2.f * z}, {2.f * y, -4.f * x, -2.f * r}, {2.f * z, 2.f * r, -4.f * x}};
+  const float dRy[3][3] = {{-4.f * y, 2.f * x, 2.f * r}, {2.f * x, 0.f, 2.f * z}, {-2.f * r, 2.f * z, -4.f * y}};
+  const float dRz[3][3] = {{-4.f * z, -2.f * r, 2.f * x}, {2.f * r, -4.f * z, 2.f * y}, {2.f * x, 2.f * y, 0.f}};
+  float Rt2[3][3], T1[3][3], temp[3][3];
+  for (int c = 0; c < 3; ++c)
+    for (int rr = 0; rr < 3; ++rr) Rt2[c][rr] = 2.0f * R[rr][c];
+  glm_mul(Rt2, Gm, T1);
+  glm_mul(T1, R, temp);
+  gs[0] = temp[0][0] * s[0];
+  gs[1] = temp[1][1] * s[1];
+  gs[2] = temp[2][2] * s[2];
+  float SR[3][3], Xr[3][3], Xx[3][3], Xy[3][3], Xz[3][3];
+  glm_mul(S, R, SR);
+  glm_mul(S, dRr, Xr);
+  glm_mul(S, dRx, Xx);
+  glm_mul(S, dRy, Xy);
+  glm_mul(S, dRz, Xz);
+  float gr = 0.f, gxq = 0.f, gyq = 0.f, gzq = 0.f;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      gr += Gm[i][j] * (Xr[j][i] * SR[i][j] + SR[j][i] * Xr[i][j]);
+      gxq += Gm[i][j] * (Xx[j][i] * SR[i][j] + SR[j][i] * Xx[i][j]);
+      gyq += Gm[i][j] * (Xy[j][i] * SR[i][j] + SR[j][i] * Xy[i][j]);
+      gzq += Gm[i][j] * (Xz[j][i] * SR[i][j] + SR[j][i] * Xz[i][j]);
+    }
+  gq[0] = gr;
+  gq[1] = gxq;
+  gq[2] = gyq;
+  gq[3] = gzq;
+}
+
+/* Fused geometry backward as the rasterizer backward uses it
+ * (backward_splat.cu:364-417): means2D + cov2D chain + Jacobian + Sigma. */
 void oracle_geom_backward(int64_t n, const float* cam, const float* quats, const float* scales,
                           const float* view, float fx, float fy, int W, int H, float near_p,
                           float far_p, const float* g_means2d, const float* g_cov2d,
@@ -510,105 +607,124 @@ void oracle_geom_backward(int64_t n, const float* cam, const float* quats, const
 #pragma omp parallel for schedule(static)
   for (int64_t g = 0; g < n; ++g) {
     const float tx = cam[g * 3 + 0], ty = cam[g * 3 + 1], tz = cam[g * 3 + 2];
-    const int clipped = (tz <= near_p || tz >= far_p);
     float J[2][3], sig9[9], sig[3][3], JW[2][3], cv[2][2];
     jacobian(tx, ty, tz, fx, fy, lim_x, lim_y, near_p, far_p, J);
     oracle_cov3d(quats + g * 4, scales + g * 3, sig9);
     for (int i = 0; i < 3; ++i)
       for (int j = 0; j < 3; ++j) sig[i][j] = sig9[i * 3 + j];
     cov2d_chain(J, Wm, sig, JW, cv);
-
-    /* means2D backward */
-    float m0 = 0.f, m1 = 0.f, m2 = 0.f;
-    if (!clipped) {
-      const float z2 = tz * tz;
-      const float gx_ = g_means2d[g * 2 + 0], gy_ = g_means2d[g * 2 + 1];
-      m0 = -fx * gx_ / tz;
-      m1 = -fy * gy_ / tz;
-      m2 = (fx * tx * gx_ / z2) + (fy * ty * gy_ / z2);
-    }
-    /* cov2D backward, G2 = grad_cov2D viewed (2,2) */
+    float gm[3], gj[3], dSig[3][3], dJ[2][3];
+    means2d_bwd(tx, ty, tz, fx, fy, near_p, far_p, g_means2d[g * 2 + 0], g_means2d[g * 2 + 1], gm);
     const float G2[2][2] = {{g_cov2d[g * 4 + 0], g_cov2d[g * 4 + 1]},
                             {g_cov2d[g * 4 + 2], g_cov2d[g * 4 + 3]}};
-    float dC[2][3], dB[2][3], X[2][3], dSig[3][3], dA[2][3], dJ[2][3];
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 3; ++j) dC[i][j] = dot2(G2[i][0], J[0][j], G2[i][1], J[1][j]);
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 3; ++j) dB[i][j] = dot3(dC[i][0], Wm[0][j], dC[i][1], Wm[1][j], dC[i][2], Wm[2][j]);
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 3; ++j) X[i][j] = dot2(G2[i][0], JW[0][j], G2[i][1], JW[1][j]);
-    for (int i = 0; i < 3; ++i)
-      for (int j = 0; j < 3; ++j) dSig[i][j] = dot2(JW[0][i], X[0][j], JW[1][i], X[1][j]);
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 3; ++j) dA[i][j] = dot3(dB[i][0], sig[j][0], dB[i][1], sig[j][1], dB[i][2], sig[j][2]);
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 3; ++j) dJ[i][j] = dot3(dA[i][0], Wm[j][0], dA[i][1], Wm[j][1], dA[i][2], Wm[j][2]);
+    cov2d_chain_bwd(G2, J, Wm, sig, JW, dSig, dJ);
     if (dsig_out) memcpy(dsig_out + g * 9, dSig, sizeof(float) * 9);
     if (dJ_out) memcpy(dJ_out + g * 6, dJ, sizeof(float) * 6);
+    jacobian_bwd(tx, ty, tz, fx, fy, lim_x, lim_y, near_p, far_p, dJ, gj);
+    g_cam[g * 3 + 0] = gm[0] + gj[0];
+    g_cam[g * 3 + 1] = gm[1] + gj[1];
+    g_cam[g * 3 + 2] = gm[2] + gj[2];
+    cov3d_bwd(dSig, quats + g * 4, scales + g * 3, g_quat + g * 4, g_scale + g * 3);
+  }
+}
 
-    /* Jacobian backward */
-    float j0 = 0.f, j1 = 0.f, j2 = 0.f;
-    if (!clipped) {
-      const float tz2 = tz * tz;
-      const float tz3 = tz2 * tz;
-      const float tx_tz = tx / tz;
-      const float ty_tz = ty / tz;
-      const float xm = (tx_tz < -lim_x || tx_tz > lim_x) ? 0.0f : 1.0f;
-      const float ym = (ty_tz < -lim_y || ty_tz > lim_y) ? 0.0f : 1.0f;
-      const float dJ00_dtz = -fx / tz2;
-      const float dJ02_dtx = xm * (-fx / tz2);
-      const float dJ02_dtz = xm * (2.0f * fx * tx / tz3);
-      const float dJ11_dtz = -fy / tz2;
-      const float dJ12_dty = ym * (-fy / tz2);
-      const float dJ12_dtz = ym * (2.0f * fy * ty / tz3);
-      j0 = dJ[0][2] * dJ02_dtx;
-      j1 = dJ[1][2] * dJ12_dty;
-      j2 = dJ[0][0] * dJ00_dtz + dJ[0][2] * dJ02_dtz + dJ[1][1] * dJ11_dtz + dJ[1][2] * dJ12_dtz;
-    }
-    g_cam[g * 3 + 0] = m0 + j0;
-    g_cam[g * 3 + 1] = m1 + j1;
-    g_cam[g * 3 + 2] = m2 + j2;
+/* ----------------------------------------- standalone geometry operators */
 
-    /* Sigma backward in GLM storage */
-    const float* q = quats + g * 4;
-    const float* s = scales + g * 3;
+/* compute_cov3d_backward (backward.cu:274-320). */
+void oracle_cov3d_backward(int64_t n, const float* grad9, const float* quats, const float* scales,
+                           float* g_quat, float* g_scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < n; ++g) {
     float Gm[3][3];
     for (int i = 0; i < 3; ++i)
-      for (int j = 0; j < 3; ++j) Gm[i][j] = dSig[i][j];
-    float R[3][3], S[3][3];
-    float r, x, y, z;
-    rotation(q, R, &r, &x, &y, &z);
-    diag3(s, S);
-    const float dRr[3][3] = {{0.f, -2.f * z, 2.f * y}, {2.f * z, 0.f, -2.f * x}, {-2.f * y, 2.f * x, 0.f}};
-    const float dRx[3][3] = {{0.f, 2.f * y, 2.f * z}, {2.f * y, -4.f * x, -2.f * r}, {2.f * z, 2.f * r, -4.f * x}};
-    const float dRy[3][3] = {{-4.f * y, 2.f * x, 2.f * r}, {2.f * x, 0.f, 2.f * z}, {-2.f * r, 2.f * z, -4.f * y}};
-    const float dRz[3][3] = {{-4.f * z, -2.f * r, 2.f * x}, {2.f * r, -4.f * z, 2.f * y}, {2.f * x, 2.f * y, 0.f}};
-    float Rt2[3][3], T1[3][3], temp[3][3];
-    for (int c = 0; c < 3; ++c)
-      for (int rr = 0; rr < 3; ++rr) Rt2[c][rr] = 2.0f * R[rr][c];
-    glm_mul(Rt2, Gm, T1);
-    glm_mul(T1, R, temp);
-    g_scale[g * 3 + 0] = temp[0][0] * s[0];
-    g_scale[g * 3 + 1] = temp[1][1] * s[1];
-    g_scale[g * 3 + 2] = temp[2][2] * s[2];
-    float SR[3][3], Xr[3][3], Xx[3][3], Xy[3][3], Xz[3][3];
-    glm_mul(S, R, SR);
-    glm_mul(S, dRr, Xr);
-    glm_mul(S, dRx, Xx);
-    glm_mul(S, dRy, Xy);
-    glm_mul(S, dRz, Xz);
-    float gr = 0.f, gxq = 0.f, gyq = 0.f, gzq = 0.f;
+      for (int j = 0; j < 3; ++j) Gm[i][j] = grad9[g * 9 + i * 3 + j];
+    cov3d_bwd(Gm, quats + g * 4, scales + g * 3, g_quat + g * 4, g_scale + g * 3);
+  }
+}
+
+/* compute_jacobian_backward (backward.cu:322-361). */
+void oracle_jacobian_backward(int64_t n, const float* grad6, const float* cam, float fx, float fy,
+                              int W, int H, float near_p, float far_p, float* g_cam) {
+  float lim_x, lim_y;
+  lims(W, H, fx, fy, &lim_x, &lim_y);
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < n; ++g) {
+    float dJ[2][3];
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 3; ++j) dJ[i][j] = grad6[g * 6 + i * 3 + j];
+    jacobian_bwd(cam[g * 3 + 0], cam[g * 3 + 1], cam[g * 3 + 2], fx, fy, lim_x, lim_y, near_p,
+                 far_p, dJ, g_cam + g * 3);
+  }
+}
+
+/* compute_cov2d_backward (backward.cu:363-450) on the saved J, Sigma, W, JW
+ * as given; grad_cam from the Jacobian chain only. */
+void oracle_cov2d_backward(int64_t n, const float* grad4, const float* cam, const float* quats,
+                           const float* scales, const float* J6, const float* sig9,
+                           const float* W9, const float* JW6, float fx, float fy, int W, int H,
+                           float near_p, float far_p, float* g_cam, float* g_quat,
+                           float* g_scale) {
+  float lim_x, lim_y;
+  lims(W, H, fx, fy, &lim_x, &lim_y);
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < n; ++g) {
+    float J[2][3], sig[3][3], Wm[3][3], JW[2][3], dSig[3][3], dJ[2][3];
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 3; ++j) {
+        J[i][j] = J6[g * 6 + i * 3 + j];
+        JW[i][j] = JW6[g * 6 + i * 3 + j];
+      }
     for (int i = 0; i < 3; ++i)
       for (int j = 0; j < 3; ++j) {
-        gr += Gm[i][j] * (Xr[j][i] * SR[i][j] + SR[j][i] * Xr[i][j]);
-        gxq += Gm[i][j] * (Xx[j][i] * SR[i][j] + SR[j][i] * Xx[i][j]);
-        gyq += Gm[i][j] * (Xy[j][i] * SR[i][j] + SR[j][i] * Xy[i][j]);
-        gzq += Gm[i][j] * (Xz[j][i] * SR[i][j] + SR[j][i] * Xz[i][j]);
+        sig[i][j] = sig9[g * 9 + i * 3 + j];
+        Wm[i][j] = W9[g * 9 + i * 3 + j];
       }
-    g_quat[g * 4 + 0] = gr;
-    g_quat[g * 4 + 1] = gxq;
-    g_quat[g * 4 + 2] = gyq;
-    g_quat[g * 4 + 3] = gzq;
+    const float G2[2][2] = {{grad4[g * 4 + 0], grad4[g * 4 + 1]}, {grad4[g * 4 + 2], grad4[g * 4 + 3]}};
+    cov2d_chain_bwd(G2, J, Wm, sig, JW, dSig, dJ);
+    jacobian_bwd(cam[g * 3 + 0], cam[g * 3 + 1], cam[g * 3 + 2], fx, fy, lim_x, lim_y, near_p,
+                 far_p, dJ, g_cam + g * 3);
+    cov3d_bwd(dSig, quats + g * 4, scales + g * 3, g_quat + g * 4, g_scale + g * 3);
+  }
+}
+
+/* compute_means2d_backward (backward.cu:545-585). */
+void oracle_means2d_backward(int64_t n, const float* grad2, const float* cam, float fx, float fy,
+                             float near_p, float far_p, float* g_cam) {
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < n; ++g)
+    means2d_bwd(cam[g * 3 + 0], cam[g * 3 + 1], cam[g * 3 + 2], fx, fy, near_p, far_p,
+                grad2[g * 2 + 0], grad2[g * 2 + 1], g_cam + g * 3);
+}
+
+/* invert_cov2d_kernel (forward.cu:333-356). */
+void oracle_invert_cov2d(int64_t n, const float* cov4, float* out4) {
+  for (int64_t g = 0; g < n; ++g) {
+    const float a = cov4[g * 4 + 0], b = cov4[g * 4 + 1], c = cov4[g * 4 + 2], d = cov4[g * 4 + 3];
+    const float det = a * d - b * c;
+    const float inv_det = 1.0f / det;
+    out4[g * 4 + 0] = d * inv_det;
+    out4[g * 4 + 1] = -b * inv_det;
+    out4[g * 4 + 2] = -c * inv_det;
+    out4[g * 4 + 3] = a * inv_det;
+  }
+}
+
+/* invert_cov2d_backward_kernel (backward.cu:500-543): -(A^-1 (G A^-1)). */
+void oracle_invert_cov2d_backward(int64_t n, const float* g4, const float* cov4, float* out4) {
+  for (int64_t g = 0; g < n; ++g) {
+    const float a = cov4[g * 4 + 0], b = cov4[g * 4 + 1], c = cov4[g * 4 + 2], d = cov4[g * 4 + 3];
+    const float det = a * d - b * c;
+    const float inv_det = 1.0f / det;
+    const float ia = d * inv_det, ib = -b * inv_det, ic = -c * inv_det, id = a * inv_det;
+    const float ga = g4[g * 4 + 0], gb = g4[g * 4 + 1], gc = g4[g * 4 + 2], gd = g4[g * 4 + 3];
+    const float ta = ga * ia + gb * ic;
+    const float tb = ga * ib + gb * id;
+    const float tc = gc * ia + gd * ic;
+    const float td = gc * ib + gd * id;
+    out4[g * 4 + 0] = -(ia * ta + ib * tc);
+    out4[g * 4 + 1] = -(ia * tb + ib * td);
+    out4[g * 4 + 2] = -(ic * ta + id * tc);
+    out4[g * 4 + 3] = -(ic * tb + id * td);
   }
 }
 

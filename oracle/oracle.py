@@ -68,6 +68,15 @@ def lib():
     L.oracle_geom_backward.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _flt, _flt, _int,
                                        _int, _flt, _flt, _f32p, _f32p, _f32p, _f32p, _f32p,
                                        _f32p, _f32p]
+    L.oracle_cov3d_backward.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _f32p]
+    L.oracle_jacobian_backward.argtypes = [_i64, _f32p, _f32p, _flt, _flt, _int, _int, _flt,
+                                           _flt, _f32p]
+    L.oracle_cov2d_backward.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                        _f32p, _flt, _flt, _int, _int, _flt, _flt, _f32p,
+                                        _f32p, _f32p]
+    L.oracle_means2d_backward.argtypes = [_i64, _f32p, _f32p, _flt, _flt, _flt, _flt, _f32p]
+    L.oracle_invert_cov2d.argtypes = [_i64, _f32p, _f32p]
+    L.oracle_invert_cov2d_backward.argtypes = [_i64, _f32p, _f32p, _f32p]
     L.oracle_asm_spectral.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _int, _int,
                                       _flt, _flt, _flt, _flt, _int]
     L.oracle_asm_consts.argtypes = [_flt, _flt, _flt, _int, _f32p]
@@ -215,6 +224,82 @@ def geom_backward(g: Gaussians, cam: Camera, grad_means2d, grad_cov2d, want_link
     if want_links:
         return gc, gq, gs, dsig.reshape(n, 3, 3), dJ.reshape(n, 2, 3)
     return gc, gq, gs
+
+
+# ---------------------------------------------- standalone geometry operators
+# (the reference's compute_*_{forward,backward}, binding.cpp:14-25)
+
+def cov3d_forward(quats, scales):
+    """compute_cov3d_forward (forward.cu:138-181): (N,3,3)."""
+    L = lib()
+    q, s = _f32(quats), _f32(scales)
+    out = np.zeros((q.shape[0], 9), np.float32)
+    for i in range(q.shape[0]):
+        L.oracle_cov3d(q[i], s[i], out[i])
+    return out.reshape(-1, 3, 3)
+
+
+def cov3d_backward(grad, quats, scales):
+    """compute_cov3d_backward (backward.cu:274-320)."""
+    n = quats.shape[0]
+    gq = np.zeros((n, 4), np.float32)
+    gs = np.zeros((n, 3), np.float32)
+    lib().oracle_cov3d_backward(n, _f32(grad).reshape(n, 9), _f32(quats), _f32(scales), gq, gs)
+    return gq, gs
+
+
+def jacobian_backward(grad, cam_means, fx, fy, W, H, near, far):
+    """compute_jacobian_backward (backward.cu:322-361)."""
+    n = cam_means.shape[0]
+    out = np.zeros((n, 3), np.float32)
+    lib().oracle_jacobian_backward(n, _f32(grad).reshape(n, 6), _f32(cam_means), fx, fy, W, H,
+                                   near, far, out)
+    return out
+
+
+def cov2d_forward(g: Gaussians, cam: Camera):
+    """compute_cov2d_forward (forward.cu:221-294): cov2D, J, Sigma, W rep, JW."""
+    pr = project(g, cam)
+    n = g.n
+    W = np.broadcast_to(_f32(cam.view).reshape(1, 3, 3), (n, 3, 3)).copy()
+    return pr["cov2d"].reshape(n, 2, 2), pr["J"], pr["sigma"], W, pr["JW"]
+
+
+def cov2d_backward(grad, cam_means, quats, scales, J, sig, W, JW, fx, fy, Wd, Hd, near, far):
+    """compute_cov2d_backward (backward.cu:363-450) on the saved intermediates."""
+    n = cam_means.shape[0]
+    gc = np.zeros((n, 3), np.float32)
+    gq = np.zeros((n, 4), np.float32)
+    gs = np.zeros((n, 3), np.float32)
+    lib().oracle_cov2d_backward(n, _f32(grad).reshape(n, 4), _f32(cam_means), _f32(quats),
+                                _f32(scales), _f32(J).reshape(n, 6), _f32(sig).reshape(n, 9),
+                                _f32(W).reshape(n, 9), _f32(JW).reshape(n, 6), fx, fy, Wd, Hd,
+                                near, far, gc, gq, gs)
+    return gc, gq, gs
+
+
+def means2d_backward(grad, cam_means, fx, fy, near, far):
+    """compute_means2d_backward (backward.cu:545-585)."""
+    n = cam_means.shape[0]
+    out = np.zeros((n, 3), np.float32)
+    lib().oracle_means2d_backward(n, _f32(grad), _f32(cam_means), fx, fy, near, far, out)
+    return out
+
+
+def invert_cov2d(cov):
+    """invert_cov2d_forward (forward.cu:396-432)."""
+    n = cov.shape[0]
+    out = np.zeros((n, 4), np.float32)
+    lib().oracle_invert_cov2d(n, _f32(cov).reshape(n, 4), out)
+    return out.reshape(n, 2, 2)
+
+
+def invert_cov2d_backward(grad, cov):
+    """invert_cov2d_backward (backward.cu:587-627)."""
+    n = cov.shape[0]
+    out = np.zeros((n, 4), np.float32)
+    lib().oracle_invert_cov2d_backward(n, _f32(grad).reshape(n, 4), _f32(cov).reshape(n, 4), out)
+    return out.reshape(n, 2, 2)
 
 
 def visible_indices(g: Gaussians, cam: Camera):

@@ -489,6 +489,94 @@ def test_jacobian_backward_is_derivative_unclamped(oracle_mod):
     np.testing.assert_allclose(gc, exp, rtol=1e-4, atol=1e-8)
 
 
+# ------------------------------------------- standalone geometry operators
+
+def test_invert_cov2d_is_inverse(oracle_mod):
+    rng = np.random.default_rng(12)
+    A = rng.normal(size=(50, 2, 2))
+    A = A @ A.transpose(0, 2, 1) + 0.5 * np.eye(2)
+    inv = oracle_mod.invert_cov2d(A.astype(np.float32)).astype(np.float64)
+    np.testing.assert_allclose(A @ inv, np.broadcast_to(np.eye(2), A.shape), atol=1e-5)
+
+
+def test_invert_cov2d_backward_is_derivative(oracle_mod):
+    """For symmetric A, -(A^-1 G A^-1) is the derivative of <G, A^-1>."""
+    rng = np.random.default_rng(13)
+    n = 10
+    A = rng.normal(size=(n, 2, 2))
+    A = A @ A.transpose(0, 2, 1) + 0.5 * np.eye(2)
+    G = rng.normal(size=(n, 2, 2))
+    got = oracle_mod.invert_cov2d_backward(G.astype(np.float32), A.astype(np.float32))
+    h = 1e-6
+    fd = np.zeros_like(A)
+    for i in range(2):
+        for j in range(2):
+            Ap, Am = A.copy(), A.copy()
+            Ap[:, i, j] += h
+            Am[:, i, j] -= h
+            fd[:, i, j] = ((G * np.linalg.inv(Ap)).sum((1, 2)) -
+                           (G * np.linalg.inv(Am)).sum((1, 2))) / (2 * h)
+    np.testing.assert_allclose(got, fd, rtol=1e-4, atol=1e-5)
+
+
+def test_standalone_ops_compose_to_fused_geometry_backward(oracle_mod):
+    """means2d_backward + cov2d_backward (on cov2d_forward's saved J, Sigma,
+    W, JW) reproduce the fused geometry backward bit for bit, and
+    cov3d_backward of its dL/dSigma gives its quaternion/scale gradients."""
+    g, cam = _geom_case(oracle_mod)
+    rng = np.random.default_rng(14)
+    gm = rng.normal(size=(g.n, 2)).astype(np.float32)
+    G2 = rng.normal(size=(g.n, 4)).astype(np.float32)
+    gc, gq, gs, dsig, _ = oracle_mod.geom_backward(g, cam, gm, G2, want_links=True)
+    cov, J, sig, W, JW = oracle_mod.cov2d_forward(g, cam)
+    c_cam, c_q, c_s = oracle_mod.cov2d_backward(G2, g.cam_means, g.quats, g.scales, J, sig, W,
+                                                JW, cam.fx, cam.fy, cam.width, cam.height,
+                                                cam.near, cam.far)
+    m_cam = oracle_mod.means2d_backward(gm, g.cam_means, cam.fx, cam.fy, cam.near, cam.far)
+    np.testing.assert_array_equal(m_cam + c_cam, gc)
+    np.testing.assert_array_equal(c_q, gq)
+    np.testing.assert_array_equal(c_s, gs)
+    q2, s2 = oracle_mod.cov3d_backward(dsig, g.quats, g.scales)
+    np.testing.assert_array_equal(q2, gq)
+    np.testing.assert_array_equal(s2, gs)
+    np.testing.assert_array_equal(oracle_mod.cov3d_forward(g.quats, g.scales), sig)
+
+
+def test_standalone_jacobian_backward_is_derivative(oracle_mod):
+    """compute_jacobian_backward: derivative of <dJ, J(t)> where no clamp is
+    active, and the x/y terms drop where tx/tz or ty/tz is clamped."""
+    g, cam = _geom_case(oracle_mod)
+    rng = np.random.default_rng(15)
+    dJ = rng.normal(size=(g.n, 2, 3))
+    got = oracle_mod.jacobian_backward(dJ.astype(np.float32), g.cam_means, cam.fx, cam.fy,
+                                       cam.width, cam.height, cam.near, cam.far)
+    t = g.cam_means.astype(np.float64)
+
+    def loss(t):
+        x, y, z = t[:, 0], t[:, 1], t[:, 2]
+        f = cam.fx
+        J = np.zeros((len(z), 2, 3))
+        J[:, 0, 0] = f / z
+        J[:, 0, 2] = -f * x / z ** 2
+        J[:, 1, 1] = f / z
+        J[:, 1, 2] = -f * y / z ** 2
+        return (dJ * J).sum((1, 2))
+
+    h = 1e-6
+    fd = np.zeros_like(t)
+    for k in range(3):
+        tp, tm = t.copy(), t.copy()
+        tp[:, k] += h
+        tm[:, k] -= h
+        fd[:, k] = (loss(tp) - loss(tm)) / (2 * h)
+    np.testing.assert_allclose(got, fd, rtol=1e-4, atol=1e-4)
+    # A point far off axis: tx/tz beyond the 1.3 * tan(fov/2) clamp.
+    far_pt = np.array([[40.0, 0.1, 4.0]], np.float32)
+    gc = oracle_mod.jacobian_backward(np.ones((1, 2, 3), np.float32), far_pt, cam.fx, cam.fy,
+                                      cam.width, cam.height, cam.near, cam.far)
+    assert gc[0, 0] == 0.0 and gc[0, 1] != 0.0
+
+
 # ------------------------------------------------------------------- ASM
 
 PITCH = 3.74e-6
