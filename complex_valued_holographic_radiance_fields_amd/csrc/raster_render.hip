@@ -47,6 +47,10 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
   *n = static_cast<int>(b - a);
 }
 
+// -log2(e)/2: the backward stages the conic pre-scaled by it, so the
+// Gaussian's exponent comes out in base 2 with the -1/2 folded in.
+constexpr float kBwdConicScale = -0.72134752044448170368f;
+
 // exp(x) through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
@@ -254,10 +258,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     maxlast = max(maxlast, wmax[w]);
   }
 
-  float accr[C], acci[C], lastr[C], lasti[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) accr[c] = acci[c] = lastr[c] = lasti[c] = 0.0f;
-  float last_alpha = 0.0f;
+  float R = 0.0f, S_last = 0.0f, last_alpha = 0.0f;
   const float half_w = 0.5f * static_cast<float>(p.W);
   const float half_h = 0.5f * static_cast<float>(p.H);
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
@@ -315,9 +316,14 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     const int cnt = tot[0];
     if (qm != 0u) {
       const int slot = off[0];
+      // quad 0: (mx, my, kc*cxx, kc*cxy); quad 1: (kc*czz, o*w, -, -) with
+      // kc = -log2(e)/2, so the exponent of G = exp2(.) is dx*u + dy*v with
+      // u = kc*(cxx dx + cxy dy) and v = kc*(cxy dx + czz dy).
+      s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
+                                     kBwdConicScale * rq[0].w);
+      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, rq[1].z * wpl, 0.0f, 0.0f);
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) s_rec[slot * NQ + q] = rq[q];
-      s_rec[slot * NQ + 1].w = wpl;
+      for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = rq[q];
       s_k[slot] = k;
       s_g[slot] = g;
 #pragma unroll
@@ -331,69 +337,65 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] : nl;
     for (int hi = nl - 1; hi >= 0; hi -= G) {
+      // Branch-free: every lane evaluates every member of the group and a
+      // single predicate `ok` (list position < n_contrib, power <= 0,
+      // alpha >= 1/255) selects the state updates and zeroes the partials.
       float buf[64];
-#pragma unroll
-      for (int i = 0; i < 64; ++i) buf[i] = 0.0f;
       bool any = false;
 #pragma unroll
       for (int m = 0; m < G; ++m) {
         const int li = hi - m;
-        if (li < 0) break;
-        const int slot = s_wl[wave][li];
+        const bool valid = li >= 0;
+        const int slot = s_wl[wave][valid ? li : 0];
         const int kk = s_k[slot];
-        if (inside && kk < last) {
-          const float4 a = s_rec[slot * NQ];
-          const float4 b = s_rec[slot * NQ + 1];
-          const float dx = a.x - pxf, dy = a.y - pyf;
-          const float cxx = a.z, cxy = a.w, czz = b.y;
-          const float power = -0.5f * (cxx * dx * dx + czz * dy * dy) - cxy * dx * dy;
-          if (power <= 0.0f) {
-            const float Gv = fast_exp(power);
-            const float alpha = fminf(kMaxAlpha, b.z * Gv * b.w);
-            if (alpha >= kMinAlphaBwd) {
-              T = T * __builtin_amdgcn_rcpf(1.0f - alpha);
-              const float dcol = alpha * T;
-              float amp[8];
-              {
-                const float4 c0 = s_rec[slot * NQ + 2];
-                const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
-                amp[0] = c0.x;
-                amp[1] = c0.y;
-                amp[2] = c0.z;
-                amp[3] = c0.w;
-                amp[4] = c1.x;
-                amp[5] = c1.y;
-                amp[6] = c1.z;
-                amp[7] = c1.w;
-              }
-              float dLda = 0.0f;
+        const float4 a = s_rec[slot * NQ];
+        const float4 b = s_rec[slot * NQ + 1];
+        const float dx = a.x - pxf, dy = a.y - pyf;
+        const float u = fmaf(a.z, dx, a.w * dy);
+        const float v = fmaf(b.x, dy, a.w * dx);
+        const float pw = fmaf(dx, u, dy * v);  // = log2(e) * power
+        const float Gv = __builtin_amdgcn_exp2f(pw);
+        const float alpha = fminf(kMaxAlpha, b.y * Gv);
+        const bool ok = valid && kk < last && pw <= 0.0f && alpha >= kMinAlphaBwd;
+        any = any || ok;
+        T = ok ? T * __builtin_amdgcn_rcpf(1.0f - alpha) : T;
+        const float dcol = ok ? alpha * T : 0.0f;
+        // Re(colour * conj(g)) summed over channels; the reference's complex
+        // recurrence acc = la*last + (1-la)*acc is linear, so only its
+        // projection R = sum_c Re(acc_c conj(g_c)) is carried.
+        float S;
+        {
+          const float4 c0 = s_rec[slot * NQ + 2];
+          const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
+          const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+          S = amp[0] * gre[0];
+          S = fmaf(amp[1], gim[0], S);
 #pragma unroll
-              for (int c = 0; c < C; ++c) {
-                const float cr = amp[2 * c], ci = amp[2 * c + 1];
-                // last_alpha*last + (1-last_alpha)*acc, as acc + last_alpha*(last-acc)
-                accr[c] = fmaf(last_alpha, lastr[c] - accr[c], accr[c]);
-                acci[c] = fmaf(last_alpha, lasti[c] - acci[c], acci[c]);
-                lastr[c] = cr;
-                lasti[c] = ci;
-                dLda = fmaf(cr - accr[c], gre[c], dLda);
-                dLda = fmaf(ci - acci[c], gim[c], dLda);
-                buf[m * NV + 6 + c] = dcol * gre[c];
-                buf[m * NV + 6 + C + c] = dcol * gim[c];
-              }
-              dLda *= T;
-              last_alpha = alpha;
-              const float Q = Gv * dLda;
-              buf[m * NV + 0] = Q * fmaf(dx, cxx, dy * cxy);
-              buf[m * NV + 1] = Q * fmaf(dy, czz, dx * cxy);
-              buf[m * NV + 2] = Q * dx * dx;
-              buf[m * NV + 3] = Q * dx * dy;
-              buf[m * NV + 4] = Q * dy * dy;
-              buf[m * NV + 5] = Q;
-              any = true;
-            }
+          for (int c = 1; c < C; ++c) {
+            S = fmaf(amp[2 * c], gre[c], S);
+            S = fmaf(amp[2 * c + 1], gim[c], S);
           }
         }
+        const float Rn = fmaf(last_alpha, S_last - R, R);
+        R = ok ? Rn : R;
+        S_last = ok ? S : S_last;
+        last_alpha = ok ? alpha : last_alpha;
+        const float Q = ok ? Gv * ((S - R) * T) : 0.0f;
+        const float Qdx = Q * dx, Qdy = Q * dy;
+        buf[m * NV + 0] = Q * u;
+        buf[m * NV + 1] = Q * v;
+        buf[m * NV + 2] = Qdx * dx;
+        buf[m * NV + 3] = Qdx * dy;
+        buf[m * NV + 4] = Qdy * dy;
+        buf[m * NV + 5] = Q;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          buf[m * NV + 6 + c] = dcol * gre[c];
+          buf[m * NV + 6 + C + c] = dcol * gim[c];
+        }
       }
+#pragma unroll
+      for (int i = G * NV; i < 64; ++i) buf[i] = 0.0f;
       if (__ballot(any) != 0ull) {
         const float tot_v = transpose_reduce64(buf);
         if (lane < G * NV) {
@@ -409,16 +411,15 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       if (val == 0.0f) continue;
       const int j = e / NV, i = e - j * NV;
       const int gg = s_g[j];
-      const float4 b = s_rec[j * NQ + 1];
-      const float ow = b.z * b.w;
+      const float ow = s_rec[j * NQ + 1].y;
       int slot;
       float scale;
-      if (i == 0) {
+      if (i == 0) {  // partials carry u = kc*(cxx dx + cxy dy)
         slot = 0;
-        scale = -half_w * ow;
+        scale = -half_w * ow / kBwdConicScale;
       } else if (i == 1) {
         slot = 1;
-        scale = -half_h * ow;
+        scale = -half_h * ow / kBwdConicScale;
       } else if (i < 5) {
         slot = i;
         scale = -0.5f * ow;
