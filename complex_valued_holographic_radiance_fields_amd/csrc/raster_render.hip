@@ -47,14 +47,9 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
   *n = static_cast<int>(b - a);
 }
 
-// -log2(e)/2: the backward stages the conic pre-scaled by it, so the
+// -log2(e)/2: the render kernels stage the conic pre-scaled by it, so the
 // Gaussian's exponent comes out in base 2 with the -1/2 folded in.
 constexpr float kBwdConicScale = -0.72134752044448170368f;
-
-// exp(x) through the hardware base-2 exponential.
-__device__ __forceinline__ float fast_exp(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-}
 
 // Ballot compaction of one flag per thread across the block.  Returns the
 // compacted position of this thread's entry and the block-wide count.
@@ -79,8 +74,8 @@ template <int C>
 __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   constexpr int NQ = rec_quads(C);
   constexpr int RS = rec_stride(C);
+  constexpr int kUnroll = 8;
   __shared__ float4 s_rec[kBlock * NQ];
-  __shared__ int s_k[kBlock];
   __shared__ int s_wt[kBlock / 64];
 
   int tile, plane;
@@ -114,48 +109,59 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     const int pos = block_compact(mem, s_wt, &cnt);
     if (mem) {
       const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
+      float4 rq[NQ];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) s_rec[pos * NQ + q] = src[q];
-      s_rec[pos * NQ + 1].w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
-      s_k[pos] = k;
+      for (int q = 0; q < NQ; ++q) rq[q] = src[q];
+      const float w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
+      // quad 0: (mx, my, kc*i00, kc*i01); quad 1: (kc*i10, kc*i11, o*w, -),
+      // kc = -log2(e)/2: the exponent of G = exp2(.) is then a quadratic
+      // form with the -1/2 and the change of base folded in.
+      s_rec[pos * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
+                                    kBwdConicScale * rq[0].w);
+      s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].x, kBwdConicScale * rq[1].y,
+                                        rq[1].z * w, __int_as_float(k + 1));
+#pragma unroll
+      for (int q = 2; q < NQ; ++q) s_rec[pos * NQ + q] = rq[q];
+    }
+    // Pad the staged batch to a multiple of kUnroll with members no pixel
+    // can use: a positive-definite exponent 1e12 (power > 0), so they never
+    // contribute or count.
+    const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
+    if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
+      const int q0 = static_cast<int>(threadIdx.x) * NQ;
+      s_rec[q0] = make_float4(1e6f, 1e6f, 1.0f, 0.0f);
+      s_rec[q0 + 1] = make_float4(0.0f, 1.0f, 0.0f, __int_as_float(0));
+#pragma unroll
+      for (int q = 2; q < NQ; ++q) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     __syncthreads();
-    if (!done) {
-      for (int j = 0; j < cnt; ++j) {
+    // Branch-free per member: lanes that are done or outside the Gaussian's
+    // support (power > 0) take alpha = 0, which leaves T and the field
+    // exactly unchanged; a wave leaves the batch once all its lanes are done.
+    for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
+      if (__all(done)) break;
+#pragma unroll
+      for (int jj = 0; jj < kUnroll; ++jj) {
+        const int j = j0 + jj;
         const float4 a = s_rec[j * NQ];
         const float4 b = s_rec[j * NQ + 1];
         const float dx = a.x - pxf, dy = a.y - pyf;
-        const float power =
-            -0.5f * fmaf(dx, fmaf(a.z, dx, b.x * dy), dy * fmaf(a.w, dx, b.y * dy));
-        if (power > 0.0f) continue;
-        const float G = fast_exp(power);
-        const float alpha = fminf(kMaxAlpha, b.z * G * b.w);
-        const float Tn = T * (1.0f - alpha);
+        const float pw = fmaf(dx, fmaf(a.z, dx, b.x * dy), dy * fmaf(a.w, dx, b.y * dy));
+        const float G = __builtin_amdgcn_exp2f(pw);
+        const bool ok = !done && !(pw > 0.0f);  // NaN passes, as the reference
+        const float alpha = ok ? fminf(kMaxAlpha, b.z * G) : 0.0f;
         const float sT = alpha * T;
-        float amp[8];
-        {
-          const float4 c0 = s_rec[j * NQ + 2];
-          const float4 c1 = s_rec[j * NQ + (NQ > 3 ? 3 : 2)];
-          amp[0] = c0.x;
-          amp[1] = c0.y;
-          amp[2] = c0.z;
-          amp[3] = c0.w;
-          amp[4] = c1.x;
-          amp[5] = c1.y;
-          amp[6] = c1.z;
-          amp[7] = c1.w;
-        }
+        const float4 c0 = s_rec[j * NQ + 2];
+        const float4 c1 = s_rec[j * NQ + (NQ > 3 ? 3 : 2)];
+        const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
         for (int c = 0; c < C; ++c) {
           acc[2 * c] = fmaf(sT, amp[2 * c], acc[2 * c]);
           acc[2 * c + 1] = fmaf(sT, amp[2 * c + 1], acc[2 * c + 1]);
         }
-        T = Tn;
-        last = s_k[j] + 1;
-        if (Tn < kTermT) {
-          done = true;
-          break;
-        }
+        T = T * (1.0f - alpha);
+        last = ok ? __float_as_int(b.w) : last;
+        done = done || (ok && T < kTermT);
       }
     }
   }
@@ -356,7 +362,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         const float pw = fmaf(dx, u, dy * v);  // = log2(e) * power
         const float Gv = __builtin_amdgcn_exp2f(pw);
         const float alpha = fminf(kMaxAlpha, b.y * Gv);
-        const bool ok = valid && kk < last && pw <= 0.0f && alpha >= kMinAlphaBwd;
+        const bool ok = valid && kk < last && !(pw > 0.0f) && alpha >= kMinAlphaBwd;
         any = any || ok;
         T = ok ? T * __builtin_amdgcn_rcpf(1.0f - alpha) : T;
         const float dcol = ok ? alpha * T : 0.0f;
