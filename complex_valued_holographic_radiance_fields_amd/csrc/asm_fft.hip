@@ -176,49 +176,65 @@ struct Dft<5, INV> : DftOdd<5, INV> {};
 template <bool INV>
 struct Dft<7, INV> : DftOdd<7, INV> {};
 
-// LDS address of element (i, b) of a batch of B transforms of length N.
-// Each 32-element (256 B) chunk is rotated by 4 * (chunk % 8) slots: the
-// strided butterfly stores of the first Stockham stages (stride R*B or R
-// elements) then fall on distinct bank pairs, and contiguous accesses stay
-// conflict-free because the rotation permutes within a chunk.
-__device__ __forceinline__ int swz(int a) { return (a & ~31) | ((a + ((a >> 3) & 28)) & 31); }
-
-template <int N, int B, bool ROWS>
-__device__ __forceinline__ int lidx(int i, int b) {
-  return swz(ROWS ? b * N + i : i * B + b);
+// LDS layout.  A batch of B = 4 transforms of length N is interleaved:
+// element i of transform b is at 4*i + b, so rows and columns share one
+// layout and one thread's butterfly inputs (and outputs) sit at a base
+// address plus a stride.  Four padding slots follow every 32 elements: the
+// first stage's stride-32 stores then land on distinct bank pairs, and for
+// every stride that is a multiple of 32 (all strides of these plans but the
+// first stage's loads at N = 160, 2016) the padded addresses stay a base
+// plus a compile-time offset.
+__device__ __forceinline__ constexpr int pad(int a) { return a + ((a >> 5) << 2); }
+template <int N>
+constexpr int lds_elems() {
+  return pad(kFftBatch * N - 1) + 1;
 }
+// Elements per thread when a block copies its B x N batch.
+template <int N>
+constexpr int kCopyIters = (kFftBatch * N + kFftThreads - 1) / kFftThreads;
 
-template <int N, int B, int R, int NS, bool INV, bool ROWS>
-__device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw_in) {
+template <int N, int R, int NS, bool INV>
+__device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
+  constexpr int B = kFftBatch;
   constexpr int NR = N / R;
   constexpr int NB = B * NR;
   constexpr int BPT = (NB + kFftThreads - 1) / kFftThreads;
-  // The thread index and the twiddle table pointer pass through empty asm
+  constexpr int LS = B * NR;  // load stride between butterfly inputs
+  constexpr int SS = B * NS;  // store stride between butterfly outputs
+  constexpr bool lin_load = LS % 32 == 0;
+  constexpr bool lin_store = SS % 32 == 0 || (NS == 1 && (B * R) % 32 == 0);
+  constexpr int LSP = LS / 32 * 36;
+  constexpr int SSP = SS % 32 == 0 ? SS / 32 * 36 : SS;
+  // The thread index and a zero twiddle offset pass through empty asm
   // statements, so a caller that runs the transform inside a loop (the plane
   // loop of the column passes) cannot hoist this stage's addresses and
-  // twiddle loads out of the loop and hold them in registers for its whole
-  // length.
+  // twiddle loads out of the loop and hold them in registers throughout.
   int tid = static_cast<int>(threadIdx.x);
   asm volatile("" : "+v"(tid));
-  const float2* tw = tw_in;
-  asm volatile("" : "+s"(tw));
+  int twoff = 0;
+  asm volatile("" : "+s"(twoff));
   float2 y[BPT][R];
-  int ob[BPT], bb[BPT];
+  int ob[BPT];
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
     const int q = tid + u * kFftThreads;
     ob[u] = -1;
     if (BPT * kFftThreads == NB || q < NB) {
-      const int j = ROWS ? q % NR : q / B;
-      const int b = ROWS ? q / NR : q % B;
+      const int j = q >> 2;  // butterfly index within its transform
       const int k = j % NS;
       float2 x[R];
+      if (lin_load) {
+        const int base = pad(q);
 #pragma unroll
-      for (int t = 0; t < R; ++t) x[t] = lds[lidx<N, B, ROWS>(j + t * NR, b)];
+        for (int t = 0; t < R; ++t) x[t] = lds[base + t * LSP];
+      } else {
+#pragma unroll
+        for (int t = 0; t < R; ++t) x[t] = lds[pad(q + t * LS)];
+      }
       if (NS > 1) {
 #pragma unroll
         for (int t = 1; t < R; ++t) {
-          float2 w = tw[t * k * (N / (NS * R))];
+          float2 w = tw[twoff + t * k * (N / (NS * R))];
           if (INV) w.y = -w.y;
           x[t] = cmulf(x[t], w);
         }
@@ -226,25 +242,31 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
       Dft<R, INV>::run(x);
 #pragma unroll
       for (int t = 0; t < R; ++t) y[u][t] = x[t];
-      ob[u] = (j / NS) * NS * R + k;
-      bb[u] = b;
+      // Stockham output position (j/NS)*NS*R + k + t*NS, interleaved.
+      const int a0 = q + B * (j / NS) * NS * (R - 1);
+      ob[u] = lin_store ? pad(a0) : a0;
     }
   }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
     if (ob[u] >= 0) {
+      if (lin_store) {
 #pragma unroll
-      for (int t = 0; t < R; ++t) lds[lidx<N, B, ROWS>(ob[u] + t * NS, bb[u])] = y[u][t];
+        for (int t = 0; t < R; ++t) lds[ob[u] + t * SSP] = y[u][t];
+      } else {
+#pragma unroll
+        for (int t = 0; t < R; ++t) lds[pad(ob[u] + t * SS)] = y[u][t];
+      }
     }
   }
   __syncthreads();
 }
 
-template <int N, int B, bool INV, bool ROWS, int NS, int R, int... Rest>
+template <int N, bool INV, int NS, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, B, R, NS, INV, ROWS>(lds, tw);
-  if constexpr (sizeof...(Rest) > 0) run_stages<N, B, INV, ROWS, NS * R, Rest...>(lds, tw);
+  fft_stage<N, R, NS, INV>(lds, tw);
+  if constexpr (sizeof...(Rest) > 0) run_stages<N, INV, NS * R, Rest...>(lds, tw);
 }
 
 template <int N>
@@ -252,9 +274,9 @@ struct Plan;
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct Plan<NN> {                                                                 \
-    template <int B, bool INV, bool ROWS>                                           \
+    template <bool INV>                                                             \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<NN, B, INV, ROWS, 1, __VA_ARGS__>(lds, tw);                        \
+      run_stages<NN, INV, 1, __VA_ARGS__>(lds, tw);                                 \
     }                                                                               \
   };
 HRF_FFT_PLAN(128, 8, 4, 4)
@@ -324,25 +346,35 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
                                                          const float2* __restrict__ tw) {
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
-  __shared__ float2 lds[B * N];
+  __shared__ float2 lds[lds_elems<N>()];
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
-  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
-    const int rr = e / N, i = e - rr * N;
-    const int r = r0 + rr;
-    const int col = i - c_in;
-    float2 v = make_float2(0.0f, 0.0f);
-    if (r < h && col >= 0 && col < w_in)
-      v = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
-    lds[swz(e)] = v;
+  {
+    // All of a thread's loads are issued before the first LDS write.
+    float2 v[kCopyIters<N>];
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int rr = e & 3, i = e >> 2;  // 16 lanes per row: 128-byte runs
+      const int r = r0 + rr;
+      const int col = i - c_in;
+      v[it] = make_float2(0.0f, 0.0f);
+      if (e < B * N && r < h && col >= 0 && col < w_in)
+        v[it] = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
+    }
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      if (e < B * N) lds[pad(e)] = v[it];
+    }
   }
   __syncthreads();
-  Plan<N>::template run<B, false, true>(lds, tw);
+  Plan<N>::template run<false>(lds, tw);
   for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
-    const int cb = e / (B * B), rr = (e / B) % B, b = e % B;
+    const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
     const int r = r0 + rr;
-    if (r < h) dst[tile_off(img, ncb, cb, h, r, b, B)] = lds[swz(rr * N + cb * B + b)];
+    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, B)] = lds[pad(4 * (4 * cb + bc) + rr)];
   }
 }
 
@@ -356,24 +388,34 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restri
                                                           const float2* __restrict__ tw) {
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
-  __shared__ float2 lds[B * N];
+  __shared__ float2 lds[lds_elems<N>()];
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
-  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
-    const int cb = e / (B * B), rr = (e / B) % B, b = e % B;
-    const int r = r0 + rr;
-    float2 v = make_float2(0.0f, 0.0f);
-    if (r < h) v = src[tile_off(img, ncb, cb, h, r, b, B)];
-    lds[swz(rr * N + cb * B + b)] = v;
+  {
+    float2 v[kCopyIters<N>];
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
+      const int r = r0 + rr;
+      v[it] = make_float2(0.0f, 0.0f);
+      if (e < B * N && r < h) v[it] = src[tile_off(img, ncb, cb, h, r, bc, B)];
+    }
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
+      if (e < B * N) lds[pad(4 * (4 * cb + bc) + rr)] = v[it];
+    }
   }
   __syncthreads();
-  Plan<N>::template run<B, true, true>(lds, tw);
+  Plan<N>::template run<true>(lds, tw);
   for (int e = threadIdx.x; e < B * w_out; e += kFftThreads) {
-    const int rr = e / w_out, i = e - rr * w_out;
+    const int rr = e & 3, i = e >> 2;
     const int r = r0 + rr;
     if (r < h) {
-      const float2 v = lds[swz(rr * N + c_out + i)];
+      const float2 v = lds[pad(4 * (c_out + i) + rr)];
       dst[(static_cast<int64_t>(img) * h + r) * w_out + i] = cscale(v, scale);
     }
   }
@@ -402,7 +444,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
   constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
-  __shared__ float2 lds[B * N];
+  __shared__ float2 lds[lds_elems<N>()];
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
@@ -428,14 +470,16 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   for (int p = 0; p < P; ++p) {
     __syncthreads();
     const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
+    // (kz and acc are live here, so the copy is not unrolled: its load
+    // buffer would not fit the register budget.)
     for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
       const int r = e / B - r_pad;
       float2 v = make_float2(0.0f, 0.0f);
       if (r >= 0 && r < H) v = src[e - r_pad * B];
-      lds[swz(e)] = v;
+      lds[pad(e)] = v;
     }
     __syncthreads();
-    Plan<N>::template run<B, false, false>(lds, tw);
+    Plan<N>::template run<false>(lds, tw);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const float d = mc.d[p];
 #pragma unroll
@@ -449,7 +493,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
         if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
           float sn, cs;
           sincosf(d * kz[u], &sn, &cs);
-          const float2 x = lds[swz(q)];
+          const float2 x = lds[pad(q)];
           acc[u].x += x.x * cs - x.y * sn;
           acc[u].y += x.x * sn + x.y * cs;
         }
@@ -460,12 +504,12 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
 #pragma unroll
   for (int u = 0; u < EPT; ++u) {
     const int q = threadIdx.x + u * kFftThreads;
-    if (q < B * N) lds[swz(q)] = acc[u];
+    if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<B, true, false>(lds, tw);
+  Plan<N>::template run<true>(lds, tw);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, B);
-  for (int e = threadIdx.x; e < B * S; e += kFftThreads) dst[e] = lds[swz(e + s_crop * B)];
+  for (int e = threadIdx.x; e < B * S; e += kFftThreads) dst[e] = lds[pad(e + s_crop * B)];
 }
 
 // B': adjoint column pass.  X tiled (C, S, N) row spectra of the padded
@@ -480,20 +524,29 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
   constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
-  __shared__ float2 lds[B * N];
+  __shared__ float2 lds[lds_elems<N>()];
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
 
   const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, B);
-  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
-    const int r = e / B - s_pad;
-    float2 v = make_float2(0.0f, 0.0f);
-    if (r >= 0 && r < S) v = src[e - s_pad * B];
-    lds[swz(e)] = v;
+  {
+    float2 v[kCopyIters<N>];
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int r = e / B - s_pad;
+      v[it] = make_float2(0.0f, 0.0f);
+      if (e < B * N && r >= 0 && r < S) v[it] = src[e - s_pad * B];
+    }
+#pragma unroll
+    for (int it = 0; it < kCopyIters<N>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+      if (e < B * N) lds[pad(e)] = v[it];
+    }
   }
   __syncthreads();
-  Plan<N>::template run<B, false, false>(lds, tw);
+  Plan<N>::template run<false>(lds, tw);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
@@ -508,7 +561,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
       coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &inap);
       const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
       if (inap && prop) kz[u] = kk;
-      gs[u] = lds[swz(q)];
+      gs[u] = lds[pad(q)];
     }
   }
   for (int p = 0; p < P; ++p) {
@@ -531,13 +584,13 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
             r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
           }
         }
-        lds[swz(q)] = r;
+        lds[pad(q)] = r;
       }
     }
     __syncthreads();
-    Plan<N>::template run<B, true, false>(lds, tw);
+    Plan<N>::template run<true>(lds, tw);
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
-    for (int e = threadIdx.x; e < B * H; e += kFftThreads) dst[e] = lds[swz(e + r_crop * B)];
+    for (int e = threadIdx.x; e < B * H; e += kFftThreads) dst[e] = lds[pad(e + r_crop * B)];
   }
 }
 
