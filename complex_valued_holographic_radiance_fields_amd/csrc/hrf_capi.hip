@@ -401,29 +401,50 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
 
   // Pair emission in depth-rank order, then a stable sort on the tile id.
   const int end_bit = bits_for(f.ntiles);
-  const bool odd = (radix_passes(end_bit) % 2) == 1;
-  uint32_t* vals_a = odd ? b.vals_s : reinterpret_cast<uint32_t*>(point_list);
-  uint32_t* vals_b = odd ? reinterpret_cast<uint32_t*>(point_list) : b.vals_s;
-  {
-    HRF_STAGE("emit", s);
-    HRF_TRY(launch_emit_pairs(w.off, w.order, w.rect, n, num_pairs, f.gx, b.keys_a, vals_a, s));
-  }
-  bool in_b = false;
-  {
-    HRF_STAGE("tile_sort", s);
-    HRF_TRY(radix_sort_pairs(b.keys_a, vals_a, b.keys_b, vals_b, num_pairs, end_bit, b.radix,
-                             &in_b, s));
-  }
-  const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
-  // The sorted values must end in point_list whatever the pass count did
-  // (a single pair is never moved by the sort).
-  const uint32_t* sorted_vals = in_b ? vals_b : vals_a;
-  if (sorted_vals != reinterpret_cast<uint32_t*>(point_list))
-    HRF_HIP(hipMemcpyAsync(point_list, sorted_vals, num_pairs * sizeof(uint32_t),
-                           hipMemcpyDeviceToDevice, s));
-  {
-    HRF_STAGE("ranges", s);
-    HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
+  const int vbits = bits_for(static_cast<int>(n < 0x7FFFFFFF ? n : 0x7FFFFFFF));
+  if (end_bit + vbits <= 32) {
+    // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
+    {
+      HRF_STAGE("emit", s);
+      HRF_TRY(launch_emit_packed(w.off, w.order, w.rect, n, f.gx, vbits, b.keys_a, s));
+    }
+    bool in_b = false;
+    {
+      HRF_STAGE("tile_sort", s);
+      HRF_TRY(radix_sort_keys(b.keys_a, b.keys_b, num_pairs, vbits, end_bit, b.radix, &in_b,
+                              s));
+    }
+    {
+      HRF_STAGE("ranges", s);
+      HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
+                                   ranges, f.ntiles, s));
+    }
+  } else {
+    const bool odd = (radix_passes(end_bit) % 2) == 1;
+    uint32_t* vals_a = odd ? b.vals_s : reinterpret_cast<uint32_t*>(point_list);
+    uint32_t* vals_b = odd ? reinterpret_cast<uint32_t*>(point_list) : b.vals_s;
+    {
+      HRF_STAGE("emit", s);
+      HRF_TRY(launch_emit_pairs(w.off, w.order, w.rect, n, num_pairs, f.gx, b.keys_a, vals_a,
+                                s));
+    }
+    bool in_b = false;
+    {
+      HRF_STAGE("tile_sort", s);
+      HRF_TRY(radix_sort_pairs(b.keys_a, vals_a, b.keys_b, vals_b, num_pairs, end_bit, b.radix,
+                               &in_b, s));
+    }
+    const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
+    // The sorted values must end in point_list whatever the pass count did
+    // (a single pair is never moved by the sort).
+    const uint32_t* sorted_vals = in_b ? vals_b : vals_a;
+    if (sorted_vals != reinterpret_cast<uint32_t*>(point_list))
+      HRF_HIP(hipMemcpyAsync(point_list, sorted_vals, num_pairs * sizeof(uint32_t),
+                             hipMemcpyDeviceToDevice, s));
+    {
+      HRF_STAGE("ranges", s);
+      HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
+    }
   }
 
   rp.ranges = ranges;

@@ -186,6 +186,11 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      hipStream_t s, const uint32_t* run_flag = nullptr);
 int launch_check_sorted(const uint32_t* keys, int64_t n, uint32_t* flag, hipStream_t s);
 int radix_passes(int end_bit);
+// Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
+// (the other bits ride along unsorted), in ceil(nbits/8) passes of equal
+// digit width; same scratch and ping-pong convention as radix_sort_pairs.
+int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
+                    uint32_t* scratch, bool* result_in_b, hipStream_t s);
 
 int launch_gather_counts(const uint32_t* order, const uint32_t* tiles,
                          uint32_t* cnt, int64_t n, hipStream_t s);
@@ -195,6 +200,11 @@ int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* r
                       hipStream_t s);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
+// Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
+int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint2* rect, int64_t n,
+                       int gx, int vbits, uint32_t* words, hipStream_t s);
+int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
+                         int32_t* ranges, int ntiles, hipStream_t s);
 int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,
                            int64_t* visible, hipStream_t s);
 int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s);

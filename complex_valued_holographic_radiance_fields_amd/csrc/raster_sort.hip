@@ -109,40 +109,51 @@ int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream
 
 // ----------------------------------------------------------- radix sort --
 
+// Digit histogram of each block's kRadixTile keys: digit = (key >> shift) &
+// mask with at most 2^RB values; hist is digit-major ([digit][block]) so
+// one exclusive scan gives every (digit, block) output offset.
+template <int RB>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
+                                                              uint32_t mask,
                                                               uint32_t* __restrict__ hist,
                                                               int nblocks,
                                                               const uint32_t* __restrict__ run_flag) {
+  constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_hist[kRadixBins];
-  s_hist[threadIdx.x] = 0;
+  __shared__ uint32_t s_hist[kBins];
+  if (threadIdx.x < kBins) s_hist[threadIdx.x] = 0;
   __syncthreads();
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kRadixTile;
 #pragma unroll
   for (int i = 0; i < kRadixItems; ++i) {
     const int64_t idx = base + i * kRadixThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&s_hist[(keys[idx] >> shift) & 0xFF], 1u);
+    if (idx < n) atomicAdd(&s_hist[(keys[idx] >> shift) & mask], 1u);
   }
   __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = s_hist[threadIdx.x];
+  if (threadIdx.x < kBins)
+    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = s_hist[threadIdx.x];
 }
 
 // Stable scatter.  Wave w owns the contiguous sub-range
 // [base + w*512, base + (w+1)*512) processed as 8 iterations of 64 keys;
 // the rank of a key among equal digits before it is found with a ballot
-// match (8 ballots) plus per-wave LDS digit counters, then offset by the
-// counts of the lower waves and the global digit/block offset.
+// match (RB ballots) plus per-wave LDS digit counters, then offset by the
+// counts of the lower waves and the global digit/block offset.  With fewer
+// digit values (RB < 8) a block's keys fall into fewer, longer output runs.
+template <int RB, bool VALS>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
-    const uint32_t* __restrict__ hist_scan, int nblocks, const uint32_t* __restrict__ run_flag) {
+    uint32_t mask, const uint32_t* __restrict__ hist_scan, int nblocks,
+    const uint32_t* __restrict__ run_flag) {
+  constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_cnt[kRadixWaves][kRadixBins];
+  __shared__ uint32_t s_cnt[kRadixWaves][kBins];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int w = 0; w < kRadixWaves; ++w) s_cnt[w][threadIdx.x] = 0;
+  for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
+    s_cnt[e / kBins][e % kBins] = 0;
   __syncthreads();
 
   const int64_t wbase = static_cast<int64_t>(blockIdx.x) * kRadixTile +
@@ -155,12 +166,12 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const int64_t idx = wbase + it * 64 + lane;
     const bool valid = idx < n;
     key[it] = valid ? kin[idx] : 0u;
-    val[it] = valid ? vin[idx] : 0u;
-    const int d = valid ? static_cast<int>((key[it] >> shift) & 0xFF) : 0;
+    if (VALS) val[it] = valid ? vin[idx] : 0u;
+    const int d = valid ? static_cast<int>((key[it] >> shift) & mask) : 0;
     dig[it] = valid ? d : -1;
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < RB; ++b) {
       const bool bit = (d >> b) & 1;
       const uint64_t bb = __ballot(bit);
       peers &= bit ? bb : ~bb;
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
   }
   __syncthreads();
   // Per-digit prefix over waves plus the global offset of (digit, block).
-  {
+  if (threadIdx.x < kBins) {
     const int d = threadIdx.x;
     uint32_t run = hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x];
 #pragma unroll
@@ -189,7 +200,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     if (dig[it] >= 0) {
       const uint32_t pos = s_cnt[wave][dig[it]] + rank[it];
       kout[pos] = key[it];
-      vout[pos] = val[it];
+      if (VALS) vout[pos] = val[it];
     }
   }
 }
@@ -270,6 +281,60 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
   }
 }
 
+// Packed emission: one word (tile << vbits) | gaussian per pair, in the same
+// order as k_emit.
+__global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ off,
+                                                             const uint32_t* __restrict__ order,
+                                                             const uint2* __restrict__ rect,
+                                                             int64_t n, int gx, int vbits,
+                                                             uint32_t* __restrict__ words) {
+  __shared__ uint64_t s_off[kEmitThreads + 1];
+  __shared__ uint32_t s_g[kEmitThreads];
+  __shared__ uint2 s_rect[kEmitThreads];
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
+  const int64_t r = rb + threadIdx.x;
+  const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
+  if (threadIdx.x < nr) {
+    s_off[threadIdx.x] = off[r];
+    const uint32_t g = order[r];
+    s_g[threadIdx.x] = g;
+    s_rect[threadIdx.x] = rect[g];
+  }
+  if (threadIdx.x == 0) s_off[nr] = off[rb + nr];
+  __syncthreads();
+  const uint64_t e0 = s_off[0], e1 = s_off[nr];
+  for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
+    int lo = 0, hi = nr;  // s_off[lo] <= e < s_off[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= e)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const uint2 rc = s_rect[lo];
+    const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
+    const uint32_t w = maxx - minx;
+    const uint32_t i = static_cast<uint32_t>(e - s_off[lo]);
+    const uint32_t ty = miny + i / w, tx = minx + i % w;
+    words[e] = ((ty * static_cast<uint32_t>(gx) + tx) << vbits) | s_g[lo];
+  }
+}
+
+// Sorted packed words -> point_list (the gaussian field) and tile ranges.
+__global__ void k_unpack_ranges(const uint32_t* __restrict__ words, int64_t k, int vbits,
+                                int32_t* __restrict__ point_list, int32_t* __restrict__ ranges) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= k) return;
+  const uint32_t w = words[i];
+  const uint32_t t = w >> vbits;
+  point_list[i] = static_cast<int32_t>(w & ((1u << vbits) - 1u));
+  if (i == 0 || (words[i - 1] >> vbits) != t)
+    ranges[2 * static_cast<int64_t>(t)] = static_cast<int32_t>(i);
+  if (i == k - 1 || (words[i + 1] >> vbits) != t)
+    ranges[2 * static_cast<int64_t>(t) + 1] = static_cast<int32_t>(i + 1);
+}
+
 __global__ void k_tile_ranges(const uint32_t* __restrict__ keys, int64_t k,
                               int32_t* __restrict__ ranges) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -317,38 +382,103 @@ size_t radix_scratch_elems(int64_t n) {
   return 2 * hist + scan_scratch_elems(static_cast<int64_t>(hist)) + 4;
 }
 
+namespace {
+
+template <int RB, bool VALS>
+int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
+               int64_t n, int nb, int shift, uint32_t mask, uint32_t* scratch,
+               const uint32_t* run_flag, hipStream_t s) {
+  const int64_t hist_n = static_cast<int64_t>(nb) << RB;
+  uint32_t* hist = scratch;
+  uint32_t* hist_scan = scratch + hist_n;
+  uint32_t* scan_tmp = scratch + 2 * hist_n;
+  hipLaunchKernelGGL(k_radix_hist<RB>, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
+                     mask, hist, nb, run_flag);
+  HRF_LAUNCH_CHECK();
+  HRF_TRY(scan_exclusive_u32(hist, hist_scan, hist_n, scan_tmp, s));
+  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(nb), dim3(kRadixThreads), 0, s, src_k,
+                     src_v, dst_k, dst_v, n, shift, mask, hist_scan, nb, run_flag);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int block_count(int64_t n, int* nb) {
+  const int64_t nb64 = (n + kRadixTile - 1) / kRadixTile;
+  if (nb64 > 0x7FFFFFFF) {
+    set_error("radix sort: too many keys (%lld)", static_cast<long long>(n));
+    return HRF_ERR_INVALID;
+  }
+  *nb = static_cast<int>(nb64);
+  return HRF_OK;
+}
+
+}  // namespace
+
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
                      int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s,
                      const uint32_t* run_flag) {
   *result_in_b = false;
   if (n <= 1) return HRF_OK;
   const int passes = radix_passes(end_bit);
-  const int64_t nb64 = (n + kRadixTile - 1) / kRadixTile;
-  if (nb64 > 0x7FFFFFFF) {
-    set_error("radix sort: too many keys (%lld)", static_cast<long long>(n));
-    return HRF_ERR_INVALID;
-  }
-  const int nb = static_cast<int>(nb64);
-  const int64_t hist_n = static_cast<int64_t>(nb) * kRadixBins;
-  uint32_t* hist = scratch;
-  uint32_t* hist_scan = scratch + hist_n;
-  uint32_t* scan_tmp = scratch + 2 * hist_n;
+  int nb = 0;
+  HRF_TRY(block_count(n, &nb));
   uint32_t *src_k = ka, *src_v = va, *dst_k = kb, *dst_v = vb;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = pass * 8;
-    hipLaunchKernelGGL(k_radix_hist, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
-                       hist, nb, run_flag);
-    HRF_LAUNCH_CHECK();
-    HRF_TRY(scan_exclusive_u32(hist, hist_scan, hist_n, scan_tmp, s));
-    hipLaunchKernelGGL(k_radix_scatter, dim3(nb), dim3(kRadixThreads), 0, s, src_k, src_v,
-                       dst_k, dst_v, n, shift, hist_scan, nb, run_flag);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY((radix_pass<8, true>(src_k, src_v, dst_k, dst_v, n, nb, pass * 8, 0xFFu, scratch,
+                                 run_flag, s)));
     uint32_t* tk = src_k;
     uint32_t* tv = src_v;
     src_k = dst_k;
     src_v = dst_v;
     dst_k = tk;
     dst_v = tv;
+  }
+  *result_in_b = (passes % 2) == 1;
+  return HRF_OK;
+}
+
+int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
+                    uint32_t* scratch, bool* result_in_b, hipStream_t s) {
+  *result_in_b = false;
+  if (n <= 1 || nbits <= 0) return HRF_OK;
+  const int passes = (nbits + 7) / 8;
+  const int rb = (nbits + passes - 1) / passes;  // digit bits, <= 8
+  int nb = 0;
+  HRF_TRY(block_count(n, &nb));
+  uint32_t *src = ka, *dst = kb;
+  int done = 0;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int bits = nbits - done < rb ? nbits - done : rb;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int shift = lo_bit + done;
+    int rc;
+    switch (rb) {
+      case 1: case 2: case 3: case 4:
+        rc = radix_pass<4, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s);
+        break;
+      case 5:
+        rc = radix_pass<5, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s);
+        break;
+      case 6:
+        rc = radix_pass<6, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s);
+        break;
+      case 7:
+        rc = radix_pass<7, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s);
+        break;
+      default:
+        rc = radix_pass<8, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s);
+        break;
+    }
+    HRF_TRY(rc);
+    done += bits;
+    uint32_t* t = src;
+    src = dst;
+    dst = t;
   }
   *result_in_b = (passes % 2) == 1;
   return HRF_OK;
@@ -399,6 +529,25 @@ int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* r
   if (k <= 0 || n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, off,
                      order, rect, n, gx, keys, vals);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint2* rect, int64_t n,
+                       int gx, int vbits, uint32_t* words, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
+                     off, order, rect, n, gx, vbits, words);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
+                         int32_t* ranges, int ntiles, hipStream_t s) {
+  HRF_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2 * int64_t(ntiles), s));
+  if (k <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_unpack_ranges, dim3(blocks_for(k, 256)), dim3(256), 0, s, words, k,
+                     vbits, point_list, ranges);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

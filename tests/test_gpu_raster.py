@@ -204,3 +204,21 @@ def test_bad_channels_raise(hrf):
                            torch.ones((n, 4), device=d), torch.ones((n, 4), device=d),
                            torch.ones(n, device=d), torch.ones((n, 1), device=d), 10.0, 10.0,
                            8.0, 8.0, torch.eye(3, device=d), (16, 16), (16, 16), 1.0, 1000.0)
+
+
+def test_forward_parity_wide_keys(hrf, oracle_mod):
+    """Tile id and gaussian index need more than 32 bits together (16384
+    tiles, 270k Gaussians): the binning takes the separate key/value sort
+    path instead of the packed one."""
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    spec = scenes.SceneSpec("wide", 6, 270_000, 2048, 2048, 1, [515e-9], [-2e-3], "uniform",
+                            log_scale_mean=-6.0, log_scale_std=0.3)
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    print(f"wide keys: N={g.n} K={ref['K']}", flush=True)
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
