@@ -177,29 +177,44 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   }
 }
 
-// Conservative screen-space box of the region where a Gaussian can reach
-// alpha >= 1/255 in the backward (power = -q/2 with q = d^T A d, A the conic):
-// alpha = min(.99, o*G*w) >= 1/255 needs q <= 2 ln(255 o w).  The box is
-// widened by 0.1% + 0.01 in q and again in extent, far beyond the rounding of
-// the exp/power evaluation, so culling with it never drops a contribution.
-// Returns false when no pixel can qualify (o*w below 1/255).  A non-positive
-// definite conic or NaN yields an infinite box (never culled).
-__device__ __forceinline__ bool alpha_box(float cxx, float cxy, float czz, float ow,
-                                          float* ex, float* ey) {
-  if (ow * 255.0f < 0.999f) return false;
-  const float q = 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
-  const float det = cxx * czz - cxy * cxy;
-  if (!(det > 0.0f) || !(cxx > 0.0f) || !(czz > 0.0f)) {
-    *ex = *ey = INFINITY;
-    return true;
-  }
-  *ex = sqrtf(q * czz / det) * 1.0001f + 1e-3f;
-  *ey = sqrtf(q * cxx / det) * 1.0001f + 1e-3f;
-  return true;
+// Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
+// only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
+// d = mean - pixel).  alpha_threshold returns that bound widened by 0.1% +
+// 0.01, far beyond the rounding of the exp/power evaluation, or -1 when no
+// pixel can qualify (o*w below 1/255).
+__device__ __forceinline__ float alpha_threshold(float ow) {
+  if (ow * 255.0f < 0.999f) return -1.0f;
+  return 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
+}
+
+// min of q over x1 = mx - px in [xlo, xhi] at a fixed x2 = my - py (or the
+// same with the roles swapped): the 1-D minimiser of the convex quadratic,
+// clamped to the interval.
+__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float x2, float lo,
+                                          float hi) {
+  const float x1 = fminf(fmaxf(-a12 * x2 / a11, lo), hi);
+  return x1 * (a11 * x1 + 2.0f * a12 * x2) + a22 * x2 * x2;
+}
+
+// Exact test: does q(d) <= thr hold anywhere in the box of pixel centres
+// [x0, x0+7] x [y0, y0+7]?  q is convex, so if the mean is outside the box
+// the minimum over the box lies on one of its four edges.  A conic that is
+// not positive definite (or NaN) is never culled.
+__device__ __forceinline__ bool box_reaches(float mx, float my, float cxx, float cxy, float czz,
+                                            float thr, float x0, float y0) {
+  const float x1 = x0 + 7.0f, y1 = y0 + 7.0f;
+  if (!(cxx > 0.0f) || !(czz > 0.0f) || !(cxx * czz - cxy * cxy > 0.0f)) return true;
+  if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
+  const float dxl = mx - x1, dxh = mx - x0, dyl = my - y1, dyh = my - y0;
+  float m = edge_min(cxx, cxy, czz, dyl, dxl, dxh);
+  m = fminf(m, edge_min(cxx, cxy, czz, dyh, dxl, dxh));
+  m = fminf(m, edge_min(czz, cxy, cxx, dxl, dyl, dyh));
+  m = fminf(m, edge_min(czz, cxy, cxx, dxh, dyl, dyh));
+  return m <= thr;
 }
 
 // Backward.  Waves own 8x8 quadrants of the tile.  Per batch, every staged
-// Gaussian gets a 4-bit quadrant mask (its alpha >= 1/255 box intersects the
+// Gaussian gets a 4-bit quadrant mask (its alpha >= 1/255 region meets the
 // quadrant and its list position is below that quadrant's max n_contrib);
 // each wave walks only its own compacted list, back to front, in groups of
 // G members whose 6+2C partial sums per lane are reduced together with one
@@ -285,13 +300,13 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
         for (int q = 0; q < NQ; ++q) rq[q] = src[q];
         wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
-        float ex, ey;
-        if (alpha_box(rq[0].z, rq[0].w, rq[1].y, rq[1].z * wpl, &ex, &ey)) {
+        const float thr = alpha_threshold(rq[1].z * wpl);
+        if (thr >= 0.0f) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float x0 = tx0 + (w & 1) * 8, y0 = ty0 + (w >> 1) * 8;
-            const bool hit = k < wmax[w] && !(rq[0].x + ex < x0 || rq[0].x - ex > x0 + 7.0f ||
-                                              rq[0].y + ey < y0 || rq[0].y - ey > y0 + 7.0f);
+            const bool hit = k < wmax[w] && box_reaches(rq[0].x, rq[0].y, rq[0].z, rq[0].w,
+                                                        rq[1].y, thr, x0, y0);
             qm |= hit ? (1u << w) : 0u;
           }
         }
