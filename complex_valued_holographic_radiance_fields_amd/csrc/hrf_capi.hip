@@ -307,8 +307,10 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   pp.tiles = w.tiles;
   pp.dkey = w.dkey;
   pp.vis = w.vis;
+  pp.sort_flag = w.sort_flag;
   {
     HRF_STAGE("project", s);
+    HRF_TRY(launch_fill_u32(w.sort_flag, 0u, 1, s));
     HRF_TRY(launch_project(pp, s));
   }
 
@@ -316,15 +318,14 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // sorted order ends in the first buffer pair).
   {
     // The reference's caller hands Gaussians over already sorted by depth
-    // (Scene.render, model.py:1387); the device checks that and the four
-    // passes then skip themselves (a stable sort of sorted keys is the
-    // identity).
+    // (Scene.render, model.py:1387); k_project flags any key below its
+    // predecessor's, and without that flag every pass (histograms, scans,
+    // scatters) skips itself on the device and the order stays the
+    // identity (a stable sort of sorted keys).
     HRF_STAGE("depth_sort", s);
-    HRF_TRY(launch_iota(w.order, n, s));
-    HRF_TRY(launch_check_sorted(w.dkey, n, w.sort_flag, s));
     bool in_b = false;
     HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s,
-                             w.sort_flag));
+                             w.sort_flag, true));
     if (in_b) {
       set_error("internal: depth sort expected an even pass count");
       return HRF_ERR_INVALID;
@@ -332,7 +333,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   }
   {
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_gather_counts(w.order, w.tiles, w.cnt, n, s));
+    HRF_TRY(launch_gather_counts(w.order, w.sort_flag, w.tiles, w.cnt, n, s));
     HRF_TRY(scan_exclusive_u64(w.cnt, w.off, n, w.scan64, s));
     HRF_TRY(scan_exclusive_u32(w.vis, w.vis_off, n, w.scan32, s));
     hipLaunchKernelGGL(k_totals, dim3(1), dim3(64), 0, s, w.off, w.cnt, w.vis_off, w.vis, n,
@@ -406,7 +407,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
       HRF_STAGE("emit", s);
-      HRF_TRY(launch_emit_packed(w.off, w.order, w.rect, n, f.gx, vbits, b.keys_a, s));
+      HRF_TRY(launch_emit_packed(w.off, w.order, w.sort_flag, w.rect, n, f.gx, vbits, b.keys_a,
+                                 s));
     }
     bool in_b = false;
     {
@@ -425,8 +427,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     uint32_t* vals_b = odd ? reinterpret_cast<uint32_t*>(point_list) : b.vals_s;
     {
       HRF_STAGE("emit", s);
-      HRF_TRY(launch_emit_pairs(w.off, w.order, w.rect, n, num_pairs, f.gx, b.keys_a, vals_a,
-                                s));
+      HRF_TRY(launch_emit_pairs(w.off, w.order, w.sort_flag, w.rect, n, num_pairs, f.gx,
+                                b.keys_a, vals_a, s));
     }
     bool in_b = false;
     {

@@ -138,6 +138,7 @@ struct ProjectParams {
   uint32_t* tiles;  // n
   uint32_t* dkey;   // n: depth sort key
   uint32_t* vis;    // n: 0/1
+  uint32_t* sort_flag;  // set to 1 when some depth key is below its predecessor's
 };
 int launch_project(const ProjectParams& p, hipStream_t s);
 
@@ -181,10 +182,12 @@ int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n,
 // passes do nothing on the device while *run_flag == 0 (callers use an even
 // pass count then, so the data stays in (ka,va) either way).
 size_t radix_scratch_elems(int64_t n);
+// With index_values, the values are taken to be 0..n-1 (va is only used as
+// a buffer).
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
-                     hipStream_t s, const uint32_t* run_flag = nullptr);
-int launch_check_sorted(const uint32_t* keys, int64_t n, uint32_t* flag, hipStream_t s);
+                     hipStream_t s, const uint32_t* run_flag = nullptr,
+                     bool index_values = false);
 int radix_passes(int end_bit);
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
 // (the other bits ride along unsorted), in ceil(nbits/8) passes of equal
@@ -192,17 +195,19 @@ int radix_passes(int end_bit);
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s);
 
-int launch_gather_counts(const uint32_t* order, const uint32_t* tiles,
-                         uint32_t* cnt, int64_t n, hipStream_t s);
-int launch_iota(uint32_t* v, int64_t n, hipStream_t s);
-int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* rect,
-                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s);
+// The depth-order permutation is order[] when *sorted_flag != 0 and the
+// identity otherwise.
+int launch_gather_counts(const uint32_t* order, const uint32_t* sorted_flag,
+                         const uint32_t* tiles, uint32_t* cnt, int64_t n, hipStream_t s);
+int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
+                      const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
+                      uint32_t* vals, hipStream_t s);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
-int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint2* rect, int64_t n,
-                       int gx, int vbits, uint32_t* words, hipStream_t s);
+int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
+                       const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
+                       hipStream_t s);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
 int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,

@@ -16,6 +16,11 @@ namespace {
 using namespace geom;
 
 
+__device__ __forceinline__ uint32_t depth_key(float z) {
+  const uint32_t bits = __float_as_uint(z);
+  return (bits & 0x80000000u) ? (bits & 0x7FFFFFFFu) : (bits | 0x80000000u);
+}
+
 __global__ __launch_bounds__(256) void k_project(ProjectParams p) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (g >= p.n) return;
@@ -94,8 +99,11 @@ __global__ __launch_bounds__(256) void k_project(ProjectParams p) {
   p.rect[g] = rect;
 
   // Depth key (rasterizer_splat.cu:150-158): ascending key == front to back.
-  uint32_t bits = __float_as_uint(z);
-  p.dkey[g] = (bits & 0x80000000u) ? (bits & 0x7FFFFFFFu) : (bits | 0x80000000u);
+  const uint32_t dk = depth_key(z);
+  p.dkey[g] = dk;
+  // Keys already non-decreasing (the reference's caller sorts by depth)
+  // make the stable depth sort the identity; it then skips itself.
+  if (p.sort_flag && g > 0 && depth_key(p.z[g - 1]) > dk) *p.sort_flag = 1u;
   // Visibility: defined as 0.2 < z_cam and near < z_cam < far (the
   // reference's checkFrustum reads its 3x3 matrix out of bounds).
   p.vis[g] = (tz > 0.2f && tz > p.near_plane && tz < p.far_plane) ? 1u : 0u;

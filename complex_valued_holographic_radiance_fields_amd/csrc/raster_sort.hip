@@ -54,7 +54,9 @@ template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kScanThreads) void k_scan_local(const Tin* __restrict__ in,
                                                              Tout* __restrict__ out,
                                                              Tout* __restrict__ sums,
-                                                             int64_t n) {
+                                                             int64_t n,
+                                                             const uint32_t* __restrict__ run_flag) {
+  if (run_flag && *run_flag == 0u) return;
   __shared__ Tout s_wave[kScanThreads / 64];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
                        static_cast<int64_t>(threadIdx.x) * kScanItems;
@@ -80,7 +82,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_local(const Tin* __restri
 template <typename T>
 __global__ __launch_bounds__(kScanThreads) void k_scan_add(T* __restrict__ out,
                                                            const T* __restrict__ sums,
-                                                           int64_t n) {
+                                                           int64_t n,
+                                                           const uint32_t* __restrict__ run_flag) {
+  if (run_flag && *run_flag == 0u) return;
   const T add = sums[blockIdx.x];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
   for (int i = threadIdx.x; i < kScanTile; i += kScanThreads) {
@@ -89,19 +93,21 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_add(T* __restrict__ out,
   }
 }
 
-// Recursive exclusive scan.  Scratch holds the block-sum pyramid.
+// Recursive exclusive scan.  Scratch holds the block-sum pyramid.  With
+// run_flag, every level does nothing on the device while *run_flag == 0.
 template <typename Tin, typename Tout>
-int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream_t s) {
+int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream_t s,
+                   const uint32_t* run_flag = nullptr) {
   if (n <= 0) return HRF_OK;
   const int64_t nb = (n + kScanTile - 1) / kScanTile;
   Tout* sums = scratch;
   hipLaunchKernelGGL((k_scan_local<Tin, Tout>), dim3(static_cast<unsigned>(nb)),
-                     dim3(kScanThreads), 0, s, in, out, sums, n);
+                     dim3(kScanThreads), 0, s, in, out, sums, n, run_flag);
   HRF_LAUNCH_CHECK();
   if (nb > 1) {
-    HRF_TRY((scan_exclusive<Tout, Tout>(sums, sums, nb, scratch + nb, s)));
+    HRF_TRY((scan_exclusive<Tout, Tout>(sums, sums, nb, scratch + nb, s, run_flag)));
     hipLaunchKernelGGL((k_scan_add<Tout>), dim3(static_cast<unsigned>(nb)),
-                       dim3(kScanThreads), 0, s, out, sums, n);
+                       dim3(kScanThreads), 0, s, out, sums, n, run_flag);
     HRF_LAUNCH_CHECK();
   }
   return HRF_OK;
@@ -166,7 +172,9 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const int64_t idx = wbase + it * 64 + lane;
     const bool valid = idx < n;
     key[it] = valid ? kin[idx] : 0u;
-    if (VALS) val[it] = valid ? vin[idx] : 0u;
+    // vin == nullptr: the values are the element indices (first pass of a
+    // sort whose payload is the identity permutation).
+    if (VALS) val[it] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
     const int d = valid ? static_cast<int>((key[it] >> shift) & mask) : 0;
     dig[it] = valid ? d : -1;
     uint64_t peers = __ballot(valid);
@@ -205,11 +213,6 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
   }
 }
 
-__global__ void k_iota(uint32_t* v, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) v[i] = static_cast<uint32_t>(i);
-}
-
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -220,19 +223,19 @@ __global__ void k_fill_f32(float* p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
-// flag = 1 when keys are not already non-decreasing (then the stable sort
-// must run; otherwise it is the identity and is skipped on the device).
-__global__ void k_check_sorted(const uint32_t* __restrict__ keys, int64_t n,
-                               uint32_t* __restrict__ flag) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i + 1 < n && keys[i] > keys[i + 1]) *flag = 1u;
+// Depth-order permutation: order[i] when the depth sort ran (*sorted_flag
+// != 0), the identity otherwise (the keys were already in order).
+__device__ __forceinline__ uint32_t ordered(const uint32_t* order, const uint32_t* sorted_flag,
+                                           int64_t i) {
+  return *sorted_flag ? order[i] : static_cast<uint32_t>(i);
 }
 
 __global__ void k_gather_counts(const uint32_t* __restrict__ order,
+                                const uint32_t* __restrict__ sorted_flag,
                                 const uint32_t* __restrict__ tiles,
                                 uint32_t* __restrict__ cnt, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) cnt[i] = tiles[order[i]];
+  if (i < n) cnt[i] = tiles[ordered(order, sorted_flag, i)];
 }
 
 // Pair emission.  A block owns 256 consecutive ranks; it stages their
@@ -244,6 +247,7 @@ __global__ void k_gather_counts(const uint32_t* __restrict__ order,
 constexpr int kEmitThreads = 256;
 __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ off,
                                                       const uint32_t* __restrict__ order,
+                                                      const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
                                                       int gx, uint32_t* __restrict__ keys,
                                                       uint32_t* __restrict__ vals) {
@@ -255,7 +259,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
   const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
   if (threadIdx.x < nr) {
     s_off[threadIdx.x] = off[r];
-    const uint32_t g = order[r];
+    const uint32_t g = ordered(order, sorted_flag, r);
     s_g[threadIdx.x] = g;
     s_rect[threadIdx.x] = rect[g];
   }
@@ -285,6 +289,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
 // order as k_emit.
 __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ off,
                                                              const uint32_t* __restrict__ order,
+                                                             const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
                                                              int64_t n, int gx, int vbits,
                                                              uint32_t* __restrict__ words) {
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
   const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
   if (threadIdx.x < nr) {
     s_off[threadIdx.x] = off[r];
-    const uint32_t g = order[r];
+    const uint32_t g = ordered(order, sorted_flag, r);
     s_g[threadIdx.x] = g;
     s_rect[threadIdx.x] = rect[g];
   }
@@ -395,7 +400,7 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
   hipLaunchKernelGGL(k_radix_hist<RB>, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
                      mask, hist, nb, run_flag);
   HRF_LAUNCH_CHECK();
-  HRF_TRY(scan_exclusive_u32(hist, hist_scan, hist_n, scan_tmp, s));
+  HRF_TRY((scan_exclusive<uint32_t, uint32_t>(hist, hist_scan, hist_n, scan_tmp, s, run_flag)));
   hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(nb), dim3(kRadixThreads), 0, s, src_k,
                      src_v, dst_k, dst_v, n, shift, mask, hist_scan, nb, run_flag);
   HRF_LAUNCH_CHECK();
@@ -416,7 +421,7 @@ int block_count(int64_t n, int* nb) {
 
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
                      int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s,
-                     const uint32_t* run_flag) {
+                     const uint32_t* run_flag, bool index_values) {
   *result_in_b = false;
   if (n <= 1) return HRF_OK;
   const int passes = radix_passes(end_bit);
@@ -424,7 +429,8 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
   HRF_TRY(block_count(n, &nb));
   uint32_t *src_k = ka, *src_v = va, *dst_k = kb, *dst_v = vb;
   for (int pass = 0; pass < passes; ++pass) {
-    HRF_TRY((radix_pass<8, true>(src_k, src_v, dst_k, dst_v, n, nb, pass * 8, 0xFFu, scratch,
+    const uint32_t* vin = (pass == 0 && index_values) ? nullptr : src_v;
+    HRF_TRY((radix_pass<8, true>(src_k, vin, dst_k, dst_v, n, nb, pass * 8, 0xFFu, scratch,
                                  run_flag, s)));
     uint32_t* tk = src_k;
     uint32_t* tv = src_v;
@@ -484,22 +490,6 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
   return HRF_OK;
 }
 
-int launch_iota(uint32_t* v, int64_t n, hipStream_t s) {
-  if (n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_iota, dim3(blocks_for(n, 256)), dim3(256), 0, s, v, n);
-  HRF_LAUNCH_CHECK();
-  return HRF_OK;
-}
-
-int launch_check_sorted(const uint32_t* keys, int64_t n, uint32_t* flag, hipStream_t s) {
-  HRF_TRY(launch_fill_u32(flag, 0u, 1, s));
-  if (n <= 1) return HRF_OK;
-  hipLaunchKernelGGL(k_check_sorted, dim3(blocks_for(n - 1, 256)), dim3(256), 0, s, keys, n,
-                     flag);
-  HRF_LAUNCH_CHECK();
-  return HRF_OK;
-}
-
 int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_fill_u32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
@@ -514,30 +504,31 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
   return HRF_OK;
 }
 
-int launch_gather_counts(const uint32_t* order, const uint32_t* tiles, uint32_t* cnt,
-                         int64_t n, hipStream_t s) {
+int launch_gather_counts(const uint32_t* order, const uint32_t* sorted_flag,
+                         const uint32_t* tiles, uint32_t* cnt, int64_t n, hipStream_t s) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_gather_counts, dim3(blocks_for(n, 256)), dim3(256), 0, s, order,
-                     tiles, cnt, n);
+                     sorted_flag, tiles, cnt, n);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
-int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint2* rect,
-                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s) {
+int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
+                      const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
+                      uint32_t* vals, hipStream_t s) {
   if (k <= 0 || n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, off,
-                     order, rect, n, gx, keys, vals);
+                     order, sorted_flag, rect, n, gx, keys, vals);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
-int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint2* rect, int64_t n,
-                       int gx, int vbits, uint32_t* words, hipStream_t s) {
+int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
+                       const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
+                       hipStream_t s) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     off, order, rect, n, gx, vbits, words);
+                     off, order, sorted_flag, rect, n, gx, vbits, words);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
