@@ -89,6 +89,7 @@ SIGNATURES = {
         _vp]),
     "hrf_release_caches": (None, []),
     "hrf_trace_enable": (ctypes.c_int, [ctypes.c_int]),
+    "hrf_trace_only": (ctypes.c_int, [ctypes.c_char_p]),
     "hrf_trace_reset": (None, []),
     "hrf_trace_read": (ctypes.c_int, [ctypes.c_char_p, _P(_i64), _P(_f64)]),
 }
@@ -130,6 +131,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def trace_enable(on: bool) -> None:
     check(load().hrf_trace_enable(1 if on else 0))
+
+
+def trace_only(stage: str | None) -> None:
+    """Trace only `stage` (None: every stage)."""
+    check(load().hrf_trace_only(stage.encode() if stage else None))
 
 
 def trace_reset() -> None:

@@ -1,6 +1,8 @@
 // hrf_trace.hip — optional per-stage timing with hipEvents recorded on the
 // stream each stage is launched on.  Off by default; when off, a stage scope
-// costs one relaxed atomic load.
+// costs one relaxed atomic load.  Each traced stage adds two event records
+// to the stream (a few microseconds of queue time each), so a throughput
+// measurement traces one stage at most (hrf_trace_only).
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -21,6 +23,11 @@ struct Record {
 
 std::atomic<int> g_on{0};
 std::mutex g_mu;
+// When non-empty, only this stage is traced (guarded by g_mu).
+std::string& only() {
+  static std::string s;
+  return s;
+}
 std::vector<Record>& records() {
   static std::vector<Record> r;
   return r;
@@ -46,6 +53,7 @@ hipEvent_t take_event() {
 StageTimer::StageTimer(const char* stage, hipStream_t s) : stage_(stage), s_(s) {
   if (!g_on.load(std::memory_order_relaxed)) return;
   std::lock_guard<std::mutex> lock(g_mu);
+  if (!only().empty() && only() != stage) return;
   start_ = take_event();
   stop_ = take_event();
   if (start_ && stop_ && hipEventRecord(start_, s_) == hipSuccess) {
@@ -70,6 +78,12 @@ extern "C" {
 
 int hrf_trace_enable(int on) {
   hrf::g_on.store(on ? 1 : 0);
+  return HRF_OK;
+}
+
+int hrf_trace_only(const char* stage) {
+  std::lock_guard<std::mutex> lock(hrf::g_mu);
+  hrf::only() = stage ? stage : "";
   return HRF_OK;
 }
 

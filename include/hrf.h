@@ -255,6 +255,10 @@ void hrf_release_caches(void);
  * stage of the calls above is bracketed by a pair of hipEvents recorded on
  * the caller's stream. */
 int hrf_trace_enable(int on);
+/* Restricts tracing to one stage (NULL or "" traces every stage).  Each
+ * traced stage adds two event records to the caller's stream, which costs
+ * queue time: trace a single stage while measuring throughput. */
+int hrf_trace_only(const char* stage);
 /* Clears all recorded stage events. */
 void hrf_trace_reset(void);
 /* Waits for the recorded events of `stage` and returns the number of
