@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 import torch  # noqa: F401  (loads the HIP runtime before libhrf.so)
 
@@ -53,7 +54,7 @@ SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hrf_raster_backward_workspace_size": (_sz, [_i64, _i32, _i32]),
     "hrf_raster_backward": (ctypes.c_int, [
-        _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz,
+        _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp, _sz,
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hrf_cov3d_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "hrf_cov3d_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
@@ -148,3 +149,29 @@ def trace_read(stage: str):
     ms = _f64(0.0)
     check(load().hrf_trace_read(stage.encode(), ctypes.byref(n), ctypes.byref(ms)))
     return int(n.value), float(ms.value)
+
+
+# Grow-only scratch buffers, one per (purpose, device, stream, host thread).
+# A workspace is only touched by the kernels of the call that receives it, all
+# enqueued on that call's stream, so handing the same memory to the next call
+# from the same thread on the same stream is ordered by the stream itself
+# (another thread could enqueue between a call's two phases, hence the thread
+# in the key).
+_WORKSPACES: dict = {}
+
+
+def workspace(purpose: str, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """A uint8 device buffer of at least `nbytes` bytes for `purpose` on
+    (`device`, `stream`) for the calling host thread."""
+    key = (purpose, str(device), int(stream), threading.get_ident())
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def release_workspaces() -> None:
+    """Drops the cached workspaces (the memory returns to torch's allocator)."""
+    _WORKSPACES.clear()
+

@@ -467,7 +467,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const void* grad_field,
                         const float* final_T, const int32_t* n_contrib,
                         const int32_t* point_list, const int32_t* ranges, int64_t num_pairs,
-                        void* ws, size_t ws_bytes, float* grad_cam, float* grad_z,
+                        void* ws, size_t ws_bytes, const void* fwd_geom_ws,
+                        size_t fwd_geom_ws_bytes, float* grad_cam, float* grad_z,
                         float* grad_quats, float* grad_scales, float* grad_colours,
                         float* grad_phase, float* grad_opacities, float* grad_plane_probs,
                         void* stream) {
@@ -494,16 +495,31 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
   Carver cv(ws);
   BwdWs w = carve_bwd(cv, n, g->channels, g->planes);
 
-  ProjectParams pp = project_params(g, cam, f);
-  pp.rec = w.rec;
-  pp.pmask = w.pmask;
-  pp.rect = w.rect;
-  pp.tiles = w.tiles;
-  pp.dkey = w.dkey;
-  pp.vis = w.vis;
+  // Render records: those the forward saved in its geometry workspace (the
+  // same inputs give the same records), else recomputed here.
+  const float* rec = w.rec;
+  const uint32_t* pmask = w.pmask;
+  if (fwd_geom_ws) {
+    HRF_TRY(check_ws(const_cast<void*>(fwd_geom_ws), fwd_geom_ws_bytes,
+                     hrf_raster_geom_workspace_size(n, g->channels, g->planes),
+                     "forward geometry"));
+    Carver cg(const_cast<void*>(fwd_geom_ws));
+    const GeomWs fw = carve_geom(cg, n, g->channels);
+    rec = fw.rec;
+    pmask = fw.pmask;
+  }
   {
     HRF_STAGE("project", s);
-    HRF_TRY(launch_project(pp, s));
+    if (!fwd_geom_ws) {
+      ProjectParams pp = project_params(g, cam, f);
+      pp.rec = w.rec;
+      pp.pmask = w.pmask;
+      pp.rect = w.rect;
+      pp.tiles = w.tiles;
+      pp.dkey = w.dkey;
+      pp.vis = w.vis;
+      HRF_TRY(launch_project(pp, s));
+    }
     HRF_TRY(launch_fill_f32(w.acc, 0.0f, n * acc_stride(g->channels, g->planes), s));
   }
 
@@ -511,8 +527,8 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     RenderParams rp{};
     rp.ranges = ranges;
     rp.plist = point_list;
-    rp.pmask = w.pmask;
-    rp.rec = w.rec;
+    rp.pmask = pmask;
+    rp.rec = rec;
     rp.pprobs = g->plane_probs;
     rp.n = n;
     rp.num_pairs = num_pairs;

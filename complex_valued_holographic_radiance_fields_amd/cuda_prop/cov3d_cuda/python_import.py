@@ -61,9 +61,11 @@ class SplatTileCuda(Function):
         ctx.tile_size = tile_size
         ctx.near_plane = near_plane
         ctx.far_plane = far_plane
-        output, forward_info = get_rasterizer().forward(
+        # The forward's render records travel with the context, so the
+        # backward does not recompute the projection.
+        output, forward_info, ctx.geometry = _rast.forward(
             cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs, fx, fy,
-            px, py, view_matrix, img_size, tile_size, near_plane, far_plane)
+            px, py, view_matrix, img_size, tile_size, near_plane, far_plane, keep_geometry=True)
         ctx.forward_info = forward_info
         visible_indices = forward_info[-1]
         ctx.mark_non_differentiable(visible_indices)
@@ -74,11 +76,12 @@ class SplatTileCuda(Function):
         (cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
          view_matrix) = ctx.saved_tensors
         final_Ts, n_contrib, point_list, ranges, _visible = ctx.forward_info
-        grads = get_rasterizer().backward(
+        grads = _rast.backward(
             grad_output.contiguous(), cam_means_3D, z_vals, quats, scales, colours, phase,
             opacities, plane_probs, ctx.fx, ctx.fy, ctx.px, ctx.py, view_matrix, ctx.img_size,
             ctx.tile_size, final_Ts, n_contrib, point_list, ranges, ctx.near_plane,
-            ctx.far_plane)
+            ctx.far_plane, geometry=ctx.geometry)
+        ctx.geometry = None
         return (*grads, None, None, None, None, None, None, None, None, None)
 
 

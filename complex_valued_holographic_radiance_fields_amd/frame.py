@@ -26,15 +26,17 @@ class Frame:
         self.prop_dist = [-d for d in spec.distances]
         self.fwd_state = None
         self.fields = None
+        self.geometry = None
 
     def forward(self):
         t = self.t
-        field, info = rasterizer.forward(
+        field, info, geom = rasterizer.forward(
             t["cam_means"], t["z"], t["quats"], t["scales"], t["colours"], t["phase"],
             t["opac"], t["pprobs"], self.fx, self.fy, self.px, self.py, t["view"], self.img,
-            (16, 16), NEAR, FAR)
+            (16, 16), NEAR, FAR, keep_geometry=True)
         self.fields = field
         self.fwd_state = info
+        self.geometry = geom
         holo = propagation.multiplane(field, self.spec.wavelengths, PITCH, self.prop_dist,
                                       (self.S, self.S), float(self.S))
         return holo
@@ -48,7 +50,8 @@ class Frame:
         return rasterizer.backward(gf, t["cam_means"], t["z"], t["quats"], t["scales"],
                                    t["colours"], t["phase"], t["opac"], t["pprobs"], self.fx,
                                    self.fy, self.px, self.py, t["view"], self.img, (16, 16),
-                                   final_T, n_contrib, point_list, ranges, NEAR, FAR)
+                                   final_T, n_contrib, point_list, ranges, NEAR, FAR,
+                                   geometry=self.geometry)
 
     @property
     def num_pairs(self) -> int:

@@ -43,7 +43,7 @@ def _c64(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def _workspace(P: int, C: int, S: int, dev) -> tuple[torch.Tensor, int]:
     nbytes = _lib.load().hrf_asm_workspace_size(P, C, S)
-    return torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
+    return _lib.workspace("asm", dev, _lib.stream_ptr(dev), nbytes), nbytes
 
 
 def propagate(field: torch.Tensor, wavelength, pixel_pitch, distance, size,

@@ -85,9 +85,13 @@ class _Inputs:
 
 def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
             fx, fy, px, py, view_matrix, img_size: Sequence[int], tile_size=(16, 16),
-            near_plane=1.0, far_plane=1000.0):
+            near_plane=1.0, far_plane=1000.0, keep_geometry: bool = False):
     """Rasterizer::forward -> (field (P,C,H,W) complex64,
-    (final_Ts, n_contrib, point_list, ranges, visible_indices))."""
+    (final_Ts, n_contrib, point_list, ranges, visible_indices)).
+
+    keep_geometry=True appends a third element: the forward's geometry
+    workspace (a uint8 tensor), which backward(..., geometry=) reuses instead
+    of recomputing the projection."""
     if tuple(int(t) for t in tile_size) != (16, 16):
         # The reference ignores tile_size and always uses 16x16 tiles
         # (config.h:16-17); any other request is accepted and ignored the same way.
@@ -100,17 +104,22 @@ def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plan
     with torch.cuda.device(dev):
         stream = _lib.stream_ptr(dev)
         gbytes = lib.hrf_raster_geom_workspace_size(inp.n, C, P)
-        geom_ws = torch.empty(max(gbytes, 1), dtype=torch.uint8, device=dev)
+        if keep_geometry:
+            geom_ws = torch.empty(max(gbytes, 1), dtype=torch.uint8, device=dev)
+        else:
+            geom_ws = _lib.workspace("raster_geom", dev, stream, gbytes)
+        # Outputs whose size does not depend on the pair count are allocated
+        # before the count read-back, so little host work follows that sync.
+        field = torch.empty((P, C, H, W), dtype=torch.complex64, device=dev)
+        final_T = torch.empty((P, H, W), dtype=torch.float32, device=dev)
+        n_contrib = torch.empty((P, H, W), dtype=torch.int32, device=dev)
+        ranges = torch.empty((inp.ntiles, 2), dtype=torch.int32, device=dev)
         K = ctypes.c_int64(0)
         V = ctypes.c_int64(0)
         _lib.check(lib.hrf_raster_forward_prepare(ctypes.byref(inp.g), ctypes.byref(inp.c),
                                                   geom_ws.data_ptr(), gbytes, stream,
                                                   ctypes.byref(K), ctypes.byref(V)))
         K, V = int(K.value), int(V.value)
-        field = torch.empty((P, C, H, W), dtype=torch.complex64, device=dev)
-        final_T = torch.empty((P, H, W), dtype=torch.float32, device=dev)
-        n_contrib = torch.empty((P, H, W), dtype=torch.int32, device=dev)
-        ranges = torch.empty((inp.ntiles, 2), dtype=torch.int32, device=dev)
         if K == 0:
             point_list = torch.zeros(1, dtype=torch.int32, device=dev)
             visible = torch.zeros(0, dtype=torch.int64, device=dev)
@@ -120,20 +129,26 @@ def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plan
             point_list = torch.empty(K, dtype=torch.int32, device=dev)
             visible = torch.empty(V, dtype=torch.int64, device=dev)
             bbytes = lib.hrf_raster_binning_workspace_size(K, W, H)
-            bin_ws = torch.empty(bbytes, dtype=torch.uint8, device=dev)
+            bin_ws = _lib.workspace("raster_bin", dev, stream, bbytes)
         _lib.check(lib.hrf_raster_forward_render(
             ctypes.byref(inp.g), ctypes.byref(inp.c), geom_ws.data_ptr(), gbytes,
             _lib.ptr(bin_ws), bbytes, K, V if K > 0 else 0, field.data_ptr(),
             final_T.data_ptr(), n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
             visible.data_ptr() if visible.numel() else None, stream))
+    if keep_geometry:
+        return field, (final_T, n_contrib, point_list, ranges, visible), geom_ws
     return field, (final_T, n_contrib, point_list, ranges, visible)
 
 
 def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
              plane_probs, fx, fy, px, py, view_matrix, img_size, tile_size, final_Ts,
-             n_contrib, point_list, ranges, near_plane=1.0, far_plane=1000.0):
+             n_contrib, point_list, ranges, near_plane=1.0, far_plane=1000.0,
+             geometry: torch.Tensor | None = None):
     """Rasterizer::backward -> [grad_cam_means_3D, grad_z_vals, grad_quats, grad_scales,
-    grad_colours, grad_phase, grad_opacities, grad_plane_probs]."""
+    grad_colours, grad_phase, grad_opacities, grad_plane_probs].
+
+    geometry: the workspace forward(..., keep_geometry=True) returned for these
+    same inputs, or None to recompute the projection."""
     inp = _Inputs(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
                   fx, fy, px, py, view_matrix, img_size, near_plane, far_plane)
     lib = _lib.load()
@@ -169,11 +184,12 @@ def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, o
     with torch.cuda.device(dev):
         stream = _lib.stream_ptr(dev)
         wbytes = lib.hrf_raster_backward_workspace_size(n, C, P)
-        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev)
+        ws = _lib.workspace("raster_bwd", dev, stream, wbytes)
         _lib.check(lib.hrf_raster_backward(
             ctypes.byref(inp.g), ctypes.byref(inp.c), go.data_ptr(), final_Ts.data_ptr(),
             n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
-            int(point_list.numel()), ws.data_ptr(), wbytes, g_cam.data_ptr(), g_z.data_ptr(),
+            int(point_list.numel()), ws.data_ptr(), wbytes, _lib.ptr(geometry),
+            int(geometry.numel()) if geometry is not None else 0, g_cam.data_ptr(), g_z.data_ptr(),
             g_q.data_ptr(), g_s.data_ptr(), g_col.data_ptr(), g_ph.data_ptr(), g_o.data_ptr(),
             g_pl.data_ptr(), stream))
     return [g_cam, g_z, g_q, g_s, g_col, g_ph, g_o, g_pl]

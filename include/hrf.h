@@ -105,6 +105,10 @@ size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t p
  * Outputs, all fully overwritten: grad_cam (N,3), grad_z (N) (always 0),
  * grad_quats (N,4), grad_scales (N,3), grad_colours (N,C), grad_phase (N,C),
  * grad_opacities (N), grad_plane_probs (N,P).
+ * fwd_geom_ws (optional, may be NULL): the geometry workspace the forward of
+ * these same inputs used, kept unchanged since; its render records are then
+ * reused instead of recomputing the projection (the reference recomputes
+ * means2D and cov2D, rasterizer_splat.cu:606-617).
  * Replaces Rasterizer::backward (rasterizer_splat.cu:551-684),
  * backward_splat.cu:78-417 and backward.cu. */
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
@@ -112,6 +116,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
                         const int32_t* n_contrib, const int32_t* point_list,
                         const int32_t* ranges, int64_t num_pairs,
                         void* ws, size_t ws_bytes,
+                        const void* fwd_geom_ws, size_t fwd_geom_ws_bytes,
                         float* grad_cam, float* grad_z, float* grad_quats,
                         float* grad_scales, float* grad_colours, float* grad_phase,
                         float* grad_opacities, float* grad_plane_probs,
