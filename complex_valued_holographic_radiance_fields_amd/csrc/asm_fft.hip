@@ -31,6 +31,7 @@
 #include <mutex>
 #include <vector>
 
+#include "fast_trig.h"
 #include "hrf_internal.h"
 
 namespace hrf {
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
         coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
         if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
           float sn, cs;
-          sincosf(d * kz[u], &sn, &cs);
+          sincos_big(d * kz[u], &sn, &cs);
           const float2 x = lds[pad(q)];
           acc[u].x += x.x * cs - x.y * sn;
           acc[u].y += x.x * sn + x.y * cs;
@@ -580,7 +581,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
           coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
           if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
             float sn, cs;
-            sincosf(nd * kz[u], &sn, &cs);
+            sincos_big(nd * kz[u], &sn, &cs);
             r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
           }
         }

@@ -40,3 +40,24 @@ def test_wave_sum_lane63(wlib):
     out = torch.zeros(64, dtype=torch.float32, device="cuda")
     assert wlib.wave_test_sum(xin.data_ptr(), out.data_ptr()) == 0
     assert out[63].item() == x.sum()
+
+
+def test_sincos_big_accuracy(wlib):
+    """sin/cos of the transfer-function phase (float arguments up to 1e5 rad,
+    as d*kz reaches) against float64 sin/cos of the same float values."""
+    import torch
+
+    f = wlib.trig_test_sincos
+    f.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int]
+    f.restype = ctypes.c_int
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.uniform(-1e5, 1e5, 200_000), rng.uniform(-10, 10, 50_000),
+                        np.array([0.0, np.pi, -np.pi, 2 * np.pi, 1e5])]).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    s = torch.empty_like(xt)
+    c = torch.empty_like(xt)
+    assert f(xt.data_ptr(), s.data_ptr(), c.data_ptr(), x.size) == 0
+    xd = x.astype(np.float64)
+    err = max(np.abs(s.cpu().numpy() - np.sin(xd)).max(), np.abs(c.cpu().numpy() - np.cos(xd)).max())
+    print(f"sincos_big max abs error {err:.2e}", flush=True)
+    assert err < 2e-6
