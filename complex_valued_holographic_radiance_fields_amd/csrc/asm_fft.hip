@@ -327,6 +327,10 @@ struct AsmFftConsts {
   float d[kMaxPlanes];
   float fxmax[kMaxPlanes * kMaxChannels];
   float fymax[kMaxPlanes * kMaxChannels];
+  // 1 when the band limit of (plane, channel) passes every frequency of the
+  // grid (decided on the host with the device's float arithmetic), so the
+  // per-element test can be skipped.
+  unsigned char band_all[kMaxPlanes * kMaxChannels];
 };
 
 // Intermediate spectra are stored tile-major: image `img` (h rows of N
@@ -482,16 +486,21 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
     __syncthreads();
     Plan<N>::template run<false>(lds, tw);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
+    const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
       const int q = threadIdx.x + u * kFftThreads;
       if (q < B * N && kz[u] >= 0.0f) {
-        const int i = q / B, b = q % B;
-        float fxv, fyv;
-        bool inap;
-        coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
-        if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
+        bool within = band_all;
+        if (!within) {
+          const int i = q / B, b = q % B;
+          float fxv, fyv;
+          bool inap;
+          coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
+          within = fabsf(fxv) < fxm && fabsf(fyv) < fym;
+        }
+        if (within) {
           float sn, cs;
           sincos_big(d * kz[u], &sn, &cs);
           const float2 x = lds[pad(q)];
@@ -568,6 +577,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
   for (int p = 0; p < P; ++p) {
     __syncthreads();
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
+    const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float nd = -mc.d[p];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
@@ -575,11 +585,15 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
       if (q < B * N) {
         float2 r = make_float2(0.0f, 0.0f);
         if (kz[u] >= 0.0f) {
-          const int i = q / B, b = q % B;
-          float fxv, fyv;
-          bool inap;
-          coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
-          if (fabsf(fxv) < fxm && fabsf(fyv) < fym) {
+          bool within = band_all;
+          if (!within) {
+            const int i = q / B, b = q % B;
+            float fxv, fyv;
+            bool inap;
+            coords(i, k0 + b, N, sfreq, -1.0f, &fxv, &fyv, &inap);
+            within = fabsf(fxv) < fxm && fabsf(fyv) < fym;
+          }
+          if (within) {
             float sn, cs;
             sincos_big(nd * kz[u], &sn, &cs);
             r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
@@ -634,6 +648,11 @@ AsmFftConsts fft_consts(int P, int C, int M, double pitch, const float* wl, cons
       const AsmConsts a = asm_consts(wl[c], dist[p], static_cast<float>(pitch), M, M);
       mc.fxmax[p * kMaxChannels + c] = a.fx_max;
       mc.fymax[p * kMaxChannels + c] = a.fy_max;
+      // |fx| on the grid is at most float(M/2) * (float)(1/(M*pitch)), the
+      // value of the most negative bin; the device tests |f| < f_max.
+      const float fmax_grid = static_cast<float>(M / 2) *
+                              static_cast<float>(1.0 / (static_cast<double>(M) * pitch));
+      mc.band_all[p * kMaxChannels + c] = (fmax_grid < a.fx_max && fmax_grid < a.fy_max) ? 1 : 0;
     }
   }
   return mc;
