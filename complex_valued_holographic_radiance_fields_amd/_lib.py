@@ -51,11 +51,12 @@ SIGNATURES = {
         _P(HrfGaussians), _P(HrfCamera), _vp, _sz, _vp, _P(_i64), _P(_i64)]),
     "hrf_raster_forward_render": (ctypes.c_int, [
         _P(HrfGaussians), _P(HrfCamera), _vp, _sz, _vp, _sz, _i64, _i64,
-        _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "hrf_raster_plane_lists_size": (_sz, [_i64, _i32, _i32, _i32]),
     "hrf_raster_backward_workspace_size": (_sz, [_i64, _i32, _i32]),
     "hrf_raster_backward": (ctypes.c_int, [
         _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp, _sz,
-        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+        _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hrf_cov3d_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "hrf_cov3d_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "hrf_jacobian_forward": (ctypes.c_int, [_vp, _i64, _f32, _f32, _i32, _i32, _f32, _f32,

@@ -148,6 +148,20 @@ BinWs carve_bin(Carver& cv, int64_t k) {
   return w;
 }
 
+// Plane member lists: P*K (gaussian, position) entries, then T*P counts.
+struct SubWs {
+  int2* entries;
+  int32_t* counts;
+};
+
+SubWs carve_sub(Carver& cv, int64_t k, int ntiles, int P) {
+  SubWs w;
+  const int64_t m = k > 0 ? k : 1;
+  w.entries = cv.take<int2>(static_cast<size_t>(m) * (P > 0 ? P : 1));
+  w.counts = cv.take<int32_t>(static_cast<size_t>(ntiles > 0 ? ntiles : 1) * (P > 0 ? P : 1));
+  return w;
+}
+
 struct BwdWs {
   float* rec;
   uint32_t* pmask;
@@ -274,6 +288,15 @@ size_t hrf_raster_binning_workspace_size(int64_t num_pairs, int32_t width, int32
   return cv.bytes();
 }
 
+size_t hrf_raster_plane_lists_size(int64_t num_pairs, int32_t width, int32_t height,
+                                   int32_t planes) {
+  if (num_pairs < 0 || width <= 0 || height <= 0 || planes <= 0) return 0;
+  const int ntiles = ((width + kTile - 1) / kTile) * ((height + kTile - 1) / kTile);
+  Carver cv(nullptr);
+  carve_sub(cv, num_pairs, ntiles, planes);
+  return cv.bytes();
+}
+
 size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t planes) {
   Carver cv(nullptr);
   carve_bwd(cv, n, channels < 1 ? 1 : (channels > 3 ? 3 : channels),
@@ -357,7 +380,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
                               size_t geom_ws_bytes, void* bin_ws, size_t bin_ws_bytes,
                               int64_t num_pairs, int64_t num_visible, void* field,
                               float* final_T, int32_t* n_contrib, int32_t* point_list,
-                              int32_t* ranges, int64_t* visible, void* stream) {
+                              int32_t* ranges, int64_t* visible, void* plane_lists,
+                              size_t plane_lists_bytes, void* stream) {
   HRF_TRY(check_raster_args(g, cam));
   if (num_pairs < 0 || num_pairs > 0x7FFFFFFFLL || num_visible < 0 || num_visible > g->n) {
     set_error("invalid pair/visible counts (%lld, %lld)", static_cast<long long>(num_pairs),
@@ -456,6 +480,15 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.pprobs = g->plane_probs;
   rp.n = n;
   rp.num_pairs = num_pairs;
+  if (plane_lists) {
+    HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
+                     hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
+                     "plane lists"));
+    Carver cs(plane_lists);
+    const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
+    rp.sub_out = sw.entries;
+    rp.sub_cnt_out = sw.counts;
+  }
   {
     HRF_STAGE("render_fwd", s);
     HRF_TRY(launch_render_forward(rp, s));
@@ -468,7 +501,8 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
                         const float* final_T, const int32_t* n_contrib,
                         const int32_t* point_list, const int32_t* ranges, int64_t num_pairs,
                         void* ws, size_t ws_bytes, const void* fwd_geom_ws,
-                        size_t fwd_geom_ws_bytes, float* grad_cam, float* grad_z,
+                        size_t fwd_geom_ws_bytes, const void* plane_lists,
+                        size_t plane_lists_bytes, float* grad_cam, float* grad_z,
                         float* grad_quats, float* grad_scales, float* grad_colours,
                         float* grad_phase, float* grad_opacities, float* grad_plane_probs,
                         void* stream) {
@@ -542,6 +576,16 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     rp.final_T_in = final_T;
     rp.n_contrib_in = n_contrib;
     rp.acc = w.acc;
+    if (plane_lists) {
+      HRF_TRY(check_ws(const_cast<void*>(plane_lists), plane_lists_bytes,
+                       hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height,
+                                                   g->planes),
+                       "plane lists"));
+      Carver cs(const_cast<void*>(plane_lists));
+      const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
+      rp.sub = sw.entries;
+      rp.sub_cnt = sw.counts;
+    }
     HRF_STAGE("render_bwd", s);
     HRF_TRY(launch_render_backward(rp, s));
   }

@@ -233,6 +233,16 @@ struct RenderParams {
   const float* final_T_in;
   const int32_t* n_contrib_in;
   float* acc;
+  // Plane member lists (optional).  Entry i of (tile t, plane q) is the
+  // (gaussian, tile-list position) pair of the i-th member of plane q in
+  // t's list, stored at q*num_pairs + r0(t) + i; sub_cnt[t*P + q] members.
+  // The forward writes them (sub_out) for the batches it composites; the
+  // backward then reads them (sub) instead of re-filtering every tile list
+  // per plane.
+  int2* sub_out;
+  int32_t* sub_cnt_out;
+  const int2* sub;
+  const int32_t* sub_cnt;
 };
 int launch_render_forward(const RenderParams& p, hipStream_t s);
 int launch_render_empty(const RenderParams& p, hipStream_t s);

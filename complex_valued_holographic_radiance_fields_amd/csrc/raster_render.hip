@@ -94,6 +94,9 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   for (int i = 0; i < 2 * C; ++i) acc[i] = 0.0f;
   int last = 0;
   bool done = !inside;
+  int listed = 0;  // plane members of the batches composited so far
+  int2* const sub_out =
+      p.sub_out ? p.sub_out + static_cast<int64_t>(plane) * p.num_pairs + r0 : nullptr;
 
   for (int base = 0; base < n; base += kBlock) {
     if (__syncthreads_and(done)) break;
@@ -108,6 +111,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
     if (mem) {
+      if (sub_out) sub_out[listed + pos] = make_int2(g, k);
       const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
       float4 rq[NQ];
 #pragma unroll
@@ -126,6 +130,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     // Pad the staged batch to a multiple of kUnroll with members no pixel
     // can use: a positive-definite exponent 1e12 (power > 0), so they never
     // contribute or count.
+    listed += cnt;
     const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
     if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
       const int q0 = static_cast<int>(threadIdx.x) * NQ;
@@ -166,6 +171,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     }
   }
 
+  if (sub_out && threadIdx.x == 0) p.sub_cnt_out[tile * p.P + plane] = listed;
   if (inside) {
     const int64_t HW = static_cast<int64_t>(p.W) * p.H;
     const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
@@ -220,7 +226,7 @@ __device__ __forceinline__ bool box_reaches(float mx, float my, float cxx, float
 // G members whose 6+2C partial sums per lane are reduced together with one
 // transpose_reduce64.  Skipping a member for a whole wave is exact: every
 // lane of that wave would skip it (alpha < 1/255 or position >= n_contrib).
-template <int C>
+template <int C, bool kSub>
 __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   constexpr int NQ = rec_quads(C);
   constexpr int RS = rec_stride(C);
@@ -284,18 +290,38 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   const float half_h = 0.5f * static_cast<float>(p.H);
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
 
-  for (int end = maxlast; end > 0; end -= kBlock) {
+  // Entries walked: list positions [0, maxlast) of the tile list, or the
+  // whole member list of this plane (entries at positions >= maxlast are
+  // then culled by the quadrant bounds below).
+  int lim = maxlast;
+  const int2* sub = nullptr;
+  if (kSub) {
+    const int c = p.sub_cnt[tile * p.P + plane];
+    lim = c < 0 ? 0 : (c > n ? n : c);
+    sub = p.sub + static_cast<int64_t>(plane) * p.num_pairs + r0;
+  }
+  for (int end = lim; end > 0; end -= kBlock) {
     const int start = end > kBlock ? end - kBlock : 0;
     __syncthreads();
-    const int k = start + static_cast<int>(threadIdx.x);
+    const int idx = start + static_cast<int>(threadIdx.x);
+    int k = idx;
     int g = 0;
     unsigned qm = 0;
     float4 rq[NQ];
     float wpl = 0.0f;
-    if (k < end) {
-      g = p.plist[r0 + k];
-      if (static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
-          ((p.pmask[g] >> plane) & 1u)) {
+    if (idx < end) {
+      bool member;
+      if (kSub) {
+        const int2 e = sub[idx];
+        g = e.x;
+        k = e.y;
+        member = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n);
+      } else {
+        g = p.plist[r0 + idx];
+        member = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+                 ((p.pmask[g] >> plane) & 1u);
+      }
+      if (member) {
         const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) rq[q] = src[q];
@@ -494,13 +520,16 @@ int launch_render_backward(const RenderParams& p, hipStream_t s) {
   if (nblocks <= 0) return HRF_OK;
   switch (p.C) {
     case 1:
-      hipLaunchKernelGGL(k_render_bwd<1>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (p.sub) hipLaunchKernelGGL((k_render_bwd<1, true>), dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL((k_render_bwd<1, false>), dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     case 2:
-      hipLaunchKernelGGL(k_render_bwd<2>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (p.sub) hipLaunchKernelGGL((k_render_bwd<2, true>), dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL((k_render_bwd<2, false>), dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     case 3:
-      hipLaunchKernelGGL(k_render_bwd<3>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (p.sub) hipLaunchKernelGGL((k_render_bwd<3, true>), dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL((k_render_bwd<3, false>), dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     default:
       set_error("render backward: channels must be 1..3 (got %d)", p.C);

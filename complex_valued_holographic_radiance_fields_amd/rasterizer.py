@@ -8,7 +8,7 @@ behaviour, with errors raised as RuntimeError instead of printed.
 from __future__ import annotations
 
 import ctypes
-from typing import Sequence, Tuple
+from typing import NamedTuple, Optional, Sequence, Tuple
 
 import torch
 
@@ -83,15 +83,30 @@ class _Inputs:
         return ((self.W + 15) // 16) * ((self.H + 15) // 16)
 
 
+# Largest plane member list buffer (P*K*8 bytes + counts) a forward keeps for
+# its backward; beyond it the backward filters the tile lists itself.
+PLANE_LISTS_MAX_BYTES = 32 << 30
+
+
+class ForwardGeometry(NamedTuple):
+    """What forward(..., keep_geometry=True) hands to backward(geometry=):
+    the geometry workspace (render records of these inputs) and the plane
+    member lists of this forward's tile lists (None when not kept)."""
+    workspace: torch.Tensor
+    plane_lists: Optional[torch.Tensor]
+
+
 def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
             fx, fy, px, py, view_matrix, img_size: Sequence[int], tile_size=(16, 16),
             near_plane=1.0, far_plane=1000.0, keep_geometry: bool = False):
     """Rasterizer::forward -> (field (P,C,H,W) complex64,
     (final_Ts, n_contrib, point_list, ranges, visible_indices)).
 
-    keep_geometry=True appends a third element: the forward's geometry
-    workspace (a uint8 tensor), which backward(..., geometry=) reuses instead
-    of recomputing the projection."""
+    keep_geometry=True appends a third element, a ForwardGeometry: the
+    forward's geometry workspace, which backward(..., geometry=) reuses
+    instead of recomputing the projection, and the per-(tile, plane) member
+    lists of the tile lists, which the backward walks instead of filtering
+    each tile list once per plane."""
     if tuple(int(t) for t in tile_size) != (16, 16):
         # The reference ignores tile_size and always uses 16x16 tiles
         # (config.h:16-17); any other request is accepted and ignored the same way.
@@ -130,25 +145,40 @@ def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plan
             visible = torch.empty(V, dtype=torch.int64, device=dev)
             bbytes = lib.hrf_raster_binning_workspace_size(K, W, H)
             bin_ws = _lib.workspace("raster_bin", dev, stream, bbytes)
+        plane_lists = None
+        sbytes = 0
+        if keep_geometry and K > 0:
+            sbytes = lib.hrf_raster_plane_lists_size(K, W, H, P)
+            if sbytes <= PLANE_LISTS_MAX_BYTES:
+                plane_lists = torch.empty(sbytes, dtype=torch.uint8, device=dev)
+            else:
+                sbytes = 0
         _lib.check(lib.hrf_raster_forward_render(
             ctypes.byref(inp.g), ctypes.byref(inp.c), geom_ws.data_ptr(), gbytes,
             _lib.ptr(bin_ws), bbytes, K, V if K > 0 else 0, field.data_ptr(),
             final_T.data_ptr(), n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
-            visible.data_ptr() if visible.numel() else None, stream))
+            visible.data_ptr() if visible.numel() else None, _lib.ptr(plane_lists), sbytes,
+            stream))
     if keep_geometry:
-        return field, (final_T, n_contrib, point_list, ranges, visible), geom_ws
+        return (field, (final_T, n_contrib, point_list, ranges, visible),
+                ForwardGeometry(geom_ws, plane_lists))
     return field, (final_T, n_contrib, point_list, ranges, visible)
 
 
 def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
              plane_probs, fx, fy, px, py, view_matrix, img_size, tile_size, final_Ts,
              n_contrib, point_list, ranges, near_plane=1.0, far_plane=1000.0,
-             geometry: torch.Tensor | None = None):
+             geometry: ForwardGeometry | torch.Tensor | None = None):
     """Rasterizer::backward -> [grad_cam_means_3D, grad_z_vals, grad_quats, grad_scales,
     grad_colours, grad_phase, grad_opacities, grad_plane_probs].
 
-    geometry: the workspace forward(..., keep_geometry=True) returned for these
-    same inputs, or None to recompute the projection."""
+    geometry: the ForwardGeometry forward(..., keep_geometry=True) returned
+    for these same inputs and forward outputs (or just its workspace), or
+    None to recompute the projection and filter the tile lists here."""
+    if isinstance(geometry, ForwardGeometry):
+        geom_ws, plane_lists = geometry.workspace, geometry.plane_lists
+    else:
+        geom_ws, plane_lists = geometry, None
     inp = _Inputs(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
                   fx, fy, px, py, view_matrix, img_size, near_plane, far_plane)
     lib = _lib.load()
@@ -188,8 +218,10 @@ def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, o
         _lib.check(lib.hrf_raster_backward(
             ctypes.byref(inp.g), ctypes.byref(inp.c), go.data_ptr(), final_Ts.data_ptr(),
             n_contrib.data_ptr(), point_list.data_ptr(), ranges.data_ptr(),
-            int(point_list.numel()), ws.data_ptr(), wbytes, _lib.ptr(geometry),
-            int(geometry.numel()) if geometry is not None else 0, g_cam.data_ptr(), g_z.data_ptr(),
+            int(point_list.numel()), ws.data_ptr(), wbytes, _lib.ptr(geom_ws),
+            int(geom_ws.numel()) if geom_ws is not None else 0, _lib.ptr(plane_lists),
+            int(plane_lists.numel()) if plane_lists is not None else 0, g_cam.data_ptr(),
+            g_z.data_ptr(),
             g_q.data_ptr(), g_s.data_ptr(), g_col.data_ptr(), g_ph.data_ptr(), g_o.data_ptr(),
             g_pl.data_ptr(), stream))
     return [g_cam, g_z, g_q, g_s, g_col, g_ph, g_o, g_pl]

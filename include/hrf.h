@@ -95,7 +95,20 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
                               int64_t num_pairs, int64_t num_visible,
                               void* field, float* final_T, int32_t* n_contrib,
                               int32_t* point_list, int32_t* ranges, int64_t* visible,
+                              void* plane_lists, size_t plane_lists_bytes,
                               void* stream);
+
+/* Bytes of the optional plane member lists for K pairs on a W x H image
+ * with P planes: P*K (gaussian, list position) int32 pairs (plane q's list
+ * of tile t starts at q*K + ranges[t][0]), then, from the next 256-byte
+ * boundary, T*P int32 counts (tile-major).  hrf_raster_forward_render fills them (plane_lists non-NULL)
+ * with each (tile, plane)'s members, in list order, over the entries its
+ * compositing visited; hrf_raster_backward given the same buffer walks
+ * those lists instead of filtering every tile list once per plane.  No
+ * counterpart in the reference (its backward re-reads the whole tile list
+ * per plane, backward_splat.cu:148-306). */
+size_t hrf_raster_plane_lists_size(int64_t num_pairs, int32_t width, int32_t height,
+                                   int32_t planes);
 
 /* Bytes of workspace hrf_raster_backward needs. */
 size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t planes);
@@ -109,6 +122,8 @@ size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t p
  * these same inputs used, kept unchanged since; its render records are then
  * reused instead of recomputing the projection (the reference recomputes
  * means2D and cov2D, rasterizer_splat.cu:606-617).
+ * plane_lists (optional, may be NULL): the plane member lists the forward of
+ * these same inputs wrote (same point_list, ranges and n_contrib).
  * Replaces Rasterizer::backward (rasterizer_splat.cu:551-684),
  * backward_splat.cu:78-417 and backward.cu. */
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
@@ -117,6 +132,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
                         const int32_t* ranges, int64_t num_pairs,
                         void* ws, size_t ws_bytes,
                         const void* fwd_geom_ws, size_t fwd_geom_ws_bytes,
+                        const void* plane_lists, size_t plane_lists_bytes,
                         float* grad_cam, float* grad_z, float* grad_quats,
                         float* grad_scales, float* grad_colours, float* grad_phase,
                         float* grad_opacities, float* grad_plane_probs,

@@ -224,3 +224,106 @@ def test_forward_parity_wide_keys(hrf, oracle_mod):
     np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
     np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
+def _plane_list_scene(case):
+    import dataclasses
+
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    if case == "dense":
+        # Opaque, large Gaussians: ~40% of the pixels reach T < 1e-4, so the
+        # forward stops early and the plane lists end before the tile lists.
+        spec = dataclasses.replace(scenes.small("dense", 4000, 48, 48, 2, 3, "uniform", seed=21),
+                                   log_scale_mean=-2.5)
+        sc = scenes.generate(spec)
+        sc.opac[:] = 0.95
+        return sc
+    sc = _scene("planes3", 8000, 128, 128, 3, 3, "object")
+    if case == "soft":
+        # Soft plane weights: Gaussians in several planes, some weights at
+        # zero or below the 1e-6 cutoff.
+        rng = np.random.default_rng(8)
+        w = rng.uniform(0, 1, size=sc.pprobs.shape).astype(np.float32)
+        w[rng.uniform(size=w.shape) < 0.3] = 0.0
+        w[rng.uniform(size=w.shape) < 0.05] = 5e-7
+        sc.pprobs[:] = w
+    return sc
+
+
+@pytest.mark.parametrize("case", ["onehot", "soft", "dense"])
+def test_backward_with_plane_lists(hrf, oracle_mod, case):
+    """The forward's plane member lists (kept for the backward): each
+    (tile, plane) list is exactly that plane's members of the tile list, in
+    list order, cut after the last batch the forward composited (never before
+    any pixel's n_contrib); the backward walking them matches the oracle's
+    backward on the same forward state and the backward that filters the tile
+    lists itself (both sum float atomics, so to rounding: rel-L2 < 1e-6)."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import rasterizer, scenes
+
+    sc = _plane_list_scene(case)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    t = scenes.to_torch(sc)
+    W, H = sc.spec.width, sc.spec.height
+    args = (t["cam_means"], t["z"], t["quats"], t["scales"], t["colours"], t["phase"], t["opac"],
+            t["pprobs"], sc.fx, sc.fy, sc.px, sc.py, t["view"])
+    field, info, geom = rasterizer.forward(*args, (W, H), (16, 16), 1.0, 1000.0,
+                                           keep_geometry=True)
+    fT, nc, pl, ranges, _ = info
+    torch.cuda.synchronize()
+    assert geom.plane_lists is not None
+    P, K = g.P, int(pl.numel())
+    print(f"case={case} N={g.n} K={K} P={P}", flush=True)
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    if case == "dense":
+        assert float((fT < 1e-4).float().mean()) > 0.2
+
+    # Plane lists: P*K (gaussian, position) pairs, then, from the next
+    # 256-byte boundary, T*P counts.
+    buf = geom.plane_lists.cpu().numpy()
+    ntiles = ranges.shape[0]
+    ent = buf[:P * K * 8].view(np.int32).reshape(P, K, 2)
+    c0 = (P * K * 8 + 255) // 256 * 256
+    cnt = buf[c0:c0 + ntiles * P * 4].view(np.int32).reshape(ntiles, P)
+    pl_np, r_np, nc_np = pl.cpu().numpy(), ranges.cpu().numpy(), nc.cpu().numpy()
+    member = g.pprobs >= np.float32(1e-6)
+    gx = (W + 15) // 16
+    truncated = 0
+    for tile in range(ntiles):
+        r0, r1 = r_np[tile]
+        ty, tx = divmod(tile, gx)
+        for p in range(P):
+            ks = np.nonzero(member[pl_np[r0:r1], p])[0]
+            c = int(cnt[tile, p])
+            assert 0 <= c <= len(ks)
+            got = ent[p, r0:r0 + c]
+            np.testing.assert_array_equal(got[:, 1], ks[:c])
+            np.testing.assert_array_equal(got[:, 0], pl_np[r0 + ks[:c]])
+            if c < len(ks):
+                truncated += 1
+                tile_nc = nc_np[p, ty * 16:(ty + 1) * 16, tx * 16:(tx + 1) * 16]
+                assert ks[c] >= tile_nc.max()
+    if case == "dense":
+        assert truncated > 0
+
+    rng = np.random.default_rng(6)
+    gf = ((rng.normal(size=(P, g.C, H, W)) + 1j * rng.normal(size=(P, g.C, H, W))) *
+          np.sqrt(0.5)).astype(np.complex64)
+    gft = torch.from_numpy(gf).cuda()
+    with_lists = rasterizer.backward(gft, *args, (W, H), (16, 16), fT, nc, pl, ranges, 1.0, 1000.0,
+                                     geometry=geom)
+    filtered = rasterizer.backward(gft, *args, (W, H), (16, 16), fT, nc, pl, ranges, 1.0, 1000.0)
+    state = dict(ref, final_T=fT.cpu().numpy(), n_contrib=nc_np, point_list=pl_np, ranges=r_np)
+    rb = oracle_mod.rasterize_backward(g, cam, state, gf)
+    names = ["cam", "z", "quats", "scales", "colours", "phase", "opac", "plane"]
+    for name, a, b in zip(names, with_lists, filtered):
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        if name == "z":
+            assert np.all(a == 0)
+            continue
+        assert rel_l2(a, b) < 1e-6, name
+        err = rel_l2(a, rb[name])
+        print(f"{case} grad_{name}: rel_l2={err:.3e}", flush=True)
+        assert err < TOL, (name, err)
