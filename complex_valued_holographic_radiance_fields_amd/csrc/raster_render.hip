@@ -11,8 +11,9 @@
 // their records (mean, conic, opacity, weight, complex amplitude) in LDS;
 // every lane then reads each record with a uniform-address (broadcast) LDS
 // load.  Blocks are mapped to (tile, plane) XCD-aware: the 8 XCDs receive
-// blocks round-robin, so consecutive logical ids are given to one XCD and the
-// P planes of a tile (and neighbouring tiles) share that XCD's L2.
+// blocks round-robin, so runs of consecutive tiles (all their planes) are
+// given to one XCD and share its L2, while the runs interleave over the XCDs
+// so that every XCD gets an even share of the dense image regions.
 //
 // Backward gradients: waves own 8x8 quadrants; each batch stages records
 // with a per-quadrant cull mask (exact: alpha >= 1/255 box and n_contrib
@@ -28,10 +29,22 @@
 namespace hrf {
 namespace {
 
+// Hardware block b runs on XCD b % 8.  Logical ids (tile-major, planes
+// innermost) are dealt to the XCDs in runs of kRunTiles tiles: each XCD
+// receives whole runs (neighbouring tiles share Gaussians in its L2), and
+// the runs of all 8 XCDs advance together through the image, so the dense
+// rows of a scene are spread over every XCD instead of loading a few.
+constexpr int kRunTiles = 4;
+
 __device__ __forceinline__ void map_block(int b, int nb, int P, int* tile, int* plane) {
-  const int q = nb >> 3, r = nb & 7;
-  const int x = b & 7, i = b >> 3;
-  const int logical = (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+  const int c = kRunTiles * P;  // logical ids per run
+  const int full = nb - nb % (8 * c);
+  int logical = b;
+  if (b < full) {
+    const int x = b & 7, i = b >> 3;
+    const int run = i / c, off = i - run * c;
+    logical = (run * 8 + x) * c + off;
+  }
   *tile = logical / P;
   *plane = logical - (*tile) * P;
 }
