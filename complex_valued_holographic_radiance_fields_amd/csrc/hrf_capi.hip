@@ -148,17 +148,21 @@ BinWs carve_bin(Carver& cv, int64_t k) {
   return w;
 }
 
-// Plane member lists: P*K (gaussian, position) entries, then T*P counts.
+// Plane member lists: P*K (gaussian, position) entries, T*P counts, and the
+// backward's block order over the T*P (tile, plane) ids.
 struct SubWs {
   int2* entries;
   int32_t* counts;
+  int32_t* order;
 };
 
 SubWs carve_sub(Carver& cv, int64_t k, int ntiles, int P) {
   SubWs w;
   const int64_t m = k > 0 ? k : 1;
+  const size_t tp = static_cast<size_t>(ntiles > 0 ? ntiles : 1) * (P > 0 ? P : 1);
   w.entries = cv.take<int2>(static_cast<size_t>(m) * (P > 0 ? P : 1));
-  w.counts = cv.take<int32_t>(static_cast<size_t>(ntiles > 0 ? ntiles : 1) * (P > 0 ? P : 1));
+  w.counts = cv.take<int32_t>(tp);
+  w.order = cv.take<int32_t>(tp);
   return w;
 }
 
@@ -480,6 +484,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.pprobs = g->plane_probs;
   rp.n = n;
   rp.num_pairs = num_pairs;
+  int32_t* order_out = nullptr;
   if (plane_lists) {
     HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
                      hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
@@ -488,10 +493,13 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
     rp.sub_out = sw.entries;
     rp.sub_cnt_out = sw.counts;
+    order_out = sw.order;
   }
   {
     HRF_STAGE("render_fwd", s);
     HRF_TRY(launch_render_forward(rp, s));
+    if (order_out)
+      HRF_TRY(launch_order_by_cost(rp.sub_cnt_out, f.ntiles * g->planes, order_out, s));
   }
   if (num_visible > 0) HRF_TRY(launch_compact_visible(w.vis, w.vis_off, n, visible, s));
   return HRF_OK;
@@ -585,6 +593,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
       const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
       rp.sub = sw.entries;
       rp.sub_cnt = sw.counts;
+      rp.order = sw.order;
     }
     HRF_STAGE("render_bwd", s);
     HRF_TRY(launch_render_backward(rp, s));

@@ -243,10 +243,16 @@ struct RenderParams {
   int32_t* sub_cnt_out;
   const int2* sub;
   const int32_t* sub_cnt;
+  // Backward block order over the T*P (tile, plane) ids (with sub): longest
+  // member list first.
+  const int32_t* order;
 };
 int launch_render_forward(const RenderParams& p, hipStream_t s);
 int launch_render_empty(const RenderParams& p, hipStream_t s);
 int launch_render_backward(const RenderParams& p, hipStream_t s);
+// order[0..m) = the ids 0..m-1 sorted by cnt[id] descending (in logarithmic
+// buckets, 8 per octave; arbitrary order inside a bucket).
+int launch_order_by_cost(const int32_t* cnt, int m, int32_t* order, hipStream_t s);
 
 // ASM (band-limited angular spectrum).
 struct AsmConsts {

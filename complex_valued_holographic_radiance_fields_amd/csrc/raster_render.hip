@@ -254,7 +254,16 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   __shared__ int s_wmax[4];
 
   int tile, plane;
-  map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
+  if (kSub) {
+    // Longest member list first (list scheduling): the forward's per-(tile,
+    // plane) member counts order the blocks.
+    const int id = p.order[blockIdx.x];
+    if (static_cast<unsigned>(id) >= gridDim.x) return;
+    tile = id / p.P;
+    plane = id - tile * p.P;
+  } else {
+    map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
+  }
   const int tx = tile % p.gx, ty = tile / p.gx;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pxi = tx * kTile + (wave & 1) * 8 + (lane & 7);
@@ -495,6 +504,54 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   }
 }
 
+// Cost bucket of a member count: 8 buckets per octave of (c + 1).
+__device__ __forceinline__ int cost_bucket(int c) {
+  const unsigned v = static_cast<unsigned>(c < 0 ? 0 : c) + 1u;
+  const int e = 31 - __clz(v);
+  const unsigned mant = e >= 3 ? (v >> (e - 3)) & 7u : (v << (3 - e)) & 7u;
+  return e * 8 + static_cast<int>(mant);
+}
+
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBins = 256;
+
+__global__ __launch_bounds__(kOrderThreads) void k_order_by_cost(const int32_t* cnt, int m,
+                                                                 int32_t* order) {
+  __shared__ int s_bin[kOrderBins];
+  for (int i = threadIdx.x; i < kOrderBins; i += kOrderThreads) s_bin[i] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += kOrderThreads) atomicAdd(&s_bin[cost_bucket(cnt[i])], 1);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    // Exclusive scan over the bins from the highest bucket down: lane l owns
+    // bins 255-4l .. 252-4l.
+    const int lane = threadIdx.x;
+    int v[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = s_bin[kOrderBins - 1 - 4 * lane - j];
+      sum += v[j];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(inc, d, 64);
+      if (lane >= d) inc += t;
+    }
+    int run = inc - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s_bin[kOrderBins - 1 - 4 * lane - j] = run;
+      run += v[j];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += kOrderThreads) {
+    const int pos = atomicAdd(&s_bin[cost_bucket(cnt[i])], 1);
+    order[pos] = i;
+  }
+}
+
 __global__ void k_render_empty(float2* field, float* final_T, int32_t* n_contrib,
                                int64_t npix, int PC, int P) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -548,6 +605,13 @@ int launch_render_backward(const RenderParams& p, hipStream_t s) {
       set_error("render backward: channels must be 1..3 (got %d)", p.C);
       return HRF_ERR_INVALID;
   }
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_order_by_cost(const int32_t* cnt, int m, int32_t* order, hipStream_t s) {
+  if (m <= 0) return HRF_OK;
+  hipLaunchKernelGGL(k_order_by_cost, dim3(1), dim3(kOrderThreads), 0, s, cnt, m, order);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

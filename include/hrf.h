@@ -100,8 +100,9 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
 
 /* Bytes of the optional plane member lists for K pairs on a W x H image
  * with P planes: P*K (gaussian, list position) int32 pairs (plane q's list
- * of tile t starts at q*K + ranges[t][0]), then, from the next 256-byte
- * boundary, T*P int32 counts (tile-major).  hrf_raster_forward_render fills them (plane_lists non-NULL)
+ * of tile t starts at q*K + ranges[t][0]), then, each from the next
+ * 256-byte boundary, T*P int32 counts (tile-major) and the T*P (tile, plane)
+ * ids t*P + q ordered by count, largest first (the backward's block order).  hrf_raster_forward_render fills them (plane_lists non-NULL)
  * with each (tile, plane)'s members, in list order, over the entries its
  * compositing visited; hrf_raster_backward given the same buffer walks
  * those lists instead of filtering every tile list once per plane.  No
