@@ -43,8 +43,11 @@ constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
 
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
 __device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+// Twiddle product with explicit fused multiply-adds (the library is built
+// with contraction off for the bit-exact geometry code; the transforms only
+// need fp32 accuracy).
 __device__ __forceinline__ float2 cmulf(float2 a, float2 b) {
-  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+  return make_float2(fmaf(a.x, b.x, -(a.y * b.y)), fmaf(a.x, b.y, a.y * b.x));
 }
 __device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
 // multiply by -i (forward) or +i (inverse)
@@ -84,10 +87,14 @@ struct Dft<8, INV> {
     float2 o[4] = {x[1], x[3], x[5], x[7]};
     Dft<4, INV>::run(e);
     Dft<4, INV>::run(o);
+    // o1 * e^{-/+ i pi/4} and o3 * e^{-/+ 3i pi/4}: two adds and two
+    // multiplies each.
     constexpr float c = 0.70710678118654752f;
-    const float sg = INV ? 1.0f : -1.0f;
-    const float2 w1 = make_float2(c, sg * c), w3 = make_float2(-c, sg * c);
-    const float2 o1 = cmulf(o[1], w1), o2 = mul_mi<INV>(o[2]), o3 = cmulf(o[3], w3);
+    const float2 o1 = INV ? make_float2((o[1].x - o[1].y) * c, (o[1].x + o[1].y) * c)
+                          : make_float2((o[1].x + o[1].y) * c, (o[1].y - o[1].x) * c);
+    const float2 o3 = INV ? make_float2(-(o[3].x + o[3].y) * c, (o[3].x - o[3].y) * c)
+                          : make_float2((o[3].y - o[3].x) * c, -(o[3].x + o[3].y) * c);
+    const float2 o2 = mul_mi<INV>(o[2]);
     x[0] = cadd(e[0], o[0]);
     x[4] = csub(e[0], o[0]);
     x[1] = cadd(e[1], o1);

@@ -97,14 +97,13 @@ struct GeomWs {
   uint32_t* dkey_b;
   uint32_t* order;
   uint32_t* order_b;
-  uint32_t* cnt;
   uint64_t* off;  // n + 1
   uint32_t* vis;
   uint32_t* vis_off;
   uint64_t* scan64;
   uint32_t* scan32;
   uint32_t* radix;
-  uint64_t* totals;  // [K, V]
+  uint64_t* totals;  // [K, V, unsorted-depth flag]
   uint32_t* sort_flag;
 };
 
@@ -119,7 +118,6 @@ GeomWs carve_geom(Carver& cv, int64_t n, int C) {
   w.dkey_b = cv.take<uint32_t>(m);
   w.order = cv.take<uint32_t>(m);
   w.order_b = cv.take<uint32_t>(m);
-  w.cnt = cv.take<uint32_t>(m);
   w.off = cv.take<uint64_t>(m + 1);
   w.vis = cv.take<uint32_t>(m);
   w.vis_off = cv.take<uint32_t>(m);
@@ -216,17 +214,6 @@ ProjectParams project_params(const hrf_gaussians* g, const hrf_camera* cam, cons
   p.near_plane = cam->near_plane;
   p.far_plane = cam->far_plane;
   return p;
-}
-
-__global__ void k_totals(const uint64_t* off, const uint32_t* cnt, const uint32_t* vis_off,
-                         const uint32_t* vis, int64_t n, uint64_t* off_end,
-                         uint64_t* totals) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    const uint64_t k = off[n - 1] + cnt[n - 1];
-    off_end[0] = k;
-    totals[0] = k;
-    totals[1] = static_cast<uint64_t>(vis_off[n - 1]) + vis[n - 1];
-  }
 }
 
 int bits_for(int ntiles) {
@@ -341,39 +328,39 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
     HRF_TRY(launch_project(pp, s));
   }
 
-  // Stable depth ordering of the Gaussians (32-bit keys, 4 passes: the
-  // sorted order ends in the first buffer pair).
-  {
-    // The reference's caller hands Gaussians over already sorted by depth
-    // (Scene.render, model.py:1387); k_project flags any key below its
-    // predecessor's, and without that flag every pass (histograms, scans,
-    // scatters) skips itself on the device and the order stays the
-    // identity (a stable sort of sorted keys).
-    HRF_STAGE("depth_sort", s);
-    bool in_b = false;
-    HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s,
-                             w.sort_flag, true));
-    if (in_b) {
-      set_error("internal: depth sort expected an even pass count");
-      return HRF_ERR_INVALID;
-    }
-  }
+  // Offsets in index order: K and V do not depend on the order, and the
+  // reference's caller hands Gaussians over already sorted by depth
+  // (Scene.render, model.py:1387), where index order is depth order.
   {
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_gather_counts(w.order, w.sort_flag, w.tiles, w.cnt, n, s));
-    HRF_TRY(scan_exclusive_u64(w.cnt, w.off, n, w.scan64, s));
-    HRF_TRY(scan_exclusive_u32(w.vis, w.vis_off, n, w.scan32, s));
-    hipLaunchKernelGGL(k_totals, dim3(1), dim3(64), 0, s, w.off, w.cnt, w.vis_off, w.vis, n,
-                       w.off + n, w.totals);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(launch_offsets(nullptr, w.tiles, w.vis, n, w.off, w.vis_off, w.scan64, w.scan32,
+                           w.sort_flag, w.totals, s));
   }
-  uint64_t host_tot[2] = {0, 0};
+  uint64_t host_tot[3] = {0, 0, 0};
   HRF_HIP(hipMemcpyAsync(host_tot, w.totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
   HRF_HIP(hipStreamSynchronize(s));
   if (host_tot[0] > 0x7FFFFFFFull) {
     set_error("pair count %llu exceeds the int32 point_list/ranges format",
               static_cast<unsigned long long>(host_tot[0]));
     return HRF_ERR_OVERFLOW;
+  }
+  if (host_tot[2] != 0) {
+    // k_project found a depth key below its predecessor's: stable depth
+    // ordering of the Gaussians (32-bit keys, 4 passes: the sorted order
+    // ends in the first buffer pair), then the pair offsets in that order.
+    {
+      HRF_STAGE("depth_sort", s);
+      bool in_b = false;
+      HRF_TRY(radix_sort_pairs(w.dkey, w.order, w.dkey_b, w.order_b, n, 32, w.radix, &in_b, s,
+                               nullptr, true));
+      if (in_b) {
+        set_error("internal: depth sort expected an even pass count");
+        return HRF_ERR_INVALID;
+      }
+    }
+    HRF_STAGE("scan", s);
+    HRF_TRY(launch_offsets(w.order, w.tiles, w.vis, n, w.off, w.vis_off, w.scan64, w.scan32,
+                           w.sort_flag, w.totals, s));
   }
   *num_pairs = static_cast<int64_t>(host_tot[0]);
   *num_visible = static_cast<int64_t>(host_tot[1]);

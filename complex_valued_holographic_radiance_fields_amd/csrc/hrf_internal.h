@@ -169,12 +169,8 @@ struct GeomBwdParams {
 };
 int launch_geom_backward(const GeomBwdParams& p, hipStream_t s);
 
-// Scans (exclusive).  Scratch sizing: scan_scratch_elems(n).
+// Scan scratch sizing (block-sum pyramid of an n-element scan).
 size_t scan_scratch_elems(int64_t n);
-int scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n,
-                       uint32_t* scratch, hipStream_t s);
-int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n,
-                       uint64_t* scratch, hipStream_t s);
 
 // Stable LSD radix sort of (u32 key, u32 value) pairs over bits
 // [0, end_bit).  Ping-pongs between (ka,va) and (kb,vb); returns in
@@ -195,10 +191,16 @@ int radix_passes(int end_bit);
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s);
 
-// The depth-order permutation is order[] when *sorted_flag != 0 and the
-// identity otherwise.
-int launch_gather_counts(const uint32_t* order, const uint32_t* sorted_flag,
-                         const uint32_t* tiles, uint32_t* cnt, int64_t n, hipStream_t s);
+// Exclusive pair offsets off[0..n] (off[n] = K) of the tile counts taken in
+// depth-rank order (tiles[order[i]]; order == nullptr: index order) and
+// exclusive visible offsets vis_off (index order); totals receives
+// [K, V, *sort_flag].  bsum_p / bsum_v: ceil(n / 2048) elements each.
+int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t* vis,
+                   int64_t n, uint64_t* off, uint32_t* vis_off, uint64_t* bsum_p,
+                   uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
+                   hipStream_t s);
+// The depth-order permutation used by the emit kernels is order[] when
+// *sorted_flag != 0 and the identity otherwise.
 int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
                       const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
                       uint32_t* vals, hipStream_t s);

@@ -230,12 +230,154 @@ __device__ __forceinline__ uint32_t ordered(const uint32_t* order, const uint32_
   return *sorted_flag ? order[i] : static_cast<uint32_t>(i);
 }
 
-__global__ void k_gather_counts(const uint32_t* __restrict__ order,
-                                const uint32_t* __restrict__ sorted_flag,
-                                const uint32_t* __restrict__ tiles,
-                                uint32_t* __restrict__ cnt, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) cnt[i] = tiles[ordered(order, sorted_flag, i)];
+// Pair and visible offsets (three launches for both scans).  Pair counts
+// are taken in depth-rank order (tiles[order[i]], or tiles[i] with no
+// order), visibility flags in index order.
+//   k_offsets_reduce: per-block sums of both arrays;
+//   k_offsets_blocks: one block scans the block sums in place (exclusive) and
+//     writes the totals [K, V, *sort_flag] and off[n] = K;
+//   k_offsets_scan: per-block exclusive scans plus the block prefixes.
+__device__ __forceinline__ void load_counts(const uint32_t* __restrict__ order,
+                                            const uint32_t* __restrict__ tiles,
+                                            const uint32_t* __restrict__ vis, int64_t n,
+                                            int64_t base, uint32_t (&t)[kScanItems],
+                                            uint32_t (&v)[kScanItems]) {
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    const int64_t idx = base + i;
+    t[i] = 0u;
+    v[i] = 0u;
+    if (idx < n) {
+      t[i] = tiles[order ? order[idx] : static_cast<uint32_t>(idx)];
+      v[i] = vis[idx];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_offsets_reduce(
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ tiles,
+    const uint32_t* __restrict__ vis, int64_t n, uint64_t* __restrict__ bsum_p,
+    uint32_t* __restrict__ bsum_v) {
+  __shared__ uint64_t s_p[kScanThreads / 64];
+  __shared__ uint32_t s_v[kScanThreads / 64];
+  uint32_t t[kScanItems], v[kScanItems];
+  load_counts(order, tiles, vis, n,
+              static_cast<int64_t>(blockIdx.x) * kScanTile +
+                  static_cast<int64_t>(threadIdx.x) * kScanItems,
+              t, v);
+  uint64_t sp = 0;
+  uint32_t sv = 0;
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    sp += t[i];
+    sv += v[i];
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    sp += __shfl_xor(sp, d, 64);
+    sv += __shfl_xor(sv, d, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_p[wave] = sp;
+    s_v[wave] = sv;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t a = 0;
+    uint32_t b = 0;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+      a += s_p[w];
+      b += s_v[w];
+    }
+    bsum_p[blockIdx.x] = a;
+    bsum_v[blockIdx.x] = b;
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_offsets_blocks(
+    uint64_t* __restrict__ bsum_p, uint32_t* __restrict__ bsum_v, int64_t nb,
+    uint64_t* __restrict__ off_end, const uint32_t* __restrict__ sort_flag,
+    uint64_t* __restrict__ totals) {
+  __shared__ uint64_t s_wp[kScanThreads / 64];
+  __shared__ uint32_t s_wv[kScanThreads / 64];
+  uint64_t carry_p = 0;
+  uint32_t carry_v = 0;
+  for (int64_t base = 0; base < nb; base += kScanTile) {
+    const int64_t b0 = base + static_cast<int64_t>(threadIdx.x) * kScanItems;
+    uint64_t p[kScanItems];
+    uint32_t v[kScanItems];
+    uint64_t rp = 0;
+    uint32_t rv = 0;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+      const int64_t idx = b0 + i;
+      const uint64_t xp = idx < nb ? bsum_p[idx] : 0ull;
+      const uint32_t xv = idx < nb ? bsum_v[idx] : 0u;
+      p[i] = rp;
+      v[i] = rv;
+      rp += xp;
+      rv += xv;
+    }
+    uint64_t tp;
+    uint32_t tv;
+    const uint64_t op = block_exclusive_scan<uint64_t>(rp, &tp, s_wp);
+    const uint32_t ov = block_exclusive_scan<uint32_t>(rv, &tv, s_wv);
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+      const int64_t idx = b0 + i;
+      if (idx < nb) {
+        bsum_p[idx] = carry_p + op + p[i];
+        bsum_v[idx] = carry_v + ov + v[i];
+      }
+    }
+    carry_p += tp;
+    carry_v += tv;
+    __syncthreads();  // s_wp / s_wv are reused by the next chunk
+  }
+  if (threadIdx.x == 0) {
+    off_end[0] = carry_p;
+    totals[0] = carry_p;
+    totals[1] = carry_v;
+    totals[2] = *sort_flag;
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ tiles,
+    const uint32_t* __restrict__ vis, int64_t n, const uint64_t* __restrict__ bsum_p,
+    const uint32_t* __restrict__ bsum_v, uint64_t* __restrict__ off,
+    uint32_t* __restrict__ vis_off) {
+  __shared__ uint64_t s_wp[kScanThreads / 64];
+  __shared__ uint32_t s_wv[kScanThreads / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+                       static_cast<int64_t>(threadIdx.x) * kScanItems;
+  uint32_t t[kScanItems], v[kScanItems];
+  load_counts(order, tiles, vis, n, base, t, v);
+  uint64_t p[kScanItems];
+  uint32_t q[kScanItems];
+  uint64_t rp = 0;
+  uint32_t rv = 0;
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    p[i] = rp;
+    q[i] = rv;
+    rp += t[i];
+    rv += v[i];
+  }
+  uint64_t tp;
+  uint32_t tv;
+  const uint64_t op = block_exclusive_scan<uint64_t>(rp, &tp, s_wp) + bsum_p[blockIdx.x];
+  const uint32_t ov = block_exclusive_scan<uint32_t>(rv, &tv, s_wv) + bsum_v[blockIdx.x];
+#pragma unroll
+  for (int i = 0; i < kScanItems; ++i) {
+    const int64_t idx = base + i;
+    if (idx < n) {
+      off[idx] = op + p[i];
+      vis_off[idx] = ov + q[i];
+    }
+  }
 }
 
 // Pair emission.  A block owns 256 consecutive ranks; it stages their
@@ -369,15 +511,6 @@ size_t scan_scratch_elems(int64_t n) {
   return total + 4;
 }
 
-int scan_exclusive_u32(const uint32_t* in, uint32_t* out, int64_t n, uint32_t* scratch,
-                       hipStream_t s) {
-  return scan_exclusive<uint32_t, uint32_t>(in, out, n, scratch, s);
-}
-
-int scan_exclusive_u64(const uint32_t* in, uint64_t* out, int64_t n, uint64_t* scratch,
-                       hipStream_t s) {
-  return scan_exclusive<uint32_t, uint64_t>(in, out, n, scratch, s);
-}
 
 int radix_passes(int end_bit) { return (end_bit + 7) / 8; }
 
@@ -504,11 +637,20 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
   return HRF_OK;
 }
 
-int launch_gather_counts(const uint32_t* order, const uint32_t* sorted_flag,
-                         const uint32_t* tiles, uint32_t* cnt, int64_t n, hipStream_t s) {
+int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t* vis,
+                   int64_t n, uint64_t* off, uint32_t* vis_off, uint64_t* bsum_p,
+                   uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
+                   hipStream_t s) {
   if (n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_gather_counts, dim3(blocks_for(n, 256)), dim3(256), 0, s, order,
-                     sorted_flag, tiles, cnt, n);
+  const int64_t nb = (n + kScanTile - 1) / kScanTile;
+  hipLaunchKernelGGL(k_offsets_reduce, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0,
+                     s, order, tiles, vis, n, bsum_p, bsum_v);
+  HRF_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_offsets_blocks, dim3(1), dim3(kScanThreads), 0, s, bsum_p, bsum_v, nb,
+                     off + n, sort_flag, totals);
+  HRF_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_offsets_scan, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, s,
+                     order, tiles, vis, n, bsum_p, bsum_v, off, vis_off);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
