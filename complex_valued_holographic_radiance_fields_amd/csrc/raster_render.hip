@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
           acc[2 * c] = fmaf(sT, amp[2 * c], acc[2 * c]);
           acc[2 * c + 1] = fmaf(sT, amp[2 * c + 1], acc[2 * c + 1]);
         }
-        T = T * (1.0f - alpha);
+        T = T - sT;  // T (1 - alpha), reusing alpha T
         last = ok ? __float_as_int(b.w) : last;
         done = done || (ok && T < kTermT);
       }
