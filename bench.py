@@ -102,6 +102,77 @@ def algorithmic_bytes(N, K, P, C, W, H, S, T):
                 per_launch=per_launch)
 
 
+def measure_preprocess(spec, dev, no_cpu):
+    """The fused Scene.render glue (hrf_preprocess_*) on the same scene as
+    model parameters: forward (selection + gathers + activations) and
+    backward, timed with hipEvents; not part of the frame (the metric starts
+    at the rasterizer's inputs).  Compulsory bytes: forward reads the means
+    (12 B per Gaussian) and the selected rows' parameters and writes the
+    rasterizer inputs; backward reads the output gradients and the selected
+    parameters and writes the N parameter-gradient rows."""
+    import numpy as np
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import preprocess, scenes
+
+    p = scenes.generate_params(spec)
+    keys = ("means", "pre_quats", "pre_scales", "colours", "pre_phase", "pre_opac", "pre_plane")
+    t = {k: torch.from_numpy(np.ascontiguousarray(p[k])).to(dev) for k in keys + ("R", "T")}
+    args = [t[k] for k in keys]
+    N, C, P = p["means"].shape[0], p["colours"].shape[1], p["pre_plane"].shape[1]
+
+    def fwd():
+        return preprocess.forward(*args, t["R"], t["T"], scenes.NEAR, scenes.FAR)
+
+    out = fwd()
+    M = int(out[-1].numel())
+    grads = [torch.ones_like(o) for o in out[:-1]]
+
+    def bwd(o):
+        return preprocess.backward(grads, *args, t["R"], o[-1])
+
+    for _ in range(3):
+        bwd(fwd())
+    torch.cuda.synchronize()
+    reps = 20
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    f_ms, b_ms = [], []
+    for _ in range(reps):
+        ev[0].record()
+        o = fwd()
+        ev[1].record()
+        bwd(o)
+        ev[2].record()
+        torch.cuda.synchronize()
+        f_ms.append(ev[0].elapsed_time(ev[1]))
+        b_ms.append(ev[1].elapsed_time(ev[2]))
+    f_ms, b_ms = float(np.median(f_ms)), float(np.median(b_ms))
+    row_in = 16 + 12 + 8 * C + 4 + 4 * P + 12        # selected parameter row read
+    row_out = 12 + 4 + 16 + 12 + 8 * C + 4 + 4 * P + 8  # rasterizer inputs + idx written
+    fwd_b = 12 * N + M * (row_in + row_out)
+    bwd_b = M * (row_out + 16 + 12 + 4 + 4 * P) + N * (12 + 16 + 12 + 8 * C + 4 + 4 * P)
+    ach = (fwd_b + bwd_b) / ((f_ms + b_ms) * 1e-3) / 1e9
+    res = {"workload": f"{spec.name} parameters: {N} Gaussians, {M} selected",
+           "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+           "timing": f"median of {reps} (forward includes its count read-back)",
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                        "alg_bytes": int(fwd_b + bwd_b)},
+           "cpu_torch": None}
+    if not no_cpu:
+        try:
+            from oracle import cpu_baseline
+
+            cf, cb = cpu_baseline.time_preprocess(p)
+            res["cpu_torch"] = {"fwd_ms": round(cf, 1), "bwd_ms": round(cb, 1),
+                                "cores": torch.get_num_threads(),
+                                "kind": "reference op sequence on CPU torch "
+                                        "(oracle/cpu_baseline.py), full N, best of 2"}
+        except Exception as e:  # reported, never fatal to the GPU measurement
+            res["cpu_torch"] = {"failed": repr(e)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -236,6 +307,8 @@ def main():
                 "avg_launch_ms": round(dom_live, 4),
                 "bytes_per_launch": int(B["per_launch"][dom]), "traffic_source": src}
 
+    pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
+
     cpu = None
     if not args.no_cpu_baseline:
         try:
@@ -281,6 +354,7 @@ def main():
         "stages_from": f"stage-traced pass of {prof_steps} frames",
         "roofline": roof,
         "cpu_baseline": cpu,
+        "preprocess": pre,
     }
     print(json.dumps(out), flush=True)
 

@@ -40,6 +40,27 @@ class HrfCamera(ctypes.Structure):
     ]
 
 
+class HrfSceneParams(ctypes.Structure):
+    _fields_ = [
+        ("means", ctypes.c_void_p), ("pre_quats", ctypes.c_void_p),
+        ("pre_scales", ctypes.c_void_p), ("colours", ctypes.c_void_p),
+        ("pre_phase", ctypes.c_void_p), ("pre_opacities", ctypes.c_void_p),
+        ("pre_plane", ctypes.c_void_p), ("n", ctypes.c_int64), ("channels", ctypes.c_int32),
+        ("planes", ctypes.c_int32),
+    ]
+
+
+class HrfSelectedGrads(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in
+                ("cam", "z", "quats", "scales", "colours", "phase", "opacities", "plane_probs")]
+
+
+class HrfParamGrads(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in
+                ("means", "pre_quats", "pre_scales", "colours", "pre_phase", "pre_opacities",
+                 "pre_plane")]
+
+
 _P = ctypes.POINTER
 # name -> (restype, argtypes); exactly the entry points of include/hrf.h.
 SIGNATURES = {
@@ -57,6 +78,13 @@ SIGNATURES = {
     "hrf_raster_backward": (ctypes.c_int, [
         _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp, _sz,
         _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hrf_preprocess_workspace_size": (_sz, [_i64]),
+    "hrf_preprocess_select": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _f32, _f32, _vp, _sz,
+                                             _vp, _P(_i64)]),
+    "hrf_preprocess_forward": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _vp, _sz, _i64,
+                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hrf_preprocess_backward": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _i64,
+                                               _P(HrfSelectedGrads), _P(HrfParamGrads), _vp]),
     "hrf_cov3d_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "hrf_cov3d_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "hrf_jacobian_forward": (ctypes.c_int, [_vp, _i64, _f32, _f32, _i32, _i32, _f32, _f32,

@@ -38,6 +38,7 @@ SOURCES = [
     "asm_prop.hip",
     "asm_fft.hip",
     "hrf_capi.hip",
+    "preprocess.hip",
     "hrf_trace.hip",
 ]
 

@@ -1,0 +1,385 @@
+// preprocess.hip — the caller-side glue of Scene.render ahead of the
+// rasterizer, fused: world -> camera transform, near/far + z >= 0 filter,
+// ascending depth order, the gathers and the parameter activations, and the
+// backward of all of it (scatter back to the N parameter rows).
+//
+// Reference: Scene.render (model.py:1365-1402), compute_depth_values
+// (model.py:1105-1112), get_idxs_to_filter_and_sort (model.py:1121-1125),
+// Gaussians.apply_activations (model.py:594-608), STEFunction
+// (model.py:41-56), and the transform in Scene.splat (model.py:1161-1162).
+// The reference runs ~15 torch ops and a global torch.sort; here the
+// selection is one transform kernel, the flag scan shared with the binning,
+// one compaction, a stable 32-bit radix sort of the selected depth keys, and
+// one gather kernel that applies every activation.
+#include <cmath>
+
+#include "hrf_internal.h"
+
+namespace hrf {
+namespace {
+
+constexpr int kPreThreads = 256;
+
+struct View {
+  float r[9];  // R row-major: cam_j = sum_i m_i R[i][j] + T[j]
+  float t[3];
+};
+
+__device__ __forceinline__ View load_view(const float* __restrict__ R,
+                                          const float* __restrict__ T) {
+  View v;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) v.r[i] = R[i];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) v.t[i] = T[i];
+  return v;
+}
+
+// X_cam = X_world @ R + T, left to right without contraction
+// (model.py:1110: means_3D @ R + T; pytorch3d's world-to-view transform of
+// Scene.splat computes the same product).
+__device__ __forceinline__ void to_camera(const View& v, float m0, float m1, float m2,
+                                          float* c) {
+#pragma unroll
+  for (int j = 0; j < 3; ++j) c[j] = m0 * v.r[j] + m1 * v.r[3 + j] + m2 * v.r[6 + j] + v.t[j];
+}
+
+// Selection flag and depth sort key of every Gaussian: kept when
+// near < z < far (model.py:1382-1385) and z >= 0 (model.py:1123); the key
+// orders non-negative floats (-0 counts as 0).
+__global__ __launch_bounds__(kPreThreads) void k_pre_select(
+    const float* __restrict__ means, int64_t n, const float* __restrict__ R,
+    const float* __restrict__ T, float near_plane, float far_plane,
+    uint32_t* __restrict__ flag, uint32_t* __restrict__ key) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= n) return;
+  const View v = load_view(R, T);
+  float c[3];
+  to_camera(v, means[3 * g], means[3 * g + 1], means[3 * g + 2], c);
+  const float z = c[2];
+  const bool keep = z > near_plane && z < far_plane && z >= 0.0f;
+  flag[g] = keep ? 1u : 0u;
+  key[g] = __float_as_uint(z) & 0x7FFFFFFFu;
+}
+
+__global__ __launch_bounds__(kPreThreads) void k_pre_compact(
+    const uint32_t* __restrict__ flag, const uint32_t* __restrict__ pos,
+    const uint32_t* __restrict__ key, int64_t n, uint32_t* __restrict__ ckey,
+    uint32_t* __restrict__ cidx) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= n || !flag[g]) return;
+  const uint32_t p = pos[g];
+  ckey[p] = key[g];
+  cidx[p] = static_cast<uint32_t>(g);
+}
+
+// torch.remainder(x, 2*pi) with the divisor as float32: fmod (exact), then
+// the sign of the divisor (model.py:602).
+__device__ __forceinline__ float remainder_2pi(float x) {
+  const float b = 6.28318530717958647692f;
+  float r = fmodf(x, b);
+  if (r != 0.0f && (r < 0.0f) != (b < 0.0f)) r += b;
+  return r;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Gather + activations for the m selected Gaussians in depth order.
+__global__ __launch_bounds__(kPreThreads) void k_pre_gather(
+    hrf_scene_params sp, const float* __restrict__ R, const float* __restrict__ T,
+    const uint32_t* __restrict__ sidx, int64_t m, float* __restrict__ cam,
+    float* __restrict__ zv, float* __restrict__ quats, float* __restrict__ scales,
+    float* __restrict__ colours, float* __restrict__ phase, float* __restrict__ opac,
+    float* __restrict__ pprobs, int64_t* __restrict__ idxs) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const int64_t g = sidx[i];
+  const int C = sp.channels, P = sp.planes;
+  const View v = load_view(R, T);
+  float c[3];
+  to_camera(v, sp.means[3 * g], sp.means[3 * g + 1], sp.means[3 * g + 2], c);
+  cam[3 * i] = c[0];
+  cam[3 * i + 1] = c[1];
+  cam[3 * i + 2] = c[2];
+  zv[i] = c[2];
+  // F.normalize(q, dim=1): q / max(||q||_2, 1e-12)
+  const float q0 = sp.pre_quats[4 * g], q1 = sp.pre_quats[4 * g + 1];
+  const float q2 = sp.pre_quats[4 * g + 2], q3 = sp.pre_quats[4 * g + 3];
+  const float nrm = fmaxf(sqrtf(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3), 1e-12f);
+  quats[4 * i] = q0 / nrm;
+  quats[4 * i + 1] = q1 / nrm;
+  quats[4 * i + 2] = q2 / nrm;
+  quats[4 * i + 3] = q3 / nrm;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) scales[3 * i + j] = expf(sp.pre_scales[3 * g + j]);
+  for (int j = 0; j < C; ++j) {
+    colours[i * C + j] = sp.colours[g * C + j];
+    phase[i * C + j] = remainder_2pi(sp.pre_phase[g * C + j]);
+  }
+  opac[i] = sigmoidf_(sp.pre_opacities[g]);
+  // one_hot(argmax): first maximal entry, NaN counting as the maximum.
+  int best = 0;
+  float bv = sp.pre_plane[g * P];
+  for (int p = 1; p < P; ++p) {
+    const float x = sp.pre_plane[g * P + p];
+    if (!(bv != bv) && (x > bv || x != x)) {
+      bv = x;
+      best = p;
+    }
+  }
+  for (int p = 0; p < P; ++p) pprobs[i * P + p] = p == best ? 1.0f : 0.0f;
+  idxs[i] = g;
+}
+
+// Backward of the gather + activations, scattered to parameter rows.
+// Rows that were not selected are zeroed by k_pre_zero first.
+__global__ __launch_bounds__(kPreThreads) void k_pre_zero(hrf_param_grads d, int64_t n, int C,
+                                                          int P) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= n) return;
+  for (int j = 0; j < 3; ++j) {
+    d.means[3 * g + j] = 0.0f;
+    d.pre_scales[3 * g + j] = 0.0f;
+  }
+  for (int j = 0; j < 4; ++j) d.pre_quats[4 * g + j] = 0.0f;
+  for (int j = 0; j < C; ++j) {
+    d.colours[g * C + j] = 0.0f;
+    d.pre_phase[g * C + j] = 0.0f;
+  }
+  d.pre_opacities[g] = 0.0f;
+  for (int p = 0; p < P; ++p) d.pre_plane[g * P + p] = 0.0f;
+}
+
+__global__ __launch_bounds__(kPreThreads) void k_pre_backward(
+    hrf_scene_params sp, const float* __restrict__ R, const int64_t* __restrict__ idxs,
+    int64_t m, hrf_selected_grads gin, hrf_param_grads d) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const int64_t g = idxs[i];
+  if (g < 0 || g >= sp.n) return;
+  const int C = sp.channels, P = sp.planes;
+  // cam = m @ R + T and z = cam.z: d m_k = sum_j g_cam_j R[k][j] + g_z R[k][2]
+  const float gc0 = gin.cam[3 * i], gc1 = gin.cam[3 * i + 1];
+  const float gc2 = gin.cam[3 * i + 2] + (gin.z ? gin.z[i] : 0.0f);
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    d.means[3 * g + k] = gc0 * R[3 * k] + gc1 * R[3 * k + 1] + gc2 * R[3 * k + 2];
+  // normalize: dq = (g - y (y . g)) / n for n > eps, g / eps otherwise
+  const float q0 = sp.pre_quats[4 * g], q1 = sp.pre_quats[4 * g + 1];
+  const float q2 = sp.pre_quats[4 * g + 2], q3 = sp.pre_quats[4 * g + 3];
+  const float raw = sqrtf(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+  const float gq[4] = {gin.quats[4 * i], gin.quats[4 * i + 1], gin.quats[4 * i + 2],
+                       gin.quats[4 * i + 3]};
+  if (raw > 1e-12f) {
+    const float y[4] = {q0 / raw, q1 / raw, q2 / raw, q3 / raw};
+    const float dot = y[0] * gq[0] + y[1] * gq[1] + y[2] * gq[2] + y[3] * gq[3];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d.pre_quats[4 * g + j] = (gq[j] - y[j] * dot) / raw;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d.pre_quats[4 * g + j] = gq[j] / 1e-12f;
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    d.pre_scales[3 * g + j] = gin.scales[3 * i + j] * expf(sp.pre_scales[3 * g + j]);
+  for (int j = 0; j < C; ++j) {
+    d.colours[g * C + j] = gin.colours[i * C + j];
+    d.pre_phase[g * C + j] = gin.phase[i * C + j];
+  }
+  const float s = sigmoidf_(sp.pre_opacities[g]);
+  d.pre_opacities[g] = gin.opacities[i] * (s * (1.0f - s));
+  // STEFunction.backward: grad * softmax(x / 0.001) (model.py:50-56)
+  float mx = -INFINITY;
+  for (int p = 0; p < P; ++p) mx = fmaxf(mx, sp.pre_plane[g * P + p] / 0.001f);
+  float den = 0.0f;
+  for (int p = 0; p < P; ++p) den += expf(sp.pre_plane[g * P + p] / 0.001f - mx);
+  for (int p = 0; p < P; ++p) {
+    const float sm = expf(sp.pre_plane[g * P + p] / 0.001f - mx) / den;
+    d.pre_plane[g * P + p] = gin.plane_probs[i * P + p] * sm;
+  }
+}
+
+struct PreWs {
+  uint32_t* flag;
+  uint32_t* pos;
+  uint32_t* key;
+  uint32_t* ckey;
+  uint32_t* cidx;
+  uint32_t* ckey_b;
+  uint32_t* cidx_b;
+  uint64_t* off;
+  uint64_t* bsum_p;
+  uint32_t* bsum_v;
+  uint64_t* totals;
+  uint32_t* zero;
+  uint32_t* radix;
+};
+
+PreWs carve_pre(Carver& cv, int64_t n) {
+  PreWs w;
+  const int64_t m = n > 0 ? n : 1;
+  w.flag = cv.take<uint32_t>(m);
+  w.pos = cv.take<uint32_t>(m);
+  w.key = cv.take<uint32_t>(m);
+  w.ckey = cv.take<uint32_t>(m);
+  w.cidx = cv.take<uint32_t>(m);
+  w.ckey_b = cv.take<uint32_t>(m);
+  w.cidx_b = cv.take<uint32_t>(m);
+  w.off = cv.take<uint64_t>(m + 1);
+  w.bsum_p = cv.take<uint64_t>(scan_scratch_elems(m));
+  w.bsum_v = cv.take<uint32_t>(scan_scratch_elems(m));
+  w.totals = cv.take<uint64_t>(4);
+  w.zero = cv.take<uint32_t>(4);
+  w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
+  return w;
+}
+
+int check_params(const hrf_scene_params* sp) {
+  if (!sp || sp->n < 0 || sp->channels < 1 || sp->planes < 1 || sp->planes > kMaxPlanes) {
+    set_error("preprocess: invalid parameters (need n >= 0, channels >= 1, planes 1..%d)",
+              kMaxPlanes);
+    return HRF_ERR_INVALID;
+  }
+  if (sp->n > 0 && (!sp->means || !sp->pre_quats || !sp->pre_scales || !sp->colours ||
+                    !sp->pre_phase || !sp->pre_opacities || !sp->pre_plane)) {
+    set_error("preprocess: null parameter pointer");
+    return HRF_ERR_INVALID;
+  }
+  if (sp->n > 0x7FFFFFFFLL) {
+    set_error("preprocess: %lld Gaussians exceed the 32-bit index range",
+              static_cast<long long>(sp->n));
+    return HRF_ERR_INVALID;
+  }
+  return HRF_OK;
+}
+
+}  // namespace
+}  // namespace hrf
+
+using namespace hrf;
+
+extern "C" {
+
+size_t hrf_preprocess_workspace_size(int64_t n) {
+  Carver cv(nullptr);
+  carve_pre(cv, n);
+  return cv.bytes();
+}
+
+int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const float* T,
+                          float near_plane, float far_plane, void* ws, size_t ws_bytes,
+                          void* stream, int64_t* num_selected) {
+  HRF_TRY(check_params(sp));
+  if (!num_selected || !R || !T) {
+    set_error("preprocess: null R/T or count output");
+    return HRF_ERR_INVALID;
+  }
+  *num_selected = 0;
+  const int64_t n = sp->n;
+  if (n == 0) return HRF_OK;
+  const size_t need = hrf_preprocess_workspace_size(n);
+  if (!ws || ws_bytes < need) {
+    set_error("preprocess workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
+    return HRF_ERR_WORKSPACE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv(ws);
+  PreWs w = carve_pre(cv, n);
+  HRF_STAGE("pre_select", s);
+  HRF_TRY(launch_fill_u32(w.zero, 0u, 1, s));
+  hipLaunchKernelGGL(k_pre_select, dim3(blocks_for(n, kPreThreads)), dim3(kPreThreads), 0, s,
+                     sp->means, n, R, T, near_plane, far_plane, w.flag, w.key);
+  HRF_LAUNCH_CHECK();
+  // Exclusive positions of the kept Gaussians (the binning's offsets scan,
+  // with the flags as both of its inputs); totals[1] = kept count.
+  HRF_TRY(launch_offsets(nullptr, w.flag, w.flag, n, w.off, w.pos, w.bsum_p, w.bsum_v, w.zero,
+                         w.totals, s));
+  hipLaunchKernelGGL(k_pre_compact, dim3(blocks_for(n, kPreThreads)), dim3(kPreThreads), 0, s,
+                     w.flag, w.pos, w.key, n, w.ckey, w.cidx);
+  HRF_LAUNCH_CHECK();
+  uint64_t tot[2] = {0, 0};
+  HRF_HIP(hipMemcpyAsync(tot, w.totals, sizeof(tot), hipMemcpyDeviceToHost, s));
+  HRF_HIP(hipStreamSynchronize(s));
+  const int64_t m = static_cast<int64_t>(tot[1]);
+  if (m > 1) {
+    // Stable ascending depth order (ties keep index order); 4 passes, so
+    // the result ends in (ckey, cidx).
+    bool in_b = false;
+    HRF_TRY(radix_sort_pairs(w.ckey, w.cidx, w.ckey_b, w.cidx_b, m, 32, w.radix, &in_b, s));
+    if (in_b) {
+      set_error("internal: preprocess sort expected an even pass count");
+      return HRF_ERR_INVALID;
+    }
+  }
+  *num_selected = m;
+  return HRF_OK;
+}
+
+int hrf_preprocess_forward(const hrf_scene_params* sp, const float* R, const float* T,
+                           const void* ws, size_t ws_bytes, int64_t num_selected,
+                           float* cam_means, float* z_vals, float* quats, float* scales,
+                           float* colours, float* phase, float* opacities, float* plane_probs,
+                           int64_t* idxs, void* stream) {
+  HRF_TRY(check_params(sp));
+  const int64_t m = num_selected;
+  if (m < 0 || m > sp->n) {
+    set_error("preprocess: invalid selected count %lld", static_cast<long long>(m));
+    return HRF_ERR_INVALID;
+  }
+  if (m == 0) return HRF_OK;
+  if (!R || !T || !cam_means || !z_vals || !quats || !scales || !colours || !phase ||
+      !opacities || !plane_probs || !idxs) {
+    set_error("preprocess: null output pointer");
+    return HRF_ERR_INVALID;
+  }
+  const size_t need = hrf_preprocess_workspace_size(sp->n);
+  if (!ws || ws_bytes < need) {
+    set_error("preprocess workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
+    return HRF_ERR_WORKSPACE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv(const_cast<void*>(ws));
+  PreWs w = carve_pre(cv, sp->n);
+  HRF_STAGE("pre_gather", s);
+  hipLaunchKernelGGL(k_pre_gather, dim3(blocks_for(m, kPreThreads)), dim3(kPreThreads), 0, s,
+                     *sp, R, T, w.cidx, m, cam_means, z_vals, quats, scales, colours, phase,
+                     opacities, plane_probs, idxs);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int hrf_preprocess_backward(const hrf_scene_params* sp, const float* R, const int64_t* idxs,
+                            int64_t num_selected, const hrf_selected_grads* grads,
+                            const hrf_param_grads* out, void* stream) {
+  HRF_TRY(check_params(sp));
+  if (!grads || !out || !out->means || !out->pre_quats || !out->pre_scales || !out->colours ||
+      !out->pre_phase || !out->pre_opacities || !out->pre_plane) {
+    set_error("preprocess backward: null gradient pointer");
+    return HRF_ERR_INVALID;
+  }
+  const int64_t n = sp->n, m = num_selected;
+  if (m < 0 || m > n) {
+    set_error("preprocess backward: invalid selected count %lld", static_cast<long long>(m));
+    return HRF_ERR_INVALID;
+  }
+  if (n == 0) return HRF_OK;
+  if (m > 0 && (!R || !idxs || !grads->cam || !grads->quats || !grads->scales ||
+                !grads->colours || !grads->phase || !grads->opacities ||
+                !grads->plane_probs)) {
+    set_error("preprocess backward: null input pointer");
+    return HRF_ERR_INVALID;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  HRF_STAGE("pre_backward", s);
+  hipLaunchKernelGGL(k_pre_zero, dim3(blocks_for(n, kPreThreads)), dim3(kPreThreads), 0, s,
+                     *out, n, sp->channels, sp->planes);
+  HRF_LAUNCH_CHECK();
+  if (m > 0) {
+    hipLaunchKernelGGL(k_pre_backward, dim3(blocks_for(m, kPreThreads)), dim3(kPreThreads), 0,
+                       s, *sp, R, idxs, m, *grads, *out);
+    HRF_LAUNCH_CHECK();
+  }
+  return HRF_OK;
+}
+
+}  // extern "C"

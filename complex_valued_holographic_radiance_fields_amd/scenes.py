@@ -112,8 +112,9 @@ def _camera(spec: SceneSpec):
     return R, T, np.float32(f), np.float32(f), np.float32(W / 2.0), np.float32(H / 2.0)
 
 
-def generate(spec: SceneSpec, with_grad: bool = True) -> Scene:
-    rng = np.random.default_rng(1000 + spec.index)
+def _draw(spec: SceneSpec, rng):
+    """World-space means and post-activation parameters of all spec.n
+    Gaussians, drawn from rng in a fixed order."""
     n = spec.n
     W, H = spec.width, spec.height
     counts = {}
@@ -159,7 +160,17 @@ def generate(spec: SceneSpec, with_grad: bool = True) -> Scene:
     logits = rng.normal(size=(n, spec.planes)) * 10.0
     pprobs = np.eye(spec.planes, dtype=np.float32)[np.argmax(logits, axis=1)]
     opac = np.full(n, 1.0 / (1.0 + math.exp(-1.0)), np.float32)
+    return dict(means=means, ls=ls, scales=scales, quats=quats, colours=colours, phase=phase,
+                logits=logits, pprobs=pprobs, opac=opac, counts=counts)
 
+
+def generate(spec: SceneSpec, with_grad: bool = True) -> Scene:
+    rng = np.random.default_rng(1000 + spec.index)
+    n = spec.n
+    C = len(spec.wavelengths)
+    d = _draw(spec, rng)
+    means, scales, quats, colours = d["means"], d["scales"], d["quats"], d["colours"]
+    phase, pprobs, opac, counts = d["phase"], d["pprobs"], d["opac"], d["counts"]
     R, T, fx, fy, px, py = _camera(spec)
     cam = (means @ R + T).astype(np.float32)
     z = cam[:, 2].copy()
@@ -178,6 +189,30 @@ def generate(spec: SceneSpec, with_grad: bool = True) -> Scene:
         g = (rng.normal(size=(C, S, S)) + 1j * rng.normal(size=(C, S, S))) * math.sqrt(0.5)
         sc.grad_holo = g.astype(np.complex64)
     return sc
+
+
+def generate_params(spec: SceneSpec) -> dict:
+    """The same Gaussians as generate(spec), as the model's parameters before
+    Scene.render: world-space means, pre-activation quats (unnormalised),
+    log-scales, colours, phase (shifted by whole turns), opacity and
+    plane-assignment logits, all N rows unsorted, plus the camera R, T.
+    render_preprocess of these gives generate(spec)'s inputs up to rounding."""
+    rng = np.random.default_rng(1000 + spec.index)
+    n = spec.n
+    d = _draw(spec, rng)
+    R, T, _, _, _, _ = _camera(spec)
+    extra = np.random.default_rng(7000 + spec.index)
+    C = d["colours"].shape[1]
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)  # noqa: E731
+    return dict(
+        means=f32(d["means"]),
+        pre_quats=f32(d["quats"] * extra.uniform(0.5, 2.0, size=(n, 1))),
+        pre_scales=f32(d["ls"]),
+        colours=f32(d["colours"]),
+        pre_phase=f32(d["phase"] + 2.0 * math.pi * extra.integers(-2, 3, size=(n, C))),
+        pre_opac=np.ones(n, np.float32),
+        pre_plane=f32(d["logits"]),
+        R=f32(R), T=f32(T))
 
 
 def to_torch(sc: Scene, device="cuda"):

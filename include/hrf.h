@@ -270,6 +270,84 @@ int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes,
 /* Releases cached hipFFT plans and FFT twiddle tables (optional). */
 void hrf_release_caches(void);
 
+/* ---------------- render preprocess (Scene.render's glue) -----------------
+ * The caller-side steps between the model's parameters and the rasterizer
+ * (Scene.render, model.py:1365-1402; Scene.splat's world-to-view transform,
+ * model.py:1161-1162): X_cam = X_world @ R + T, keep near < z < far and
+ * z >= 0 (model.py:1382-1385,1121-1125), ascending stable depth order, the
+ * gathers, and Gaussians.apply_activations (model.py:594-608): exp(scales),
+ * F.normalize(quats), phase mod 2*pi, sigmoid(opacities), one_hot(argmax)
+ * plane probabilities (STEFunction, model.py:41-56).  The reference sorts
+ * with torch.sort (order of equal depths unspecified); here ties keep the
+ * index order. */
+typedef struct hrf_scene_params {
+  const float* means;         /* (N,3) world-space means */
+  const float* pre_quats;     /* (N,4) */
+  const float* pre_scales;    /* (N,3) log scales */
+  const float* colours;       /* (N,C) */
+  const float* pre_phase;     /* (N,C) */
+  const float* pre_opacities; /* (N) */
+  const float* pre_plane;     /* (N,P) plane-assignment logits */
+  int64_t n;
+  int32_t channels; /* C >= 1 */
+  int32_t planes;   /* P in 1..32 */
+} hrf_scene_params;
+
+/* Gradients of the M selected rows (the outputs of hrf_preprocess_forward). */
+typedef struct hrf_selected_grads {
+  const float* cam;         /* (M,3) */
+  const float* z;           /* (M), NULL = zero */
+  const float* quats;       /* (M,4) */
+  const float* scales;      /* (M,3) */
+  const float* colours;     /* (M,C) */
+  const float* phase;       /* (M,C) */
+  const float* opacities;   /* (M) */
+  const float* plane_probs; /* (M,P) */
+} hrf_selected_grads;
+
+/* Gradients of the N parameter rows; fully overwritten (rows that were not
+ * selected get zeros). */
+typedef struct hrf_param_grads {
+  float* means;
+  float* pre_quats;
+  float* pre_scales;
+  float* colours;
+  float* pre_phase;
+  float* pre_opacities;
+  float* pre_plane;
+} hrf_param_grads;
+
+/* Workspace of hrf_preprocess_select / _forward for N Gaussians; it carries
+ * the selection from one call to the next. */
+size_t hrf_preprocess_workspace_size(int64_t n);
+
+/* Camera transform, selection and depth order; returns the selected count M
+ * (one host sync, as the reference's torch.where / masked_select).  R (3,3)
+ * row-major and T (3) are device pointers (camera.R[0], camera.T[0]).
+ * Replaces model.py:1377-1388. */
+int hrf_preprocess_select(const hrf_scene_params* params, const float* R, const float* T,
+                          float near_plane, float far_plane, void* ws, size_t ws_bytes,
+                          void* stream, int64_t* num_selected);
+
+/* Gathers and activations of the M selected Gaussians, in depth order:
+ * cam_means (M,3), z_vals (M), quats (M,4), scales (M,3), colours (M,C),
+ * phase (M,C), opacities (M), plane_probs (M,P) and idxs (M) int64, the
+ * parameter row of each.  Replaces model.py:1389-1402 and 1161-1162. */
+int hrf_preprocess_forward(const hrf_scene_params* params, const float* R, const float* T,
+                           const void* ws, size_t ws_bytes, int64_t num_selected,
+                           float* cam_means, float* z_vals, float* quats, float* scales,
+                           float* colours, float* phase, float* opacities,
+                           float* plane_probs, int64_t* idxs, void* stream);
+
+/* Backward of hrf_preprocess_forward: the gradients of its outputs -> the
+ * parameter gradients (autograd of the reference's gathers and activations;
+ * the plane logits get grad * softmax(logits / 0.001), STEFunction.backward,
+ * model.py:50-56).  No workspace. */
+int hrf_preprocess_backward(const hrf_scene_params* params, const float* R,
+                            const int64_t* idxs, int64_t num_selected,
+                            const hrf_selected_grads* grads, const hrf_param_grads* out,
+                            void* stream);
+
 /* ---------------- stage tracing (no counterpart in the reference, which
  * prints per-phase CUDA event times from train.py:263-344) ---------------- */
 
@@ -288,7 +366,8 @@ void hrf_trace_reset(void);
  * Stages: project, depth_sort, scan, emit, tile_sort, ranges, render_fwd,
  * render_bwd, geom_bwd; fused propagation: asm_rows_in, asm_col_fwd,
  * asm_col_adj, asm_rows_out; hipFFT propagation: asm_pad, asm_fft,
- * asm_mac_fwd, asm_mac_adj, asm_crop. */
+ * asm_mac_fwd, asm_mac_adj, asm_crop; preprocess: pre_select, pre_gather,
+ * pre_backward. */
 int hrf_trace_read(const char* stage, int64_t* launches, double* total_ms);
 
 #ifdef __cplusplus

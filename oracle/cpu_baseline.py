@@ -202,3 +202,55 @@ def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
             f"64x64 tiles fwd+bwd (random sample, scaled by tile count) + 1 of {P * C} ASM "
             f"fwd+bwd (scaled by P*C) + projection setup; {spec.name} N={sc.cam_means.shape[0]}")
     return total_s * 1000.0, desc
+
+
+# ------------------------------------------------- render preprocess (glue)
+class _STE(torch.autograd.Function):
+    """STEFunction (model.py:41-56): one-hot forward, softmax(x/0.001) backward."""
+
+    @staticmethod
+    def forward(ctx, x):
+        ctx.save_for_backward(x)
+        return torch.nn.functional.one_hot(torch.argmax(x, dim=1), num_classes=x.size(1)).float()
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        return g * torch.nn.functional.softmax(x / 0.001, dim=1)
+
+
+def preprocess_torch(means, pq, ps, col, ph, po, pp, R, T, near=1.0, far=1000.0):
+    """Scene.render's steps before splat, as the reference runs them
+    (model.py:1377-1402, 1105-1125, 594-608; the transform of Scene.splat,
+    model.py:1161-1162), on CPU torch.  Returns the rasterizer inputs."""
+    import torch.nn.functional as F
+
+    z_all = (means @ R + T)[:, -1]
+    valid = torch.where((z_all > near) & (z_all < far))[0]
+    srt, ind = torch.sort(z_all[valid].detach())
+    idxs = valid[torch.masked_select(ind, srt >= 0)]
+    m = means[idxs]
+    cam = m @ R + T
+    return (cam, (m @ R + T)[:, -1], F.normalize(pq[idxs]), torch.exp(ps[idxs]), col[idxs],
+            ph[idxs] % (2.0 * math.pi), torch.sigmoid(po[idxs]), _STE.apply(pp[idxs]), idxs)
+
+
+def time_preprocess(params: dict, reps: int = 2):
+    """Forward + backward (sum of the outputs as the loss) of preprocess_torch
+    over the given numpy parameters; returns (fwd_ms, bwd_ms)."""
+    leaves = [torch.from_numpy(params[k].copy()).requires_grad_(True) for k in
+              ("means", "pre_quats", "pre_scales", "colours", "pre_phase", "pre_opac",
+               "pre_plane")]
+    R, T = torch.from_numpy(params["R"]), torch.from_numpy(params["T"])
+    fwd, bwd = [], []
+    for _ in range(reps):
+        for x in leaves:
+            x.grad = None
+        t0 = time.perf_counter()
+        out = preprocess_torch(*leaves, R, T)
+        t1 = time.perf_counter()
+        sum(o.sum() for o in out[:-1]).backward()
+        t2 = time.perf_counter()
+        fwd.append((t1 - t0) * 1e3)
+        bwd.append((t2 - t1) * 1e3)
+    return min(fwd), min(bwd)

@@ -428,3 +428,125 @@ def multiplane_adjoint(grad_holo, H, W, wavelengths, distances, pitch, S, apertu
             out[p, c] = asm_adjoint(grad_holo[c], H, W, wavelengths[c], pitch, distances[p], S,
                                     aperture)
     return out
+
+
+# ------------------------------------------------------- render preprocess ---
+# Scene.render's glue ahead of splat_tile_cuda (model.py:1365-1402, 1105-1125,
+# 594-608, 41-56; the world-to-view transform of Scene.splat, model.py:
+# 1161-1162), restated in numpy float32 with one rounding per operation.
+
+TWO_PI_F32 = np.float32(2.0 * np.pi)  # torch casts the Python scalar to float32
+
+
+def _camera_points(means, R, T):
+    """X @ R + T, left to right per component (model.py:1110)."""
+    m = _f32(means)
+    R = _f32(R).reshape(3, 3)
+    T = _f32(T).reshape(3)
+    out = np.empty_like(m)
+    for j in range(3):
+        out[:, j] = ((m[:, 0] * R[0, j] + m[:, 1] * R[1, j]) + m[:, 2] * R[2, j]) + T[j]
+    return out
+
+
+def _remainder_2pi(x):
+    """torch.remainder(x, 2*pi) in float32: exact fmod, then the divisor's sign
+    (model.py:602)."""
+    x = _f32(x)
+    r = np.fmod(x, TWO_PI_F32)
+    fix = (r != 0) & ((r < 0) != (TWO_PI_F32 < 0))
+    return np.where(fix, (r + TWO_PI_F32).astype(np.float32), r).astype(np.float32)
+
+
+def _normalize(q):
+    """F.normalize(q, dim=1): q / max(||q||_2, 1e-12)."""
+    q = _f32(q)
+    s = ((q[:, 0] * q[:, 0] + q[:, 1] * q[:, 1]) + q[:, 2] * q[:, 2]) + q[:, 3] * q[:, 3]
+    nrm = np.maximum(np.sqrt(s), np.float32(1e-12)).astype(np.float32)
+    return (q / nrm[:, None]).astype(np.float32), np.sqrt(s).astype(np.float32)
+
+
+def _sigmoid(x):
+    x = _f32(x)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def _one_hot_argmax(logits):
+    """one_hot(argmax(., dim=1)): first maximal entry; NaN counts as maximal."""
+    x = _f32(logits)
+    n, P = x.shape
+    best = np.zeros(n, np.int64)
+    bv = x[:, 0].copy()
+    for p in range(1, P):
+        v = x[:, p]
+        take = ~np.isnan(bv) & ((v > bv) | np.isnan(v))
+        best = np.where(take, p, best)
+        bv = np.where(take, v, bv)
+    out = np.zeros((n, P), np.float32)
+    out[np.arange(n), best] = 1.0
+    return out
+
+
+def _ste_softmax(logits):
+    """softmax(logits / 0.001, dim=1) in float32 (STEFunction.backward)."""
+    v = (_f32(logits) / np.float32(0.001)).astype(np.float32)
+    e = np.exp(v - v.max(axis=1, keepdims=True)).astype(np.float32)
+    return (e / e.sum(axis=1, dtype=np.float32, keepdims=True)).astype(np.float32)
+
+
+def preprocess_select(means, R, T, near, far):
+    """Selected parameter rows in ascending depth order (stable: equal depths
+    keep the row order)."""
+    cam = _camera_points(means, R, T)
+    z = cam[:, 2]
+    keep = np.nonzero((z > np.float32(near)) & (z < np.float32(far)) & (z >= 0))[0]
+    order = np.argsort(z[keep], kind="stable")
+    return keep[order].astype(np.int64)
+
+
+def preprocess_forward(means, pre_quats, pre_scales, colours, pre_phase, pre_opac, pre_plane,
+                       R, T, near=1.0, far=1000.0):
+    """-> dict(cam, z, quats, scales, colours, phase, opacities, plane_probs, idxs)."""
+    idx = preprocess_select(means, R, T, near, far)
+    cam = _camera_points(_f32(means)[idx], R, T)
+    q, _ = _normalize(_f32(pre_quats)[idx])
+    return dict(cam=cam, z=cam[:, 2].copy(), quats=q,
+                scales=np.exp(_f32(pre_scales)[idx]).astype(np.float32),
+                colours=_f32(colours)[idx].copy(), phase=_remainder_2pi(_f32(pre_phase)[idx]),
+                opacities=_sigmoid(_f32(pre_opac).reshape(-1)[idx]),
+                plane_probs=_one_hot_argmax(_f32(pre_plane)[idx]), idxs=idx)
+
+
+def preprocess_backward(grads, means, pre_quats, pre_scales, colours, pre_phase, pre_opac,
+                        pre_plane, R, idxs):
+    """grads: dict with keys cam, z (optional), quats, scales, colours, phase,
+    opacities, plane_probs (selected rows) -> parameter gradients (N rows)."""
+    n = _f32(means).shape[0]
+    C = _f32(colours).shape[1]
+    P = _f32(pre_plane).shape[1]
+    R = _f32(R).reshape(3, 3)
+    idx = np.asarray(idxs, np.int64)
+    out = dict(means=np.zeros((n, 3), np.float32), pre_quats=np.zeros((n, 4), np.float32),
+               pre_scales=np.zeros((n, 3), np.float32), colours=np.zeros((n, C), np.float32),
+               pre_phase=np.zeros((n, C), np.float32), pre_opac=np.zeros(n, np.float32),
+               pre_plane=np.zeros((n, P), np.float32))
+    gc = _f32(grads["cam"]).copy()
+    if grads.get("z") is not None:
+        gc[:, 2] = gc[:, 2] + _f32(grads["z"])
+    for k in range(3):
+        out["means"][idx, k] = (gc[:, 0] * R[k, 0] + gc[:, 1] * R[k, 1]) + gc[:, 2] * R[k, 2]
+    q = _f32(pre_quats)[idx]
+    y, raw = _normalize(q)
+    gq = _f32(grads["quats"])
+    dot = ((y[:, 0] * gq[:, 0] + y[:, 1] * gq[:, 1]) + y[:, 2] * gq[:, 2]) + y[:, 3] * gq[:, 3]
+    big = raw > np.float32(1e-12)
+    safe = np.where(big, raw, np.float32(1.0)).astype(np.float32)
+    dq = np.where(big[:, None], (gq - y * dot[:, None]) / safe[:, None], gq / np.float32(1e-12))
+    out["pre_quats"][idx] = dq.astype(np.float32)
+    out["pre_scales"][idx] = _f32(grads["scales"]) * np.exp(_f32(pre_scales)[idx])
+    out["colours"][idx] = _f32(grads["colours"])
+    out["pre_phase"][idx] = _f32(grads["phase"])
+    s = _sigmoid(_f32(pre_opac).reshape(-1)[idx])
+    out["pre_opac"][idx] = _f32(grads["opacities"]) * (s * (np.float32(1.0) - s))
+    out["pre_plane"][idx] = _f32(grads["plane_probs"]) * _ste_softmax(_f32(pre_plane)[idx])
+    return out

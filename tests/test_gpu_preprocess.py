@@ -1,0 +1,150 @@
+"""GPU parity of the fused render preprocess (hrf_preprocess_*, the glue of
+Scene.render ahead of the rasterizer) against the oracle.
+
+Bars: selected rows (idxs) bit-exact; camera means, z, normalised quaternions,
+colours, phase mod 2*pi and one-hot plane probabilities bit-exact (same
+operations, one rounding each, no contraction); exp / sigmoid outputs within
+2 ulp-level relative error (device expf vs numpy exp); gradients rel-L2
+< 1e-6.  Cases include a zero quaternion and one below F.normalize's eps,
+negative phases, tied plane logits, NaN logits, equal depths, rows behind
+the near plane or beyond the far plane, and an empty selection."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+KEYS = ("cam", "z", "quats", "scales", "colours", "phase", "opacities", "plane_probs")
+PNAMES = ("means", "pre_quats", "pre_scales", "colours", "pre_phase", "pre_opac", "pre_plane")
+
+
+def _params(n=5000, P=3, C=3, seed=2):
+    rng = np.random.default_rng(seed)
+    means = rng.uniform(-4, 4, size=(n, 3)).astype(np.float32)
+    means[20] = means[21]                           # equal depths
+    pq = rng.normal(size=(n, 4)).astype(np.float32)
+    pq[:3] = [[2, 0, 0, 0], [0, 0, 0, 0], [1e-14, 0, 0, 0]]
+    ps = rng.normal(-3, 1, size=(n, 3)).astype(np.float32)
+    col = rng.uniform(0, 1, size=(n, C)).astype(np.float32)
+    ph = rng.normal(0, 10, size=(n, C)).astype(np.float32)
+    po = rng.normal(0, 2, size=n).astype(np.float32)
+    pp = (rng.normal(size=(n, P)) * 10).astype(np.float32)
+    if P >= 3:
+        pp[4, :3] = [1.0, 3.0, 3.0]
+        pp[5, 0] = np.nan
+        pp[6, 1] = np.nan
+    th = 0.4
+    R = np.array([[math.cos(th), 0, math.sin(th)], [0, 1, 0], [-math.sin(th), 0, math.cos(th)]],
+                 np.float32)
+    T = np.array([0.2, -0.1, 3.0], np.float32)
+    return means, pq, ps, col, ph, po, pp, R, T
+
+
+def _t(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _run(prm, near, far):
+    from complex_valued_holographic_radiance_fields_amd import preprocess
+
+    return preprocess.forward(*[_t(a) for a in prm], near, far)
+
+
+@pytest.mark.parametrize("near,far,P,C", [(1.0, 1000.0, 3, 3), (2.5, 5.0, 2, 1), (1.0, 4.0, 5, 2)])
+def test_forward_matches_oracle(hrf, oracle_mod, near, far, P, C):
+    prm = _params(P=P, C=C, seed=P + C)
+    ref = oracle_mod.preprocess_forward(*prm, near=near, far=far)
+    out = _run(prm, near, far)
+    print(f"preprocess n={len(prm[0])} selected={len(ref['idxs'])} P={P} C={C}", flush=True)
+    np.testing.assert_array_equal(out[-1].cpu().numpy(), ref["idxs"])
+    got = dict(zip(KEYS, [o.cpu().numpy() for o in out[:-1]]))
+    for k in ("cam", "z", "quats", "colours", "phase", "plane_probs"):
+        np.testing.assert_array_equal(got[k], ref[k], err_msg=k)
+    for k in ("scales", "opacities"):
+        np.testing.assert_allclose(got[k], ref[k], rtol=3e-7, err_msg=k)
+
+
+def test_backward_matches_oracle(hrf, oracle_mod):
+    from complex_valued_holographic_radiance_fields_amd import preprocess
+
+    prm = _params(seed=11)
+    ref = oracle_mod.preprocess_forward(*prm)
+    m = len(ref["idxs"])
+    rng = np.random.default_rng(12)
+    g = {k: rng.normal(size=ref[k].shape).astype(np.float32) for k in KEYS}
+    exp = oracle_mod.preprocess_backward(g, *prm[:7], prm[7], ref["idxs"])
+    got = preprocess.backward([_t(g[k]) for k in KEYS], *[_t(a) for a in prm[:7]], _t(prm[7]),
+                              _t(ref["idxs"]))
+    print(f"preprocess backward selected={m}", flush=True)
+    for name, t in zip(PNAMES, got):
+        a = t.cpu().numpy()
+        # NaN plane logits give NaN softmax gradients on both sides (as torch)
+        np.testing.assert_array_equal(np.isnan(a), np.isnan(exp[name]), err_msg=name)
+        assert rel_l2(np.nan_to_num(a), np.nan_to_num(exp[name])) < 1e-6, name
+    rest = np.setdiff1d(np.arange(len(prm[0])), ref["idxs"])
+    assert np.all(got[0].cpu().numpy()[rest] == 0)
+
+
+def test_autograd_function(hrf):
+    """RenderPreprocess through autograd gives the direct backward."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import preprocess
+
+    prm = _params(n=800, seed=13)
+    leaves = [_t(a).requires_grad_(True) for a in prm[:7]]
+    R, T = _t(prm[7]), _t(prm[8])
+    out = preprocess.render_preprocess(*leaves, R, T, 1.0, 1000.0)
+    gs = [torch.randn_like(o) for o in out[:-1]]
+    sum((o * g).sum() for o, g in zip(out[:-1], gs)).backward()
+    direct = preprocess.backward(gs, *[x.detach() for x in leaves], R, out[-1])
+    for leaf, d in zip(leaves, direct):
+        torch.testing.assert_close(leaf.grad, d, rtol=0, atol=0, equal_nan=True)
+
+
+def test_empty_selection(hrf):
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import preprocess
+
+    prm = list(_params(n=300, seed=14))
+    prm[0] = prm[0].copy()
+    prm[0][:, 2] = -50.0  # everything lands behind the camera (z < 0)
+    R = np.eye(3, dtype=np.float32)
+    T = np.zeros(3, np.float32)
+    out = preprocess.forward(*[_t(a) for a in prm[:7]], _t(R), _t(T), 1.0, 1000.0)
+    assert all(o.shape[0] == 0 for o in out)
+    grads = preprocess.backward([None] * 8, *[_t(a) for a in prm[:7]], _t(R), out[-1])
+    assert all(float(torch.abs(g).sum()) == 0.0 for g in grads)
+
+
+def test_headline_params_reproduce_the_scene(hrf, oracle_mod):
+    """At the headline size (1M Gaussians) the preprocess of generate_params
+    gives the oracle's selection bit for bit and the scene generate() builds
+    (its numpy matmul rounds differently: compared to 1e-6)."""
+    from complex_valued_holographic_radiance_fields_amd import preprocess, scenes
+
+    spec = scenes.config("headline")
+    p = scenes.generate_params(spec)
+    prm = (p["means"], p["pre_quats"], p["pre_scales"], p["colours"], p["pre_phase"],
+           p["pre_opac"], p["pre_plane"], p["R"], p["T"])
+    out = preprocess.forward(*[_t(a) for a in prm], scenes.NEAR, scenes.FAR)
+    idx = out[-1].cpu().numpy()
+    print(f"headline preprocess selected={len(idx)}", flush=True)
+    np.testing.assert_array_equal(idx, oracle_mod.preprocess_select(p["means"], p["R"], p["T"],
+                                                                    scenes.NEAR, scenes.FAR))
+    sc = scenes.generate(spec, with_grad=False)
+    assert len(idx) == sc.cam_means.shape[0]
+    z = out[1].cpu().numpy()
+    assert np.all(np.diff(z) >= 0)
+    np.testing.assert_allclose(out[0].cpu().numpy(), sc.cam_means, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(out[2].cpu().numpy(), sc.quats, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(out[3].cpu().numpy(), sc.scales, rtol=1e-6)
+    # phases agree as angles (a value within rounding of 0 may wrap to 2*pi)
+    dphi = np.angle(np.exp(1j * (out[5].cpu().numpy().astype(np.float64) - sc.phase)))
+    assert np.abs(dphi).max() < 3e-5
+    np.testing.assert_array_equal(out[7].cpu().numpy(), sc.pprobs)
+    np.testing.assert_allclose(out[6].cpu().numpy(), sc.opac, rtol=1e-6)

@@ -661,3 +661,165 @@ def test_asm_adjoint_identity(oracle_mod):
     lhs = np.vdot(Ax, y)
     rhs = np.vdot(x, Ahy)
     assert abs(lhs - rhs) / abs(lhs) < 1e-5
+
+
+# ------------------------------------------------------- render preprocess
+# The oracle's preprocess (oracle.preprocess_*) is pinned against torch on
+# the CPU running the reference's own op sequence (model.py:1105-1112,
+# 1121-1125, 1377-1402, 594-608, 41-56: matmul + add, masks, sort, gathers,
+# F.normalize, torch.exp, torch.remainder, torch.sigmoid,
+# F.one_hot(argmax), and autograd through them with the straight-through
+# function), plus brute-force selection order and closed forms.
+
+def _pre_params(n=400, P=3, C=3, seed=2):
+    rng = np.random.default_rng(seed)
+    means = rng.uniform(-3, 3, size=(n, 3)).astype(np.float32)
+    pq = rng.normal(size=(n, 4)).astype(np.float32)
+    pq[:3] = [[2, 0, 0, 0], [0, 0, 0, 0], [1e-14, 0, 0, 0]]  # unit, zero, below eps
+    ps = rng.normal(-3, 1, size=(n, 3)).astype(np.float32)
+    col = rng.uniform(0, 1, size=(n, C)).astype(np.float32)
+    ph = rng.normal(0, 10, size=(n, C)).astype(np.float32)
+    ph[3, :] = [-1.0, 0.0, 7.0]
+    po = rng.normal(0, 2, size=n).astype(np.float32)
+    pp = (rng.normal(size=(n, P)) * 10).astype(np.float32)
+    pp[4] = [1.0, 3.0, 3.0][:P] if P == 3 else pp[4]  # tie -> first maximal index
+    th = 0.4
+    R = np.array([[math.cos(th), 0, math.sin(th)], [0, 1, 0], [-math.sin(th), 0, math.cos(th)]],
+                 np.float32)
+    T = np.array([0.2, -0.1, 3.0], np.float32)
+    return means, pq, ps, col, ph, po, pp, R, T
+
+
+def _torch_reference_preprocess(means, pq, ps, col, ph, po, pp, R, T, near, far):
+    """The reference's op sequence on CPU torch (float32), differentiable."""
+    import torch
+    import torch.nn.functional as F
+
+    class STE(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            ctx.save_for_backward(x)
+            return F.one_hot(torch.argmax(x, dim=1), num_classes=x.size(1)).float()
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            return g * F.softmax(x / 0.001, dim=1)
+
+    t = [torch.from_numpy(a.copy()).requires_grad_(True) for a in (means, pq, ps, col, ph, po,
+                                                                    pp)]
+    Rt, Tt = torch.from_numpy(R), torch.from_numpy(T)
+    with torch.no_grad():
+        z_all = (t[0] @ Rt + Tt)[:, -1]
+        valid = torch.where((z_all > near) & (z_all < far))[0]
+        srt, ind = torch.sort(z_all[valid], stable=True)
+        idxs = valid[torch.masked_select(ind, srt >= 0)]
+    m_sel = t[0][idxs]
+    cam = m_sel @ Rt + Tt
+    out = dict(cam=cam, z=(m_sel @ Rt + Tt)[:, -1], quats=F.normalize(t[1][idxs]),
+               scales=torch.exp(t[2][idxs]), colours=t[3][idxs],
+               phase=t[4][idxs] % (2.0 * math.pi), opacities=torch.sigmoid(t[5][idxs]),
+               plane_probs=STE.apply(t[6][idxs]), idxs=idxs)
+    return out, t
+
+
+def test_preprocess_forward_matches_torch_ops(oracle_mod):
+    prm = _pre_params()
+    ref, _ = _torch_reference_preprocess(*prm, 1.0, 1000.0)
+    got = oracle_mod.preprocess_forward(*prm, near=1.0, far=1000.0)
+    np.testing.assert_array_equal(got["idxs"], ref["idxs"].numpy())
+    for k in ("cam", "z", "quats", "colours", "phase", "plane_probs"):
+        np.testing.assert_allclose(got[k], ref[k].detach().numpy(), rtol=2e-7, atol=1e-7,
+                                   err_msg=k)
+    for k in ("scales", "opacities"):
+        np.testing.assert_allclose(got[k], ref[k].detach().numpy(), rtol=4e-7, err_msg=k)
+
+
+def test_preprocess_backward_matches_torch_autograd(oracle_mod):
+    import torch
+
+    prm = _pre_params(seed=5)
+    ref, leaves = _torch_reference_preprocess(*prm, 1.0, 1000.0)
+    rng = np.random.default_rng(6)
+    keys = ("cam", "z", "quats", "scales", "colours", "phase", "opacities", "plane_probs")
+    g = {k: rng.normal(size=tuple(ref[k].shape)).astype(np.float32) for k in keys}
+    loss = sum((ref[k] * torch.from_numpy(g[k])).sum() for k in keys)
+    loss.backward()
+    got = oracle_mod.preprocess_backward(g, *prm[:7], prm[7], ref["idxs"].numpy())
+    names = ("means", "pre_quats", "pre_scales", "colours", "pre_phase", "pre_opac", "pre_plane")
+    for name, leaf in zip(names, leaves):
+        assert rel_l2(got[name], leaf.grad.numpy()) < 1e-6, name
+
+
+def test_preprocess_selection_brute_force(oracle_mod):
+    prm = _pre_params(n=300, seed=8)
+    means, R, T = prm[0], prm[7], prm[8]
+    means[10] = means[11]  # equal depths keep the row order
+    z = np.array([float(np.float32(np.float32(np.float32(m[0] * R[0, 2]) + np.float32(m[1] * R[1, 2]))
+                                    + np.float32(m[2] * R[2, 2])) + T[2]) for m in means])
+    near, far = 2.0, 4.5
+    keep = [i for i in range(len(z)) if near < z[i] < far and z[i] >= 0]
+    expect = sorted(keep, key=lambda i: (z[i], i))
+    np.testing.assert_array_equal(oracle_mod.preprocess_select(means, R, T, near, far), expect)
+
+
+def test_preprocess_closed_forms(oracle_mod):
+    q, _ = oracle_mod._normalize(np.array([[2, 0, 0, 0], [0, 3, 4, 0], [0, 0, 0, 0]], np.float32))
+    f3, f4, f5 = np.float32(3), np.float32(4), np.float32(5)
+    np.testing.assert_array_equal(q, np.array([[1, 0, 0, 0], [0, f3 / f5, f4 / f5, 0],
+                                               [0, 0, 0, 0]], np.float32))
+    two_pi = np.float32(2 * math.pi)
+    np.testing.assert_array_equal(oracle_mod._remainder_2pi(np.float32([-1.0, 0.0, 7.0, -two_pi])),
+                                  np.float32([two_pi - np.float32(1.0), 0.0, 7.0 - two_pi, 0.0]))
+    np.testing.assert_array_equal(oracle_mod._sigmoid(np.float32([0.0])), [0.5])
+    np.testing.assert_array_equal(
+        oracle_mod._one_hot_argmax(np.float32([[1, 3, 3], [np.nan, 5, 1], [0, np.nan, np.nan]])),
+        [[0, 1, 0], [1, 0, 0], [0, 1, 0]])
+    # softmax(x / 0.001) of logits 0.001 apart: e^{v} / sum e^{v}, v = (0, 1, 0)
+    sm = oracle_mod._ste_softmax(np.float32([[0.0, 0.001, 0.0]]))
+    e = math.e
+    np.testing.assert_allclose(sm, [[1 / (2 + e), e / (2 + e), 1 / (2 + e)]], rtol=1e-6)
+
+
+def test_preprocess_backward_finite_differences(oracle_mod):
+    """Means, log-scales, quaternion and opacity gradients are derivatives of
+    the forward (float64 central differences of a float64 restatement)."""
+    prm = _pre_params(n=40, seed=9)
+    idx = oracle_mod.preprocess_select(prm[0], prm[7], prm[8], 1.0, 1000.0)
+    rng = np.random.default_rng(10)
+    m = len(idx)
+    g = dict(cam=rng.normal(size=(m, 3)), z=rng.normal(size=m), quats=rng.normal(size=(m, 4)),
+             scales=rng.normal(size=(m, 3)), colours=np.zeros((m, 3)), phase=np.zeros((m, 3)),
+             opacities=rng.normal(size=m), plane_probs=np.zeros((m, 3)))
+    got = oracle_mod.preprocess_backward(g, *prm[:7], prm[7], idx)
+    R, T = prm[7].astype(np.float64), prm[8].astype(np.float64)
+
+    def loss(means, pq, ps, po):
+        cam = means[idx] @ R + T
+        q = pq[idx] / np.maximum(np.linalg.norm(pq[idx], axis=1, keepdims=True), 1e-12)
+        return ((cam * g["cam"]).sum() + (cam[:, 2] * g["z"]).sum() + (q * g["quats"]).sum() +
+                (np.exp(ps[idx]) * g["scales"]).sum() +
+                (g["opacities"] / (1 + np.exp(-po[idx]))).sum())
+
+    base = [prm[0].astype(np.float64), prm[1].astype(np.float64), prm[2].astype(np.float64),
+            prm[5].astype(np.float64)]
+    ok_rows = [i for i in idx if np.linalg.norm(prm[1][i]) > 1e-6]
+    for which, name in enumerate(("means", "pre_quats", "pre_scales", "pre_opac")):
+        arr = base[which]
+        for i in ok_rows[:6]:
+            for j in range(arr.shape[1] if arr.ndim == 2 else 1):
+                h = 1e-6
+                a = [b.copy() for b in base]
+                b_ = [b.copy() for b in base]
+                if arr.ndim == 2:
+                    a[which][i, j] += h
+                    b_[which][i, j] -= h
+                else:
+                    a[which][i] += h
+                    b_[which][i] -= h
+                fd = (loss(*a) - loss(*b_)) / (2 * h)
+                v = got[name][i, j] if arr.ndim == 2 else got[name][i]
+                assert abs(v - fd) <= 2e-4 * max(1.0, abs(fd)), (name, i, j, v, fd)
+    # rows that were not selected get zero gradients
+    rest = np.setdiff1d(np.arange(len(prm[0])), idx)
+    assert np.all(got["means"][rest] == 0) and np.all(got["pre_plane"][rest] == 0)
