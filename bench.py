@@ -30,7 +30,7 @@ STAGES = ["project", "depth_sort", "scan", "emit", "tile_sort", "ranges", "rende
 
 
 # Stage -> kernel name in the rocprofv3 summaries under profiles/.
-STAGE_KERNEL = {"render_bwd": "k_render_bwd<{C}>", "render_fwd": "k_render_fwd<{C}>",
+STAGE_KERNEL = {"render_bwd": "k_render_bwd<{C}, true>", "render_fwd": "k_render_fwd<{C}>",
                 "project": "k_project", "geom_bwd": "k_geom_backward",
                 "asm_col_fwd": "k_col_fwd<{M}>", "asm_col_adj": "k_col_adj<{M}>",
                 "asm_rows_in": "k_rows_in<{M}>", "asm_rows_out": "k_rows_out<{M}>",
@@ -84,8 +84,11 @@ def algorithmic_bytes(N, K, P, C, W, H, S, T):
     AF_fused = 8 * P * C * W * H + 2 * pcx + 2 * csz + 8 * C * S * S
     AB_fused = 8 * C * S * S + 2 * csz + 2 * pcx + 8 * P * C * W * H
     per_launch = {
-        "render_fwd": 4 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H + 8 * T,
-        "render_bwd": (8 * P * C * W * H + 8 * P * W * H + 4 * K + N * g_rec +
+        # the forward also writes each plane's member list (8 B per member,
+        # K members when every Gaussian sits on one plane), which the
+        # backward reads instead of the 4-byte point list
+        "render_fwd": 4 * K + N * g_rec + 8 * P * C * W * H + 8 * P * W * H + 8 * T + 8 * K,
+        "render_bwd": (8 * P * C * W * H + 8 * P * W * H + 8 * K + N * g_rec +
                        N * (28 + 4 * P + 8 * C) + 8 * T),
         "project": N * g_in + N * (g_rec + 24),
         "geom_bwd": N * g_in + N * (20 + 4 * P + 8 * C) + N * (40 + 4 * P + 8 * C),
