@@ -245,13 +245,22 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   constexpr int RS = rec_stride(C);
   constexpr int NV = 6 + 2 * C;
   constexpr int G = 64 / NV;
-  __shared__ float4 s_rec[kBlock * NQ];
-  __shared__ int s_k[kBlock];
+  // Slot kBlock of s_rec is a dummy member that no pixel can use (mean far
+  // away, list position beyond every n_contrib): the per-wave lists are
+  // padded with it to a multiple of G, so the member loop needs no bounds.
+  constexpr int kDummy = kBlock;
+  __shared__ float4 s_rec[(kBlock + 1) * NQ];
   __shared__ int s_g[kBlock];
   __shared__ float s_acc[kBlock * NV];
-  __shared__ unsigned short s_wl[4][kBlock];
+  __shared__ unsigned short s_wl[4][kBlock + G];
   __shared__ int s_cnt[4][5];
   __shared__ int s_wmax[4];
+  if (threadIdx.x < NQ) {
+    s_rec[kDummy * NQ + threadIdx.x] =
+        threadIdx.x == 0   ? make_float4(1e6f, 1e6f, kBwdConicScale, 0.0f)
+        : threadIdx.x == 1 ? make_float4(kBwdConicScale, 0.0f, __int_as_float(0x7FFFFFFF), 0.0f)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
 
   int tile, plane;
   if (kSub) {
@@ -385,26 +394,34 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     const int cnt = tot[0];
     if (qm != 0u) {
       const int slot = off[0];
-      // quad 0: (mx, my, kc*cxx, kc*cxy); quad 1: (kc*czz, o*w, -, -) with
+      // quad 0: (mx, my, kc*cxx, kc*cxy); quad 1: (kc*czz, o*w, k, -) with
       // kc = -log2(e)/2, so the exponent of G = exp2(.) is dx*u + dy*v with
       // u = kc*(cxx dx + cxy dy) and v = kc*(cxy dx + czz dy).
       s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
                                      kBwdConicScale * rq[0].w);
-      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, rq[1].z * wpl, 0.0f, 0.0f);
+      // quad 1 also carries the list position (int bits) for the n_contrib test
+      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, rq[1].z * wpl,
+                                         __int_as_float(k), 0.0f);
 #pragma unroll
       for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = rq[q];
-      s_k[slot] = k;
       s_g[slot] = g;
+      // Each wave's list is stored after its padding, so it ends at a
+      // multiple of G.
 #pragma unroll
       for (int w = 0; w < 4; ++w)
-        if ((qm >> w) & 1u) s_wl[w][off[1 + w]] = static_cast<unsigned short>(slot);
+        if ((qm >> w) & 1u)
+          s_wl[w][(G - tot[1 + w] % G) % G + off[1 + w]] = static_cast<unsigned short>(slot);
+    }
+    if (static_cast<int>(threadIdx.x) < 4 * G) {
+      const int w = threadIdx.x / G, j = threadIdx.x - w * G;
+      if (j < (G - tot[1 + w] % G) % G) s_wl[w][j] = static_cast<unsigned short>(kDummy);
     }
     for (int e = threadIdx.x; e < cnt * NV; e += kBlock) s_acc[e] = 0.0f;
     __syncthreads();
 
-    int nl = 0;
+    int nl = 0;  // this wave's padded list length (a multiple of G)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] : nl;
+    for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] + (G - tot[1 + w] % G) % G : nl;
     for (int hi = nl - 1; hi >= 0; hi -= G) {
       // Branch-free: every lane evaluates every member of the group and a
       // single predicate `ok` (list position < n_contrib, power <= 0,
@@ -413,19 +430,17 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       bool any = false;
 #pragma unroll
       for (int m = 0; m < G; ++m) {
-        const int li = hi - m;
-        const bool valid = li >= 0;
-        const int slot = s_wl[wave][valid ? li : 0];
-        const int kk = s_k[slot];
+        const int slot = s_wl[wave][hi - m];
         const float4 a = s_rec[slot * NQ];
         const float4 b = s_rec[slot * NQ + 1];
+        const int kk = __float_as_int(b.z);
         const float dx = a.x - pxf, dy = a.y - pyf;
         const float u = fmaf(a.z, dx, a.w * dy);
         const float v = fmaf(b.x, dy, a.w * dx);
         const float pw = fmaf(dx, u, dy * v);  // = log2(e) * power
         const float Gv = __builtin_amdgcn_exp2f(pw);
         const float alpha = fminf(kMaxAlpha, b.y * Gv);
-        const bool ok = valid && kk < last && !(pw > 0.0f) && alpha >= kMinAlphaBwd;
+        const bool ok = kk < last && !(pw > 0.0f) && alpha >= kMinAlphaBwd;
         any = any || ok;
         T = ok ? T * __builtin_amdgcn_rcpf(1.0f - alpha) : T;
         const float dcol = ok ? alpha * T : 0.0f;
@@ -469,8 +484,8 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         const float tot_v = transpose_reduce64(buf);
         if (lane < G * NV) {
           const int m = lane / NV, v = lane - m * NV;
-          const int li = hi - m;
-          if (li >= 0 && tot_v != 0.0f) atomicAdd(&s_acc[s_wl[wave][li] * NV + v], tot_v);
+          const int sl = s_wl[wave][hi - m];
+          if (sl != kDummy && tot_v != 0.0f) atomicAdd(&s_acc[sl * NV + v], tot_v);
         }
       }
     }
