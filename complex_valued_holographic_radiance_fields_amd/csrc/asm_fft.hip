@@ -201,7 +201,13 @@ constexpr int lds_elems() {
 template <int N>
 constexpr int kCopyIters = (kFftBatch * N + kFftThreads - 1) / kFftThreads;
 
-template <int N, int R, int NS, bool INV>
+// Twiddles are stored per stage, in the order the butterflies use them:
+// the stage with radix R after NS points have been combined holds
+// w(k, t) = exp(-2 pi i t k / (NS R)) at OFF + k (R - 1) + t - 1 for
+// k < NS, 1 <= t < R (OFF = sum of NS (R - 1) over the earlier stages; N - 1
+// entries in all).  A butterfly then reads its R - 1 twiddles at one base
+// address plus constant offsets.
+template <int N, int R, int NS, bool INV, int OFF>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
   constexpr int B = kFftBatch;
   constexpr int NR = N / R;
@@ -240,9 +246,10 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
         for (int t = 0; t < R; ++t) x[t] = lds[pad(q + t * LS)];
       }
       if (NS > 1) {
+        const float2* wk = tw + (twoff + OFF + k * (R - 1) - 1);
 #pragma unroll
         for (int t = 1; t < R; ++t) {
-          float2 w = tw[twoff + t * k * (N / (NS * R))];
+          float2 w = wk[t];
           if (INV) w.y = -w.y;
           x[t] = cmulf(x[t], w);
         }
@@ -271,11 +278,24 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   __syncthreads();
 }
 
-template <int N, bool INV, int NS, int R, int... Rest>
+template <int N, bool INV, int NS, int OFF, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, R, NS, INV>(lds, tw);
-  if constexpr (sizeof...(Rest) > 0) run_stages<N, INV, NS * R, Rest...>(lds, tw);
+  fft_stage<N, R, NS, INV, OFF>(lds, tw);
+  if constexpr (sizeof...(Rest) > 0)
+    run_stages<N, INV, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
+
+// The plans (radix sequence per length), shared by the device transforms
+// and the host's twiddle tables.
+#define HRF_FFT_PLANS(X) \
+  X(128, 8, 4, 4)        \
+  X(160, 8, 4, 5)        \
+  X(192, 8, 8, 3)        \
+  X(512, 8, 8, 8)        \
+  X(1024, 8, 8, 4, 4)    \
+  X(1600, 8, 8, 5, 5)    \
+  X(2016, 8, 4, 7, 3, 3) \
+  X(2048, 8, 8, 8, 4)
 
 template <int N>
 struct Plan;
@@ -284,18 +304,40 @@ struct Plan;
   struct Plan<NN> {                                                                 \
     template <bool INV>                                                             \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<NN, INV, 1, __VA_ARGS__>(lds, tw);                                 \
+      run_stages<NN, INV, 1, 0, __VA_ARGS__>(lds, tw);                              \
     }                                                                               \
   };
-HRF_FFT_PLAN(128, 8, 4, 4)
-HRF_FFT_PLAN(160, 8, 4, 5)
-HRF_FFT_PLAN(192, 8, 8, 3)
-HRF_FFT_PLAN(512, 8, 8, 8)
-HRF_FFT_PLAN(1024, 8, 8, 4, 4)
-HRF_FFT_PLAN(1600, 8, 8, 5, 5)
-HRF_FFT_PLAN(2016, 8, 4, 7, 3, 3)
-HRF_FFT_PLAN(2048, 8, 8, 8, 4)
+HRF_FFT_PLANS(HRF_FFT_PLAN)
 #undef HRF_FFT_PLAN
+
+// Host: the radix sequence of a plan (empty for lengths without one).
+std::vector<int> plan_radices(int N) {
+#define HRF_FFT_RADICES(NN, ...) \
+  if (N == NN) return std::vector<int>{__VA_ARGS__};
+  HRF_FFT_PLANS(HRF_FFT_RADICES)
+#undef HRF_FFT_RADICES
+  return {};
+}
+
+// Lengths whose twiddle table (N - 1 entries) is copied into LDS at block
+// start: it fits beside the batch without costing a block per CU.
+template <int N>
+constexpr bool kTwInLds = N <= 1600;
+template <int N>
+constexpr int kTwLdsElems = kTwInLds<N> ? N : 1;
+
+// Copies the table into LDS (when kTwInLds) and returns the pointer the
+// transforms read; the caller's next __syncthreads publishes it.
+template <int N>
+__device__ __forceinline__ const float2* stage_twiddles(float2* s_tw,
+                                                        const float2* __restrict__ tw) {
+  if constexpr (kTwInLds<N>) {
+    for (int i = threadIdx.x; i < N - 1; i += kFftThreads) s_tw[i] = tw[i];
+    return s_tw;
+  } else {
+    return tw;
+  }
+}
 
 // Transfer-function geometry of natural-order spectral element (row i,
 // column k): frequencies as torch.fft.fftfreq float32 values and the
@@ -359,6 +401,8 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
   __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 s_tw[kTwLdsElems<N>];
+  const float2* twp = stage_twiddles<N>(s_tw, tw);
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
@@ -382,7 +426,7 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
     }
   }
   __syncthreads();
-  Plan<N>::template run<false>(lds, tw);
+  Plan<N>::template run<false>(lds, twp);
   for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
     const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
     const int r = r0 + rr;
@@ -401,6 +445,8 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restri
   constexpr int B = kFftBatch;
   constexpr int ncb = N / B;
   __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 s_tw[kTwLdsElems<N>];
+  const float2* twp = stage_twiddles<N>(s_tw, tw);
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
@@ -422,7 +468,7 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restri
     }
   }
   __syncthreads();
-  Plan<N>::template run<true>(lds, tw);
+  Plan<N>::template run<true>(lds, twp);
   for (int e = threadIdx.x; e < B * w_out; e += kFftThreads) {
     const int rr = e & 3, i = e >> 2;
     const int r = r0 + rr;
@@ -457,6 +503,8 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   constexpr int ncb = N / B;
   constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
   __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 s_tw[kTwLdsElems<N>];
+  const float2* twp = stage_twiddles<N>(s_tw, tw);
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
@@ -491,7 +539,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
       lds[pad(e)] = v;
     }
     __syncthreads();
-    Plan<N>::template run<false>(lds, tw);
+    Plan<N>::template run<false>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -524,7 +572,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<true>(lds, tw);
+  Plan<N>::template run<true>(lds, twp);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, B);
   for (int e = threadIdx.x; e < B * S; e += kFftThreads) dst[e] = lds[pad(e + s_crop * B)];
 }
@@ -542,6 +590,8 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
   constexpr int ncb = N / B;
   constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
   __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 s_tw[kTwLdsElems<N>];
+  const float2* twp = stage_twiddles<N>(s_tw, tw);
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
@@ -563,7 +613,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
     }
   }
   __syncthreads();
-  Plan<N>::template run<false>(lds, tw);
+  Plan<N>::template run<false>(lds, twp);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
@@ -610,7 +660,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
       }
     }
     __syncthreads();
-    Plan<N>::template run<true>(lds, tw);
+    Plan<N>::template run<true>(lds, twp);
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
     for (int e = threadIdx.x; e < B * H; e += kFftThreads) dst[e] = lds[pad(e + r_crop * B)];
   }
@@ -633,11 +683,26 @@ int twiddles(int N, const float2** out) {
     *out = it->second;
     return HRF_OK;
   }
-  std::vector<float2> h(N);
-  for (int m = 0; m < N; ++m) {
-    const double a = -kTwoPiD * static_cast<double>(m) / static_cast<double>(N);
-    h[m] = make_float2(static_cast<float>(std::cos(a)), static_cast<float>(std::sin(a)));
+  // Per-stage tables (see fft_stage): w(k, t) = exp(-2 pi i t k / (NS R)),
+  // computed in double as exp(-2 pi i m / N) with m = t k N / (NS R).
+  std::vector<float2> h;
+  h.reserve(N);
+  int ns = 1;
+  for (int r : plan_radices(N)) {
+    for (int k = 0; k < ns; ++k)
+      for (int t = 1; t < r; ++t) {
+        const long long m = static_cast<long long>(t) * k * (N / (ns * r));
+        const double a = -kTwoPiD * static_cast<double>(m) / static_cast<double>(N);
+        h.push_back(make_float2(static_cast<float>(std::cos(a)),
+                                static_cast<float>(std::sin(a))));
+      }
+    ns *= r;
   }
+  if (ns != N || static_cast<int>(h.size()) != N - 1) {
+    set_error("internal: FFT plan for %d does not multiply out", N);
+    return HRF_ERR_INVALID;
+  }
+  h.push_back(make_float2(1.0f, 0.0f));  // pad to N entries
   float2* d = nullptr;
   HRF_HIP(hipMalloc(&d, N * sizeof(float2)));
   HRF_HIP(hipMemcpy(d, h.data(), N * sizeof(float2), hipMemcpyHostToDevice));
@@ -774,7 +839,7 @@ int fused_asm_adjoint(const float2* gholo, int P, int C, int H, int W, int S, do
 
 void fused_fft_release_all() {
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  for (auto& kv : tw_tables()) hipFree(kv.second);
+  for (auto& kv : tw_tables()) (void)hipFree(kv.second);
   tw_tables().clear();
 }
 
