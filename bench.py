@@ -176,6 +176,70 @@ def measure_preprocess(spec, dev, no_cpu):
     return res
 
 
+def bench_cfg3(args, dev):
+    """Config 3, the propagation-only microbench: a (3, 2048, 2048) field to
+    8 distances on the 4096 grid, forward (D*C outputs) + adjoint (sum over
+    distances back to the field) per step, through the multi-distance entry
+    points.  Byte model: the one SURVEY gives for config 3."""
+    import numpy as np
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import _lib, propagation, scenes
+
+    field, wl, dist = scenes.cfg3_fields()
+    C, S = field.shape[0], field.shape[1]
+    D, M = len(dist), 2 * S
+    x = torch.from_numpy(field).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    y = torch.randn((D, C, S, S), dtype=torch.complex64, device=dev, generator=gen)
+
+    def step():
+        propagation.multidistance(x, wl, scenes.PITCH, dist, (S, S), float(S))
+        propagation.multidistance_adjoint(y, (S, S), wl, scenes.PITCH, dist, (S, S), float(S))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    fwd_b = C * (8 * S * S + 16 * M * M) + D * C * (32 * M * M + 8 * S * S)
+    adj_b = D * C * (8 * S * S + 32 * M * M) + C * (16 * M * M + 8 * S * S)
+    ach = (fwd_b + adj_b) / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        t0 = time.perf_counter()
+        cpu_baseline.asm_torch(torch.from_numpy(field[0]), wl[0], scenes.PITCH, dist[0], S,
+                               float(S))
+        one = (time.perf_counter() - t0) * 1e3
+        # the adjoint costs what the forward does: 2 * D * C single propagations
+        cpu = {"value": round(one * 2 * D * C, 1), "unit": "ms/step",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": "one 2048x2048 propagation of the pure-torch ASM "
+                         "(oracle/cpu_baseline.py, python_function.py:35-78), scaled by 2*D*C"}
+    out = {"metric": "config 3 propagation microbench: (3,2048,2048) field to 8 distances, "
+                     "fwd+adjoint, ms/step", "value": round(ms, 3), "unit": "ms/step",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic",
+           "config": {"workload": f"cfg3: ({C},{S},{S}) c64 to {D} distances, grid {M}, "
+                                  "fwd+adjoint", "channels": C, "size": S, "distances": D,
+                      "fft_grid": M, "parallelism": "single-gpu"},
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                        "traffic": None, "kernel": "whole step (hipFFT transforms + MAC/pad/crop)",
+                        "bytes_per_step": int(fwd_b + adj_b)},
+           "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -210,6 +274,9 @@ def main():
             dst = src * 2.0
         torch.cuda.synchronize()
         del src, dst
+    if args.config in ("cfg3", "3"):
+        bench_cfg3(args, dev)
+        return
     spec = scenes.config(args.config)
     t_gen = time.perf_counter()
     sc = scenes.generate(spec)

@@ -155,6 +155,33 @@ __global__ __launch_bounds__(256) void k_mac_adj(const float2* __restrict__ spec
   }
 }
 
+// One distance of a multi-distance propagation: out[c] = spec[c] T[c] A
+// with phase sign*d*kz (sign = +1 forward, -1 adjoint: conj(T)); with
+// accumulate the product is added to out (the adjoint's sum over distances).
+__global__ __launch_bounds__(256) void k_mac_dist(const float2* __restrict__ spec, int C, int M,
+                                                  float sfreq, float ap, MacConsts mc,
+                                                  float sign, int accumulate,
+                                                  float2* __restrict__ out) {
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  const int64_t elem = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (elem >= MM) return;
+  float fxv, fyv, apv;
+  spectral_coords(elem, M, sfreq, ap, &fxv, &fyv, &apv);
+  for (int c = 0; c < C; ++c) {
+    float2 r = make_float2(0.0f, 0.0f);
+    if (apv != 0.0f) {
+      const float2 tr = transfer(mc.k[c], fxv, fyv, mc.fxmax[c], mc.fymax[c], sign * mc.d[0]);
+      r = cmul(spec[static_cast<int64_t>(c) * MM + elem], tr);
+    }
+    float2* o = out + static_cast<int64_t>(c) * MM + elem;
+    if (accumulate) {
+      const float2 prev = *o;
+      r = make_float2(prev.x + r.x, prev.y + r.y);
+    }
+    *o = r;
+  }
+}
+
 // Centred zero pad (batch,h,w) -> (batch,M,M); start = M/2 - n/2 as the
 // reference's odak zero_pad (python_function.py:129).
 __global__ void k_pad(const float2* __restrict__ in, int batch, int h, int w,
@@ -289,6 +316,18 @@ int launch_asm_mac_adjoint(const float2* spec, int P, int C, int M, double pitch
   const int64_t MM = static_cast<int64_t>(M) * M;
   hipLaunchKernelGGL(k_mac_adj, dim3(blocks_for(MM, 256)), dim3(256), 0, s, spec, P, C, M,
                      freq_step(M, pitch), aperture, mc, out);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_asm_mac_distance(const float2* spec, int C, int M, double pitch,
+                            const float* wavelengths, float distance, float aperture,
+                            bool adjoint, bool accumulate, float2* out, hipStream_t s) {
+  const MacConsts mc = make_consts(1, C, M, pitch, wavelengths, &distance);
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  hipLaunchKernelGGL(k_mac_dist, dim3(blocks_for(MM, 256)), dim3(256), 0, s, spec, C, M,
+                     freq_step(M, pitch), aperture, mc, adjoint ? -1.0f : 1.0f,
+                     accumulate ? 1 : 0, out);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

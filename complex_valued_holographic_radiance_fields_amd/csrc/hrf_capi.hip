@@ -769,6 +769,113 @@ int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes, int32_
   return HRF_OK;
 }
 
+size_t hrf_asm_multidistance_workspace_size(int32_t channels, int32_t size) {
+  if (channels < 1 || size < 1) return 0;
+  const int64_t M = 2 * static_cast<int64_t>(size);
+  Carver cv(nullptr);
+  cv.take<float2>(static_cast<size_t>(channels) * M * M);
+  cv.take<float2>(static_cast<size_t>(channels) * M * M);
+  return cv.bytes();
+}
+
+int hrf_asm_multidistance_forward(const void* field, int32_t num_distances, int32_t channels,
+                                  int32_t height, int32_t width, int32_t size,
+                                  const float* wavelengths, const float* distances,
+                                  double pixel_pitch, float aperture, void* out, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  HRF_TRY(check_asm(1, channels, height, width, size));
+  if (num_distances < 1 || !field || !wavelengths || !distances || !out) {
+    set_error("asm multi-distance: null pointer or no distance");
+    return HRF_ERR_INVALID;
+  }
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_asm_multidistance_workspace_size(channels, size),
+                   "asm multi-distance"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = 2 * size;
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  const int64_t SS = static_cast<int64_t>(size) * size;
+  Carver cv(ws);
+  float2* spec = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  float2* buf = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  // The C channel spectra are computed once and shared by every distance.
+  {
+    HRF_STAGE("asm_pad", s);
+    HRF_TRY(launch_asm_pad(static_cast<const float2*>(field), channels, height, width, spec, M,
+                           s));
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(spec, M, channels, false, s));
+  }
+  for (int d = 0; d < num_distances; ++d) {
+    {
+      HRF_STAGE("asm_mac_fwd", s);
+      HRF_TRY(launch_asm_mac_distance(spec, channels, M, pixel_pitch, wavelengths, distances[d],
+                                      aperture, false, false, buf, s));
+    }
+    {
+      HRF_STAGE("asm_fft", s);
+      HRF_TRY(fft_c2c(buf, M, channels, true, s));
+    }
+    {
+      HRF_STAGE("asm_crop", s);
+      HRF_TRY(launch_asm_crop(buf, channels, M, size, size,
+                              static_cast<float>(1.0 / static_cast<double>(MM)),
+                              static_cast<float2*>(out) + d * channels * SS, s));
+    }
+  }
+  return HRF_OK;
+}
+
+int hrf_asm_multidistance_adjoint(const void* grad_out, int32_t num_distances, int32_t channels,
+                                  int32_t height, int32_t width, int32_t size,
+                                  const float* wavelengths, const float* distances,
+                                  double pixel_pitch, float aperture, void* grad_field,
+                                  void* ws, size_t ws_bytes, void* stream) {
+  HRF_TRY(check_asm(1, channels, height, width, size));
+  if (num_distances < 1 || !grad_out || !wavelengths || !distances || !grad_field) {
+    set_error("asm multi-distance: null pointer or no distance");
+    return HRF_ERR_INVALID;
+  }
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_asm_multidistance_workspace_size(channels, size),
+                   "asm multi-distance"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = 2 * size;
+  const int64_t MM = static_cast<int64_t>(M) * M;
+  const int64_t SS = static_cast<int64_t>(size) * size;
+  Carver cv(ws);
+  float2* acc = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  float2* buf = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  // sum_d conj(T_d) FFT(pad g_d) in the spectral domain, one inverse FFT.
+  for (int d = 0; d < num_distances; ++d) {
+    {
+      HRF_STAGE("asm_pad", s);
+      HRF_TRY(launch_asm_pad(static_cast<const float2*>(grad_out) + d * channels * SS,
+                             channels, size, size, buf, M, s));
+    }
+    {
+      HRF_STAGE("asm_fft", s);
+      HRF_TRY(fft_c2c(buf, M, channels, false, s));
+    }
+    {
+      HRF_STAGE("asm_mac_adj", s);
+      HRF_TRY(launch_asm_mac_distance(buf, channels, M, pixel_pitch, wavelengths, distances[d],
+                                      aperture, true, d > 0, acc, s));
+    }
+  }
+  {
+    HRF_STAGE("asm_fft", s);
+    HRF_TRY(fft_c2c(acc, M, channels, true, s));
+  }
+  {
+    HRF_STAGE("asm_crop", s);
+    HRF_TRY(launch_asm_crop(acc, channels, M, height, width,
+                            static_cast<float>(1.0 / static_cast<double>(MM)),
+                            static_cast<float2*>(grad_field), s));
+  }
+  return HRF_OK;
+}
+
 int hrf_asm_forward(const void* field, int32_t height, int32_t width, int32_t size,
                     float wavelength, double pixel_pitch, float distance, float aperture,
                     void* out, void* ws, size_t ws_bytes, void* stream) {

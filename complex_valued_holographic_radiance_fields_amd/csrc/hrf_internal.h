@@ -280,6 +280,11 @@ int launch_asm_mac_forward(const float2* spec, int P, int C, int M, double pitch
 int launch_asm_mac_adjoint(const float2* spec, int P, int C, int M, double pitch,
                            const float* wavelengths, const float* distances,
                            float aperture, float2* out, hipStream_t s);
+// One distance of a multi-distance propagation over C channel spectra:
+// out[c] (+)= spec[c] * T(wavelengths[c], distance) * A, conj(T) for adjoint.
+int launch_asm_mac_distance(const float2* spec, int C, int M, double pitch,
+                            const float* wavelengths, float distance, float aperture,
+                            bool adjoint, bool accumulate, float2* out, hipStream_t s);
 int fft_c2c(float2* buf, int M, int batch, bool inverse, hipStream_t s);
 void fft_release_all();
 

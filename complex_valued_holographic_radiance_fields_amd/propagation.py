@@ -3,7 +3,9 @@
 ``propagate`` / ``propagate_adjoint`` are BandlimitedPropagationFunction's
 forward/backward (cuda_prop/python_function.py:111-218); ``multiplane`` /
 ``multiplane_adjoint`` fuse Scene.splat's per-(plane, wavelength) loop and
-Python sum (model.py:1251-1272); ``spectral_forward`` / ``spectral_backward``
+Python sum (model.py:1251-1272); ``multidistance`` / ``multidistance_adjoint``
+propagate one field per wavelength to many distances with the forward
+transforms shared; ``spectral_forward`` / ``spectral_backward``
 are the ``cuda_modules.bandlimited_propagation_forward/backward`` bindings
 (cuda_prop/cpp/module_def.cpp:4-24).
 """
@@ -138,6 +140,76 @@ def multiplane_adjoint(grad_holo: torch.Tensor, field_hw, wavelengths, pixel_pit
             _as_float(pixel_pitch), _as_float(aperture_size), out.data_ptr(), ws.data_ptr(), nb,
             _lib.stream_ptr(grad_holo.device)))
     return out
+
+
+def _floats(vals):
+    return [_as_float(v) for v in (vals.tolist() if isinstance(vals, torch.Tensor) else vals)]
+
+
+def multidistance(fields: torch.Tensor, wavelengths, pixel_pitch, distances, size,
+                  aperture_size=-1.0) -> torch.Tensor:
+    """fields (C,H,W) -> (D,C,S,S) with out[d,c] = propagate(fields[c],
+    wavelengths[c], distances[d]); each channel is transformed once for all
+    distances (the propagation microbench runs BandlimitedPropagation per
+    (distance, wavelength), python_function.py:220-226)."""
+    fields = _c64(fields, "fields")
+    if fields.dim() != 3:
+        raise RuntimeError(f"fields must be (C, H, W); got {tuple(fields.shape)}")
+    C, H, W = fields.shape
+    wl, ds = _floats(wavelengths), _floats(distances)
+    if len(wl) != C or len(ds) < 1:
+        raise RuntimeError(f"need {C} wavelengths and at least one distance")
+    S = _square_size(size)
+    out = torch.empty((len(ds), C, S, S), dtype=torch.complex64, device=fields.device)
+    lib = _lib.load()
+    with torch.cuda.device(fields.device):
+        nb = lib.hrf_asm_multidistance_workspace_size(C, S)
+        ws = _lib.workspace("asm_md", fields.device, _lib.stream_ptr(fields.device), nb)
+        _lib.check(lib.hrf_asm_multidistance_forward(
+            fields.data_ptr(), len(ds), C, H, W, S, _host_f32(wl), _host_f32(ds),
+            _as_float(pixel_pitch), _as_float(aperture_size), out.data_ptr(), ws.data_ptr(), nb,
+            _lib.stream_ptr(fields.device)))
+    return out
+
+
+def multidistance_adjoint(grad_out: torch.Tensor, field_hw, wavelengths, pixel_pitch,
+                          distances, size, aperture_size=-1.0) -> torch.Tensor:
+    """(D,C,S,S) gradient -> (C,H,W) gradient (exact adjoint of
+    ``multidistance``)."""
+    grad_out = _c64(grad_out, "grad_output")
+    wl, ds = _floats(wavelengths), _floats(distances)
+    C, D = len(wl), len(ds)
+    S = _square_size(size)
+    H, W = int(field_hw[0]), int(field_hw[1])
+    if tuple(grad_out.shape) != (D, C, S, S):
+        raise RuntimeError(f"grad_output must be (D,C,S,S)=({D},{C},{S},{S}); "
+                           f"got {tuple(grad_out.shape)}")
+    out = torch.empty((C, H, W), dtype=torch.complex64, device=grad_out.device)
+    lib = _lib.load()
+    with torch.cuda.device(grad_out.device):
+        nb = lib.hrf_asm_multidistance_workspace_size(C, S)
+        ws = _lib.workspace("asm_md", grad_out.device, _lib.stream_ptr(grad_out.device), nb)
+        _lib.check(lib.hrf_asm_multidistance_adjoint(
+            grad_out.data_ptr(), D, C, H, W, S, _host_f32(wl), _host_f32(ds),
+            _as_float(pixel_pitch), _as_float(aperture_size), out.data_ptr(), ws.data_ptr(), nb,
+            _lib.stream_ptr(grad_out.device)))
+    return out
+
+
+class MultiDistancePropagation(torch.autograd.Function):
+    """Differentiable ``multidistance``."""
+
+    @staticmethod
+    def forward(ctx, fields, wavelengths, pixel_pitch, distances, size, aperture_size=-1.0):
+        ctx.args = (tuple(fields.shape[1:]), wavelengths, pixel_pitch, distances, size,
+                    aperture_size)
+        return multidistance(fields, wavelengths, pixel_pitch, distances, size, aperture_size)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        hw, wl, pitch, ds, size, ap = ctx.args
+        return (multidistance_adjoint(grad_out, hw, wl, pitch, ds, size, ap), None, None, None,
+                None, None)
 
 
 def _spectral(args, adjoint: bool):

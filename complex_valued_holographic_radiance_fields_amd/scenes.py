@@ -215,6 +215,19 @@ def generate_params(spec: SceneSpec) -> dict:
         R=f32(R), T=f32(T))
 
 
+def cfg3_fields(size: int = 2048, channels: int = 3, seed: int = 3):
+    """Config 3, the propagation-only microbench: a seeded complex64 field
+    (C, size, size) with amplitude U(0,1) and phase U(0, 2 pi), the RGB
+    wavelengths, and 8 distances log-spaced over 0.1-10 mm; 2x padding, so
+    the grid is 2*size."""
+    rng = np.random.default_rng(1000 + seed)
+    amp = rng.uniform(0.0, 1.0, size=(channels, size, size))
+    ph = rng.uniform(0.0, 2.0 * math.pi, size=(channels, size, size))
+    field = (amp * np.exp(1j * ph)).astype(np.complex64)
+    distances = [float(np.float32(v)) for v in np.logspace(-4, -2, 8)]
+    return field, RGB[:channels], distances
+
+
 def to_torch(sc: Scene, device="cuda"):
     """Scene -> dict of torch tensors on ``device`` (float32)."""
     import torch

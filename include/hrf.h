@@ -267,6 +267,30 @@ int hrf_asm_multiplane_adjoint(const void* grad_hologram, int32_t planes,
                                float aperture, void* grad_fields, void* ws,
                                size_t ws_bytes, void* stream);
 
+/* One field per wavelength, many distances: fields (C,H,W) c64 ->
+ * out (D,C,S,S) c64 with out[d,c] = propagate(fields[c], wavelengths[c],
+ * distances[d]).  Each channel is transformed once and shared by all D
+ * distances (C + D*C transforms instead of 2*D*C).  Replaces the
+ * per-(distance, wavelength) BandlimitedPropagation calls of the
+ * propagation microbench (python_function.py:220-226).  Any even size
+ * (hipFFT transforms). */
+size_t hrf_asm_multidistance_workspace_size(int32_t channels, int32_t size);
+int hrf_asm_multidistance_forward(const void* fields, int32_t num_distances,
+                                  int32_t channels, int32_t height, int32_t width,
+                                  int32_t size, const float* wavelengths,
+                                  const float* distances, double pixel_pitch,
+                                  float aperture, void* out, void* ws, size_t ws_bytes,
+                                  void* stream);
+/* Adjoint: grad out (D,C,S,S) -> grad fields (C,H,W) = sum over d of the
+ * single-distance adjoints, summed in the spectral domain (D*C + C
+ * transforms). */
+int hrf_asm_multidistance_adjoint(const void* grad_out, int32_t num_distances,
+                                  int32_t channels, int32_t height, int32_t width,
+                                  int32_t size, const float* wavelengths,
+                                  const float* distances, double pixel_pitch,
+                                  float aperture, void* grad_fields, void* ws,
+                                  size_t ws_bytes, void* stream);
+
 /* Releases cached hipFFT plans and FFT twiddle tables (optional). */
 void hrf_release_caches(void);
 
