@@ -83,13 +83,14 @@ SIGNATURES = {
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
     "hrf_asm_multidistance_adjoint": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp,
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
-    "hrf_preprocess_workspace_size": (_sz, [_i64]),
+    "hrf_preprocess_workspace_size": (_sz, [_i64, _i32, _i32]),
     "hrf_preprocess_select": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _f32, _f32, _vp, _sz,
                                              _vp, _P(_i64)]),
     "hrf_preprocess_forward": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _vp, _sz, _i64,
                                               _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hrf_preprocess_backward": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _i64,
-                                               _P(HrfSelectedGrads), _P(HrfParamGrads), _vp]),
+                                               _P(HrfSelectedGrads), _P(HrfParamGrads), _vp,
+                                               _sz, _vp]),
     "hrf_cov3d_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
     "hrf_cov3d_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "hrf_jacobian_forward": (ctypes.c_int, [_vp, _i64, _f32, _f32, _i32, _i32, _f32, _f32,

@@ -15,9 +15,13 @@ Mirrors what the reference does between the model's parameters and
   the straight-through one_hot(argmax) plane assignment (``STEFunction``,
   model.py:41-56, whose backward is grad * softmax(logits / 0.001)).
 
-Everything runs in two HIP kernels plus the binning's flag scan and radix sort
-(``include/hrf.h``: hrf_preprocess_*), with one host sync for the selected
-count, as the reference's ``torch.where`` / ``masked_select`` have.
+The forward runs a selection kernel over the parameters in index order (it
+also computes every activation into one packed record per kept row), the
+binning's flag scan and radix sort, and one gather of the records in depth
+order (``include/hrf.h``: hrf_preprocess_*), with one host sync for the
+selected count, as the reference's ``torch.where`` / ``masked_select`` have.
+The backward packs the output gradients in depth order and then writes the
+parameter gradients in index order.
 """
 from __future__ import annotations
 
@@ -89,7 +93,7 @@ def forward(means, pre_act_quats, pre_act_scales, colours, pre_act_phase, pre_ac
     dev = prm.device
     with torch.cuda.device(dev):
         stream = _lib.stream_ptr(dev)
-        wbytes = lib.hrf_preprocess_workspace_size(prm.n)
+        wbytes = lib.hrf_preprocess_workspace_size(prm.n, prm.C, prm.P)
         ws = _lib.workspace("preprocess", dev, stream, wbytes)
         m = ctypes.c_int64(0)
         _lib.check(lib.hrf_preprocess_select(ctypes.byref(prm.c), R.data_ptr(), T.data_ptr(),
@@ -142,9 +146,12 @@ def backward(grads, means, pre_act_quats, pre_act_scales, colours, pre_act_phase
     lib = _lib.load()
     with torch.cuda.device(prm.device):
         stream = _lib.stream_ptr(prm.device)
+        wbytes = lib.hrf_preprocess_workspace_size(prm.n, prm.C, prm.P)
+        ws = _lib.workspace("preprocess", prm.device, stream, wbytes)
         _lib.check(lib.hrf_preprocess_backward(ctypes.byref(prm.c), R.data_ptr(),
                                                idxs.data_ptr(), m, ctypes.byref(gin),
-                                               ctypes.byref(gout), stream))
+                                               ctypes.byref(gout), _lib.ptr(ws), wbytes,
+                                               stream))
     out[5] = out[5].reshape(pre_act_opacities.shape)
     return out
 

@@ -341,9 +341,10 @@ typedef struct hrf_param_grads {
   float* pre_plane;
 } hrf_param_grads;
 
-/* Workspace of hrf_preprocess_select / _forward for N Gaussians; it carries
- * the selection from one call to the next. */
-size_t hrf_preprocess_workspace_size(int64_t n);
+/* Workspace of hrf_preprocess_select / _forward / _backward for N Gaussians
+ * with C colour channels and P planes; it carries the selection from
+ * _select to _forward (the backward needs nothing from them). */
+size_t hrf_preprocess_workspace_size(int64_t n, int32_t channels, int32_t planes);
 
 /* Camera transform, selection and depth order; returns the selected count M
  * (one host sync, as the reference's torch.where / masked_select).  R (3,3)
@@ -366,11 +367,11 @@ int hrf_preprocess_forward(const hrf_scene_params* params, const float* R, const
 /* Backward of hrf_preprocess_forward: the gradients of its outputs -> the
  * parameter gradients (autograd of the reference's gathers and activations;
  * the plane logits get grad * softmax(logits / 0.001), STEFunction.backward,
- * model.py:50-56).  No workspace. */
+ * model.py:50-56).  ws: hrf_preprocess_workspace_size bytes. */
 int hrf_preprocess_backward(const hrf_scene_params* params, const float* R,
                             const int64_t* idxs, int64_t num_selected,
                             const hrf_selected_grads* grads, const hrf_param_grads* out,
-                            void* stream);
+                            void* ws, size_t ws_bytes, void* stream);
 
 /* ---------------- stage tracing (no counterpart in the reference, which
  * prints per-phase CUDA event times from train.py:263-344) ---------------- */

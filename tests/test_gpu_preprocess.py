@@ -69,18 +69,19 @@ def test_forward_matches_oracle(hrf, oracle_mod, near, far, P, C):
         np.testing.assert_allclose(got[k], ref[k], rtol=3e-7, err_msg=k)
 
 
-def test_backward_matches_oracle(hrf, oracle_mod):
+@pytest.mark.parametrize("near,far,P,C", [(1.0, 1000.0, 3, 3), (1.0, 4.0, 5, 2)])
+def test_backward_matches_oracle(hrf, oracle_mod, near, far, P, C):
     from complex_valued_holographic_radiance_fields_amd import preprocess
 
-    prm = _params(seed=11)
-    ref = oracle_mod.preprocess_forward(*prm)
+    prm = _params(P=P, C=C, seed=11)
+    ref = oracle_mod.preprocess_forward(*prm, near=near, far=far)
     m = len(ref["idxs"])
     rng = np.random.default_rng(12)
     g = {k: rng.normal(size=ref[k].shape).astype(np.float32) for k in KEYS}
     exp = oracle_mod.preprocess_backward(g, *prm[:7], prm[7], ref["idxs"])
     got = preprocess.backward([_t(g[k]) for k in KEYS], *[_t(a) for a in prm[:7]], _t(prm[7]),
                               _t(ref["idxs"]))
-    print(f"preprocess backward selected={m}", flush=True)
+    print(f"preprocess backward selected={m} P={P} C={C}", flush=True)
     for name, t in zip(PNAMES, got):
         a = t.cpu().numpy()
         # NaN plane logits give NaN softmax gradients on both sides (as torch)
