@@ -144,9 +144,11 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __
 // Stable scatter.  Wave w owns the contiguous sub-range
 // [base + w*512, base + (w+1)*512) processed as 8 iterations of 64 keys;
 // the rank of a key among equal digits before it is found with a ballot
-// match (RB ballots) plus per-wave LDS digit counters, then offset by the
-// counts of the lower waves and the global digit/block offset.  With fewer
-// digit values (RB < 8) a block's keys fall into fewer, longer output runs.
+// match (RB ballots) plus per-wave LDS digit counters.  The block's keys are
+// then reordered by digit in LDS (stable: digit, wave, rank), and written
+// out from there in order: consecutive threads store consecutive elements
+// of each digit's output run, so the global stores coalesce instead of
+// spreading every wave-wide store over up to 2^RB runs.
 template <int RB, bool VALS>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
@@ -156,14 +158,19 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
   constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_cnt[kRadixWaves][kBins];
+  __shared__ uint32_t s_delta[kBins];  // global offset of the digit minus its local offset
+  __shared__ uint32_t s_wsum[kRadixWaves];
+  __shared__ uint32_t s_key[kRadixTile];
+  __shared__ uint32_t s_val[VALS ? kRadixTile : 1];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
     s_cnt[e / kBins][e % kBins] = 0;
   __syncthreads();
 
-  const int64_t wbase = static_cast<int64_t>(blockIdx.x) * kRadixTile +
-                        static_cast<int64_t>(wave) * (kRadixItems * 64);
+  const int64_t bbase = static_cast<int64_t>(blockIdx.x) * kRadixTile;
+  const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
+  const int nvalid = static_cast<int>(n - bbase < kRadixTile ? n - bbase : kRadixTile);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
   int dig[kRadixItems];
@@ -191,10 +198,29 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     if (valid && before == 0) s_cnt[wave][d] = prev + static_cast<uint32_t>(__popcll(peers));
   }
   __syncthreads();
-  // Per-digit prefix over waves plus the global offset of (digit, block).
+  // Per digit: the counts of the lower waves (s_cnt becomes each wave's
+  // local start), the block total, and an exclusive scan of the totals over
+  // the digits (the digit's local start in the reordered block).
+  uint32_t tot = 0;
   if (threadIdx.x < kBins) {
     const int d = threadIdx.x;
-    uint32_t run = hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kRadixWaves; ++w) tot += s_cnt[w][d];
+  }
+  uint32_t incl = tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  if (threadIdx.x < kBins) {
+    const int d = threadIdx.x;
+    uint32_t loc = incl - tot;
+    for (int w = 0; w < wave; ++w) loc += s_wsum[w];
+    s_delta[d] = hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x] - loc;
+    uint32_t run = loc;
 #pragma unroll
     for (int w = 0; w < kRadixWaves; ++w) {
       const uint32_t c = s_cnt[w][d];
@@ -206,9 +232,20 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
 #pragma unroll
   for (int it = 0; it < kRadixItems; ++it) {
     if (dig[it] >= 0) {
-      const uint32_t pos = s_cnt[wave][dig[it]] + rank[it];
-      kout[pos] = key[it];
-      if (VALS) vout[pos] = val[it];
+      const uint32_t lp = s_cnt[wave][dig[it]] + rank[it];
+      s_key[lp] = key[it];
+      if (VALS) s_val[lp] = val[it];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    const int i = it * kRadixThreads + static_cast<int>(threadIdx.x);
+    if (i < nvalid) {
+      const uint32_t k = s_key[i];
+      const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
+      kout[pos] = k;
+      if (VALS) vout[pos] = s_val[i];
     }
   }
 }
