@@ -134,15 +134,17 @@ struct BinWs {
   uint32_t* keys_b;
   uint32_t* vals_s;
   uint32_t* radix;
+  int32_t* diff;  // tile-count difference array (grids that fit the LDS bound)
 };
 
-BinWs carve_bin(Carver& cv, int64_t k) {
+BinWs carve_bin(Carver& cv, int64_t k, int gx, int gy) {
   BinWs w;
   const int64_t m = k > 0 ? k : 1;
   w.keys_a = cv.take<uint32_t>(m);
   w.keys_b = cv.take<uint32_t>(m);
   w.vals_s = cv.take<uint32_t>(m);
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
+  w.diff = cv.take<int32_t>(tile_diff_fits(gx, gy) ? tile_diff_elems(gx, gy) : 1);
   return w;
 }
 
@@ -272,10 +274,9 @@ size_t hrf_raster_geom_workspace_size(int64_t n, int32_t channels, int32_t plane
 }
 
 size_t hrf_raster_binning_workspace_size(int64_t num_pairs, int32_t width, int32_t height) {
-  (void)width;
-  (void)height;
+  if (num_pairs < 0 || width <= 0 || height <= 0) return 0;
   Carver cv(nullptr);
-  carve_bin(cv, num_pairs);
+  carve_bin(cv, num_pairs, (width + kTile - 1) / kTile, (height + kTile - 1) / kTile);
   return cv.bytes();
 }
 
@@ -413,28 +414,40 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   Carver cg(geom_ws);
   GeomWs w = carve_geom(cg, n, g->channels);
   Carver cb(bin_ws);
-  BinWs b = carve_bin(cb, num_pairs);
+  BinWs b = carve_bin(cb, num_pairs, f.gx, f.gy);
 
   // Pair emission in depth-rank order, then a stable sort on the tile id.
   const int end_bit = bits_for(f.ntiles);
   const int vbits = bits_for(static_cast<int>(n < 0x7FFFFFFF ? n : 0x7FFFFFFF));
+  // Usual case: the tile ranges come from the Gaussians' rectangles (no
+  // pass over the sorted pairs); the emit launch clears their scratch.
+  const bool diff_ranges = tile_diff_fits(f.gx, f.gy);
+  const int diff_n = diff_ranges ? static_cast<int>(tile_diff_elems(f.gx, f.gy)) : 0;
   if (end_bit + vbits <= 32) {
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_packed(w.off, w.order, w.sort_flag, w.rect, n, f.gx, vbits, b.keys_a,
-                                 s));
+                                 s, b.diff, diff_n));
     }
     bool in_b = false;
+    // The last sort pass writes the gaussian bits straight into point_list;
+    // otherwise the sorted words are unpacked.
+    const bool fused = num_pairs > 1 && diff_ranges;
     {
       HRF_STAGE("tile_sort", s);
-      HRF_TRY(radix_sort_keys(b.keys_a, b.keys_b, num_pairs, vbits, end_bit, b.radix, &in_b,
-                              s));
+      HRF_TRY(radix_sort_keys(b.keys_a, b.keys_b, num_pairs, vbits, end_bit, b.radix, &in_b, s,
+                              fused ? reinterpret_cast<uint32_t*>(point_list) : nullptr,
+                              (1u << vbits) - 1u));
     }
     {
       HRF_STAGE("ranges", s);
-      HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
-                                   ranges, f.ntiles, s));
+      if (fused)
+        HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, b.diff, ranges,
+                                              s));
+      else
+        HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
+                                     ranges, f.ntiles, s));
     }
   } else {
     const bool odd = (radix_passes(end_bit) % 2) == 1;
@@ -443,7 +456,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_pairs(w.off, w.order, w.sort_flag, w.rect, n, num_pairs, f.gx,
-                                b.keys_a, vals_a, s));
+                                b.keys_a, vals_a, s, b.diff, diff_n));
     }
     bool in_b = false;
     {
@@ -460,7 +473,11 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
                              hipMemcpyDeviceToDevice, s));
     {
       HRF_STAGE("ranges", s);
-      HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
+      if (diff_ranges)
+        HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, b.diff, ranges,
+                                              s));
+      else
+        HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
     }
   }
 

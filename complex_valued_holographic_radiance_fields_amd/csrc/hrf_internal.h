@@ -188,8 +188,22 @@ int radix_passes(int end_bit);
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
 // (the other bits ride along unsorted), in ceil(nbits/8) passes of equal
 // digit width; same scratch and ping-pong convention as radix_sort_pairs.
+// final_out != nullptr (needs n > 1, nbits > 0): the last pass writes
+// word & final_mask there instead of into the ping-pong buffers.
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
-                    uint32_t* scratch, bool* result_in_b, hipStream_t s);
+                    uint32_t* scratch, bool* result_in_b, hipStream_t s,
+                    uint32_t* final_out = nullptr, uint32_t final_mask = 0xFFFFFFFFu);
+
+// Tile ranges from the Gaussians' tile rectangles (tiles[g] > 0 marks a
+// rectangle) instead of the sorted pairs: a 2-D difference array of
+// (gx+1)(gy+1) int32 in `diff` (device scratch that must hold zeros: the
+// emit launch of the same call clears it), integrated in one block.
+// Only for tile grids whose difference array fits kMaxTileDiff entries.
+constexpr int64_t kMaxTileDiff = 16000;  // 64000 B of LDS
+int64_t tile_diff_elems(int gx, int gy);
+bool tile_diff_fits(int gx, int gy);
+int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int64_t n, int gx,
+                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s);
 
 // Exclusive pair offsets off[0..n] (off[n] = K) of the tile counts taken in
 // depth-rank order (tiles[order[i]]; order == nullptr: index order) and
@@ -200,16 +214,17 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
                    uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
                    hipStream_t s);
 // The depth-order permutation used by the emit kernels is order[] when
-// *sorted_flag != 0 and the identity otherwise.
+// *sorted_flag != 0 and the identity otherwise.  Both emit kernels also
+// clear zero[0, zero_n) (the tile-count difference array, when used).
 int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
                       const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
-                      uint32_t* vals, hipStream_t s);
+                      uint32_t* vals, hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
 int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
                        const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
-                       hipStream_t s);
+                       hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
 int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,

@@ -23,6 +23,10 @@ constexpr int kRadixItems = 8;  // per thread
 constexpr int kRadixTile = kRadixThreads * kRadixItems;
 constexpr int kRadixBins = 256;
 
+constexpr int kDiffThreads = 1024;
+constexpr int kDiffItems = 4;    // Gaussians per thread per step, loads issued together
+constexpr int kDiffBlocks = 256;
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Exclusive block scan of one value per thread (wave64 shuffles + LDS).
@@ -154,7 +158,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
     uint32_t mask, const uint32_t* __restrict__ hist_scan, int nblocks,
-    const uint32_t* __restrict__ run_flag) {
+    const uint32_t* __restrict__ run_flag, uint32_t out_mask) {
   constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_cnt[kRadixWaves][kBins];
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     if (i < nvalid) {
       const uint32_t k = s_key[i];
       const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
-      kout[pos] = k;
+      kout[pos] = k & out_mask;
       if (VALS) vout[pos] = s_val[i];
     }
   }
@@ -424,12 +428,22 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
 // (coalesced).  Tile order inside a Gaussian is y outer, x inner
 // (rasterizer_splat.cu:162-173).
 constexpr int kEmitThreads = 256;
+// Clears zero[0, zero_n) with the whole grid (a scratch array that a later
+// kernel of the same call accumulates into), saving a fill launch.
+__device__ __forceinline__ void zero_prefix(int32_t* zero, int zero_n) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < zero_n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    zero[e] = 0;
+}
+
 __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ off,
                                                       const uint32_t* __restrict__ order,
                                                       const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
                                                       int gx, uint32_t* __restrict__ keys,
-                                                      uint32_t* __restrict__ vals) {
+                                                      uint32_t* __restrict__ vals,
+                                                      int32_t* __restrict__ zero, int zero_n) {
+  zero_prefix(zero, zero_n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -471,7 +485,9 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
                                                              const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
                                                              int64_t n, int gx, int vbits,
-                                                             uint32_t* __restrict__ words) {
+                                                             uint32_t* __restrict__ words,
+                                                             int32_t* __restrict__ zero, int zero_n) {
+  zero_prefix(zero, zero_n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -529,6 +545,102 @@ __global__ void k_tile_ranges(const uint32_t* __restrict__ keys, int64_t k,
     ranges[2 * static_cast<int64_t>(t) + 1] = static_cast<int32_t>(i + 1);
 }
 
+// Tile ranges without reading the sorted pairs.  Gaussian g emits one pair
+// per tile of its rectangle [minx, maxx) x [miny, maxy), so the pair count
+// of a tile is the number of rectangles covering it: a 2-D difference array
+// (+1 at (miny, minx) and (maxy, maxx), -1 at (miny, maxx) and (maxy, minx))
+// integrated twice.  Sorted by tile id, tile t's pairs start at the sum of
+// the counts of tiles < t.  Blocks accumulate the difference array in LDS
+// and flush it with one global atomic per nonzero entry.
+__global__ __launch_bounds__(kDiffThreads) void k_tile_diff(const uint32_t* __restrict__ tiles,
+                                                           const uint2* __restrict__ rect,
+                                                           int64_t n, int gx, int dn,
+                                                           int32_t* __restrict__ diff) {
+  extern __shared__ int32_t s_diff[];
+  for (int e = threadIdx.x; e < dn; e += kDiffThreads) s_diff[e] = 0;
+  __syncthreads();
+  const int gw = gx + 1;
+  constexpr int kPer = kDiffItems * kDiffThreads;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kPer; base < n;
+       base += static_cast<int64_t>(gridDim.x) * kPer) {
+    uint32_t t[kDiffItems];
+    uint2 r[kDiffItems];
+#pragma unroll
+    for (int j = 0; j < kDiffItems; ++j) {
+      const int64_t g = base + j * kDiffThreads + threadIdx.x;
+      t[j] = g < n ? tiles[g] : 0u;
+      r[j] = g < n ? rect[g] : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < kDiffItems; ++j) {
+      if (t[j] == 0u) continue;
+      const int x0 = static_cast<int>(r[j].x & 0xFFFF), y0 = static_cast<int>(r[j].x >> 16);
+      const int x1 = static_cast<int>(r[j].y & 0xFFFF), y1 = static_cast<int>(r[j].y >> 16);
+      atomicAdd(&s_diff[y0 * gw + x0], 1);
+      atomicAdd(&s_diff[y0 * gw + x1], -1);
+      atomicAdd(&s_diff[y1 * gw + x0], -1);
+      atomicAdd(&s_diff[y1 * gw + x1], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < dn; e += kDiffThreads) {
+    const int32_t v = s_diff[e];
+    if (v != 0) atomicAdd(&diff[e], v);
+  }
+}
+
+// Inclusive prefix sum of `len` LDS entries at stride `step` by one wave,
+// in chunks of 64 with a carry.
+__device__ __forceinline__ void wave_prefix_lds(int32_t* p, int len, int step) {
+  const int lane = threadIdx.x & 63;
+  int32_t carry = 0;
+  for (int c0 = 0; c0 < len; c0 += 64) {
+    const int i = c0 + lane;
+    int32_t v = i < len ? p[i * step] : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(v, o, 64);
+      if (lane >= o) v += y;
+    }
+    v += carry;
+    if (i < len) p[i * step] = v;
+    carry = __shfl(v, 63, 64);
+  }
+}
+
+// One block: integrate the difference array (rows, then columns, one wave
+// per line), then an exclusive scan of the counts in tile order; empty
+// tiles get (0, 0), as a zero-filled ranges buffer has for tiles without
+// pairs.
+__global__ __launch_bounds__(kDiffThreads) void k_ranges_from_diff(const int32_t* __restrict__ diff,
+                                                                  int gx, int gy,
+                                                                  int32_t* __restrict__ ranges) {
+  extern __shared__ int32_t s_d[];
+  __shared__ int32_t s_wave[kDiffThreads / 64];
+  constexpr int kWaves = kDiffThreads / 64;
+  const int wave = threadIdx.x >> 6;
+  const int gw = gx + 1, dn = (gx + 1) * (gy + 1);
+  for (int e = threadIdx.x; e < dn; e += kDiffThreads) s_d[e] = diff[e];
+  __syncthreads();
+  for (int y = wave; y < gy; y += kWaves) wave_prefix_lds(s_d + y * gw, gx, 1);
+  __syncthreads();
+  for (int x = wave; x < gx; x += kWaves) wave_prefix_lds(s_d + x, gy, gw);
+  __syncthreads();
+  const int nt = gx * gy;
+  const int per = (nt + kDiffThreads - 1) / kDiffThreads;
+  const int t0 = threadIdx.x * per;
+  int32_t local = 0;
+  for (int t = t0; t < t0 + per && t < nt; ++t) local += s_d[(t / gx) * gw + t % gx];
+  int32_t total;
+  int32_t start = block_exclusive_scan(local, &total, s_wave);
+  for (int t = t0; t < t0 + per && t < nt; ++t) {
+    const int32_t c = s_d[(t / gx) * gw + t % gx];
+    ranges[2 * t] = c > 0 ? start : 0;
+    ranges[2 * t + 1] = c > 0 ? start + c : 0;
+    start += c;
+  }
+}
+
 __global__ void k_compact_visible(const uint32_t* __restrict__ vis,
                                   const uint32_t* __restrict__ vis_off, int64_t n,
                                   int64_t* __restrict__ visible) {
@@ -562,7 +674,7 @@ namespace {
 template <int RB, bool VALS>
 int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
                int64_t n, int nb, int shift, uint32_t mask, uint32_t* scratch,
-               const uint32_t* run_flag, hipStream_t s) {
+               const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu) {
   const int64_t hist_n = static_cast<int64_t>(nb) << RB;
   uint32_t* hist = scratch;
   uint32_t* hist_scan = scratch + hist_n;
@@ -572,7 +684,7 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
   HRF_LAUNCH_CHECK();
   HRF_TRY((scan_exclusive<uint32_t, uint32_t>(hist, hist_scan, hist_n, scan_tmp, s, run_flag)));
   hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(nb), dim3(kRadixThreads), 0, s, src_k,
-                     src_v, dst_k, dst_v, n, shift, mask, hist_scan, nb, run_flag);
+                     src_v, dst_k, dst_v, n, shift, mask, hist_scan, nb, run_flag, out_mask);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -614,9 +726,16 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
 }
 
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
-                    uint32_t* scratch, bool* result_in_b, hipStream_t s) {
+                    uint32_t* scratch, bool* result_in_b, hipStream_t s, uint32_t* final_out,
+                    uint32_t final_mask) {
   *result_in_b = false;
-  if (n <= 1 || nbits <= 0) return HRF_OK;
+  if (n <= 1 || nbits <= 0) {
+    if (final_out) {
+      set_error("internal: radix_sort_keys final output needs n > 1 and nbits > 0");
+      return HRF_ERR_INVALID;
+    }
+    return HRF_OK;
+  }
   const int passes = (nbits + 7) / 8;
   const int rb = (nbits + passes - 1) / passes;  // digit bits, <= 8
   int nb = 0;
@@ -627,27 +746,30 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
     const int bits = nbits - done < rb ? nbits - done : rb;
     const uint32_t mask = (1u << bits) - 1u;
     const int shift = lo_bit + done;
+    const bool last = pass == passes - 1 && final_out;
+    uint32_t* out = last ? final_out : dst;
+    const uint32_t om = last ? final_mask : 0xFFFFFFFFu;
     int rc;
     switch (rb) {
       case 1: case 2: case 3: case 4:
-        rc = radix_pass<4, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s);
+        rc = radix_pass<4, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s, om);
         break;
       case 5:
-        rc = radix_pass<5, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s);
+        rc = radix_pass<5, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s, om);
         break;
       case 6:
-        rc = radix_pass<6, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s);
+        rc = radix_pass<6, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s, om);
         break;
       case 7:
-        rc = radix_pass<7, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s);
+        rc = radix_pass<7, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s, om);
         break;
       default:
-        rc = radix_pass<8, false>(src, nullptr, dst, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s);
+        rc = radix_pass<8, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
+                                  nullptr, s, om);
         break;
     }
     HRF_TRY(rc);
@@ -656,7 +778,7 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
     src = dst;
     dst = t;
   }
-  *result_in_b = (passes % 2) == 1;
+  *result_in_b = !final_out && (passes % 2) == 1;
   return HRF_OK;
 }
 
@@ -694,20 +816,47 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 
 int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
                       const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
-                      uint32_t* vals, hipStream_t s) {
+                      uint32_t* vals, hipStream_t s, int32_t* zero, int zero_n) {
   if (k <= 0 || n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, off,
-                     order, sorted_flag, rect, n, gx, keys, vals);
+                     order, sorted_flag, rect, n, gx, keys, vals, zero, zero_n);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
 int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
                        const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
-                       hipStream_t s) {
+                       hipStream_t s, int32_t* zero, int zero_n) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     off, order, sorted_flag, rect, n, gx, vbits, words);
+                     off, order, sorted_flag, rect, n, gx, vbits, words, zero, zero_n);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int64_t tile_diff_elems(int gx, int gy) {
+  return static_cast<int64_t>(gx + 1) * static_cast<int64_t>(gy + 1);
+}
+
+bool tile_diff_fits(int gx, int gy) { return tile_diff_elems(gx, gy) <= kMaxTileDiff; }
+
+int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int64_t n, int gx,
+                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s) {
+  if (!tile_diff_fits(gx, gy)) {
+    set_error("internal: tile grid %dx%d too large for the LDS difference array", gx, gy);
+    return HRF_ERR_INVALID;
+  }
+  const int dn = static_cast<int>(tile_diff_elems(gx, gy));
+  const size_t lds = static_cast<size_t>(dn) * sizeof(int32_t);
+  if (n > 0) {
+    const int64_t want = (n + kDiffItems * kDiffThreads - 1) / (kDiffItems * kDiffThreads);
+    const int blocks = static_cast<int>(want < kDiffBlocks ? want : kDiffBlocks);
+    hipLaunchKernelGGL(k_tile_diff, dim3(blocks), dim3(kDiffThreads), lds, s, tiles, rect, n, gx,
+                       dn, diff);
+    HRF_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(k_ranges_from_diff, dim3(1), dim3(kDiffThreads), lds, s, diff, gx, gy,
+                     ranges);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

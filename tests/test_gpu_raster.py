@@ -226,6 +226,25 @@ def test_forward_parity_wide_keys(hrf, oracle_mod):
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
+def test_forward_parity_large_grid_packed(hrf, oracle_mod):
+    """A tile grid whose count difference array exceeds the LDS bound (133 x
+    133 > 16000 entries) with tile id and index still in one word: the
+    packed path unpacks the sorted words for point_list and the ranges."""
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    spec = scenes.SceneSpec("grid", 7, 6000, 2112, 2112, 1, [515e-9], [-2e-3], "uniform",
+                            log_scale_mean=-5.0, log_scale_std=0.3)
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    print(f"large grid: N={g.n} K={ref['K']}", flush=True)
+    assert ref["K"] > 1
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 def _plane_list_scene(case):
     import dataclasses
 
