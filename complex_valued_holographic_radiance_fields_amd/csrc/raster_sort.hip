@@ -53,75 +53,12 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
   return wave_off + x - v;
 }
 
-// Phase 1: per-block exclusive scan of kScanTile elements, block totals out.
-template <typename Tin, typename Tout>
-__global__ __launch_bounds__(kScanThreads) void k_scan_local(const Tin* __restrict__ in,
-                                                             Tout* __restrict__ out,
-                                                             Tout* __restrict__ sums,
-                                                             int64_t n,
-                                                             const uint32_t* __restrict__ run_flag) {
-  if (run_flag && *run_flag == 0u) return;
-  __shared__ Tout s_wave[kScanThreads / 64];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
-                       static_cast<int64_t>(threadIdx.x) * kScanItems;
-  Tout vals[kScanItems];
-  Tout run = 0;
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t idx = base + i;
-    const Tout v = idx < n ? static_cast<Tout>(in[idx]) : Tout(0);
-    vals[i] = run;
-    run += v;
-  }
-  Tout total;
-  const Tout off = block_exclusive_scan<Tout>(run, &total, s_wave);
-#pragma unroll
-  for (int i = 0; i < kScanItems; ++i) {
-    const int64_t idx = base + i;
-    if (idx < n) out[idx] = vals[i] + off;
-  }
-  if (threadIdx.x == 0) sums[blockIdx.x] = total;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kScanThreads) void k_scan_add(T* __restrict__ out,
-                                                           const T* __restrict__ sums,
-                                                           int64_t n,
-                                                           const uint32_t* __restrict__ run_flag) {
-  if (run_flag && *run_flag == 0u) return;
-  const T add = sums[blockIdx.x];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-  for (int i = threadIdx.x; i < kScanTile; i += kScanThreads) {
-    const int64_t idx = base + i;
-    if (idx < n) out[idx] += add;
-  }
-}
-
-// Recursive exclusive scan.  Scratch holds the block-sum pyramid.  With
-// run_flag, every level does nothing on the device while *run_flag == 0.
-template <typename Tin, typename Tout>
-int scan_exclusive(const Tin* in, Tout* out, int64_t n, Tout* scratch, hipStream_t s,
-                   const uint32_t* run_flag = nullptr) {
-  if (n <= 0) return HRF_OK;
-  const int64_t nb = (n + kScanTile - 1) / kScanTile;
-  Tout* sums = scratch;
-  hipLaunchKernelGGL((k_scan_local<Tin, Tout>), dim3(static_cast<unsigned>(nb)),
-                     dim3(kScanThreads), 0, s, in, out, sums, n, run_flag);
-  HRF_LAUNCH_CHECK();
-  if (nb > 1) {
-    HRF_TRY((scan_exclusive<Tout, Tout>(sums, sums, nb, scratch + nb, s, run_flag)));
-    hipLaunchKernelGGL((k_scan_add<Tout>), dim3(static_cast<unsigned>(nb)),
-                       dim3(kScanThreads), 0, s, out, sums, n, run_flag);
-    HRF_LAUNCH_CHECK();
-  }
-  return HRF_OK;
-}
-
 // ----------------------------------------------------------- radix sort --
 
 // Digit histogram of each block's kRadixTile keys: digit = (key >> shift) &
-// mask with at most 2^RB values; hist is digit-major ([digit][block]) so
-// one exclusive scan gives every (digit, block) output offset.
+// mask with at most 2^RB values; hist is digit-major ([digit][block]): a
+// scan along each digit's row plus the totals of the lower digits give
+// every (digit, block) output offset.
 template <int RB>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
@@ -145,6 +82,31 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __
     hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = s_hist[threadIdx.x];
 }
 
+// Per digit (one block each): exclusive scan of the digit's per-block
+// counts across the blocks, in place, and the digit's total.  The scatter
+// adds the totals of the lower digits itself.
+constexpr int kRowScanThreads = 1024;
+__global__ __launch_bounds__(kRowScanThreads) void k_radix_rowscan(
+    uint32_t* __restrict__ hist, int nblocks, uint32_t* __restrict__ totals,
+    const uint32_t* __restrict__ run_flag) {
+  if (run_flag && *run_flag == 0u) return;
+  __shared__ uint32_t s_wave[kRowScanThreads / 64];
+  uint32_t* row = hist + static_cast<int64_t>(blockIdx.x) * nblocks;
+  const int per = (nblocks + kRowScanThreads - 1) / kRowScanThreads;
+  const int b0 = threadIdx.x * per;
+  const int b1 = b0 + per < nblocks ? b0 + per : nblocks;
+  uint32_t local = 0;
+  for (int b = b0; b < b1; ++b) local += row[b];
+  uint32_t total;
+  uint32_t run = block_exclusive_scan(local, &total, s_wave);
+  for (int b = b0; b < b1; ++b) {
+    const uint32_t c = row[b];
+    row[b] = run;
+    run += c;
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = total;
+}
+
 // Stable scatter.  Wave w owns the contiguous sub-range
 // [base + w*512, base + (w+1)*512) processed as 8 iterations of 64 keys;
 // the rank of a key among equal digits before it is found with a ballot
@@ -157,13 +119,15 @@ template <int RB, bool VALS>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
-    uint32_t mask, const uint32_t* __restrict__ hist_scan, int nblocks,
+    uint32_t mask, const uint32_t* __restrict__ hist_scan,
+    const uint32_t* __restrict__ digit_totals, int nblocks,
     const uint32_t* __restrict__ run_flag, uint32_t out_mask) {
   constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_cnt[kRadixWaves][kBins];
   __shared__ uint32_t s_delta[kBins];  // global offset of the digit minus its local offset
   __shared__ uint32_t s_wsum[kRadixWaves];
+  __shared__ uint32_t s_gsum[kRadixWaves];
   __shared__ uint32_t s_key[kRadixTile];
   __shared__ uint32_t s_val[VALS ? kRadixTile : 1];
   const int lane = lane_id();
@@ -203,27 +167,39 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
   }
   __syncthreads();
   // Per digit: the counts of the lower waves (s_cnt becomes each wave's
-  // local start), the block total, and an exclusive scan of the totals over
-  // the digits (the digit's local start in the reordered block).
-  uint32_t tot = 0;
+  // local start), the block total, and exclusive scans over the digits of
+  // the block totals (the digit's local start in the reordered block) and
+  // of the global digit totals (the digit's first output position).
+  uint32_t tot = 0, gtot = 0;
   if (threadIdx.x < kBins) {
     const int d = threadIdx.x;
 #pragma unroll
     for (int w = 0; w < kRadixWaves; ++w) tot += s_cnt[w][d];
+    gtot = digit_totals[d];
   }
-  uint32_t incl = tot;
+  uint32_t incl = tot, gincl = gtot;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const uint32_t y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
+    const uint32_t gy = __shfl_up(gincl, o, 64);
+    if (lane >= o) {
+      incl += y;
+      gincl += gy;
+    }
   }
-  if (lane == 63) s_wsum[wave] = incl;
+  if (lane == 63) {
+    s_wsum[wave] = incl;
+    s_gsum[wave] = gincl;
+  }
   __syncthreads();
   if (threadIdx.x < kBins) {
     const int d = threadIdx.x;
-    uint32_t loc = incl - tot;
-    for (int w = 0; w < wave; ++w) loc += s_wsum[w];
-    s_delta[d] = hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x] - loc;
+    uint32_t loc = incl - tot, gbase = gincl - gtot;
+    for (int w = 0; w < wave; ++w) {
+      loc += s_wsum[w];
+      gbase += s_gsum[w];
+    }
+    s_delta[d] = gbase + hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x] - loc;
     uint32_t run = loc;
 #pragma unroll
     for (int w = 0; w < kRadixWaves; ++w) {
@@ -666,7 +642,7 @@ int radix_passes(int end_bit) { return (end_bit + 7) / 8; }
 size_t radix_scratch_elems(int64_t n) {
   const int64_t nb = (n + kRadixTile - 1) / kRadixTile;
   const size_t hist = static_cast<size_t>(nb) * kRadixBins;
-  return 2 * hist + scan_scratch_elems(static_cast<int64_t>(hist)) + 4;
+  return hist + kRadixBins + 4;  // per-(digit, block) counts, digit totals
 }
 
 namespace {
@@ -677,14 +653,15 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
                const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu) {
   const int64_t hist_n = static_cast<int64_t>(nb) << RB;
   uint32_t* hist = scratch;
-  uint32_t* hist_scan = scratch + hist_n;
-  uint32_t* scan_tmp = scratch + 2 * hist_n;
+  uint32_t* totals = scratch + hist_n;
   hipLaunchKernelGGL(k_radix_hist<RB>, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
                      mask, hist, nb, run_flag);
   HRF_LAUNCH_CHECK();
-  HRF_TRY((scan_exclusive<uint32_t, uint32_t>(hist, hist_scan, hist_n, scan_tmp, s, run_flag)));
+  hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, nb,
+                     totals, run_flag);
+  HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(nb), dim3(kRadixThreads), 0, s, src_k,
-                     src_v, dst_k, dst_v, n, shift, mask, hist_scan, nb, run_flag, out_mask);
+                     src_v, dst_k, dst_v, n, shift, mask, hist, totals, nb, run_flag, out_mask);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
