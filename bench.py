@@ -34,7 +34,7 @@ STAGE_KERNEL = {"render_bwd": "k_render_bwd<{C}, true>", "render_fwd": "k_render
                 "project": "k_project", "geom_bwd": "k_geom_backward",
                 "asm_col_fwd": "k_col_fwd<{M}>", "asm_col_adj": "k_col_adj<{M}>",
                 "asm_rows_in": "k_rows_in<{M}>", "asm_rows_out": "k_rows_out<{M}>",
-                "emit": "k_emit", "ranges": "k_tile_ranges"}
+                "emit": "k_emit_packed", "ranges": "k_tile_diff"}
 
 
 def profiled_traffic(config, stage, C, M):
@@ -47,9 +47,12 @@ def profiled_traffic(config, stage, C, M):
         return None, None
     with open(path) as f:
         for line in f:
-            parts = line.split()
-            if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
-                return int(parts[2]), os.path.relpath(path, REPO)
+            # "traffic <kernel name, may hold spaces> <bytes>"
+            if not line.startswith("traffic "):
+                continue
+            head, _, val = line.rstrip().rpartition(" ")
+            if head[len("traffic "):] == name:
+                return int(val), os.path.relpath(path, REPO)
     return None, None
 
 
