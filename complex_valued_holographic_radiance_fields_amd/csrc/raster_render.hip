@@ -338,8 +338,9 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     int k = idx;
     int g = 0;
     unsigned qm = 0;
-    float4 rq[NQ];
+    float4 rq[2];  // quads 0-1 (geometry); the amplitude quads load once culled
     float wpl = 0.0f;
+    const float4* src = nullptr;
     if (idx < end) {
       bool member;
       if (kSub) {
@@ -353,9 +354,9 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
                  ((p.pmask[g] >> plane) & 1u);
       }
       if (member) {
-        const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) rq[q] = src[q];
+        src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
+        rq[0] = src[0];
+        rq[1] = src[1];
         wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
         const float thr = alpha_threshold(rq[1].z * wpl);
         if (thr >= 0.0f) {
@@ -402,8 +403,10 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       // quad 1 also carries the list position (int bits) for the n_contrib test
       s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, rq[1].z * wpl,
                                          __int_as_float(k), 0.0f);
+      // Amplitude quads only for members that survived the cull (same
+      // 64-byte record as quads 0-1, so the loads hit the cache).
 #pragma unroll
-      for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = rq[q];
+      for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = src[q];
       s_g[slot] = g;
       // Each wave's list is stored after its padding, so it ends at a
       // multiple of G.
@@ -414,7 +417,9 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     }
     if (static_cast<int>(threadIdx.x) < 4 * G) {
       const int w = threadIdx.x / G, j = threadIdx.x - w * G;
-      if (j < (G - tot[1 + w] % G) % G) s_wl[w][j] = static_cast<unsigned short>(kDummy);
+      // tot[1 + w] by selects: a runtime index would put tot[] in scratch
+      const int tw = w == 0 ? tot[1] : (w == 1 ? tot[2] : (w == 2 ? tot[3] : tot[4]));
+      if (j < (G - tw % G) % G) s_wl[w][j] = static_cast<unsigned short>(kDummy);
     }
     for (int e = threadIdx.x; e < cnt * NV; e += kBlock) s_acc[e] = 0.0f;
     __syncthreads();
