@@ -208,27 +208,53 @@ __device__ __forceinline__ float alpha_threshold(float ow) {
 
 // min of q over x1 = mx - px in [xlo, xhi] at a fixed x2 = my - py (or the
 // same with the roles swapped): the 1-D minimiser of the convex quadratic,
-// clamped to the interval.
-__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float x2, float lo,
-                                          float hi) {
-  const float x1 = fminf(fmaxf(-a12 * x2 / a11, lo), hi);
+// clamped to the interval.  r11 = 1/a11 (hardware reciprocal): q at any
+// point of the interval bounds the minimum from above, and the minimiser's
+// rounding moves q by a11 (dx)^2, far inside the threshold's margin.
+__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float r11, float x2,
+                                          float lo, float hi) {
+  const float x1 = fminf(fmaxf(-a12 * x2 * r11, lo), hi);
   return x1 * (a11 * x1 + 2.0f * a12 * x2) + a22 * x2 * x2;
 }
 
+// A Gaussian's cull region q(d) <= thr: conic, reciprocals of its diagonal,
+// and the half-extents of the region's bounding box (widened by 0.01% +
+// 1e-3 px).  pd = false (not positive definite, or NaN): never culled.
+struct CullShape {
+  float cxx, cxy, czz, rxx, rzz, ex, ey;
+  bool pd;
+};
+
+__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz, float thr) {
+  CullShape c;
+  c.cxx = cxx;
+  c.cxy = cxy;
+  c.czz = czz;
+  const float det = cxx * czz - cxy * cxy;
+  c.pd = cxx > 0.0f && czz > 0.0f && det > 0.0f;
+  const float rdet = __builtin_amdgcn_rcpf(det);
+  c.rxx = __builtin_amdgcn_rcpf(cxx);
+  c.rzz = __builtin_amdgcn_rcpf(czz);
+  c.ex = sqrtf(fmaxf(thr * czz * rdet, 0.0f)) * 1.0001f + 1e-3f;
+  c.ey = sqrtf(fmaxf(thr * cxx * rdet, 0.0f)) * 1.0001f + 1e-3f;
+  return c;
+}
+
 // Exact test: does q(d) <= thr hold anywhere in the box of pixel centres
-// [x0, x0+7] x [y0, y0+7]?  q is convex, so if the mean is outside the box
-// the minimum over the box lies on one of its four edges.  A conic that is
-// not positive definite (or NaN) is never culled.
-__device__ __forceinline__ bool box_reaches(float mx, float my, float cxx, float cxy, float czz,
-                                            float thr, float x0, float y0) {
+// [x0, x0+7] x [y0, y0+7]?  Boxes outside the region's bounding box are
+// rejected first; q is convex, so if the mean is outside the box the
+// minimum over the box lies on one of its four edges.
+__device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape& c, float thr,
+                                            float x0, float y0) {
+  if (!c.pd) return true;
   const float x1 = x0 + 7.0f, y1 = y0 + 7.0f;
-  if (!(cxx > 0.0f) || !(czz > 0.0f) || !(cxx * czz - cxy * cxy > 0.0f)) return true;
+  if (mx + c.ex < x0 || mx - c.ex > x1 || my + c.ey < y0 || my - c.ey > y1) return false;
   if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
   const float dxl = mx - x1, dxh = mx - x0, dyl = my - y1, dyh = my - y0;
-  float m = edge_min(cxx, cxy, czz, dyl, dxl, dxh);
-  m = fminf(m, edge_min(cxx, cxy, czz, dyh, dxl, dxh));
-  m = fminf(m, edge_min(czz, cxy, cxx, dxl, dyl, dyh));
-  m = fminf(m, edge_min(czz, cxy, cxx, dxh, dyl, dyh));
+  float m = edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyl, dxl, dxh);
+  m = fminf(m, edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyh, dxl, dxh));
+  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxl, dyl, dyh));
+  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxh, dyl, dyh));
   return m <= thr;
 }
 
@@ -360,11 +386,11 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
         const float thr = alpha_threshold(rq[1].z * wpl);
         if (thr >= 0.0f) {
+          const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y, thr);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float x0 = tx0 + (w & 1) * 8, y0 = ty0 + (w >> 1) * 8;
-            const bool hit = k < wmax[w] && box_reaches(rq[0].x, rq[0].y, rq[0].z, rq[0].w,
-                                                        rq[1].y, thr, x0, y0);
+            const bool hit = k < wmax[w] && box_reaches(rq[0].x, rq[0].y, cs, thr, x0, y0);
             qm |= hit ? (1u << w) : 0u;
           }
         }
