@@ -24,6 +24,21 @@ __device__ __forceinline__ float dot2(float a0, float b0, float a1, float b1) {
   return fmaf(a1, b1, a0 * b0);
 }
 
+// Division and square root: exact IEEE (kFast = false, the forward
+// projection whose outputs are bit-exact) or the hardware reciprocal /
+// square root (kFast = true, about 1 ulp: the fused raster backward, whose
+// gradients only need fp32 accuracy).
+template <bool kFast>
+__device__ __forceinline__ float fdiv(float a, float b) {
+  if constexpr (kFast) return a * __builtin_amdgcn_rcpf(b);
+  else return a / b;
+}
+template <bool kFast>
+__device__ __forceinline__ float fsqrt(float a) {
+  if constexpr (kFast) return __builtin_amdgcn_sqrtf(a);
+  else return sqrtf(a);
+}
+
 // float -> uint32 as the reference's (uint32_t) cast behaves on its target:
 // truncation toward zero, negatives and NaN saturate to 0, overflow to max.
 __device__ __forceinline__ uint32_t to_u32_sat(float f) {
@@ -35,13 +50,14 @@ __device__ __forceinline__ uint32_t to_u32_sat(float f) {
 // Rotation in GLM column-major storage: R[c][r] = v[3c+r] with the nine
 // values listed in forward.cu:41-45 (equal to the standard row-major
 // rotation matrix entry (c,r)).  Quaternion normalised in-kernel first.
+template <bool kFast = false>
 __device__ __forceinline__ void quat_rot(const float* q, float R[3][3]) {
   float r = q[0], x = q[1], y = q[2], z = q[3];
-  const float norm = sqrtf(r * r + x * x + y * y + z * z);
-  r /= norm;
-  x /= norm;
-  y /= norm;
-  z /= norm;
+  const float norm = fsqrt<kFast>(r * r + x * x + y * y + z * z);
+  r = fdiv<kFast>(r, norm);
+  x = fdiv<kFast>(x, norm);
+  y = fdiv<kFast>(y, norm);
+  z = fdiv<kFast>(z, norm);
   R[0][0] = 1.f - 2.f * (y * y + z * z);
   R[0][1] = 2.f * (x * y - r * z);
   R[0][2] = 2.f * (x * z + r * y);
@@ -83,9 +99,10 @@ __device__ __forceinline__ void glm_transpose(const float A[3][3], float T[3][3]
 
 // Sigma row-major: sig[i][j] = GLM Sigma[i][j] with Sigma = transpose(SR)*SR
 // (forward.cu:34-60).
+template <bool kFast = false>
 __device__ __forceinline__ void cov3d(const float* q, const float* s, float sig[3][3]) {
   float R[3][3], S[3][3], SR[3][3], SRt[3][3], Sg[3][3];
-  quat_rot(q, R);
+  quat_rot<kFast>(q, R);
   glm_diag(s, S);
   glm_mul(S, R, SR);
   glm_transpose(SR, SRt);
@@ -97,6 +114,7 @@ __device__ __forceinline__ void cov3d(const float* q, const float* s, float sig[
 }
 
 // Jacobian (forward.cu:64-122); returns false (J = 0) when clipped.
+template <bool kFast = false>
 __device__ __forceinline__ bool jacobian(float tx, float ty, float tz, float fx,
                                          float fy, float lim_x, float lim_y,
                                          float near_plane, float far_plane,
@@ -106,18 +124,18 @@ __device__ __forceinline__ bool jacobian(float tx, float ty, float tz, float fx,
     return false;
   }
   const float tz2 = tz * tz;
-  const float tx_tz = tx / tz;
-  const float ty_tz = ty / tz;
+  const float tx_tz = fdiv<kFast>(tx, tz);
+  const float ty_tz = fdiv<kFast>(ty, tz);
   const float ctx = fminf(fmaxf(tx_tz, -lim_x), lim_x);
   const float cty = fminf(fmaxf(ty_tz, -lim_y), lim_y);
   const float cx = ctx * tz;
   const float cy = cty * tz;
-  J[0][0] = fx / tz;
+  J[0][0] = fdiv<kFast>(fx, tz);
   J[0][1] = 0.0f;
-  J[0][2] = -(fx * cx) / tz2;
+  J[0][2] = fdiv<kFast>(-(fx * cx), tz2);
   J[1][0] = 0.0f;
-  J[1][1] = fy / tz;
-  J[1][2] = -(fy * cy) / tz2;
+  J[1][1] = fdiv<kFast>(fy, tz);
+  J[1][2] = fdiv<kFast>(-(fy * cy), tz2);
   return true;
 }
 
@@ -153,15 +171,16 @@ __device__ __forceinline__ void cov2d(const float J[2][3], const float Wm[3][3],
 
 
 // means2D backward (backward.cu:453-497): zero when clipped.
+template <bool kFast = false>
 __device__ __forceinline__ void means2d_bwd(float tx, float ty, float tz, float fx, float fy,
                                             float near_plane, float far_plane, float gmx,
                                             float gmy, float g[3]) {
   g[0] = g[1] = g[2] = 0.f;
   if (tz <= near_plane || tz >= far_plane) return;
   const float z2 = tz * tz;
-  g[0] = -fx * gmx / tz;
-  g[1] = -fy * gmy / tz;
-  g[2] = (fx * tx * gmx / z2) + (fy * ty * gmy / z2);
+  g[0] = fdiv<kFast>(-fx * gmx, tz);
+  g[1] = fdiv<kFast>(-fy * gmy, tz);
+  g[2] = fdiv<kFast>(fx * tx * gmx, z2) + fdiv<kFast>(fy * ty * gmy, z2);
 }
 
 // cov2D chain backward (backward.cu:426-439) for G2 = dL/dcov2D (2,2):
@@ -203,6 +222,7 @@ __device__ __forceinline__ void cov2d_chain_bwd(const float G2[2][2], const floa
 
 // Jacobian backward (backward.cu:201-272): clamp mask on tx/tz, ty/tz, but
 // the unclamped tx, ty in dJ02/dtz and dJ12/dtz; zero when clipped.
+template <bool kFast = false>
 __device__ __forceinline__ void jacobian_bwd(float tx, float ty, float tz, float fx, float fy,
                                              float lim_x, float lim_y, float near_plane,
                                              float far_plane, const float dJ[2][3],
@@ -211,16 +231,16 @@ __device__ __forceinline__ void jacobian_bwd(float tx, float ty, float tz, float
   if (tz <= near_plane || tz >= far_plane) return;
   const float tz2 = tz * tz;
   const float tz3 = tz2 * tz;
-  const float tx_tz = tx / tz;
-  const float ty_tz = ty / tz;
+  const float tx_tz = fdiv<kFast>(tx, tz);
+  const float ty_tz = fdiv<kFast>(ty, tz);
   const float xm = (tx_tz < -lim_x || tx_tz > lim_x) ? 0.0f : 1.0f;
   const float ym = (ty_tz < -lim_y || ty_tz > lim_y) ? 0.0f : 1.0f;
-  const float dJ00_dtz = -fx / tz2;
-  const float dJ02_dtx = xm * (-fx / tz2);
-  const float dJ02_dtz = xm * (2.0f * fx * tx / tz3);
-  const float dJ11_dtz = -fy / tz2;
-  const float dJ12_dty = ym * (-fy / tz2);
-  const float dJ12_dtz = ym * (2.0f * fy * ty / tz3);
+  const float dJ00_dtz = fdiv<kFast>(-fx, tz2);
+  const float dJ02_dtx = xm * fdiv<kFast>(-fx, tz2);
+  const float dJ02_dtz = xm * fdiv<kFast>(2.0f * fx * tx, tz3);
+  const float dJ11_dtz = fdiv<kFast>(-fy, tz2);
+  const float dJ12_dty = ym * fdiv<kFast>(-fy, tz2);
+  const float dJ12_dtz = ym * fdiv<kFast>(2.0f * fy * ty, tz3);
   g[0] = dJ[0][2] * dJ02_dtx;
   g[1] = dJ[1][2] * dJ12_dty;
   g[2] = dJ[0][0] * dJ00_dtz + dJ[0][2] * dJ02_dtz + dJ[1][1] * dJ11_dtz + dJ[1][2] * dJ12_dtz;
@@ -230,14 +250,15 @@ __device__ __forceinline__ void jacobian_bwd(float tx, float ty, float tz, float
 // dL/dSigma[i*3+j]: grad_s[k] = (2 R^T G R)[k][k] * s[k]; grad_q by the
 // reference's elementwise (Hadamard) sums over S * dR/dq (the quaternion is
 // normalised again without a chain through the normalisation).
+template <bool kFast = false>
 __device__ __forceinline__ void cov3d_bwd(const float Gm[3][3], const float* q, const float* s,
                                           float gq[4], float gs[3]) {
   float r = q[0], x = q[1], y = q[2], z = q[3];
-  const float norm = sqrtf(r * r + x * x + y * y + z * z);
-  r /= norm;
-  x /= norm;
-  y /= norm;
-  z /= norm;
+  const float norm = fsqrt<kFast>(r * r + x * x + y * y + z * z);
+  r = fdiv<kFast>(r, norm);
+  x = fdiv<kFast>(x, norm);
+  y = fdiv<kFast>(y, norm);
+  z = fdiv<kFast>(z, norm);
   float S[3][3], R[3][3];
   glm_diag(s, S);
   R[0][0] = 1.f - 2.f * (y * y + z * z);

@@ -8,6 +8,7 @@
 // follows the reference source expression by expression (no contraction);
 // the cuBLAS matmul chain is a left-to-right fmaf dot product over k.
 #include "geom_math.h"
+#include "fast_trig.h"
 #include "hrf_internal.h"
 
 namespace hrf {
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(256) void k_project(ProjectParams p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) amp[i] = 0.0f;
   for (int c = 0; c < C; ++c) {
-    float sv, cvv;
-    sincosf(p.phase[g * C + c], &sv, &cvv);
+    float sv, cvv;  // a few 1e-7 absolute for any phase: ample for gradients
+    sincos_big(p.phase[g * C + c], &sv, &cvv);
     const float col = p.colours[g * C + c];
     amp[2 * c] = col * cvv;
     amp[2 * c + 1] = col * sv;
@@ -157,8 +158,8 @@ __global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) Wm[i][j] = p.view[i * 3 + j];
   float J[2][3], sig[3][3], JW[2][3], cv[2][2];
-  jacobian(tx, ty, tz, p.fx, p.fy, p.lim_x, p.lim_y, p.near_plane, p.far_plane, J);
-  cov3d(p.quats + g * 4, p.scales + g * 3, sig);
+  jacobian<true>(tx, ty, tz, p.fx, p.fy, p.lim_x, p.lim_y, p.near_plane, p.far_plane, J);
+  cov3d<true>(p.quats + g * 4, p.scales + g * 3, sig);
   cov2d(J, Wm, sig, JW, cv);
 
   // grad means2D (accumulated by the render backward, already scaled by
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
   if (dcx != 0.f || dcy != 0.f || dcz != 0.f) {
     const float cx = cv[0][0], cy = cv[0][1], cz = cv[1][0], cw = cv[1][1];
     const float det = cx * cw - cy * cz;
-    const float di = 1.0f / det;
+    const float di = __builtin_amdgcn_rcpf(det);
     const float a1 = cw * di * di;
     const float a2 = -cy * di * di;
     const float a3 = cx * di * di;
@@ -183,16 +184,16 @@ __global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
   const float G2[2][2] = {{gxx, gxy}, {gxy, gyy}};
 
   float gm[3], dSig[3][3], dJ[2][3], gj[3];
-  means2d_bwd(tx, ty, tz, p.fx, p.fy, p.near_plane, p.far_plane, gmx, gmy, gm);
+  means2d_bwd<true>(tx, ty, tz, p.fx, p.fy, p.near_plane, p.far_plane, gmx, gmy, gm);
   cov2d_chain_bwd(G2, J, Wm, sig, JW, dSig, dJ);
-  jacobian_bwd(tx, ty, tz, p.fx, p.fy, p.lim_x, p.lim_y, p.near_plane, p.far_plane, dJ, gj);
+  jacobian_bwd<true>(tx, ty, tz, p.fx, p.fy, p.lim_x, p.lim_y, p.near_plane, p.far_plane, dJ, gj);
   p.g_cam[g * 3 + 0] = gm[0] + gj[0];
   p.g_cam[g * 3 + 1] = gm[1] + gj[1];
   p.g_cam[g * 3 + 2] = gm[2] + gj[2];
   p.g_z[g] = 0.0f;
 
   float gq[4], gs[3];
-  cov3d_bwd(dSig, p.quats + g * 4, p.scales + g * 3, gq, gs);
+  cov3d_bwd<true>(dSig, p.quats + g * 4, p.scales + g * 3, gq, gs);
 #pragma unroll
   for (int i = 0; i < 4; ++i) p.g_quat[g * 4 + i] = gq[i];
 #pragma unroll
@@ -201,8 +202,8 @@ __global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
   // Colour / phase from the per-Gaussian sums A_c = sum dcol*g_re,
   // B_c = sum dcol*g_im (backward_splat.cu:251-257 summed over pixels).
   for (int c = 0; c < C; ++c) {
-    float sv, cvv;
-    sincosf(p.phase[g * C + c], &sv, &cvv);
+    float sv, cvv;  // a few 1e-7 absolute for any phase: ample for gradients
+    sincos_big(p.phase[g * C + c], &sv, &cvv);
     const float A = a[5 + c], B = a[5 + C + c];
     const float col = p.colours[g * C + c];
     p.g_col[g * C + c] = cvv * A + sv * B;
