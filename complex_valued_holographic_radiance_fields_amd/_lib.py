@@ -61,6 +61,17 @@ class HrfParamGrads(ctypes.Structure):
                  "pre_plane")]
 
 
+class HrfAdanTensor(ctypes.Structure):
+    _fields_ = [("param", _vp), ("grad", _vp), ("exp_avg", _vp), ("exp_avg_sq", _vp),
+                ("exp_avg_diff", _vp), ("neg_pre_grad", _vp), ("numel", _i64), ("lr", _f64),
+                ("step", _i64), ("init_neg_pre_grad", _i32)]
+
+
+class HrfAdanConfig(ctypes.Structure):
+    _fields_ = [("beta1", _f64), ("beta2", _f64), ("beta3", _f64), ("eps", _f64),
+                ("weight_decay", _f64), ("clip_global_grad_norm", _f64), ("no_prox", _i32)]
+
+
 _P = ctypes.POINTER
 # name -> (restype, argtypes); exactly the entry points of include/hrf.h.
 SIGNATURES = {
@@ -83,6 +94,10 @@ SIGNATURES = {
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
     "hrf_asm_multidistance_adjoint": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp,
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
+    "hrf_grad_norm_workspace_size": (_sz, [_P(_i64), _i32]),
+    "hrf_grad_norm": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "hrf_scale_grads": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _vp, _vp]),
+    "hrf_adan_step": (ctypes.c_int, [_P(HrfAdanTensor), _i32, _P(HrfAdanConfig), _vp, _vp]),
     "hrf_preprocess_workspace_size": (_sz, [_i64, _i32, _i32]),
     "hrf_preprocess_select": (ctypes.c_int, [_P(HrfSceneParams), _vp, _vp, _f32, _f32, _vp, _sz,
                                              _vp, _P(_i64)]),

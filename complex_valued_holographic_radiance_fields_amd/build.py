@@ -39,6 +39,7 @@ SOURCES = [
     "asm_fft.hip",
     "hrf_capi.hip",
     "preprocess.hip",
+    "optim.hip",
     "hrf_trace.hip",
 ]
 

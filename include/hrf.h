@@ -373,6 +373,59 @@ int hrf_preprocess_backward(const hrf_scene_params* params, const float* R,
                             const hrf_selected_grads* grads, const hrf_param_grads* out,
                             void* ws, size_t ws_bytes, void* stream);
 
+/* ---------------- optimizer step (train.py:319-324) -----------------------
+ * The reference clips the global gradient norm (torch.nn.utils.clip_grad_norm_
+ * (parameters, 1.0)) and then steps Adan (utils/optimizer.py:288-466, the
+ * foreach path _multi_tensor_adan, :538-589) over the seven parameter
+ * tensors.  Here: one pass for the norm (fixed-order partial sums, the clip
+ * coefficient formed on the device), one pass for the update. */
+
+/* Scratch of hrf_grad_norm: one float per 2048-element chunk of each tensor
+ * plus one. */
+size_t hrf_grad_norm_workspace_size(const int64_t* numels, int32_t num_tensors);
+
+/* total_norm = ||all gradients||_2 and clip_coef = min(max_norm /
+ * (total_norm + 1e-6), 1) (NaN propagates), both device floats (either may
+ * be NULL), as clip_grad_norm_ forms them (torch/nn/utils/clip_grad.py).
+ * grads: host array of device pointers.  Replaces the norm half of
+ * train.py:319. */
+int hrf_grad_norm(const float* const* grads, const int64_t* numels, int32_t num_tensors,
+                  float max_norm, float* total_norm, float* clip_coef, void* ws,
+                  size_t ws_bytes, void* stream);
+
+/* grads *= *coef (device scalar): the rescaling half of clip_grad_norm_. */
+int hrf_scale_grads(float* const* grads, const int64_t* numels, int32_t num_tensors,
+                    const float* coef, void* stream);
+
+typedef struct hrf_adan_tensor {
+  float* param;        /* updated in place */
+  float* grad;         /* read; left holding the gradient times the scales */
+  float* exp_avg;      /* Adan state, as the reference names it */
+  float* exp_avg_sq;
+  float* exp_avg_diff;
+  float* neg_pre_grad;
+  int64_t numel;
+  double lr;           /* the tensor's group learning rate */
+  int64_t step;        /* the group's step count for this step (>= 1) */
+  int32_t init_neg_pre_grad; /* 1: neg_pre_grad = -grad first (step 1 or no
+                                 state, optimizer.py:439-441) */
+} hrf_adan_tensor;
+
+typedef struct hrf_adan_config {
+  double beta1, beta2, beta3; /* (0.98, 0.92, 0.99) in the reference */
+  double eps;                 /* 1e-8 */
+  double weight_decay;        /* 0 */
+  double clip_global_grad_norm; /* Adan's own max_grad_norm clip (1 when 0) */
+  int32_t no_prox;
+} hrf_adan_config;
+
+/* One Adan step over all tensors (_multi_tensor_adan, op for op in float32,
+ * scalars formed in double on the host).  grad_scale (device float, may be
+ * NULL) multiplies the gradients first: passing hrf_grad_norm's clip_coef
+ * folds clip_grad_norm_'s rescaling into this pass. */
+int hrf_adan_step(const hrf_adan_tensor* tensors, int32_t num_tensors,
+                  const hrf_adan_config* cfg, const float* grad_scale, void* stream);
+
 /* ---------------- stage tracing (no counterpart in the reference, which
  * prints per-phase CUDA event times from train.py:263-344) ---------------- */
 

@@ -550,3 +550,65 @@ def preprocess_backward(grads, means, pre_quats, pre_scales, colours, pre_phase,
     out["pre_opac"][idx] = _f32(grads["opacities"]) * (s * (np.float32(1.0) - s))
     out["pre_plane"][idx] = _f32(grads["plane_probs"]) * _ste_softmax(_f32(pre_plane)[idx])
     return out
+
+
+# ----------------------------------------------------- optimizer step
+# train.py:319-324: torch.nn.utils.clip_grad_norm_(parameters, 1.0), then
+# Adan.step() (utils/optimizer.py:288-466), whose foreach path
+# _multi_tensor_adan (:538-589) the reference runs.  numpy float32, op by op.
+
+def clip_grad_norm(grads, max_norm):
+    """(total_norm, clip_coef, scaled grads): total = ||all grads||_2
+    (accumulated in float64, rounded once), coef = clamp(max_norm / (total +
+    1e-6), max=1) in float32 with NaN propagating (torch.clamp), every
+    gradient times coef (torch/nn/utils/clip_grad.py)."""
+    gs = [_f32(g) for g in grads]
+    ss = sum(float(np.sum(g.astype(np.float64) ** 2)) for g in gs)
+    total = np.float32(np.sqrt(ss))
+    coef = np.float32(max_norm) / (total + np.float32(1e-6))
+    coef = np.float32(1.0) if coef > np.float32(1.0) else np.float32(coef)
+    return total, coef, [g * coef for g in gs]
+
+
+def adan_step(p, g, exp_avg, exp_avg_sq, exp_avg_diff, neg_pre_grad, *, lr, step,
+              betas=(0.98, 0.92, 0.99), eps=1e-8, weight_decay=0.0, no_prox=False,
+              clip=1.0, init_neg_pre_grad=None):
+    """One Adan update of one tensor (optimizer.py:429-441 state set-up,
+    :556-589 the update); returns the new (p, g, exp_avg, exp_avg_sq,
+    exp_avg_diff, neg_pre_grad).  Python-float scalars (bias corrections,
+    step sizes) are formed in double and rounded to float32 where they meet
+    the tensors, as torch does; init_neg_pre_grad defaults to step == 1."""
+    f = np.float32
+    b1, b2, b3 = (float(b) for b in betas)
+    p, g, m, n, d = (_f32(x).copy() for x in (p, g, exp_avg, exp_avg_sq, exp_avg_diff))
+    q = _f32(neg_pre_grad).copy()
+    if init_neg_pre_grad is None:
+        init_neg_pre_grad = step == 1
+    if init_neg_pre_grad:
+        q = g * f(-clip)                                 # p.grad.clone().mul_(-clip)
+    bc1, bc2, bc3 = 1.0 - b1 ** step, 1.0 - b2 ** step, 1.0 - b3 ** step
+    g = g * f(clip)
+    q = q + g
+    m = m * f(b1)
+    m = m + f(1.0 - b1) * g
+    d = d * f(b2)
+    d = d + f(1.0 - b2) * q
+    q = q * f(b2)
+    q = q + g
+    n = n * f(b3)
+    n = n + f(1.0 - b3) * q * q
+    denom = np.sqrt(n)
+    denom = denom / f(np.sqrt(bc3))
+    denom = denom + f(eps)
+    step_size_diff = f(lr * b2 / bc2)
+    step_size = f(lr / bc1)
+    if no_prox:
+        p = p * f(1.0 - lr * weight_decay)
+        p = p + (-step_size) * (m / denom)
+        p = p + (-step_size_diff) * (d / denom)
+    else:
+        p = p + (-step_size) * (m / denom)
+        p = p + (-step_size_diff) * (d / denom)
+        p = p / f(1.0 + lr * weight_decay)
+    q = np.zeros_like(q) + f(-1.0) * g
+    return p, g, m, n, d, q

@@ -823,3 +823,94 @@ def test_preprocess_backward_finite_differences(oracle_mod):
     # rows that were not selected get zero gradients
     rest = np.setdiff1d(np.arange(len(prm[0])), idx)
     assert np.all(got["means"][rest] == 0) and np.all(got["pre_plane"][rest] == 0)
+
+
+# ------------------------------------------------------- optimizer step
+# The oracle's clip_grad_norm / adan_step (train.py:319-324,
+# utils/optimizer.py:288-589) are pinned by closed forms written from the
+# algorithm's definition (Adan, arXiv:2208.06677, Algorithm 1, with the
+# reference's bias corrections) in float64, and by the special cases where
+# betas vanish.
+
+def _adan_seq(oracle_mod, grads, lr=0.01, **kw):
+    n = grads[0].shape
+    p = np.full(n, 0.5, np.float32)
+    st = [np.zeros(n, np.float32) for _ in range(4)]
+    for k, g in enumerate(grads, start=1):
+        p, _, *st = oracle_mod.adan_step(p, g, *st, lr=lr, step=k, **kw)
+    return p, st
+
+
+def test_adan_first_step_closed_form(oracle_mod):
+    """Step 1: m = (1-b1) g, diff = 0, n = (1-b3) g^2, so the update is
+    lr * g / (|g| + eps) and neg_pre_grad ends as -g."""
+    g = np.array([3.0, -4.0, 1e-3, -2.5e-6, 0.0], np.float32)
+    p, (m, n, d, q) = _adan_seq(oracle_mod, [g], lr=0.01)
+    g64 = g.astype(np.float64)
+    np.testing.assert_allclose(p, 0.5 - 0.01 * g64 / (np.abs(g64) + 1e-8), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(m, 0.02 * g64, rtol=1e-6)
+    np.testing.assert_allclose(n, 0.01 * g64 ** 2, rtol=1e-5)
+    np.testing.assert_array_equal(d, 0.0)
+    np.testing.assert_array_equal(q, -g)
+
+
+def test_adan_two_steps_float64_recurrence(oracle_mod):
+    """Two steps against Algorithm 1 in float64: m = b1 m + (1-b1) g,
+    diff = b2 diff + (1-b2)(g - g_prev), n = b3 n + (1-b3)(g + b2 (g -
+    g_prev))^2, p -= lr/bc1 m / (sqrt(n/bc3) + eps) + lr b2/bc2 diff / (...)."""
+    rng = np.random.default_rng(5)
+    g1, g2 = (rng.normal(size=64).astype(np.float32) for _ in range(2))
+    b1, b2, b3, lr, eps = 0.98, 0.92, 0.99, 0.003, 1e-8
+    p, _ = _adan_seq(oracle_mod, [g1, g2], lr=lr)
+    a1, a2 = g1.astype(np.float64), g2.astype(np.float64)
+    m1, n1 = (1 - b1) * a1, (1 - b3) * a1 ** 2
+    p1 = 0.5 - lr / (1 - b1) * m1 / (np.sqrt(n1 / (1 - b3)) + eps)
+    m2 = b1 * m1 + (1 - b1) * a2
+    d2 = (1 - b2) * (a2 - a1)
+    n2 = b3 * n1 + (1 - b3) * (a2 + b2 * (a2 - a1)) ** 2
+    den = np.sqrt(n2 / (1 - b3 ** 2)) + eps
+    p2 = p1 - lr / (1 - b1 ** 2) * m2 / den - lr * b2 / (1 - b2 ** 2) * d2 / den
+    np.testing.assert_allclose(p, p2, rtol=2e-6, atol=1e-8)
+
+
+def test_adan_vanishing_betas(oracle_mod):
+    """b1 = b3 = 0: m = g, n = q^2 with q = g + b2 (g - g_prev); the diff
+    term alone carries b2: p2 = p1 - lr g2/(|q|+eps) - lr b2/(1-b2^2) (1-b2)
+    (g2 - g1)/(|q|+eps)."""
+    g1 = np.array([1.0, -2.0, 0.5], np.float32)
+    g2 = np.array([0.25, 1.0, -0.75], np.float32)
+    b2, lr = 0.5, 0.1
+    p, _ = _adan_seq(oracle_mod, [g1, g2], lr=lr, betas=(0.0, b2, 0.0))
+    a1, a2 = g1.astype(np.float64), g2.astype(np.float64)
+    p1 = 0.5 - lr * a1 / (np.abs(a1) + 1e-8)
+    q = np.abs(a2 + b2 * (a2 - a1)) + 1e-8
+    p2 = p1 - lr * a2 / q - lr * b2 / (1 - b2 ** 2) * (1 - b2) * (a2 - a1) / q
+    np.testing.assert_allclose(p, p2, rtol=1e-6)
+
+
+def test_adan_weight_decay_forms(oracle_mod):
+    """Decoupled decay: p / (1 + lr wd) after the step (prox form), p (1 -
+    lr wd) before it (no_prox)."""
+    g = np.array([2.0, -1.0], np.float32)
+    lr, wd = 0.05, 0.3
+    base = 0.5 - lr * g.astype(np.float64) / (np.abs(g) + 1e-8)
+    p, _ = _adan_seq(oracle_mod, [g], lr=lr, weight_decay=wd)
+    np.testing.assert_allclose(p, base / (1 + lr * wd), rtol=1e-6)
+    p, _ = _adan_seq(oracle_mod, [g], lr=lr, weight_decay=wd, no_prox=True)
+    np.testing.assert_allclose(p, 0.5 * (1 - lr * wd) - lr * g / (np.abs(g) + 1e-8), rtol=1e-6)
+
+
+def test_clip_grad_norm_closed_forms(oracle_mod):
+    """||(3, 4)|| = 5 -> coef = 1 / (5 + 1e-6); a norm below max leaves the
+    gradients (coef exactly 1); a NaN gradient makes the norm and the
+    coefficient NaN (torch.clamp propagates NaN)."""
+    total, coef, out = oracle_mod.clip_grad_norm([np.array([3.0], np.float32),
+                                                  np.array([[4.0]], np.float32)], 1.0)
+    assert total == np.float32(5.0)
+    np.testing.assert_allclose(coef, 1.0 / (5.0 + 1e-6), rtol=1e-7)
+    np.testing.assert_allclose(out[0], 3.0 / 5.0, rtol=1e-6)
+    total, coef, out = oracle_mod.clip_grad_norm([np.array([0.3, 0.4], np.float32)], 1.0)
+    assert coef == np.float32(1.0)
+    np.testing.assert_array_equal(out[0], np.array([0.3, 0.4], np.float32))
+    total, coef, _ = oracle_mod.clip_grad_norm([np.array([np.nan, 1.0], np.float32)], 1.0)
+    assert np.isnan(total) and np.isnan(coef)
