@@ -179,6 +179,64 @@ def measure_preprocess(spec, dev, no_cpu):
     return res
 
 
+def measure_optimizer(spec, dev, no_cpu):
+    """The training step's optimizer side (train.py:319-324): gradient-norm
+    clip + Adan over the seven parameter tensors of the headline scene
+    (utils/optimizer.py:46-54 learning rates), as two HIP passes (norm, then
+    the update with the clip coefficient applied inside it), timed with
+    hipEvents.  Compulsory bytes: the norm reads every gradient (4 B per
+    element); the update reads and writes param, grad and the four state
+    tensors (48 B per element)."""
+    import numpy as np
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import optim
+
+    N, C, P = spec.n, len(spec.wavelengths), spec.planes
+    groups = [("scales", 0.005, 3), ("phase", 0.0025, C), ("colours", 0.0025, C),
+              ("means", 1e-3, 3), ("opacity", 0.025, 1), ("plane assignment", 1e-3, P),
+              ("rot", 0.001, 4)]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    ps = [torch.randn((N, k), generator=gen, device=dev).requires_grad_() for _, _, k in groups]
+    for p in ps:
+        p.grad = torch.randn(p.shape, generator=gen, device=dev) * 0.1
+    opt = optim.Adan([{"params": [p], "lr": lr, "name": nm} for p, (nm, lr, _) in zip(ps, groups)],
+                     lr=0, eps=1e-8)
+    for _ in range(3):
+        optim.training_step_update(opt, ps, 1.0)
+    torch.cuda.synchronize()
+    reps = 20
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ms = []
+    for _ in range(reps):
+        ev[0].record()
+        optim.training_step_update(opt, ps, 1.0)
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms.append(ev[0].elapsed_time(ev[1]))
+    ms = float(np.median(ms))
+    E = sum(p.numel() for p in ps)
+    alg = 4 * E + 48 * E
+    ach = alg / (ms * 1e-3) / 1e9
+    res = {"workload": f"{spec.name} parameters: 7 tensors, {E} elements (N={N})",
+           "ms": round(ms, 4), "timing": f"median of {reps}, clip + Adan step",
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "alg_bytes": alg},
+           "cpu_torch": None}
+    if not no_cpu:
+        try:
+            from oracle import cpu_baseline
+
+            cms = cpu_baseline.time_adan([(N, k) for _, _, k in groups],
+                                         [lr for _, lr, _ in groups])
+            res["cpu_torch"] = {"ms": round(cms, 1), "cores": torch.get_num_threads(),
+                                "kind": "reference clip_grad_norm_ + _multi_tensor_adan on "
+                                        "CPU torch (oracle/cpu_baseline.py), full N, best of 3"}
+        except Exception as e:  # reported, never fatal to the GPU measurement
+            res["cpu_torch"] = {"failed": repr(e)}
+    return res
+
+
 def bench_cfg3(args, dev):
     """Config 3, the propagation-only microbench: a (3, 2048, 2048) field to
     8 distances on the 4096 grid, forward (D*C outputs) + adjoint (sum over
@@ -381,6 +439,7 @@ def main():
                 "bytes_per_launch": int(B["per_launch"][dom]), "traffic_source": src}
 
     pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
+    opt_step = measure_optimizer(spec, dev, args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -428,6 +487,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "preprocess": pre,
+        "optimizer": opt_step,
     }
     print(json.dumps(out), flush=True)
 

@@ -254,3 +254,53 @@ def time_preprocess(params: dict, reps: int = 2):
         fwd.append((t1 - t0) * 1e3)
         bwd.append((t2 - t1) * 1e3)
     return min(fwd), min(bwd)
+
+
+# ------------------------------------------------------- optimizer step
+def adan_foreach_torch(params, grads, states, lrs, step, betas=(0.98, 0.92, 0.99), eps=1e-8):
+    """The reference's clip + Adan step on CPU torch: clip_grad_norm_
+    (train.py:319) then the foreach sequence of _multi_tensor_adan
+    (utils/optimizer.py:538-589), one parameter group per tensor."""
+    b1, b2, b3 = betas
+    for p, g in zip(params, grads):
+        p.grad = g
+    torch.nn.utils.clip_grad_norm_(params, 1.0)
+    for i, p in enumerate(params):
+        m, n, d, q = states[i]
+        g = [p.grad]
+        if step == 1:
+            q.copy_(p.grad).mul_(-1.0)
+        bc1, bc2, bc3 = 1 - b1 ** step, 1 - b2 ** step, 1 - b3 ** step
+        torch._foreach_mul_(g, 1.0)
+        torch._foreach_add_([q], g)
+        torch._foreach_mul_([m], b1)
+        torch._foreach_add_([m], g, alpha=1 - b1)
+        torch._foreach_mul_([d], b2)
+        torch._foreach_add_([d], [q], alpha=1 - b2)
+        torch._foreach_mul_([q], b2)
+        torch._foreach_add_([q], g)
+        torch._foreach_mul_([n], b3)
+        torch._foreach_addcmul_([n], [q], [q], value=1 - b3)
+        denom = torch._foreach_sqrt([n])
+        torch._foreach_div_(denom, math.sqrt(bc3))
+        torch._foreach_add_(denom, eps)
+        torch._foreach_addcdiv_([p.data], [m], denom, value=-lrs[i] / bc1)
+        torch._foreach_addcdiv_([p.data], [d], denom, value=-lrs[i] * b2 / bc2)
+        torch._foreach_div_([p.data], 1.0)
+        torch._foreach_zero_([q])
+        torch._foreach_add_([q], g, alpha=-1.0)
+
+
+def time_adan(shapes, lrs, reps: int = 3):
+    """Best-of-reps time (ms) of one clip + Adan step over
+    parameter tensors of the given shapes on CPU torch."""
+    gen = torch.Generator().manual_seed(0)
+    params = [torch.randn(s, generator=gen) for s in shapes]
+    states = [[torch.zeros(s) for _ in range(4)] for s in shapes]
+    best = float("inf")
+    for k in range(1, reps + 1):
+        grads = [torch.randn(s, generator=gen) * 0.1 for s in shapes]
+        t0 = time.perf_counter()
+        adan_foreach_torch(params, grads, states, lrs, k)
+        best = min(best, (time.perf_counter() - t0) * 1e3)
+    return best
