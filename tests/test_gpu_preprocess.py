@@ -149,3 +149,21 @@ def test_headline_params_reproduce_the_scene(hrf, oracle_mod):
     assert np.abs(dphi).max() < 3e-5
     np.testing.assert_array_equal(out[7].cpu().numpy(), sc.pprobs)
     np.testing.assert_allclose(out[6].cpu().numpy(), sc.opac, rtol=1e-6)
+
+
+def test_checkpoint_to_preprocess(hrf, tmp_path):
+    """A reference-format checkpoint of the parameters, loaded onto the GPU,
+    feeds the preprocess exactly like the arrays it was saved from."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import checkpoint, preprocess
+
+    prm = _params(n=2000, seed=21)
+    keys = ("means", "pre_act_quats", "pre_act_scales", "colours", "pre_act_phase",
+            "pre_act_opacities", "pre_act_plane_assignment")
+    path = str(tmp_path / "scene.pth")
+    checkpoint.save_gaussians({k: torch.from_numpy(a) for k, a in zip(keys, prm[:7])}, path)
+    g = checkpoint.load_gaussians(path, device="cuda")
+    a = preprocess.forward(*[g[k] for k in keys], _t(prm[7]), _t(prm[8]), 1.0, 1000.0)
+    b = _run(prm, 1.0, 1000.0)
+    for x, y in zip(a, b):
+        torch.testing.assert_close(x, y, rtol=0, atol=0, equal_nan=True)
