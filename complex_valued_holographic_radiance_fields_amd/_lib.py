@@ -94,6 +94,12 @@ SIGNATURES = {
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
     "hrf_asm_multidistance_adjoint": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp,
                                                      _vp, _f64, _f32, _vp, _vp, _sz, _vp]),
+    "hrf_recon_fields": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i32,
+                                        _vp, _vp]),
+    "hrf_recon_intensity": (ctypes.c_int, [_vp, _i64, _vp, _vp]),
+    "hrf_recon_intensity_backward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp]),
+    "hrf_recon_fields_backward": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
+                                                 _i32, _vp, _vp, _vp, _vp]),
     "hrf_grad_norm_workspace_size": (_sz, [_P(_i64), _i32]),
     "hrf_grad_norm": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "hrf_scale_grads": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _vp, _vp]),

@@ -40,6 +40,7 @@ SOURCES = [
     "hrf_capi.hip",
     "preprocess.hip",
     "optim.hip",
+    "recon.hip",
     "hrf_trace.hip",
 ]
 

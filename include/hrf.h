@@ -373,6 +373,36 @@ int hrf_preprocess_backward(const hrf_scene_params* params, const float* R,
                             const hrf_selected_grads* grads, const hrf_param_grads* out,
                             void* ws, size_t ws_bytes, void* stream);
 
+/* ---------------- loss-side reconstruction (utils/propagator.py:548-636) ---
+ * propagator._reconstruct_impl: for each frame f and channel c with laser
+ * power w = laser_powers[f][c] != 0 (K such pairs, listed as frames[k],
+ * channels[k], powers[k], scales[k] = phase_scale[c]), the hologram field
+ * w a_c e^{i s phi_f}, propagated to every depth (the multi-distance ASM
+ * entry points above) and its intensity |u|^2.  amplitude (C, hw), phase
+ * (F, hw) float32; fields and gradients complex64 interleaved. */
+
+/* fields (K, hw) from the amplitude and phase maps (generate_complex_field,
+ * propagator.py:605-609). */
+int hrf_recon_fields(const float* amplitude, const float* phase, int32_t F, int32_t C,
+                     int64_t hw, const int32_t* frames, const int32_t* channels,
+                     const float* powers, const float* scales, int32_t K, void* fields,
+                     void* stream);
+
+/* intensity[i] = |field[i]|^2 (calculate_amplitude(.)**2, :626). */
+int hrf_recon_intensity(const void* field, int64_t n, float* intensity, void* stream);
+
+/* grad_field = 2 grad_intensity field (the backward of |u|^2). */
+int hrf_recon_intensity_backward(const void* field, const float* grad_intensity, int64_t n,
+                                 void* grad_field, void* stream);
+
+/* Backward of hrf_recon_fields: grad_amplitude (C, hw) and grad_phase
+ * (F, hw), summed over the pairs (fully overwritten). */
+int hrf_recon_fields_backward(const float* amplitude, const float* phase, int32_t F, int32_t C,
+                              int64_t hw, const int32_t* frames, const int32_t* channels,
+                              const float* powers, const float* scales, int32_t K,
+                              const void* grad_fields, float* grad_amplitude,
+                              float* grad_phase, void* stream);
+
 /* ---------------- optimizer step (train.py:319-324) -----------------------
  * The reference clips the global gradient norm (torch.nn.utils.clip_grad_norm_
  * (parameters, 1.0)) and then steps Adan (utils/optimizer.py:288-466, the

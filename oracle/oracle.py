@@ -612,3 +612,59 @@ def adan_step(p, g, exp_avg, exp_avg_sq, exp_avg_diff, neg_pre_grad, *, lr, step
         p = p / f(1.0 + lr * weight_decay)
     q = np.zeros_like(q) + f(-1.0) * g
     return p, g, m, n, d, q
+
+
+# ------------------------------------------------- loss-side reconstruction
+# propagator._reconstruct_impl (utils/propagator.py:548-636) with the
+# reference's own band-limited ASM (asm_forward above) as the propagation:
+# float64 fields w a e^{i s phi}, propagated to each depth, |u|^2.
+
+def reconstruct(phases, amplitude, wavelengths, pitch, distances, S, aperture, powers,
+                scales=None, get_complex=False):
+    """-> (F, D, C, S, S) intensities (complex with get_complex)."""
+    phases = np.asarray(phases, np.float64)
+    amplitude = np.asarray(amplitude, np.float64)
+    F, C, D = phases.shape[0], amplitude.shape[0], len(distances)
+    powers = np.asarray(powers, np.float64).reshape(F, C)
+    scales = np.ones(C) if scales is None else np.asarray(scales, np.float64)
+    out = np.zeros((F, D, C, S, S), np.complex128 if get_complex else np.float64)
+    for f in range(F):
+        for c in range(C):
+            if powers[f, c] == 0:
+                continue
+            field = powers[f, c] * amplitude[c] * np.exp(1j * phases[f] * scales[c])
+            for d in range(D):
+                u = asm_forward(field, wavelengths[c], pitch, distances[d], S, aperture)
+                out[f, d, c] = u if get_complex else np.abs(u) ** 2
+    return out
+
+
+def reconstruct_backward(grad, phases, amplitude, wavelengths, pitch, distances, S, aperture,
+                         powers, scales=None):
+    """Gradients of sum(grad * reconstruct(...)) w.r.t. (phases, amplitude):
+    dL/du = 2 g u, the propagation's adjoint (asm_adjoint), then
+    dL/da = w Re(gz e^{-i s phi}), dL/dphi = s w a Im(gz e^{-i s phi})."""
+    phases = np.asarray(phases, np.float64)
+    amplitude = np.asarray(amplitude, np.float64)
+    grad = np.asarray(grad, np.float64)
+    F, C, D = phases.shape[0], amplitude.shape[0], len(distances)
+    powers = np.asarray(powers, np.float64).reshape(F, C)
+    scales = np.ones(C) if scales is None else np.asarray(scales, np.float64)
+    g_ph = np.zeros_like(phases)
+    g_amp = np.zeros_like(amplitude)
+    for f in range(F):
+        for c in range(C):
+            w = powers[f, c]
+            if w == 0:
+                continue
+            e = np.exp(1j * phases[f] * scales[c])
+            field = w * amplitude[c] * e
+            gz = np.zeros((S, S), np.complex128)
+            for d in range(D):
+                u = asm_forward(field, wavelengths[c], pitch, distances[d], S, aperture)
+                gz += asm_adjoint(2.0 * grad[f, d, c] * u, S, S, wavelengths[c], pitch,
+                                  distances[d], S, aperture)
+            t = gz * np.conj(e)
+            g_amp[c] += w * t.real
+            g_ph[f] += scales[c] * w * amplitude[c] * t.imag
+    return g_ph, g_amp

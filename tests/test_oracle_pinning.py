@@ -914,3 +914,53 @@ def test_clip_grad_norm_closed_forms(oracle_mod):
     np.testing.assert_array_equal(out[0], np.array([0.3, 0.4], np.float32))
     total, coef, _ = oracle_mod.clip_grad_norm([np.array([np.nan, 1.0], np.float32)], 1.0)
     assert np.isnan(total) and np.isnan(coef)
+
+
+# -------------------------------------------------- loss-side reconstruction
+# oracle.reconstruct composes the pinned asm_forward with w a e^{i s phi} and
+# |u|^2; its backward is pinned by central differences.  The propagation is
+# the reference's own band-limited kernel; odak's get_propagation_kernel (the
+# reference reconstruction's kernel) is absent, so that choice is unpinned.
+
+def _recon_case():
+    rng = np.random.default_rng(17)
+    S, F, C = 8, 2, 2
+    phases = rng.uniform(-np.pi, np.pi, size=(F, S, S))
+    amp = rng.uniform(0.2, 1.0, size=(C, S, S))
+    powers = np.array([[1.0, 0.0], [0.5, 0.8]])
+    kw = dict(wavelengths=[515e-9, 639e-9], pitch=8e-6, distances=[-2e-3, 1e-3], S=S,
+              aperture=-1.0, powers=powers, scales=[1.0, 0.9])
+    return phases, amp, kw
+
+
+def test_reconstruct_pairs_and_intensity(oracle_mod):
+    """Zero laser power gives zero output; the intensity is |u|^2 of the
+    complex reconstruction."""
+    phases, amp, kw = _recon_case()
+    I = oracle_mod.reconstruct(phases, amp, **kw)
+    U = oracle_mod.reconstruct(phases, amp, get_complex=True, **kw)
+    assert np.all(I[0, :, 1] == 0) and np.all(U[0, :, 1] == 0)
+    np.testing.assert_allclose(I, np.abs(U) ** 2, rtol=1e-12, atol=1e-15)
+    assert I[1, :, 0].max() > 0 and I[1, :, 1].max() > 0
+
+
+def test_reconstruct_backward_finite_differences(oracle_mod):
+    phases, amp, kw = _recon_case()
+    rng = np.random.default_rng(18)
+    grad = rng.normal(size=(2, 2, 2, 8, 8))
+    g_ph, g_amp = oracle_mod.reconstruct_backward(grad, phases, amp, **kw)
+
+    def loss(ph, a):
+        return float(np.sum(grad * oracle_mod.reconstruct(ph, a, **kw)))
+
+    h = 1e-3
+    for (f, i, j) in [(0, 1, 2), (1, 5, 3), (1, 0, 7)]:
+        e = np.zeros_like(phases)
+        e[f, i, j] = h
+        fd = (loss(phases + e, amp) - loss(phases - e, amp)) / (2 * h)
+        assert abs(fd - g_ph[f, i, j]) <= 2e-3 * max(1.0, abs(fd)), (f, i, j, fd, g_ph[f, i, j])
+    for (c, i, j) in [(0, 2, 2), (1, 7, 1)]:
+        e = np.zeros_like(amp)
+        e[c, i, j] = h
+        fd = (loss(phases, amp + e) - loss(phases, amp - e)) / (2 * h)
+        assert abs(fd - g_amp[c, i, j]) <= 2e-3 * max(1.0, abs(fd)), (c, i, j, fd, g_amp[c, i, j])
