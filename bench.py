@@ -237,6 +237,75 @@ def measure_optimizer(spec, dev, no_cpu):
     return res
 
 
+def measure_reconstruction(spec, dev, no_cpu):
+    """The loss side right after the hologram (train.py:272-282): the
+    training propagator (3 frames, laser powers eye(3), one depth per plane
+    distance, band-limited ASM) reconstructs the (3, S, S) phase and
+    amplitude maps and backpropagates a synthetic intensity gradient.
+    Byte model: config 3's (every M x M transform one read + one write),
+    with K = 3 lit (frame, channel) pairs and D depths, plus the elementwise
+    passes (fields, intensities and their backward)."""
+    import numpy as np
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from complex_valued_holographic_radiance_fields_amd.reconstruction import Propagator
+
+    S, M = spec.size, 2 * spec.size
+    dist = [float(d) for d in spec.distances]  # args_prop.distances (train.py:859-866)
+    K, D = 3, len(dist)
+    prop = Propagator(resolution=[S, S], wavelengths=spec.wavelengths, pixel_pitch=scenes.PITCH,
+                      number_of_frames=3, propagator_type="forward", distances=dist,
+                      aperture_size=float(S))
+    gen = torch.Generator(device=dev).manual_seed(3)
+    ph = (torch.rand((3, S, S), generator=gen, device=dev) * 6.28 - 3.14).requires_grad_(True)
+    am = torch.rand((3, S, S), generator=gen, device=dev).requires_grad_(True)
+    g = torch.randn((3, D, 3, S, S), generator=gen, device=dev)
+
+    def step():
+        out = prop.reconstruct(ph, am, no_grad=False)
+        torch.autograd.backward(out, g)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    reps = 10
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(reps):
+        step()
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    fwd_b = K * (8 * S * S + 16 * M * M) + D * K * (32 * M * M + 8 * S * S)
+    adj_b = D * K * (8 * S * S + 32 * M * M) + K * (16 * M * M + 8 * S * S)
+    elem = K * S * S * (8 + 8) + D * K * S * S * (8 + 4) + D * K * S * S * (8 + 4 + 8) \
+        + K * S * S * (8 + 8 + 8)
+    alg = fwd_b + adj_b + elem
+    ach = alg / (ms * 1e-3) / 1e9
+    res = {"workload": f"{spec.name}: 3 frames x 3 channels (eye powers), {D} depths, "
+                       f"{S}x{S} on the {M} grid, fwd+bwd",
+           "ms": round(ms, 4), "timing": f"mean of {reps} (hipEvents)",
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "alg_bytes": alg},
+           "transfer_function": "the reference's band-limited ASM (odak's kernel unavailable)",
+           "cpu_torch": None}
+    if not no_cpu:
+        try:
+            from oracle import cpu_baseline
+
+            x = torch.from_numpy(np.ones((S, S), np.complex64))
+            t0 = time.perf_counter()
+            cpu_baseline.asm_torch(x, spec.wavelengths[0], scenes.PITCH, dist[0], S, float(S))
+            one = (time.perf_counter() - t0) * 1e3
+            res["cpu_torch"] = {"ms": round(one * 2 * D * K, 1), "cores": torch.get_num_threads(),
+                                "kind": "one pure-torch ASM propagation (oracle/cpu_baseline.py)"
+                                        ", scaled by 2*D*K"}
+        except Exception as e:  # reported, never fatal to the GPU measurement
+            res["cpu_torch"] = {"failed": repr(e)}
+    return res
+
+
 def bench_cfg3(args, dev):
     """Config 3, the propagation-only microbench: a (3, 2048, 2048) field to
     8 distances on the 4096 grid, forward (D*C outputs) + adjoint (sum over
@@ -440,6 +509,7 @@ def main():
 
     pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
     opt_step = measure_optimizer(spec, dev, args.no_cpu_baseline)
+    recon = measure_reconstruction(spec, dev, args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -488,6 +558,7 @@ def main():
         "cpu_baseline": cpu,
         "preprocess": pre,
         "optimizer": opt_step,
+        "reconstruction": recon,
     }
     print(json.dumps(out), flush=True)
 

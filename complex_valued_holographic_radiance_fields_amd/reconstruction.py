@@ -11,9 +11,10 @@ differentiable with ``no_grad=False`` (train.py:282).
 
 The pipeline is four HIP steps: the hologram fields w a e^{i s phi} of the
 (frame, channel) pairs with nonzero laser power (``hrf_recon_fields``), the
-multi-distance band-limited ASM (each field transformed once for all
-depths), the intensity (``hrf_recon_intensity``), and the mirror-image
-backward.  The transfer function is the reference's own band-limited ASM
+band-limited ASM to every depth (each field transformed once for all
+depths, through the multi-plane propagation kernels run with negated
+distances: the fused LDS-FFT passes where the grid size has a plan), the
+intensity (``hrf_recon_intensity``), and the mirror-image backward.  The transfer function is the reference's own band-limited ASM
 kernel (cuda_prop, the one the rasterizer's hologram uses); the reference's
 reconstruction takes it from odak's ``get_propagation_kernel``, which is not
 available here, so agreement with odak's kernel is not checked.
@@ -27,8 +28,25 @@ import torch
 from . import _lib, propagation
 
 
-# fields per multi-distance call (its channel limit)
+# fields per propagation call (the ASM entry points' channel limit)
 _BATCH = 3
+
+
+def _fan_out(fields, wavelengths, pitch, distances, S, aperture):
+    """(K,S,S) hologram fields -> (D,K,S,S): each field propagated to every
+    depth.  This is the multi-plane adjoint's data flow (one spectrum per
+    channel, one inverse transform per plane) with the distances negated:
+    conj(T(-d)) = T(d), the band limit depending on d^2 only, so the fused
+    LDS-FFT kernels serve it where the grid size has a plan."""
+    return propagation.multiplane_adjoint(fields, (S, S), wavelengths, pitch,
+                                          [-d for d in distances], S, aperture)
+
+
+def _fan_in(grads, wavelengths, pitch, distances, S, aperture):
+    """Adjoint of _fan_out: (D,K,S,S) -> (K,S,S), summed over the depths
+    (the multi-plane forward with the distances negated)."""
+    return propagation.multiplane(grads, wavelengths, pitch, [-d for d in distances], S,
+                                  aperture)
 
 
 def _pairs(laser_powers: torch.Tensor, F: int, C: int):
@@ -70,8 +88,8 @@ class _Reconstruct(torch.autograd.Function):
             _lib.check(lib.hrf_recon_fields(amplitude.data_ptr(), phases.data_ptr(), F, C, hw,
                                             fr, ch, pw, sc, K, fields.data_ptr(), stream))
         wl = [wavelengths[c] for _, c, _ in pairs]
-        u = torch.cat([propagation.multidistance(fields[k0:k0 + _BATCH], wl[k0:k0 + _BATCH],
-                                                 pitch, distances, S, aperture)
+        u = torch.cat([_fan_out(fields[k0:k0 + _BATCH], wl[k0:k0 + _BATCH], pitch, distances,
+                                S, aperture)
                        for k0 in range(0, K, _BATCH)], dim=1)  # (D,K,S,S)
         if get_complex:
             res = u
@@ -106,9 +124,9 @@ class _Reconstruct(torch.autograd.Function):
                 _lib.check(lib.hrf_recon_intensity_backward(u.data_ptr(), g.data_ptr(), u.numel(),
                                                             gu.data_ptr(), _lib.stream_ptr(dev)))
         wl = [wavelengths[c] for _, c, _ in pairs]
-        gfields = torch.cat([propagation.multidistance_adjoint(
-            gu[:, k0:k0 + _BATCH].contiguous(), (S, S), wl[k0:k0 + _BATCH], pitch, distances, S,
-            aperture) for k0 in range(0, K, _BATCH)], dim=0)
+        gfields = torch.cat([_fan_in(gu[:, k0:k0 + _BATCH].contiguous(), wl[k0:k0 + _BATCH],
+                                     pitch, distances, S, aperture)
+                             for k0 in range(0, K, _BATCH)], dim=0)
         fr, ch, pw, sc = _arrays(pairs, scales)
         g_amp = torch.empty_like(amplitude)
         g_phase = torch.empty_like(phases)
