@@ -83,6 +83,82 @@ __device__ __forceinline__ int block_compact(bool flag, int* s_wt, int* count) {
   return off + __popcll(bal & lt);
 }
 
+// Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
+// only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
+// d = mean - pixel).  alpha_threshold returns that bound widened by 0.1% +
+// 0.01, far beyond the rounding of the exp/power evaluation, or -1 when no
+// pixel can qualify (o*w below 1/255).
+__device__ __forceinline__ float alpha_threshold(float ow) {
+  if (ow * 255.0f < 0.999f) return -1.0f;
+  return 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
+}
+
+// min of q over x1 = mx - px in [xlo, xhi] at a fixed x2 = my - py (or the
+// same with the roles swapped): the 1-D minimiser of the convex quadratic,
+// clamped to the interval.  r11 = 1/a11 (hardware reciprocal): q at any
+// point of the interval bounds the minimum from above, and the minimiser's
+// rounding moves q by a11 (dx)^2, far inside the threshold's margin.
+__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float r11, float x2,
+                                          float lo, float hi) {
+  const float x1 = fminf(fmaxf(-a12 * x2 * r11, lo), hi);
+  return x1 * (a11 * x1 + 2.0f * a12 * x2) + a22 * x2 * x2;
+}
+
+// A Gaussian's cull region q(d) <= thr: conic, reciprocals of its diagonal,
+// and the half-extents of the region's bounding box (widened by 0.01% +
+// 1e-3 px).  pd = false (not positive definite, or NaN): never culled.
+struct CullShape {
+  float cxx, cxy, czz, rxx, rzz, ex, ey;
+  bool pd;
+};
+
+__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz, float thr) {
+  CullShape c;
+  c.cxx = cxx;
+  c.cxy = cxy;
+  c.czz = czz;
+  const float det = cxx * czz - cxy * cxy;
+  c.pd = cxx > 0.0f && czz > 0.0f && det > 0.0f;
+  const float rdet = __builtin_amdgcn_rcpf(det);
+  c.rxx = __builtin_amdgcn_rcpf(cxx);
+  c.rzz = __builtin_amdgcn_rcpf(czz);
+  c.ex = sqrtf(fmaxf(thr * czz * rdet, 0.0f)) * 1.0001f + 1e-3f;
+  c.ey = sqrtf(fmaxf(thr * cxx * rdet, 0.0f)) * 1.0001f + 1e-3f;
+  return c;
+}
+
+// Exact test: does q(d) <= thr hold anywhere in the box of pixel centres
+// [x0, x0+ext] x [y0, y0+ext]?  Boxes outside the region's bounding box are
+// rejected first; q is convex, so if the mean is outside the box the
+// minimum over the box lies on one of its four edges.
+__device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape& c, float thr,
+                                            float x0, float y0, float ext) {
+  if (!c.pd) return true;
+  const float x1 = x0 + ext, y1 = y0 + ext;
+  if (mx + c.ex < x0 || mx - c.ex > x1 || my + c.ey < y0 || my - c.ey > y1) return false;
+  if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
+  const float dxl = mx - x1, dxh = mx - x0, dyl = my - y1, dyh = my - y0;
+  float m = edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyl, dxl, dxh);
+  m = fminf(m, edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyh, dxl, dxh));
+  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxl, dyl, dyh));
+  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxh, dyl, dyh));
+  return m <= thr;
+}
+
+// Forward members without effect.  A Gaussian whose alpha stays below 2^-26
+// at every pixel of the tile (q > 2 ln(o w 2^26) over the tile's pixel
+// centres, widened as above) cannot change T there: alpha T is below half
+// an ulp of T, so T - alpha T rounds back to T, and the termination test and
+// final_T are exactly as if it had been composited.  Its field contribution
+// is below 2^-25 T |amplitude|.  Such members are not staged; the tile's
+// largest such list position still counts as the last contributor for
+// pixels that never terminate (every culled member has power <= 0 there, as
+// a composited one would).  Non-positive-definite conics are never culled.
+__device__ __forceinline__ float invisible_threshold(float ow) {
+  const float thr = 2.0f * __logf(ow * 67108864.0f);  // alpha < 2^-26
+  return fmaxf(thr, 0.0f) * 1.001f + 0.01f;
+}
+
 template <int C>
 __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   constexpr int NQ = rec_quads(C);
@@ -90,6 +166,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   constexpr int kUnroll = 8;
   __shared__ float4 s_rec[kBlock * NQ];
   __shared__ int s_wt[kBlock / 64];
+  __shared__ int s_kcull;  // 1 + the largest list position culled as invisible
 
   int tile, plane;
   map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
@@ -111,25 +188,37 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   int2* const sub_out =
       p.sub_out ? p.sub_out + static_cast<int64_t>(plane) * p.num_pairs + r0 : nullptr;
 
+  const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
+  if (threadIdx.x == 0) s_kcull = 0;
   for (int base = 0; base < n; base += kBlock) {
     if (__syncthreads_and(done)) break;
     const int k = base + static_cast<int>(threadIdx.x);
     bool mem = false;
     int g = 0;
+    float4 rq[2];  // geometry quads; the amplitude quads load at the LDS write
+    float w = 0.0f;
+    const float4* src = nullptr;
     if (k < n) {
       g = p.plist[r0 + k];
       mem = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
             ((p.pmask[g] >> plane) & 1u);
     }
+    if (mem) {
+      src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
+      rq[0] = src[0];
+      rq[1] = src[1];
+      w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
+      const float thr = invisible_threshold(rq[1].z * w);
+      const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y, thr);
+      if (!box_reaches(rq[0].x, rq[0].y, cs, thr, tx0, ty0, static_cast<float>(kTile - 1))) {
+        mem = false;
+        atomicMax(&s_kcull, k + 1);
+      }
+    }
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
     if (mem) {
       if (sub_out) sub_out[listed + pos] = make_int2(g, k);
-      const float4* src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
-      float4 rq[NQ];
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) rq[q] = src[q];
-      const float w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
       // quad 0: (mx, my, kc*i00, kc*i01); quad 1: (kc*i10, kc*i11, o*w, -),
       // kc = -log2(e)/2: the exponent of G = exp2(.) is then a quadratic
       // form with the -1/2 and the change of base folded in.
@@ -138,7 +227,7 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
       s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].x, kBwdConicScale * rq[1].y,
                                         rq[1].z * w, __int_as_float(k + 1));
 #pragma unroll
-      for (int q = 2; q < NQ; ++q) s_rec[pos * NQ + q] = rq[q];
+      for (int q = 2; q < NQ; ++q) s_rec[pos * NQ + q] = src[q];
     }
     // Pad the staged batch to a multiple of kUnroll with members no pixel
     // can use: a positive-definite exponent 1e12 (power > 0), so they never
@@ -185,6 +274,9 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   }
 
   if (sub_out && threadIdx.x == 0) p.sub_cnt_out[tile * p.P + plane] = listed;
+  __syncthreads();
+  // A pixel that never terminated composited every member, culled ones too.
+  if (!done) last = max(last, s_kcull);
   if (inside) {
     const int64_t HW = static_cast<int64_t>(p.W) * p.H;
     const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
@@ -194,68 +286,6 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     p.final_T[plane * HW + pix] = T;
     p.n_contrib[plane * HW + pix] = last;
   }
-}
-
-// Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
-// only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
-// d = mean - pixel).  alpha_threshold returns that bound widened by 0.1% +
-// 0.01, far beyond the rounding of the exp/power evaluation, or -1 when no
-// pixel can qualify (o*w below 1/255).
-__device__ __forceinline__ float alpha_threshold(float ow) {
-  if (ow * 255.0f < 0.999f) return -1.0f;
-  return 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
-}
-
-// min of q over x1 = mx - px in [xlo, xhi] at a fixed x2 = my - py (or the
-// same with the roles swapped): the 1-D minimiser of the convex quadratic,
-// clamped to the interval.  r11 = 1/a11 (hardware reciprocal): q at any
-// point of the interval bounds the minimum from above, and the minimiser's
-// rounding moves q by a11 (dx)^2, far inside the threshold's margin.
-__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float r11, float x2,
-                                          float lo, float hi) {
-  const float x1 = fminf(fmaxf(-a12 * x2 * r11, lo), hi);
-  return x1 * (a11 * x1 + 2.0f * a12 * x2) + a22 * x2 * x2;
-}
-
-// A Gaussian's cull region q(d) <= thr: conic, reciprocals of its diagonal,
-// and the half-extents of the region's bounding box (widened by 0.01% +
-// 1e-3 px).  pd = false (not positive definite, or NaN): never culled.
-struct CullShape {
-  float cxx, cxy, czz, rxx, rzz, ex, ey;
-  bool pd;
-};
-
-__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz, float thr) {
-  CullShape c;
-  c.cxx = cxx;
-  c.cxy = cxy;
-  c.czz = czz;
-  const float det = cxx * czz - cxy * cxy;
-  c.pd = cxx > 0.0f && czz > 0.0f && det > 0.0f;
-  const float rdet = __builtin_amdgcn_rcpf(det);
-  c.rxx = __builtin_amdgcn_rcpf(cxx);
-  c.rzz = __builtin_amdgcn_rcpf(czz);
-  c.ex = sqrtf(fmaxf(thr * czz * rdet, 0.0f)) * 1.0001f + 1e-3f;
-  c.ey = sqrtf(fmaxf(thr * cxx * rdet, 0.0f)) * 1.0001f + 1e-3f;
-  return c;
-}
-
-// Exact test: does q(d) <= thr hold anywhere in the box of pixel centres
-// [x0, x0+7] x [y0, y0+7]?  Boxes outside the region's bounding box are
-// rejected first; q is convex, so if the mean is outside the box the
-// minimum over the box lies on one of its four edges.
-__device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape& c, float thr,
-                                            float x0, float y0) {
-  if (!c.pd) return true;
-  const float x1 = x0 + 7.0f, y1 = y0 + 7.0f;
-  if (mx + c.ex < x0 || mx - c.ex > x1 || my + c.ey < y0 || my - c.ey > y1) return false;
-  if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
-  const float dxl = mx - x1, dxh = mx - x0, dyl = my - y1, dyh = my - y0;
-  float m = edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyl, dxl, dxh);
-  m = fminf(m, edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyh, dxl, dxh));
-  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxl, dyl, dyh));
-  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxh, dyl, dyh));
-  return m <= thr;
 }
 
 // Backward.  Waves own 8x8 quadrants of the tile.  Per batch, every staged
@@ -390,7 +420,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float x0 = tx0 + (w & 1) * 8, y0 = ty0 + (w >> 1) * 8;
-            const bool hit = k < wmax[w] && box_reaches(rq[0].x, rq[0].y, cs, thr, x0, y0);
+            const bool hit = k < wmax[w] && box_reaches(rq[0].x, rq[0].y, cs, thr, x0, y0, 7.0f);
             qm |= hit ? (1u << w) : 0u;
           }
         }

@@ -318,22 +318,46 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     assert np.all(np.diff(e * 8 + mant) <= 0)
     pl_np, r_np, nc_np = pl.cpu().numpy(), ranges.cpu().numpy(), nc.cpu().numpy()
     member = g.pprobs >= np.float32(1e-6)
+    # float64 alpha of a Gaussian over a tile's pixel centres
+    pr = ref["proj"]
+    m2, cov = pr["means2d"].astype(np.float64), pr["cov2d"].astype(np.float64)
+    det = cov[:, 0] * cov[:, 3] - cov[:, 1] * cov[:, 2]
+    cxx, cxy, czz = cov[:, 3] / det, -cov[:, 1] / det, cov[:, 0] / det
     gx = (W + 15) // 16
-    truncated = 0
+    truncated = invisible = 0
     for tile in range(ntiles):
         r0, r1 = r_np[tile]
         ty, tx = divmod(tile, gx)
+        px = np.tile(np.arange(16), 16) + tx * 16.0
+        py = np.repeat(np.arange(16), 16) + ty * 16.0
         for p in range(P):
+            tile_nc = nc_np[p, ty * 16:(ty + 1) * 16, tx * 16:(tx + 1) * 16]
             ks = np.nonzero(member[pl_np[r0:r1], p])[0]
             c = int(cnt[tile, p])
             assert 0 <= c <= len(ks)
             got = ent[p, r0:r0 + c]
-            np.testing.assert_array_equal(got[:, 1], ks[:c])
-            np.testing.assert_array_equal(got[:, 0], pl_np[r0 + ks[:c]])
-            if c < len(ks):
+            # the list: plane members in list order ...
+            assert np.all(np.diff(got[:, 1]) > 0) and np.all(np.isin(got[:, 1], ks))
+            np.testing.assert_array_equal(got[:, 0], pl_np[r0 + got[:, 1]])
+            # ... and every member it leaves out lies beyond every pixel's
+            # n_contrib or has alpha < 2^-25 at every pixel of the tile
+            # (culled by the forward as without effect)
+            missing = np.setdiff1d(ks, got[:, 1])
+            inner = missing[missing < tile_nc.max()]
+            if len(inner):
+                gg = pl_np[r0 + inner]
+                dx = m2[gg, 0][:, None] - px[None, :]
+                dy = m2[gg, 1][:, None] - py[None, :]
+                q = cxx[gg][:, None] * dx * dx + 2 * cxy[gg][:, None] * dx * dy \
+                    + czz[gg][:, None] * dy * dy
+                ow = g.opac[gg].astype(np.float64) * g.pprobs[gg, p]
+                alpha = ow[:, None] * np.exp(-0.5 * q)
+                assert np.all(alpha < 2.0 ** -25), (tile, p, alpha.max())
+                invisible += len(inner)
+            if np.any(missing >= tile_nc.max()):
                 truncated += 1
-                tile_nc = nc_np[p, ty * 16:(ty + 1) * 16, tx * 16:(tx + 1) * 16]
-                assert ks[c] >= tile_nc.max()
+    print(f"plane lists: {truncated} cut short, {invisible} invisible members left out",
+          flush=True)
     if case == "dense":
         assert truncated > 0
 
