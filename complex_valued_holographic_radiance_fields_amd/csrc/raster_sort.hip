@@ -456,6 +456,18 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
 
 // Packed emission: one word (tile << vbits) | gaussian per pair, in the same
 // order as k_emit.
+// Packed emission.  The block's pairs [e0, e1) (those of its kEmitThreads
+// Gaussians in rank order) are produced in chunks of kEmitChunk: each thread
+// takes kEmitPer consecutive pairs, finds the Gaussian and tile of its first
+// one (one binary search over the block's offsets, one division by the rect
+// width), then walks on (next tile in the rect, next Gaussian with pairs)
+// and stores the words in LDS (one pad word per kEmitPer, so the lanes'
+// strided stores hit distinct banks); the chunk then leaves in coalesced
+// stores.
+constexpr int kEmitPer = 16;
+constexpr int kEmitChunk = kEmitThreads * kEmitPer;
+__device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
+
 __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ off,
                                                              const uint32_t* __restrict__ order,
                                                              const uint32_t* __restrict__ sorted_flag,
@@ -467,6 +479,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
+  __shared__ uint32_t s_words[kEmitChunk + kEmitChunk / kEmitPer];
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
   const int64_t r = rb + threadIdx.x;
   const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
@@ -479,21 +492,52 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
   if (threadIdx.x == 0) s_off[nr] = off[rb + nr];
   __syncthreads();
   const uint64_t e0 = s_off[0], e1 = s_off[nr];
-  for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
-    int lo = 0, hi = nr;  // s_off[lo] <= e < s_off[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= e)
-        lo = mid;
-      else
-        hi = mid;
+  const uint32_t ugx = static_cast<uint32_t>(gx);
+  for (uint64_t c0 = e0; c0 < e1; c0 += kEmitChunk) {
+    const int clen = static_cast<int>(e1 - c0 < kEmitChunk ? e1 - c0 : kEmitChunk);
+    const int j0 = static_cast<int>(threadIdx.x) * kEmitPer;
+    if (j0 < clen) {
+      const uint64_t a = c0 + j0;
+      int lo = 0, hi = nr;  // the largest lo with s_off[lo] <= a: a < s_off[lo + 1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid] <= a)
+          lo = mid;
+        else
+          hi = mid;
+      }
+      uint64_t next = s_off[lo + 1];
+      uint2 rc = s_rect[lo];
+      uint32_t minx = rc.x & 0xFFFF, maxx = rc.y & 0xFFFF;
+      const uint32_t w0 = maxx - minx;
+      const uint32_t i0 = static_cast<uint32_t>(a - s_off[lo]);
+      uint32_t ty = (rc.x >> 16) + i0 / w0, tx = minx + i0 % w0;
+      uint32_t gb = s_g[lo];
+      const int cnt = clen - j0 < kEmitPer ? clen - j0 : kEmitPer;
+      for (int j = 0; j < cnt; ++j) {
+        const uint64_t e = a + j;
+        if (e == next) {  // this Gaussian is done: the next one with pairs
+          do {
+            ++lo;
+            next = s_off[lo + 1];
+          } while (next == e);
+          rc = s_rect[lo];
+          minx = rc.x & 0xFFFF;
+          maxx = rc.y & 0xFFFF;
+          tx = minx;
+          ty = rc.x >> 16;
+          gb = s_g[lo];
+        }
+        s_words[emit_pad(j0 + j)] = ((ty * ugx + tx) << vbits) | gb;
+        if (++tx == maxx) {
+          tx = minx;
+          ++ty;
+        }
+      }
     }
-    const uint2 rc = s_rect[lo];
-    const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
-    const uint32_t w = maxx - minx;
-    const uint32_t i = static_cast<uint32_t>(e - s_off[lo]);
-    const uint32_t ty = miny + i / w, tx = minx + i % w;
-    words[e] = ((ty * static_cast<uint32_t>(gx) + tx) << vbits) | s_g[lo];
+    __syncthreads();
+    for (int i = threadIdx.x; i < clen; i += kEmitThreads) words[c0 + i] = s_words[emit_pad(i)];
+    __syncthreads();
   }
 }
 
