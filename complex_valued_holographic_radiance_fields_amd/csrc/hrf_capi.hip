@@ -97,11 +97,10 @@ struct GeomWs {
   uint32_t* dkey_b;
   uint32_t* order;
   uint32_t* order_b;
-  uint64_t* off;  // n + 1
   uint32_t* vis;
-  uint32_t* vis_off;
-  uint64_t* scan64;
-  uint32_t* scan32;
+  uint64_t* part_t;  // per-projection-block tile sums -> pair bases (index order)
+  uint32_t* part_v;  // per-projection-block visible sums -> visible bases
+  uint64_t* part_r;  // pair bases in depth-rank order (when the depth sort runs)
   uint32_t* radix;
   uint64_t* totals;  // [K, V, unsorted-depth flag]
   uint32_t* sort_flag;
@@ -118,11 +117,11 @@ GeomWs carve_geom(Carver& cv, int64_t n, int C) {
   w.dkey_b = cv.take<uint32_t>(m);
   w.order = cv.take<uint32_t>(m);
   w.order_b = cv.take<uint32_t>(m);
-  w.off = cv.take<uint64_t>(m + 1);
+
   w.vis = cv.take<uint32_t>(m);
-  w.vis_off = cv.take<uint32_t>(m);
-  w.scan64 = cv.take<uint64_t>(scan_scratch_elems(m));
-  w.scan32 = cv.take<uint32_t>(scan_scratch_elems(m));
+  w.part_t = cv.take<uint64_t>(partial_elems(m));
+  w.part_v = cv.take<uint32_t>(partial_elems(m));
+  w.part_r = cv.take<uint64_t>(partial_elems(m));
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
   w.totals = cv.take<uint64_t>(4);
   w.sort_flag = cv.take<uint32_t>(4);
@@ -323,19 +322,21 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   pp.dkey = w.dkey;
   pp.vis = w.vis;
   pp.sort_flag = w.sort_flag;
+  pp.part_t = w.part_t;
+  pp.part_v = w.part_v;
   {
     HRF_STAGE("project", s);
     HRF_TRY(launch_fill_u32(w.sort_flag, 0u, 1, s));
     HRF_TRY(launch_project(pp, s));
   }
 
-  // Offsets in index order: K and V do not depend on the order, and the
-  // reference's caller hands Gaussians over already sorted by depth
-  // (Scene.render, model.py:1387), where index order is depth order.
+  // K and V from the projection's per-block sums (index order: K and V do
+  // not depend on the order, and the reference's caller hands Gaussians over
+  // already sorted by depth, Scene.render, model.py:1387, where index order
+  // is depth order); the sums become the blocks' pair / visible bases.
   {
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_offsets(nullptr, w.tiles, w.vis, n, w.off, w.vis_off, w.scan64, w.scan32,
-                           w.sort_flag, w.totals, s));
+    HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, w.totals, s));
   }
   uint64_t host_tot[3] = {0, 0, 0};
   HRF_HIP(hipMemcpyAsync(host_tot, w.totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
@@ -360,8 +361,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
       }
     }
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_offsets(w.order, w.tiles, w.vis, n, w.off, w.vis_off, w.scan64, w.scan32,
-                           w.sort_flag, w.totals, s));
+    HRF_TRY(launch_rank_partials(w.order, w.tiles, n, w.part_r, s));
   }
   *num_pairs = static_cast<int64_t>(host_tot[0]);
   *num_visible = static_cast<int64_t>(host_tot[1]);
@@ -427,8 +427,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
       HRF_STAGE("emit", s);
-      HRF_TRY(launch_emit_packed(w.off, w.order, w.sort_flag, w.rect, n, f.gx, vbits, b.keys_a,
-                                 s, b.diff, diff_n));
+      HRF_TRY(launch_emit_packed(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
+                                 f.gx, vbits, b.keys_a, s, b.diff, diff_n));
     }
     bool in_b = false;
     // The last sort pass writes the gaussian bits straight into point_list;
@@ -455,8 +455,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     uint32_t* vals_b = odd ? reinterpret_cast<uint32_t*>(point_list) : b.vals_s;
     {
       HRF_STAGE("emit", s);
-      HRF_TRY(launch_emit_pairs(w.off, w.order, w.sort_flag, w.rect, n, num_pairs, f.gx,
-                                b.keys_a, vals_a, s, b.diff, diff_n));
+      HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
+                                num_pairs, f.gx, b.keys_a, vals_a, s, b.diff, diff_n));
     }
     bool in_b = false;
     {
@@ -505,7 +505,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     if (order_out)
       HRF_TRY(launch_order_by_cost(rp.sub_cnt_out, f.ntiles * g->planes, order_out, s));
   }
-  if (num_visible > 0) HRF_TRY(launch_compact_visible(w.vis, w.vis_off, n, visible, s));
+  if (num_visible > 0) HRF_TRY(launch_compact_visible(w.vis, w.part_v, n, visible, s));
   return HRF_OK;
 }
 

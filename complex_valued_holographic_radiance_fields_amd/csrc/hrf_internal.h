@@ -20,6 +20,9 @@ namespace hrf {
 // Compile-time constants of the reference (wave_rasterizer/config.h:15-23).
 constexpr int kTile = 16;                     // BLOCK_X == BLOCK_Y
 constexpr int kBlock = kTile * kTile;         // threads per render block
+// Gaussians per projection block = ranks per emission block = indices per
+// visible-compaction block: the granularity of the count partial sums.
+constexpr int kProjThreads = 256;
 constexpr float kPlaneCutoff = 1e-6f;         // PLANE_PROBABILITY_CUTOFF
 constexpr float kMaxAlpha = 0.99f;            // MAX_ALPHA_VALUE
 constexpr float kMinAlphaBwd = 1.0f / 255.0f; // backward_splat.cu:218
@@ -139,6 +142,9 @@ struct ProjectParams {
   uint32_t* dkey;   // n: depth sort key
   uint32_t* vis;    // n: 0/1
   uint32_t* sort_flag;  // set to 1 when some depth key is below its predecessor's
+  // optional: per kProjThreads-block sums of tiles (u64) and vis (u32)
+  uint64_t* part_t;
+  uint32_t* part_v;
 };
 int launch_project(const ProjectParams& p, hipStream_t s);
 
@@ -216,19 +222,35 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 // The depth-order permutation used by the emit kernels is order[] when
 // *sorted_flag != 0 and the identity otherwise.  Both emit kernels also
 // clear zero[0, zero_n) (the tile-count difference array, when used).
-int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
-                      const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
-                      uint32_t* vals, hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
+// Count partials: part_t / part_v hold per-kProjThreads-block sums (from
+// k_project, index order); launch_partials_scan turns them, in place, into
+// exclusive block bases (part_t[nb] = K) and writes totals [K, V, flag].
+// launch_rank_partials forms part_r, the same for the tile counts taken in
+// depth-rank order (tiles[order[r]]), and scans it (totals untouched).
+int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n,
+                         const uint32_t* sort_flag, uint64_t* totals, hipStream_t s);
+int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n,
+                         uint64_t* part_r, hipStream_t s);
+// The emit kernels take the scanned bases: part_t (index order) or, when
+// *sorted_flag, part_r (rank order), and form each block's pair offsets
+// from the tile counts themselves.
+int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
+                      const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
+                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
+                      hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
-int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
-                       const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
-                       hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
+int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
+                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       int32_t* zero = nullptr, int zero_n = 0);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
-int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,
+// visible = indices with vis set, in order; part_v = scanned block bases.
+int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t n,
                            int64_t* visible, hipStream_t s);
+int64_t partial_elems(int64_t n);  // kProjThreads-blocks + 1
 int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s);
 int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
 

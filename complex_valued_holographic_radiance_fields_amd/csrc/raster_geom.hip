@@ -22,9 +22,7 @@ __device__ __forceinline__ uint32_t depth_key(float z) {
   return (bits & 0x80000000u) ? (bits & 0x7FFFFFFFu) : (bits | 0x80000000u);
 }
 
-__global__ __launch_bounds__(256) void k_project(ProjectParams p) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (g >= p.n) return;
+__device__ __forceinline__ void project_one(const ProjectParams& p, int64_t g) {
   const int C = p.C, P = p.P;
   const float tx = p.cam[g * 3 + 0], ty = p.cam[g * 3 + 1], tz = p.cam[g * 3 + 2];
   const float z = p.z[g];
@@ -131,7 +129,7 @@ __global__ __launch_bounds__(256) void k_project(ProjectParams p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) amp[i] = 0.0f;
   for (int c = 0; c < C; ++c) {
-    float sv, cvv;  // a few 1e-7 absolute for any phase: ample for gradients
+    float sv, cvv;  // a few 1e-7 absolute for any phase: the amplitude to fp32 accuracy
     sincos_big(p.phase[g * C + c], &sv, &cvv);
     const float col = p.colours[g * C + c];
     amp[2 * c] = col * cvv;
@@ -140,6 +138,42 @@ __global__ __launch_bounds__(256) void k_project(ProjectParams p) {
   reinterpret_cast<float4*>(r)[2] = make_float4(amp[0], amp[1], amp[2], amp[3]);
   if (rec_quads(C) > 3)
     reinterpret_cast<float4*>(r)[3] = make_float4(amp[4], amp[5], amp[6], amp[7]);
+}
+
+// One thread per Gaussian.  With part_t set, each block also leaves the sums
+// of its Gaussians' tile counts and visibility flags (kProjThreads-Gaussian
+// blocks: the granularity the pair emission and the visible compaction scan
+// at), so the offsets need no separate pass over the counts.
+__global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g < p.n) project_one(p, g);
+  if (p.part_t) {
+    __shared__ uint64_t s_t[kProjThreads / 64];
+    __shared__ uint32_t s_v[kProjThreads / 64];
+    uint64_t t = g < p.n ? p.tiles[g] : 0u;
+    uint32_t v = g < p.n ? p.vis[g] : 0u;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      t += __shfl_xor(t, d, 64);
+      v += __shfl_xor(v, d, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+      s_t[threadIdx.x >> 6] = t;
+      s_v[threadIdx.x >> 6] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t a = 0;
+      uint32_t b = 0;
+#pragma unroll
+      for (int w = 0; w < kProjThreads / 64; ++w) {
+        a += s_t[w];
+        b += s_v[w];
+      }
+      p.part_t[blockIdx.x] = a;
+      p.part_v[blockIdx.x] = b;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- backward
@@ -225,7 +259,8 @@ __global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
 
 int launch_project(const ProjectParams& p, hipStream_t s) {
   if (p.n == 0) return HRF_OK;
-  hipLaunchKernelGGL(k_project, dim3(blocks_for(p.n, 256)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(k_project, dim3(blocks_for(p.n, kProjThreads)), dim3(kProjThreads), 0, s,
+                     p);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

@@ -313,25 +313,26 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_reduce(
   }
 }
 
-__global__ __launch_bounds__(kScanThreads) void k_offsets_blocks(
+template <int THREADS = kScanThreads, int ITEMS = kScanItems>
+__global__ __launch_bounds__(THREADS) void k_offsets_blocks(
     uint64_t* __restrict__ bsum_p, uint32_t* __restrict__ bsum_v, int64_t nb,
     uint64_t* __restrict__ off_end, const uint32_t* __restrict__ sort_flag,
     uint64_t* __restrict__ totals) {
-  __shared__ uint64_t s_wp[kScanThreads / 64];
-  __shared__ uint32_t s_wv[kScanThreads / 64];
+  __shared__ uint64_t s_wp[THREADS / 64];
+  __shared__ uint32_t s_wv[THREADS / 64];
   uint64_t carry_p = 0;
   uint32_t carry_v = 0;
-  for (int64_t base = 0; base < nb; base += kScanTile) {
-    const int64_t b0 = base + static_cast<int64_t>(threadIdx.x) * kScanItems;
-    uint64_t p[kScanItems];
-    uint32_t v[kScanItems];
+  for (int64_t base = 0; base < nb; base += THREADS * ITEMS) {
+    const int64_t b0 = base + static_cast<int64_t>(threadIdx.x) * ITEMS;
+    uint64_t p[ITEMS];
+    uint32_t v[ITEMS];
     uint64_t rp = 0;
     uint32_t rv = 0;
 #pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
+    for (int i = 0; i < ITEMS; ++i) {
       const int64_t idx = b0 + i;
       const uint64_t xp = idx < nb ? bsum_p[idx] : 0ull;
-      const uint32_t xv = idx < nb ? bsum_v[idx] : 0u;
+      const uint32_t xv = (bsum_v && idx < nb) ? bsum_v[idx] : 0u;
       p[i] = rp;
       v[i] = rv;
       rp += xp;
@@ -342,11 +343,11 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_blocks(
     const uint64_t op = block_exclusive_scan<uint64_t>(rp, &tp, s_wp);
     const uint32_t ov = block_exclusive_scan<uint32_t>(rv, &tv, s_wv);
 #pragma unroll
-    for (int i = 0; i < kScanItems; ++i) {
+    for (int i = 0; i < ITEMS; ++i) {
       const int64_t idx = b0 + i;
       if (idx < nb) {
         bsum_p[idx] = carry_p + op + p[i];
-        bsum_v[idx] = carry_v + ov + v[i];
+        if (bsum_v) bsum_v[idx] = carry_v + ov + v[i];
       }
     }
     carry_p += tp;
@@ -355,10 +356,55 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_blocks(
   }
   if (threadIdx.x == 0) {
     off_end[0] = carry_p;
-    totals[0] = carry_p;
-    totals[1] = carry_v;
-    totals[2] = *sort_flag;
+    if (totals) {
+      totals[0] = carry_p;
+      totals[1] = carry_v;
+      totals[2] = *sort_flag;
+    }
   }
+}
+
+// Tile counts per kProjThreads block of ranks, taken in rank order.
+__global__ __launch_bounds__(kProjThreads) void k_rank_partials(const uint32_t* __restrict__ order,
+                                                               const uint32_t* __restrict__ tiles,
+                                                               int64_t n,
+                                                               uint64_t* __restrict__ part_r) {
+  __shared__ uint64_t s_t[kProjThreads / 64];
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kProjThreads + threadIdx.x;
+  uint64_t t = r < n ? tiles[order[r]] : 0u;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+  if ((threadIdx.x & 63) == 0) s_t[threadIdx.x >> 6] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t a = 0;
+#pragma unroll
+    for (int w = 0; w < kProjThreads / 64; ++w) a += s_t[w];
+    part_r[blockIdx.x] = a;
+  }
+}
+
+// The block's exclusive pair offsets (kProjThreads ranks) from its tile
+// counts and the scanned base: s_off[0..nr], s_off[nr] = the next block's
+// base.  Every thread of the block calls it (it synchronises).
+__device__ __forceinline__ void block_offsets(const uint64_t* __restrict__ part_t,
+                                              const uint64_t* __restrict__ part_r,
+                                              const uint32_t* __restrict__ tiles,
+                                              const uint32_t* __restrict__ order,
+                                              const uint32_t* __restrict__ sorted_flag,
+                                              int64_t rb, int nr, uint64_t* s_off,
+                                              uint64_t* s_wave) {
+  const bool ranked = *sorted_flag != 0;
+  const uint64_t* base = ranked ? part_r : part_t;
+  const int64_t r = rb + threadIdx.x;
+  uint64_t c = 0;
+  if (static_cast<int>(threadIdx.x) < nr)
+    c = tiles[ranked ? order[r] : static_cast<uint32_t>(r)];
+  uint64_t total;
+  const uint64_t ex = block_exclusive_scan<uint64_t>(c, &total, s_wave);
+  const uint64_t b0 = base[blockIdx.x];
+  if (static_cast<int>(threadIdx.x) < nr) s_off[threadIdx.x] = b0 + ex;
+  if (threadIdx.x == 0) s_off[nr] = b0 + total;
 }
 
 __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
@@ -397,13 +443,12 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
   }
 }
 
-// Pair emission.  A block owns 256 consecutive ranks; it stages their
-// exclusive offsets in LDS and its threads walk the block's output range
-// [off[r_begin], off[r_end]) with a stride of 256, each finding its rank by
-// binary search in LDS, so consecutive threads write consecutive pairs
-// (coalesced).  Tile order inside a Gaussian is y outer, x inner
-// (rasterizer_splat.cu:162-173).
-constexpr int kEmitThreads = 256;
+// Pair emission.  A block owns kEmitThreads consecutive ranks; it forms
+// their exclusive pair offsets in LDS (a block scan of their tile counts
+// plus the block's scanned base) and writes the block's output range
+// [off[r_begin], off[r_end]).  Tile order inside a Gaussian is y outer, x
+// inner (rasterizer_splat.cu:162-173).
+constexpr int kEmitThreads = kProjThreads;
 // Clears zero[0, zero_n) with the whole grid (a scratch array that a later
 // kernel of the same call accumulates into), saving a fill launch.
 __device__ __forceinline__ void zero_prefix(int32_t* zero, int zero_n) {
@@ -412,7 +457,9 @@ __device__ __forceinline__ void zero_prefix(int32_t* zero, int zero_n) {
     zero[e] = 0;
 }
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ off,
+__global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ part_t,
+                                                      const uint64_t* __restrict__ part_r,
+                                                      const uint32_t* __restrict__ tiles,
                                                       const uint32_t* __restrict__ order,
                                                       const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
@@ -423,16 +470,16 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
+  __shared__ uint64_t s_wave[kEmitThreads / 64];
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
   const int64_t r = rb + threadIdx.x;
   const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
+  block_offsets(part_t, part_r, tiles, order, sorted_flag, rb, nr, s_off, s_wave);
   if (threadIdx.x < nr) {
-    s_off[threadIdx.x] = off[r];
     const uint32_t g = ordered(order, sorted_flag, r);
     s_g[threadIdx.x] = g;
     s_rect[threadIdx.x] = rect[g];
   }
-  if (threadIdx.x == 0) s_off[nr] = off[rb + nr];
   __syncthreads();
   const uint64_t e0 = s_off[0], e1 = s_off[nr];
   for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
@@ -468,7 +515,9 @@ constexpr int kEmitPer = 16;
 constexpr int kEmitChunk = kEmitThreads * kEmitPer;
 __device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ off,
+__global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ part_t,
+                                                             const uint64_t* __restrict__ part_r,
+                                                             const uint32_t* __restrict__ tiles,
                                                              const uint32_t* __restrict__ order,
                                                              const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
@@ -480,16 +529,16 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
   __shared__ uint32_t s_words[kEmitChunk + kEmitChunk / kEmitPer];
+  __shared__ uint64_t s_wave[kEmitThreads / 64];
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
   const int64_t r = rb + threadIdx.x;
   const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
+  block_offsets(part_t, part_r, tiles, order, sorted_flag, rb, nr, s_off, s_wave);
   if (threadIdx.x < nr) {
-    s_off[threadIdx.x] = off[r];
     const uint32_t g = ordered(order, sorted_flag, r);
     s_g[threadIdx.x] = g;
     s_rect[threadIdx.x] = rect[g];
   }
-  if (threadIdx.x == 0) s_off[nr] = off[rb + nr];
   __syncthreads();
   const uint64_t e0 = s_off[0], e1 = s_off[nr];
   const uint32_t ugx = static_cast<uint32_t>(gx);
@@ -661,11 +710,15 @@ __global__ __launch_bounds__(kDiffThreads) void k_ranges_from_diff(const int32_t
   }
 }
 
-__global__ void k_compact_visible(const uint32_t* __restrict__ vis,
-                                  const uint32_t* __restrict__ vis_off, int64_t n,
-                                  int64_t* __restrict__ visible) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n && vis[i]) visible[vis_off[i]] = i;
+__global__ __launch_bounds__(kProjThreads) void k_compact_visible(
+    const uint32_t* __restrict__ vis, const uint32_t* __restrict__ part_v, int64_t n,
+    int64_t* __restrict__ visible) {
+  __shared__ uint32_t s_wave[kProjThreads / 64];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kProjThreads + threadIdx.x;
+  const uint32_t v = i < n ? vis[i] : 0u;
+  uint32_t total;
+  const uint32_t ex = block_exclusive_scan<uint32_t>(v, &total, s_wave);
+  if (v) visible[part_v[blockIdx.x] + ex] = i;
 }
 
 }  // namespace
@@ -826,8 +879,8 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
   hipLaunchKernelGGL(k_offsets_reduce, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0,
                      s, order, tiles, vis, n, bsum_p, bsum_v);
   HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_offsets_blocks, dim3(1), dim3(kScanThreads), 0, s, bsum_p, bsum_v, nb,
-                     off + n, sort_flag, totals);
+  hipLaunchKernelGGL((k_offsets_blocks<>), dim3(1), dim3(kScanThreads), 0, s, bsum_p, bsum_v,
+                     nb, off + n, sort_flag, totals);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_offsets_scan, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, s,
                      order, tiles, vis, n, bsum_p, bsum_v, off, vis_off);
@@ -835,22 +888,25 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
   return HRF_OK;
 }
 
-int launch_emit_pairs(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
-                      const uint2* rect, int64_t n, int64_t k, int gx, uint32_t* keys,
-                      uint32_t* vals, hipStream_t s, int32_t* zero, int zero_n) {
+int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
+                      const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
+                      int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
+                      hipStream_t s, int32_t* zero, int zero_n) {
   if (k <= 0 || n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, off,
-                     order, sorted_flag, rect, n, gx, keys, vals, zero, zero_n);
+  hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, part_t,
+                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals, zero, zero_n);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
-int launch_emit_packed(const uint64_t* off, const uint32_t* order, const uint32_t* sorted_flag,
-                       const uint2* rect, int64_t n, int gx, int vbits, uint32_t* words,
-                       hipStream_t s, int32_t* zero, int zero_n) {
+int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
+                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       int32_t* zero, int zero_n) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     off, order, sorted_flag, rect, n, gx, vbits, words, zero, zero_n);
+                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words, zero,
+                     zero_n);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -902,11 +958,36 @@ int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges, int nti
   return HRF_OK;
 }
 
-int launch_compact_visible(const uint32_t* vis, const uint32_t* vis_off, int64_t n,
+int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t n,
                            int64_t* visible, hipStream_t s) {
   if (n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_compact_visible, dim3(blocks_for(n, 256)), dim3(256), 0, s, vis,
-                     vis_off, n, visible);
+  hipLaunchKernelGGL(k_compact_visible, dim3(blocks_for(n, kProjThreads)), dim3(kProjThreads), 0,
+                     s, vis, part_v, n, visible);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int64_t partial_elems(int64_t n) { return (n + kProjThreads - 1) / kProjThreads + 1; }
+
+int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n,
+                         const uint32_t* sort_flag, uint64_t* totals, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  const int64_t nb = (n + kProjThreads - 1) / kProjThreads;
+  hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_t, part_v,
+                     nb, part_t + nb, sort_flag, totals);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n,
+                         uint64_t* part_r, hipStream_t s) {
+  if (n <= 0) return HRF_OK;
+  const int64_t nb = (n + kProjThreads - 1) / kProjThreads;
+  hipLaunchKernelGGL(k_rank_partials, dim3(static_cast<unsigned>(nb)), dim3(kProjThreads), 0, s,
+                     order, tiles, n, part_r);
+  HRF_LAUNCH_CHECK();
+  hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_r, nullptr,
+                     nb, part_r + nb, nullptr, nullptr);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
