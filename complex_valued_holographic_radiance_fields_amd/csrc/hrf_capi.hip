@@ -1,14 +1,18 @@
-// hrf_capi.cpp — extern "C" entry points declared in include/hrf.h.
+// hrf_capi.hip — extern "C" entry points declared in include/hrf.h.
 //
 // Host-side orchestration only: argument validation, workspace carving,
-// launch sequencing on the caller's stream, hipFFT calls.  No allocation is
-// done here except hipFFT's own plan work areas (cached per device/size).
+// launch sequencing on the caller's stream.  The only allocations are the
+// pinned read-back slots for the count read-backs (64 bytes and an event
+// each, a few per device, kept until the process ends) and, in the ASM file,
+// hipFFT's plan work areas (cached per device/size).
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "hrf_internal.h"
 
@@ -28,6 +32,42 @@ void set_error(const char* fmt, ...) {
 }
 
 const char* get_error() { return g_err.c_str(); }
+
+namespace {
+std::mutex g_rb_mu;
+std::vector<Readback*> g_rb_free;
+}  // namespace
+
+int readback_acquire(Readback** out) {
+  int dev = 0;
+  HRF_HIP(hipGetDevice(&dev));
+  {
+    std::lock_guard<std::mutex> lk(g_rb_mu);
+    for (size_t i = 0; i < g_rb_free.size(); ++i) {
+      if (g_rb_free[i]->device == dev) {
+        *out = g_rb_free[i];
+        g_rb_free.erase(g_rb_free.begin() + static_cast<std::ptrdiff_t>(i));
+        return HRF_OK;
+      }
+    }
+  }
+  Readback r{nullptr, nullptr, nullptr, dev};
+  HRF_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 8 * sizeof(uint64_t),
+                        hipHostMallocCoherent | hipHostMallocMapped));
+  HRF_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&r.dev), r.host, 0));
+  HRF_HIP(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
+  *out = new Readback(r);
+  return HRF_OK;
+}
+
+void readback_arm(Readback* r, int words) {
+  for (int i = 0; i < words; ++i) reinterpret_cast<volatile uint64_t*>(r->host)[i] = ~0ull;
+}
+
+void readback_release(Readback* r) {
+  std::lock_guard<std::mutex> lk(g_rb_mu);
+  g_rb_free.push_back(r);
+}
 
 namespace {
 
@@ -102,8 +142,11 @@ struct GeomWs {
   uint32_t* part_v;  // per-projection-block visible sums -> visible bases
   uint64_t* part_r;  // pair bases in depth-rank order (when the depth sort runs)
   uint32_t* radix;
-  uint64_t* totals;  // [K, V, unsorted-depth flag]
   uint32_t* sort_flag;
+  // Tile ranges formed in the prepare call when the tile grid's difference
+  // array fits kMaxTileDiff (the render call then reads them here).
+  int32_t* diff;
+  int32_t* ranges;
 };
 
 GeomWs carve_geom(Carver& cv, int64_t n, int C) {
@@ -123,8 +166,9 @@ GeomWs carve_geom(Carver& cv, int64_t n, int C) {
   w.part_v = cv.take<uint32_t>(partial_elems(m));
   w.part_r = cv.take<uint64_t>(partial_elems(m));
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
-  w.totals = cv.take<uint64_t>(4);
   w.sort_flag = cv.take<uint32_t>(4);
+  w.diff = cv.take<int32_t>(kMaxTileDiff);
+  w.ranges = cv.take<int32_t>(2 * kMaxTileDiff);
   return w;
 }
 
@@ -133,17 +177,15 @@ struct BinWs {
   uint32_t* keys_b;
   uint32_t* vals_s;
   uint32_t* radix;
-  int32_t* diff;  // tile-count difference array (grids that fit the LDS bound)
 };
 
-BinWs carve_bin(Carver& cv, int64_t k, int gx, int gy) {
+BinWs carve_bin(Carver& cv, int64_t k) {
   BinWs w;
   const int64_t m = k > 0 ? k : 1;
   w.keys_a = cv.take<uint32_t>(m);
   w.keys_b = cv.take<uint32_t>(m);
   w.vals_s = cv.take<uint32_t>(m);
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
-  w.diff = cv.take<int32_t>(tile_diff_fits(gx, gy) ? tile_diff_elems(gx, gy) : 1);
   return w;
 }
 
@@ -275,7 +317,7 @@ size_t hrf_raster_geom_workspace_size(int64_t n, int32_t channels, int32_t plane
 size_t hrf_raster_binning_workspace_size(int64_t num_pairs, int32_t width, int32_t height) {
   if (num_pairs < 0 || width <= 0 || height <= 0) return 0;
   Carver cv(nullptr);
-  carve_bin(cv, num_pairs, (width + kTile - 1) / kTile, (height + kTile - 1) / kTile);
+  carve_bin(cv, num_pairs);
   return cv.bytes();
 }
 
@@ -324,6 +366,14 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   pp.sort_flag = w.sort_flag;
   pp.part_t = w.part_t;
   pp.part_v = w.part_v;
+  const bool diff_ranges = tile_diff_fits(f.gx, f.gy);
+  if (diff_ranges) {
+    pp.zero = w.diff;
+    pp.zero_n = tile_diff_elems(f.gx, f.gy);
+  }
+  ReadbackSlot slot;
+  HRF_TRY(readback_acquire(&slot.r));
+  readback_arm(slot.r, 3);
   {
     HRF_STAGE("project", s);
     HRF_TRY(launch_fill_u32(w.sort_flag, 0u, 1, s));
@@ -333,14 +383,27 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // K and V from the projection's per-block sums (index order: K and V do
   // not depend on the order, and the reference's caller hands Gaussians over
   // already sorted by depth, Scene.render, model.py:1387, where index order
-  // is depth order); the sums become the blocks' pair / visible bases.
+  // is depth order); the sums become the blocks' pair / visible bases.  The
+  // scan writes [K, V, flag] straight into the pinned read-back words.
   {
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, w.totals, s));
+    HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, slot.r->dev, s));
   }
-  uint64_t host_tot[3] = {0, 0, 0};
-  HRF_HIP(hipMemcpyAsync(host_tot, w.totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
-  HRF_HIP(hipStreamSynchronize(s));
+  HRF_HIP(hipEventRecord(slot.r->ev, s));
+  // The tile ranges need only the rectangles: they run while the host waits
+  // for the counts (and the render call reads them from the workspace).
+  if (diff_ranges) {
+    HRF_STAGE("ranges", s);
+    HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s));
+  }
+  HRF_HIP(hipEventSynchronize(slot.r->ev));
+  const uint64_t host_tot[3] = {slot.r->host[0], slot.r->host[1], slot.r->host[2]};
+  if (host_tot[1] > static_cast<uint64_t>(n) || host_tot[2] > 1) {
+    set_error("internal: count read-back incomplete (V %llu, flag %llu)",
+              static_cast<unsigned long long>(host_tot[1]),
+              static_cast<unsigned long long>(host_tot[2]));
+    return HRF_ERR_INVALID;
+  }
   if (host_tot[0] > 0x7FFFFFFFull) {
     set_error("pair count %llu exceeds the int32 point_list/ranges format",
               static_cast<unsigned long long>(host_tot[0]));
@@ -414,21 +477,21 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   Carver cg(geom_ws);
   GeomWs w = carve_geom(cg, n, g->channels);
   Carver cb(bin_ws);
-  BinWs b = carve_bin(cb, num_pairs, f.gx, f.gy);
+  BinWs b = carve_bin(cb, num_pairs);
 
   // Pair emission in depth-rank order, then a stable sort on the tile id.
   const int end_bit = bits_for(f.ntiles);
   const int vbits = bits_for(static_cast<int>(n < 0x7FFFFFFF ? n : 0x7FFFFFFF));
-  // Usual case: the tile ranges come from the Gaussians' rectangles (no
-  // pass over the sorted pairs); the emit launch clears their scratch.
+  // Usual case: the prepare call formed the tile ranges from the Gaussians'
+  // rectangles in the geometry workspace (no pass over the sorted pairs);
+  // the forward render copies them into `ranges`.
   const bool diff_ranges = tile_diff_fits(f.gx, f.gy);
-  const int diff_n = diff_ranges ? static_cast<int>(tile_diff_elems(f.gx, f.gy)) : 0;
   if (end_bit + vbits <= 32) {
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_packed(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
-                                 f.gx, vbits, b.keys_a, s, b.diff, diff_n));
+                                 f.gx, vbits, b.keys_a, s));
     }
     bool in_b = false;
     // The last sort pass writes the gaussian bits straight into point_list;
@@ -440,14 +503,10 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
                               fused ? reinterpret_cast<uint32_t*>(point_list) : nullptr,
                               (1u << vbits) - 1u));
     }
-    {
+    if (!fused) {
       HRF_STAGE("ranges", s);
-      if (fused)
-        HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, b.diff, ranges,
-                                              s));
-      else
-        HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
-                                     ranges, f.ntiles, s));
+      HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
+                                   ranges, f.ntiles, s));
     }
   } else {
     const bool odd = (radix_passes(end_bit) % 2) == 1;
@@ -456,7 +515,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
-                                num_pairs, f.gx, b.keys_a, vals_a, s, b.diff, diff_n));
+                                num_pairs, f.gx, b.keys_a, vals_a, s));
     }
     bool in_b = false;
     {
@@ -471,17 +530,14 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     if (sorted_vals != reinterpret_cast<uint32_t*>(point_list))
       HRF_HIP(hipMemcpyAsync(point_list, sorted_vals, num_pairs * sizeof(uint32_t),
                              hipMemcpyDeviceToDevice, s));
-    {
+    if (!diff_ranges) {
       HRF_STAGE("ranges", s);
-      if (diff_ranges)
-        HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, b.diff, ranges,
-                                              s));
-      else
-        HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
+      HRF_TRY(launch_tile_ranges(sorted_keys, num_pairs, ranges, f.ntiles, s));
     }
   }
 
-  rp.ranges = ranges;
+  rp.ranges = diff_ranges ? w.ranges : ranges;
+  rp.ranges_out = diff_ranges ? ranges : nullptr;
   rp.plist = point_list;
   rp.pmask = w.pmask;
   rp.rec = w.rec;

@@ -60,6 +60,35 @@ const char* get_error();
     if (s_ != HRF_OK) return s_;  \
   } while (0)
 
+// -------------------------------------------------------- host read-back --
+// Small device results the host must read (pair / visible counts): pinned,
+// coherent host words that a kernel writes directly (through `dev`), and an
+// event recorded after that kernel.  Slots come from a per-process pool
+// (one slot per concurrent caller and device; never freed), so calls on
+// different streams or threads never share one.
+struct Readback {
+  uint64_t* host;  // 8 words
+  uint64_t* dev;   // the same words as a device address
+  hipEvent_t ev;
+  int device;
+};
+// A free slot of the current device (allocated on first need).
+int readback_acquire(Readback** out);
+// Sets host[0, words) to all ones before the writing kernel is queued, so a
+// write that is not visible reads as an out-of-range count, never a stale
+// one from an earlier call.
+void readback_arm(Readback* r, int words);
+void readback_release(Readback* r);
+struct ReadbackSlot {
+  Readback* r = nullptr;
+  ReadbackSlot() = default;
+  ReadbackSlot(const ReadbackSlot&) = delete;
+  ReadbackSlot& operator=(const ReadbackSlot&) = delete;
+  ~ReadbackSlot() {
+    if (r) readback_release(r);
+  }
+};
+
 // ------------------------------------------------------- workspace carving --
 // A bump allocator over a caller-provided buffer.  Run once with base ==
 // nullptr to size a workspace, then with the real buffer to carve it; both
@@ -145,6 +174,10 @@ struct ProjectParams {
   // optional: per kProjThreads-block sums of tiles (u64) and vis (u32)
   uint64_t* part_t;
   uint32_t* part_v;
+  // optional: cleared by the launch (the tile difference array that a later
+  // kernel of the same call accumulates into)
+  int32_t* zero;
+  int64_t zero_n;
 };
 int launch_project(const ProjectParams& p, hipStream_t s);
 
@@ -203,7 +236,7 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
 // Tile ranges from the Gaussians' tile rectangles (tiles[g] > 0 marks a
 // rectangle) instead of the sorted pairs: a 2-D difference array of
 // (gx+1)(gy+1) int32 in `diff` (device scratch that must hold zeros: the
-// emit launch of the same call clears it), integrated in one block.
+// projection of the same call clears it), integrated in one block.
 // Only for tile grids whose difference array fits kMaxTileDiff entries.
 constexpr int64_t kMaxTileDiff = 16000;  // 64000 B of LDS
 int64_t tile_diff_elems(int gx, int gy);
@@ -220,8 +253,7 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
                    uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
                    hipStream_t s);
 // The depth-order permutation used by the emit kernels is order[] when
-// *sorted_flag != 0 and the identity otherwise.  Both emit kernels also
-// clear zero[0, zero_n) (the tile-count difference array, when used).
+// *sorted_flag != 0 and the identity otherwise.
 // Count partials: part_t / part_v hold per-kProjThreads-block sums (from
 // k_project, index order); launch_partials_scan turns them, in place, into
 // exclusive block bases (part_t[nb] = K) and writes totals [K, V, flag].
@@ -237,14 +269,13 @@ int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n
 int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s, int32_t* zero = nullptr, int zero_n = 0);
+                      hipStream_t s);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
-                       int32_t* zero = nullptr, int zero_n = 0);
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
 // visible = indices with vis set, in order; part_v = scanned block bases.
@@ -285,6 +316,9 @@ struct RenderParams {
   // Backward block order over the T*P (tile, plane) ids (with sub): longest
   // member list first.
   const int32_t* order;
+  // Forward, optional: the plane-0 block of each tile copies its ranges
+  // entry here (ranges formed in a workspace reach the caller's array).
+  int32_t* ranges_out;
 };
 int launch_render_forward(const RenderParams& p, hipStream_t s);
 int launch_render_empty(const RenderParams& p, hipStream_t s);

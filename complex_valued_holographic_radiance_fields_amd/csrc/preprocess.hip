@@ -322,7 +322,6 @@ struct PreWs {
   uint64_t* off;
   uint64_t* bsum_p;
   uint32_t* bsum_v;
-  uint64_t* totals;
   uint32_t* zero;
   uint32_t* radix;
   float* rec;  // n records of fwd_stride(C) floats, written for kept rows
@@ -341,7 +340,6 @@ PreWs carve_pre(Carver& cv, int64_t n, int C) {
   w.off = cv.take<uint64_t>(m + 1);
   w.bsum_p = cv.take<uint64_t>(scan_scratch_elems(m));
   w.bsum_v = cv.take<uint32_t>(scan_scratch_elems(m));
-  w.totals = cv.take<uint64_t>(4);
   w.zero = cv.take<uint32_t>(4);
   w.radix = cv.take<uint32_t>(radix_scratch_elems(m));
   w.rec = cv.take<float>(m * fwd_stride(C));
@@ -421,6 +419,9 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
   hipStream_t s = static_cast<hipStream_t>(stream);
   Carver cv(ws);
   PreWs w = carve_pre(cv, n, sp->channels);
+  ReadbackSlot slot;
+  HRF_TRY(readback_acquire(&slot.r));
+  readback_arm(slot.r, 3);
   HRF_STAGE("pre_select", s);
   HRF_TRY(launch_fill_u32(w.zero, 0u, 1, s));
   const dim3 grid(blocks_for(n, kPreThreads));
@@ -432,16 +433,22 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
                        far_plane, w.flag, w.key, w.rec);
   HRF_LAUNCH_CHECK();
   // Exclusive positions of the kept Gaussians (the binning's offsets scan,
-  // with the flags as both of its inputs); totals[1] = kept count.
+  // with the flags as both of its inputs); totals[1] = kept count, written
+  // into the pinned read-back words, read while the compaction runs.
   HRF_TRY(launch_offsets(nullptr, w.flag, w.flag, n, w.off, w.pos, w.bsum_p, w.bsum_v, w.zero,
-                         w.totals, s));
+                         slot.r->dev, s));
+  HRF_HIP(hipEventRecord(slot.r->ev, s));
   hipLaunchKernelGGL(k_pre_compact, grid, dim3(kPreThreads), 0, s, w.flag, w.pos, w.key, n,
                      w.ckey, w.cidx);
   HRF_LAUNCH_CHECK();
-  uint64_t tot[2] = {0, 0};
-  HRF_HIP(hipMemcpyAsync(tot, w.totals, sizeof(tot), hipMemcpyDeviceToHost, s));
-  HRF_HIP(hipStreamSynchronize(s));
-  const int64_t m = static_cast<int64_t>(tot[1]);
+  HRF_HIP(hipEventSynchronize(slot.r->ev));
+  const uint64_t kept = slot.r->host[1];
+  if (kept > static_cast<uint64_t>(n)) {
+    set_error("internal: selection count read-back incomplete (%llu)",
+              static_cast<unsigned long long>(kept));
+    return HRF_ERR_INVALID;
+  }
+  const int64_t m = static_cast<int64_t>(kept);
   if (m > 1) {
     // Stable ascending depth order (ties keep index order); 4 passes, so
     // the result ends in (ckey, cidx).

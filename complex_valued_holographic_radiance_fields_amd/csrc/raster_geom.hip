@@ -146,6 +146,8 @@ __device__ __forceinline__ void project_one(const ProjectParams& p, int64_t g) {
 // at), so the offsets need no separate pass over the counts.
 __global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t e = g; e < p.zero_n; e += static_cast<int64_t>(gridDim.x) * kProjThreads)
+    p.zero[e] = 0;
   if (g < p.n) project_one(p, g);
   if (p.part_t) {
     __shared__ uint64_t s_t[kProjThreads / 64];

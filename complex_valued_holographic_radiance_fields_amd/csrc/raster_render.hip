@@ -176,6 +176,8 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   const bool inside = pxi < p.W && pyi < p.H;
   int r0, n;
   tile_range(p, tile, &r0, &n);
+  if (p.ranges_out && plane == 0 && threadIdx.x < 2)
+    p.ranges_out[2 * tile + threadIdx.x] = p.ranges[2 * tile + threadIdx.x];
   const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
 
   float T = 1.0f;

@@ -449,14 +449,6 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
 // [off[r_begin], off[r_end]).  Tile order inside a Gaussian is y outer, x
 // inner (rasterizer_splat.cu:162-173).
 constexpr int kEmitThreads = kProjThreads;
-// Clears zero[0, zero_n) with the whole grid (a scratch array that a later
-// kernel of the same call accumulates into), saving a fill launch.
-__device__ __forceinline__ void zero_prefix(int32_t* zero, int zero_n) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < zero_n;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    zero[e] = 0;
-}
-
 __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ part_t,
                                                       const uint64_t* __restrict__ part_r,
                                                       const uint32_t* __restrict__ tiles,
@@ -464,9 +456,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
                                                       const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
                                                       int gx, uint32_t* __restrict__ keys,
-                                                      uint32_t* __restrict__ vals,
-                                                      int32_t* __restrict__ zero, int zero_n) {
-  zero_prefix(zero, zero_n);
+                                                      uint32_t* __restrict__ vals) {
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -522,9 +512,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
                                                              const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
                                                              int64_t n, int gx, int vbits,
-                                                             uint32_t* __restrict__ words,
-                                                             int32_t* __restrict__ zero, int zero_n) {
-  zero_prefix(zero, zero_n);
+                                                             uint32_t* __restrict__ words) {
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -891,22 +879,20 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s, int32_t* zero, int zero_n) {
+                      hipStream_t s) {
   if (k <= 0 || n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, part_t,
-                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals, zero, zero_n);
+                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
-                       int32_t* zero, int zero_n) {
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s) {
   if (n <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words, zero,
-                     zero_n);
+                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
