@@ -363,7 +363,6 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   pp.tiles = w.tiles;
   pp.dkey = w.dkey;
   pp.vis = w.vis;
-  pp.sort_flag = w.sort_flag;
   pp.part_t = w.part_t;
   pp.part_v = w.part_v;
   const bool diff_ranges = tile_diff_fits(f.gx, f.gy);
@@ -376,7 +375,6 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   readback_arm(slot.r, 3);
   {
     HRF_STAGE("project", s);
-    HRF_TRY(launch_fill_u32(w.sort_flag, 0u, 1, s));
     HRF_TRY(launch_project(pp, s));
   }
 

@@ -23,6 +23,9 @@ constexpr int kBlock = kTile * kTile;         // threads per render block
 // Gaussians per projection block = ranks per emission block = indices per
 // visible-compaction block: the granularity of the count partial sums.
 constexpr int kProjThreads = 256;
+// Bit of a projection block's visible-count partial that carries its
+// unsorted-depth flag (the count itself is at most kProjThreads).
+constexpr uint32_t kPartFlag = 0x80000000u;
 constexpr float kPlaneCutoff = 1e-6f;         // PLANE_PROBABILITY_CUTOFF
 constexpr float kMaxAlpha = 0.99f;            // MAX_ALPHA_VALUE
 constexpr float kMinAlphaBwd = 1.0f / 255.0f; // backward_splat.cu:218
@@ -170,8 +173,9 @@ struct ProjectParams {
   uint32_t* tiles;  // n
   uint32_t* dkey;   // n: depth sort key
   uint32_t* vis;    // n: 0/1
-  uint32_t* sort_flag;  // set to 1 when some depth key is below its predecessor's
-  // optional: per kProjThreads-block sums of tiles (u64) and vis (u32)
+  // optional: per kProjThreads-block sums of tiles (u64) and vis (u32); bit
+  // kPartFlag of part_v is set when some depth key of the block is below its
+  // predecessor's
   uint64_t* part_t;
   uint32_t* part_v;
   // optional: cleared by the launch (the tile difference array that a later
@@ -255,12 +259,13 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 // The depth-order permutation used by the emit kernels is order[] when
 // *sorted_flag != 0 and the identity otherwise.
 // Count partials: part_t / part_v hold per-kProjThreads-block sums (from
-// k_project, index order); launch_partials_scan turns them, in place, into
-// exclusive block bases (part_t[nb] = K) and writes totals [K, V, flag].
+// k_project, index order, part_v with the kPartFlag bits); launch_partials_scan
+// turns them, in place, into exclusive block bases (part_t[nb] = K), writes
+// the OR of the flags to *sort_flag and totals [K, V, flag].
 // launch_rank_partials forms part_r, the same for the tile counts taken in
 // depth-rank order (tiles[order[r]]), and scans it (totals untouched).
-int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n,
-                         const uint32_t* sort_flag, uint64_t* totals, hipStream_t s);
+int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n, uint32_t* sort_flag,
+                         uint64_t* totals, hipStream_t s);
 int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n,
                          uint64_t* part_r, hipStream_t s);
 // The emit kernels take the scanned bases: part_t (index order) or, when

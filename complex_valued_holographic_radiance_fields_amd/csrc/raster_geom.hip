@@ -22,7 +22,8 @@ __device__ __forceinline__ uint32_t depth_key(float z) {
   return (bits & 0x80000000u) ? (bits & 0x7FFFFFFFu) : (bits | 0x80000000u);
 }
 
-__device__ __forceinline__ void project_one(const ProjectParams& p, int64_t g) {
+// Returns whether g's depth key is below its predecessor's.
+__device__ __forceinline__ bool project_one(const ProjectParams& p, int64_t g) {
   const int C = p.C, P = p.P;
   const float tx = p.cam[g * 3 + 0], ty = p.cam[g * 3 + 1], tz = p.cam[g * 3 + 2];
   const float z = p.z[g];
@@ -102,7 +103,7 @@ __device__ __forceinline__ void project_one(const ProjectParams& p, int64_t g) {
   p.dkey[g] = dk;
   // Keys already non-decreasing (the reference's caller sorts by depth)
   // make the stable depth sort the identity; it then skips itself.
-  if (p.sort_flag && g > 0 && depth_key(p.z[g - 1]) > dk) *p.sort_flag = 1u;
+  const bool unsorted = p.part_t && g > 0 && depth_key(p.z[g - 1]) > dk;
   // Visibility: defined as 0.2 < z_cam and near < z_cam < far (the
   // reference's checkFrustum reads its 3x3 matrix out of bounds).
   p.vis[g] = (tz > 0.2f && tz > p.near_plane && tz < p.far_plane) ? 1u : 0u;
@@ -138,6 +139,7 @@ __device__ __forceinline__ void project_one(const ProjectParams& p, int64_t g) {
   reinterpret_cast<float4*>(r)[2] = make_float4(amp[0], amp[1], amp[2], amp[3]);
   if (rec_quads(C) > 3)
     reinterpret_cast<float4*>(r)[3] = make_float4(amp[4], amp[5], amp[6], amp[7]);
+  return unsorted;
 }
 
 // One thread per Gaussian.  With part_t set, each block also leaves the sums
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   for (int64_t e = g; e < p.zero_n; e += static_cast<int64_t>(gridDim.x) * kProjThreads)
     p.zero[e] = 0;
-  if (g < p.n) project_one(p, g);
+  const bool unsorted = g < p.n && project_one(p, g);
   if (p.part_t) {
     __shared__ uint64_t s_t[kProjThreads / 64];
     __shared__ uint32_t s_v[kProjThreads / 64];
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
       s_t[threadIdx.x >> 6] = t;
       s_v[threadIdx.x >> 6] = v;
     }
-    __syncthreads();
+    const bool any_unsorted = __syncthreads_or(unsorted ? 1 : 0) != 0;
     if (threadIdx.x == 0) {
       uint64_t a = 0;
       uint32_t b = 0;
@@ -172,8 +174,10 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
         a += s_t[w];
         b += s_v[w];
       }
+      // The visible count (at most kProjThreads) carries the block's
+      // depth-order flag in bit 31.
       p.part_t[blockIdx.x] = a;
-      p.part_v[blockIdx.x] = b;
+      p.part_v[blockIdx.x] = b | (any_unsorted ? kPartFlag : 0u);
     }
   }
 }

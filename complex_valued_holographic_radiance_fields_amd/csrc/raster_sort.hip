@@ -240,6 +240,17 @@ __global__ void k_fill_f32(float* p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
+// 16-byte-aligned fill: kFillVec float4 stores per thread, grid-strided.
+constexpr int kFillVec = 4;
+__global__ __launch_bounds__(256) void k_fill_f32x4(float4* p, float v, int64_t n4) {
+  const float4 q = make_float4(v, v, v, v);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kFillVec; ++k, i += stride)
+    if (i < n4) p[i] = q;
+}
+
 // Depth-order permutation: order[i] when the depth sort ran (*sorted_flag
 // != 0), the identity otherwise (the keys were already in order).
 __device__ __forceinline__ uint32_t ordered(const uint32_t* order, const uint32_t* sorted_flag,
@@ -317,11 +328,12 @@ template <int THREADS = kScanThreads, int ITEMS = kScanItems>
 __global__ __launch_bounds__(THREADS) void k_offsets_blocks(
     uint64_t* __restrict__ bsum_p, uint32_t* __restrict__ bsum_v, int64_t nb,
     uint64_t* __restrict__ off_end, const uint32_t* __restrict__ sort_flag,
-    uint64_t* __restrict__ totals) {
+    uint64_t* __restrict__ totals, uint32_t* __restrict__ flag_out) {
   __shared__ uint64_t s_wp[THREADS / 64];
   __shared__ uint32_t s_wv[THREADS / 64];
   uint64_t carry_p = 0;
   uint32_t carry_v = 0;
+  uint32_t flags = 0;  // with flag_out: OR of the kPartFlag bits of bsum_v
   for (int64_t base = 0; base < nb; base += THREADS * ITEMS) {
     const int64_t b0 = base + static_cast<int64_t>(threadIdx.x) * ITEMS;
     uint64_t p[ITEMS];
@@ -332,7 +344,11 @@ __global__ __launch_bounds__(THREADS) void k_offsets_blocks(
     for (int i = 0; i < ITEMS; ++i) {
       const int64_t idx = b0 + i;
       const uint64_t xp = idx < nb ? bsum_p[idx] : 0ull;
-      const uint32_t xv = (bsum_v && idx < nb) ? bsum_v[idx] : 0u;
+      uint32_t xv = (bsum_v && idx < nb) ? bsum_v[idx] : 0u;
+      if (flag_out) {
+        flags |= xv;
+        xv &= ~kPartFlag;
+      }
       p[i] = rp;
       v[i] = rv;
       rp += xp;
@@ -354,12 +370,15 @@ __global__ __launch_bounds__(THREADS) void k_offsets_blocks(
     carry_v += tv;
     __syncthreads();  // s_wp / s_wv are reused by the next chunk
   }
+  uint32_t flag = 0;
+  if (flag_out) flag = __syncthreads_or((flags & kPartFlag) != 0 ? 1 : 0) != 0 ? 1u : 0u;
   if (threadIdx.x == 0) {
     off_end[0] = carry_p;
+    if (flag_out) *flag_out = flag;
     if (totals) {
       totals[0] = carry_p;
       totals[1] = carry_v;
-      totals[2] = *sort_flag;
+      totals[2] = flag_out ? flag : *sort_flag;
     }
   }
 }
@@ -853,8 +872,19 @@ int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s) {
 
 int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
   if (n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_fill_f32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
-  HRF_LAUNCH_CHECK();
+  int64_t head = 0;
+  if ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && n >= 1024) {
+    const int64_t n4 = n / 4;
+    hipLaunchKernelGGL(k_fill_f32x4, dim3(blocks_for(n4, 256 * kFillVec)), dim3(256), 0, s,
+                       reinterpret_cast<float4*>(p), v, n4);
+    HRF_LAUNCH_CHECK();
+    head = 4 * n4;
+  }
+  if (head < n) {
+    hipLaunchKernelGGL(k_fill_f32, dim3(blocks_for(n - head, 256)), dim3(256), 0, s, p + head, v,
+                       n - head);
+    HRF_LAUNCH_CHECK();
+  }
   return HRF_OK;
 }
 
@@ -868,7 +898,7 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
                      s, order, tiles, vis, n, bsum_p, bsum_v);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL((k_offsets_blocks<>), dim3(1), dim3(kScanThreads), 0, s, bsum_p, bsum_v,
-                     nb, off + n, sort_flag, totals);
+                     nb, off + n, sort_flag, totals, nullptr);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_offsets_scan, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, s,
                      order, tiles, vis, n, bsum_p, bsum_v, off, vis_off);
@@ -955,12 +985,12 @@ int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t 
 
 int64_t partial_elems(int64_t n) { return (n + kProjThreads - 1) / kProjThreads + 1; }
 
-int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n,
-                         const uint32_t* sort_flag, uint64_t* totals, hipStream_t s) {
+int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n, uint32_t* sort_flag,
+                         uint64_t* totals, hipStream_t s) {
   if (n <= 0) return HRF_OK;
   const int64_t nb = (n + kProjThreads - 1) / kProjThreads;
   hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_t, part_v,
-                     nb, part_t + nb, sort_flag, totals);
+                     nb, part_t + nb, nullptr, totals, sort_flag);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -973,7 +1003,7 @@ int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n
                      order, tiles, n, part_r);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_r, nullptr,
-                     nb, part_r + nb, nullptr, nullptr);
+                     nb, part_r + nb, nullptr, nullptr, nullptr);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

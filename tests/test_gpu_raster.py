@@ -79,6 +79,36 @@ def test_forward_parity_unsorted_depth(hrf, oracle_mod, case):
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
+def _swap(sc, i, j):
+    for name in ("cam_means", "z", "quats", "scales", "colours", "phase", "opac", "pprobs"):
+        a = getattr(sc, name)
+        a[[i, j]] = a[[j, i]]
+    return sc
+
+
+@pytest.mark.parametrize("at", [512, 2999], ids=["block_boundary", "last"])
+def test_forward_parity_single_depth_inversion(hrf, oracle_mod, at):
+    """Depth order broken at one place only: at the first Gaussian of a
+    256-Gaussian projection block (its predecessor is in the previous block)
+    or at the last Gaussian of a partial block.  The unsorted-depth flag
+    raised by that one block must still start the depth sort."""
+    sc = _scene(*CASES[1])
+    assert np.all(np.diff(sc.z) >= 0)
+    k = at
+    while sc.z[k - 1] == sc.z[k]:  # a pair of distinct depths ending at `at` or just before
+        k -= 1
+    _swap(sc, k - 1, k)
+    assert np.sum(np.diff(sc.z) < 0) == 1
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    print(f"inversion at {k}", flush=True)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_backward_parity(hrf, oracle_mod, case):
     import torch
