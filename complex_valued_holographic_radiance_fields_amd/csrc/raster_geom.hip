@@ -184,12 +184,50 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectParams p) {
 
 // ---------------------------------------------------------------- backward
 
-__global__ __launch_bounds__(256) void k_geom_backward(GeomBwdParams p) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (g >= p.n) return;
+// The accumulator records of a block's kGeomBwdThreads Gaussians are one
+// contiguous run of words: it is staged into LDS with consecutive lanes on
+// consecutive words (kAccUnroll loads in flight per thread), then each
+// thread reads its own record (LDS record stride padded to odd).
+constexpr int kGeomBwdThreads = 256;
+constexpr int kAccUnroll = 8;
+
+__global__ __launch_bounds__(kGeomBwdThreads) void k_geom_backward(GeomBwdParams p) {
+  extern __shared__ float s_acc[];
   const int C = p.C, P = p.P;
   const int AS = acc_stride(C, P);
-  const float* a = p.acc + g * AS;
+  const int ASP = AS | 1;
+  {
+    const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kGeomBwdThreads;
+    const int64_t rows = p.n - g0 < kGeomBwdThreads ? p.n - g0 : kGeomBwdThreads;
+    const float* src = p.acc + g0 * AS;
+    const int cnt = static_cast<int>(rows) * AS;
+    // (row, column) of word e, stepped by kGeomBwdThreads words per load
+    const int dq = kGeomBwdThreads / AS, dm = kGeomBwdThreads - dq * AS;
+    int r = static_cast<int>(threadIdx.x) / AS;
+    int c = static_cast<int>(threadIdx.x) - r * AS;
+    for (int e0 = threadIdx.x; e0 < cnt; e0 += kAccUnroll * kGeomBwdThreads) {
+      float v[kAccUnroll];
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; ++u) {
+        const int e = e0 + u * kGeomBwdThreads;
+        v[u] = e < cnt ? src[e] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kAccUnroll; ++u) {
+        if (e0 + u * kGeomBwdThreads < cnt) s_acc[r * ASP + c] = v[u];
+        r += dq;
+        c += dm;
+        if (c >= AS) {
+          c -= AS;
+          ++r;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kGeomBwdThreads + threadIdx.x;
+  if (g >= p.n) return;
+  const float* a = s_acc + threadIdx.x * ASP;
   const float tx = p.cam[g * 3 + 0], ty = p.cam[g * 3 + 1], tz = p.cam[g * 3 + 2];
 
   float Wm[3][3];
@@ -273,7 +311,10 @@ int launch_project(const ProjectParams& p, hipStream_t s) {
 
 int launch_geom_backward(const GeomBwdParams& p, hipStream_t s) {
   if (p.n == 0) return HRF_OK;
-  hipLaunchKernelGGL(k_geom_backward, dim3(blocks_for(p.n, 256)), dim3(256), 0, s, p);
+  const size_t lds = static_cast<size_t>(kGeomBwdThreads) * (acc_stride(p.C, p.P) | 1) *
+                    sizeof(float);
+  hipLaunchKernelGGL(k_geom_backward, dim3(blocks_for(p.n, kGeomBwdThreads)),
+                     dim3(kGeomBwdThreads), lds, s, p);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
