@@ -37,7 +37,8 @@
 namespace hrf {
 namespace {
 
-constexpr int kFftThreads = 512;
+constexpr int kFftThreads = 512;   // column passes
+constexpr int kRowThreads = 1024;  // row passes (same LDS batch, twice the waves)
 constexpr int kFftBatch = 4;  // rows / columns per block
 constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
 
@@ -198,8 +199,8 @@ constexpr int lds_elems() {
   return pad(kFftBatch * N - 1) + 1;
 }
 // Elements per thread when a block copies its B x N batch.
-template <int N>
-constexpr int kCopyIters = (kFftBatch * N + kFftThreads - 1) / kFftThreads;
+template <int N, int T = kFftThreads>
+constexpr int kCopyIters = (kFftBatch * N + T - 1) / T;
 
 // Twiddles are stored per stage, in the order the butterflies use them:
 // the stage with radix R after NS points have been combined holds
@@ -207,12 +208,12 @@ constexpr int kCopyIters = (kFftBatch * N + kFftThreads - 1) / kFftThreads;
 // k < NS, 1 <= t < R (OFF = sum of NS (R - 1) over the earlier stages; N - 1
 // entries in all).  A butterfly then reads its R - 1 twiddles at one base
 // address plus constant offsets.
-template <int N, int R, int NS, bool INV, int OFF>
+template <int N, int R, int NS, bool INV, int OFF, int T>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
   constexpr int B = kFftBatch;
   constexpr int NR = N / R;
   constexpr int NB = B * NR;
-  constexpr int BPT = (NB + kFftThreads - 1) / kFftThreads;
+  constexpr int BPT = (NB + T - 1) / T;
   constexpr int LS = B * NR;  // load stride between butterfly inputs
   constexpr int SS = B * NS;  // store stride between butterfly outputs
   constexpr bool lin_load = LS % 32 == 0;
@@ -231,9 +232,9 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   int ob[BPT];
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
-    const int q = tid + u * kFftThreads;
+    const int q = tid + u * T;
     ob[u] = -1;
-    if (BPT * kFftThreads == NB || q < NB) {
+    if (BPT * T == NB || q < NB) {
       const int j = q >> 2;  // butterfly index within its transform
       const int k = j % NS;
       float2 x[R];
@@ -278,11 +279,11 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   __syncthreads();
 }
 
-template <int N, bool INV, int NS, int OFF, int R, int... Rest>
+template <int T, int N, bool INV, int NS, int OFF, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, R, NS, INV, OFF>(lds, tw);
+  fft_stage<N, R, NS, INV, OFF, T>(lds, tw);
   if constexpr (sizeof...(Rest) > 0)
-    run_stages<N, INV, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
+    run_stages<T, N, INV, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
 
 // The plans (radix sequence per length), shared by the device transforms
@@ -302,9 +303,9 @@ struct Plan;
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct Plan<NN> {                                                                 \
-    template <bool INV>                                                             \
+    template <bool INV, int T = kFftThreads>                                        \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<NN, INV, 1, 0, __VA_ARGS__>(lds, tw);                              \
+      run_stages<T, NN, INV, 1, 0, __VA_ARGS__>(lds, tw);                           \
     }                                                                               \
   };
 HRF_FFT_PLANS(HRF_FFT_PLAN)
@@ -328,11 +329,11 @@ constexpr int kTwLdsElems = kTwInLds<N> ? N : 1;
 
 // Copies the table into LDS (when kTwInLds) and returns the pointer the
 // transforms read; the caller's next __syncthreads publishes it.
-template <int N>
+template <int N, int T = kFftThreads>
 __device__ __forceinline__ const float2* stage_twiddles(float2* s_tw,
                                                         const float2* __restrict__ tw) {
   if constexpr (kTwInLds<N>) {
-    for (int i = threadIdx.x; i < N - 1; i += kFftThreads) s_tw[i] = tw[i];
+    for (int i = threadIdx.x; i < N - 1; i += T) s_tw[i] = tw[i];
     return s_tw;
   } else {
     return tw;
@@ -394,7 +395,7 @@ __device__ __forceinline__ int64_t tile_off(int img, int ncb, int cb, int h, int
 // A / A': forward FFT of B rows of a plain (nimg, h, w_in) image placed at
 // column c_in of the zero-padded N-length row -> tiled (nimg, h, N).
 template <int N>
-__global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restrict__ src,
+__global__ __launch_bounds__(kRowThreads) void k_rows_in(const float2* __restrict__ src,
                                                          float2* __restrict__ dst, int nimg,
                                                          int h, int w_in, int c_in,
                                                          const float2* __restrict__ tw) {
@@ -402,16 +403,16 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
   constexpr int ncb = N / B;
   __shared__ float2 lds[lds_elems<N>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N>(s_tw, tw);
+  const float2* twp = stage_twiddles<N, kRowThreads>(s_tw, tw);
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
   {
     // All of a thread's loads are issued before the first LDS write.
-    float2 v[kCopyIters<N>];
+    float2 v[kCopyIters<N, kRowThreads>];
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
       const int rr = e & 3, i = e >> 2;  // 16 lanes per row: 128-byte runs
       const int r = r0 + rr;
       const int col = i - c_in;
@@ -420,14 +421,14 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
         v[it] = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
     }
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
       if (e < B * N) lds[pad(e)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<false>(lds, twp);
-  for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+  Plan<N>::template run<false, kRowThreads>(lds, twp);
+  for (int e = threadIdx.x; e < B * N; e += kRowThreads) {
     const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
     const int r = r0 + rr;
     if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, B)] = lds[pad(4 * (4 * cb + bc) + rr)];
@@ -437,7 +438,7 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_in(const float2* __restric
 // C / C': inverse FFT of B rows of a tiled (nimg, h, N) spectrum; keeps
 // columns [c_out, c_out + w_out) times `scale` -> plain (nimg, h, w_out).
 template <int N>
-__global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restrict__ src,
+__global__ __launch_bounds__(kRowThreads) void k_rows_out(const float2* __restrict__ src,
                                                           float2* __restrict__ dst, int nimg,
                                                           int h, int w_out, int c_out,
                                                           float scale,
@@ -446,30 +447,30 @@ __global__ __launch_bounds__(kFftThreads) void k_rows_out(const float2* __restri
   constexpr int ncb = N / B;
   __shared__ float2 lds[lds_elems<N>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N>(s_tw, tw);
+  const float2* twp = stage_twiddles<N, kRowThreads>(s_tw, tw);
   const int blocks_per_img = (h + B - 1) / B;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
   {
-    float2 v[kCopyIters<N>];
+    float2 v[kCopyIters<N, kRowThreads>];
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
       const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
       const int r = r0 + rr;
       v[it] = make_float2(0.0f, 0.0f);
       if (e < B * N && r < h) v[it] = src[tile_off(img, ncb, cb, h, r, bc, B)];
     }
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
       const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
       if (e < B * N) lds[pad(4 * (4 * cb + bc) + rr)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<true>(lds, twp);
-  for (int e = threadIdx.x; e < B * w_out; e += kFftThreads) {
+  Plan<N>::template run<true, kRowThreads>(lds, twp);
+  for (int e = threadIdx.x; e < B * w_out; e += kRowThreads) {
     const int rr = e & 3, i = e >> 2;
     const int r = r0 + rr;
     if (r < h) {
@@ -742,7 +743,7 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   {
     HRF_STAGE("asm_rows_in", s);
     const int nimg = P * C;
-    hipLaunchKernelGGL((k_rows_in<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kFftThreads), 0, s,
+    hipLaunchKernelGGL((k_rows_in<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads), 0, s,
                        fields, X, nimg, H, W, N / 2 - W / 2, tw);
     HRF_LAUNCH_CHECK();
   }
@@ -755,7 +756,7 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   {
     HRF_STAGE("asm_rows_out", s);
     const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
-    hipLaunchKernelGGL((k_rows_out<N>), dim3(C * ((S + B - 1) / B)), dim3(kFftThreads), 0, s, Z,
+    hipLaunchKernelGGL((k_rows_out<N>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s, Z,
                        holo, C, S, S, N / 2 - S / 2, scale, tw);
     HRF_LAUNCH_CHECK();
   }
@@ -773,7 +774,7 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
   const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
   {
     HRF_STAGE("asm_rows_in", s);
-    hipLaunchKernelGGL((k_rows_in<N>), dim3(C * ((S + B - 1) / B)), dim3(kFftThreads), 0, s,
+    hipLaunchKernelGGL((k_rows_in<N>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s,
                        gholo, X, C, S, S, N / 2 - S / 2, tw);
     HRF_LAUNCH_CHECK();
   }
@@ -787,7 +788,7 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
     HRF_STAGE("asm_rows_out", s);
     const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
     const int nimg = P * C;
-    hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kFftThreads), 0, s,
+    hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads), 0, s,
                        Z, gfields, nimg, H, W, N / 2 - W / 2, scale, tw);
     HRF_LAUNCH_CHECK();
   }
