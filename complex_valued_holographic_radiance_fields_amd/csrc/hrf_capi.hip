@@ -9,6 +9,8 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
+#include <chrono>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -51,7 +53,7 @@ int readback_acquire(Readback** out) {
       }
     }
   }
-  Readback r{nullptr, nullptr, nullptr, dev};
+  Readback r{nullptr, nullptr, nullptr, dev, 0};
   HRF_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 8 * sizeof(uint64_t),
                         hipHostMallocCoherent | hipHostMallocMapped));
   HRF_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&r.dev), r.host, 0));
@@ -60,8 +62,41 @@ int readback_acquire(Readback** out) {
   return HRF_OK;
 }
 
-void readback_arm(Readback* r, int words) {
-  for (int i = 0; i < words; ++i) reinterpret_cast<volatile uint64_t*>(r->host)[i] = ~0ull;
+uint64_t readback_arm(Readback* r) {
+  volatile uint64_t* h = r->host;
+  for (int i = 0; i < 4; ++i) h[i] = ~0ull;
+  std::atomic_thread_fence(std::memory_order_seq_cst);
+  r->seq = r->seq + 1 >= ~0ull - 1 ? 1 : r->seq + 1;
+  return r->seq;
+}
+
+int readback_wait(Readback* r, uint64_t tag) {
+  // The event wait can take tens of microseconds to return after the GPU
+  // signals; polling the tag word sees the kernel's last write within about
+  // a microsecond.  The poll is bounded: past kReadbackSpin the event wait
+  // (which always returns once the kernel has run) takes over.
+  constexpr auto kReadbackSpin = std::chrono::milliseconds(20);
+  const volatile uint64_t* h = r->host;
+  const auto t0 = std::chrono::steady_clock::now();
+  bool seen = false;
+  for (int i = 0;; ++i) {
+    if (h[3] == tag) {
+      seen = true;
+      break;
+    }
+    if ((i & 255) == 255 && std::chrono::steady_clock::now() - t0 > kReadbackSpin) break;
+    __builtin_ia32_pause();
+  }
+  if (!seen) {
+    HRF_HIP(hipEventSynchronize(r->ev));
+    if (h[3] != tag) {
+      set_error("internal: count read-back tag %llu not seen after the event (read %llu)",
+                static_cast<unsigned long long>(tag), static_cast<unsigned long long>(h[3]));
+      return HRF_ERR_HIP;
+    }
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
+  return HRF_OK;
 }
 
 void readback_release(Readback* r) {
@@ -372,7 +407,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   }
   ReadbackSlot slot;
   HRF_TRY(readback_acquire(&slot.r));
-  readback_arm(slot.r, 3);
+  const uint64_t tag = readback_arm(slot.r);
   {
     HRF_STAGE("project", s);
     HRF_TRY(launch_project(pp, s));
@@ -385,7 +420,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // scan writes [K, V, flag] straight into the pinned read-back words.
   {
     HRF_STAGE("scan", s);
-    HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, slot.r->dev, s));
+    HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, slot.r->dev, s, tag));
   }
   HRF_HIP(hipEventRecord(slot.r->ev, s));
   // The tile ranges need only the rectangles: they run while the host waits
@@ -394,7 +429,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
     HRF_STAGE("ranges", s);
     HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s));
   }
-  HRF_HIP(hipEventSynchronize(slot.r->ev));
+  HRF_TRY(readback_wait(slot.r, tag));
   const uint64_t host_tot[3] = {slot.r->host[0], slot.r->host[1], slot.r->host[2]};
   if (host_tot[1] > static_cast<uint64_t>(n) || host_tot[2] > 1) {
     set_error("internal: count read-back incomplete (V %llu, flag %llu)",

@@ -70,17 +70,22 @@ const char* get_error();
 // (one slot per concurrent caller and device; never freed), so calls on
 // different streams or threads never share one.
 struct Readback {
-  uint64_t* host;  // 8 words
+  uint64_t* host;  // 8 words: [0, 3) the counts, [3] the completion tag
   uint64_t* dev;   // the same words as a device address
   hipEvent_t ev;
   int device;
+  uint64_t seq;    // tags handed out so far
 };
 // A free slot of the current device (allocated on first need).
 int readback_acquire(Readback** out);
-// Sets host[0, words) to all ones before the writing kernel is queued, so a
+// Sets host[0, 4) to all ones before the writing kernel is queued, so a
 // write that is not visible reads as an out-of-range count, never a stale
-// one from an earlier call.
-void readback_arm(Readback* r, int words);
+// one from an earlier call, and returns the tag (never 0 or all ones) the
+// kernel must write to host[3] last.
+uint64_t readback_arm(Readback* r);
+// Waits for the tag (polling the pinned word for a bounded time, then the
+// event recorded after the writing kernel) and checks it arrived.
+int readback_wait(Readback* r, uint64_t tag);
 void readback_release(Readback* r);
 struct ReadbackSlot {
   Readback* r = nullptr;
@@ -251,11 +256,12 @@ int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int6
 // Exclusive pair offsets off[0..n] (off[n] = K) of the tile counts taken in
 // depth-rank order (tiles[order[i]]; order == nullptr: index order) and
 // exclusive visible offsets vis_off (index order); totals receives
-// [K, V, *sort_flag].  bsum_p / bsum_v: ceil(n / 2048) elements each.
+// [K, V, *sort_flag] and, when tag != 0, totals[3] = tag after a
+// system-scope fence (the host polls it).  bsum_p / bsum_v: ceil(n / 2048) elements each.
 int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t* vis,
                    int64_t n, uint64_t* off, uint32_t* vis_off, uint64_t* bsum_p,
                    uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
-                   hipStream_t s);
+                   hipStream_t s, uint64_t tag = 0);
 // The depth-order permutation used by the emit kernels is order[] when
 // *sorted_flag != 0 and the identity otherwise.
 // Count partials: part_t / part_v hold per-kProjThreads-block sums (from
@@ -265,7 +271,7 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 // launch_rank_partials forms part_r, the same for the tile counts taken in
 // depth-rank order (tiles[order[r]]), and scans it (totals untouched).
 int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n, uint32_t* sort_flag,
-                         uint64_t* totals, hipStream_t s);
+                         uint64_t* totals, hipStream_t s, uint64_t tag = 0);
 int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n,
                          uint64_t* part_r, hipStream_t s);
 // The emit kernels take the scanned bases: part_t (index order) or, when

@@ -421,7 +421,7 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
   PreWs w = carve_pre(cv, n, sp->channels);
   ReadbackSlot slot;
   HRF_TRY(readback_acquire(&slot.r));
-  readback_arm(slot.r, 3);
+  const uint64_t tag = readback_arm(slot.r);
   HRF_STAGE("pre_select", s);
   HRF_TRY(launch_fill_u32(w.zero, 0u, 1, s));
   const dim3 grid(blocks_for(n, kPreThreads));
@@ -436,12 +436,12 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
   // with the flags as both of its inputs); totals[1] = kept count, written
   // into the pinned read-back words, read while the compaction runs.
   HRF_TRY(launch_offsets(nullptr, w.flag, w.flag, n, w.off, w.pos, w.bsum_p, w.bsum_v, w.zero,
-                         slot.r->dev, s));
+                         slot.r->dev, s, tag));
   HRF_HIP(hipEventRecord(slot.r->ev, s));
   hipLaunchKernelGGL(k_pre_compact, grid, dim3(kPreThreads), 0, s, w.flag, w.pos, w.key, n,
                      w.ckey, w.cidx);
   HRF_LAUNCH_CHECK();
-  HRF_HIP(hipEventSynchronize(slot.r->ev));
+  HRF_TRY(readback_wait(slot.r, tag));
   const uint64_t kept = slot.r->host[1];
   if (kept > static_cast<uint64_t>(n)) {
     set_error("internal: selection count read-back incomplete (%llu)",

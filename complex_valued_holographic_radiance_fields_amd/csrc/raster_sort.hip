@@ -328,7 +328,7 @@ template <int THREADS = kScanThreads, int ITEMS = kScanItems>
 __global__ __launch_bounds__(THREADS) void k_offsets_blocks(
     uint64_t* __restrict__ bsum_p, uint32_t* __restrict__ bsum_v, int64_t nb,
     uint64_t* __restrict__ off_end, const uint32_t* __restrict__ sort_flag,
-    uint64_t* __restrict__ totals, uint32_t* __restrict__ flag_out) {
+    uint64_t* __restrict__ totals, uint32_t* __restrict__ flag_out, uint64_t tag) {
   __shared__ uint64_t s_wp[THREADS / 64];
   __shared__ uint32_t s_wv[THREADS / 64];
   uint64_t carry_p = 0;
@@ -379,6 +379,11 @@ __global__ __launch_bounds__(THREADS) void k_offsets_blocks(
       totals[0] = carry_p;
       totals[1] = carry_v;
       totals[2] = flag_out ? flag : *sort_flag;
+      if (tag) {
+        // the counts reach the host (system scope) before the tag does
+        __threadfence_system();
+        totals[3] = tag;
+      }
     }
   }
 }
@@ -891,14 +896,14 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s) {
 int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t* vis,
                    int64_t n, uint64_t* off, uint32_t* vis_off, uint64_t* bsum_p,
                    uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
-                   hipStream_t s) {
+                   hipStream_t s, uint64_t tag) {
   if (n <= 0) return HRF_OK;
   const int64_t nb = (n + kScanTile - 1) / kScanTile;
   hipLaunchKernelGGL(k_offsets_reduce, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0,
                      s, order, tiles, vis, n, bsum_p, bsum_v);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL((k_offsets_blocks<>), dim3(1), dim3(kScanThreads), 0, s, bsum_p, bsum_v,
-                     nb, off + n, sort_flag, totals, nullptr);
+                     nb, off + n, sort_flag, totals, nullptr, tag);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_offsets_scan, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, s,
                      order, tiles, vis, n, bsum_p, bsum_v, off, vis_off);
@@ -986,11 +991,11 @@ int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t 
 int64_t partial_elems(int64_t n) { return (n + kProjThreads - 1) / kProjThreads + 1; }
 
 int launch_partials_scan(uint64_t* part_t, uint32_t* part_v, int64_t n, uint32_t* sort_flag,
-                         uint64_t* totals, hipStream_t s) {
+                         uint64_t* totals, hipStream_t s, uint64_t tag) {
   if (n <= 0) return HRF_OK;
   const int64_t nb = (n + kProjThreads - 1) / kProjThreads;
   hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_t, part_v,
-                     nb, part_t + nb, nullptr, totals, sort_flag);
+                     nb, part_t + nb, nullptr, totals, sort_flag, tag);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1003,7 +1008,7 @@ int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n
                      order, tiles, n, part_r);
   HRF_LAUNCH_CHECK();
   hipLaunchKernelGGL((k_offsets_blocks<1024, 4>), dim3(1), dim3(1024), 0, s, part_r, nullptr,
-                     nb, part_r + nb, nullptr, nullptr, nullptr);
+                     nb, part_r + nb, nullptr, nullptr, nullptr, 0ull);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
