@@ -9,6 +9,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <atomic>
 #include <chrono>
 #include <cstring>
@@ -53,11 +54,10 @@ int readback_acquire(Readback** out) {
       }
     }
   }
-  Readback r{nullptr, nullptr, nullptr, dev, 0};
+  Readback r{nullptr, nullptr, dev, 0};
   HRF_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), 8 * sizeof(uint64_t),
                         hipHostMallocCoherent | hipHostMallocMapped));
   HRF_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&r.dev), r.host, 0));
-  HRF_HIP(hipEventCreateWithFlags(&r.ev, hipEventDisableTiming));
   *out = new Readback(r);
   return HRF_OK;
 }
@@ -70,27 +70,32 @@ uint64_t readback_arm(Readback* r) {
   return r->seq;
 }
 
-int readback_wait(Readback* r, uint64_t tag) {
-  // The event wait can take tens of microseconds to return after the GPU
-  // signals; polling the tag word sees the kernel's last write within about
-  // a microsecond.  The poll is bounded: past kReadbackSpin the event wait
-  // (which always returns once the kernel has run) takes over.
-  constexpr auto kReadbackSpin = std::chrono::milliseconds(20);
+int readback_wait(Readback* r, uint64_t tag, hipStream_t s) {
+  // A stream or event wait can take tens of microseconds to return after
+  // the GPU signals; polling the tag word sees the kernel's last write within
+  // about a microsecond.  The poll is bounded: past the bound a stream
+  // synchronisation (which returns once everything queued has run) takes
+  // over.
+  // HRF_READBACK_SPIN_US overrides the bound (0: always the stream wait).
+  auto spin = std::chrono::microseconds(20000);
+  if (const char* e = std::getenv("HRF_READBACK_SPIN_US")) spin = std::chrono::microseconds(std::atoll(e));
   const volatile uint64_t* h = r->host;
   const auto t0 = std::chrono::steady_clock::now();
   bool seen = false;
-  for (int i = 0;; ++i) {
-    if (h[3] == tag) {
-      seen = true;
-      break;
+  if (spin.count() > 0) {
+    for (int i = 0;; ++i) {
+      if (h[3] == tag) {
+        seen = true;
+        break;
+      }
+      if ((i & 255) == 255 && std::chrono::steady_clock::now() - t0 > spin) break;
+      __builtin_ia32_pause();
     }
-    if ((i & 255) == 255 && std::chrono::steady_clock::now() - t0 > kReadbackSpin) break;
-    __builtin_ia32_pause();
   }
   if (!seen) {
-    HRF_HIP(hipEventSynchronize(r->ev));
+    HRF_HIP(hipStreamSynchronize(s));
     if (h[3] != tag) {
-      set_error("internal: count read-back tag %llu not seen after the event (read %llu)",
+      set_error("internal: count read-back tag %llu not seen after the stream (read %llu)",
                 static_cast<unsigned long long>(tag), static_cast<unsigned long long>(h[3]));
       return HRF_ERR_HIP;
     }
@@ -422,14 +427,13 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
     HRF_STAGE("scan", s);
     HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, slot.r->dev, s, tag));
   }
-  HRF_HIP(hipEventRecord(slot.r->ev, s));
   // The tile ranges need only the rectangles: they run while the host waits
   // for the counts (and the render call reads them from the workspace).
   if (diff_ranges) {
     HRF_STAGE("ranges", s);
     HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s));
   }
-  HRF_TRY(readback_wait(slot.r, tag));
+  HRF_TRY(readback_wait(slot.r, tag, s));
   const uint64_t host_tot[3] = {slot.r->host[0], slot.r->host[1], slot.r->host[2]};
   if (host_tot[1] > static_cast<uint64_t>(n) || host_tot[2] > 1) {
     set_error("internal: count read-back incomplete (V %llu, flag %llu)",

@@ -65,14 +65,12 @@ const char* get_error();
 
 // -------------------------------------------------------- host read-back --
 // Small device results the host must read (pair / visible counts): pinned,
-// coherent host words that a kernel writes directly (through `dev`), and an
-// event recorded after that kernel.  Slots come from a per-process pool
-// (one slot per concurrent caller and device; never freed), so calls on
-// different streams or threads never share one.
+// coherent host words that a kernel writes directly (through `dev`).  Slots
+// come from a per-process pool (one slot per concurrent caller and device;
+// never freed), so calls on different streams or threads never share one.
 struct Readback {
   uint64_t* host;  // 8 words: [0, 3) the counts, [3] the completion tag
   uint64_t* dev;   // the same words as a device address
-  hipEvent_t ev;
   int device;
   uint64_t seq;    // tags handed out so far
 };
@@ -83,9 +81,10 @@ int readback_acquire(Readback** out);
 // one from an earlier call, and returns the tag (never 0 or all ones) the
 // kernel must write to host[3] last.
 uint64_t readback_arm(Readback* r);
-// Waits for the tag (polling the pinned word for a bounded time, then the
-// event recorded after the writing kernel) and checks it arrived.
-int readback_wait(Readback* r, uint64_t tag);
+// Waits for the tag (polling the pinned word for a bounded time, then
+// synchronising stream s, where the writing kernel was queued) and checks
+// it arrived.
+int readback_wait(Readback* r, uint64_t tag, hipStream_t s);
 void readback_release(Readback* r);
 struct ReadbackSlot {
   Readback* r = nullptr;

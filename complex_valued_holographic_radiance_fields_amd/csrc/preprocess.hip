@@ -437,11 +437,10 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
   // into the pinned read-back words, read while the compaction runs.
   HRF_TRY(launch_offsets(nullptr, w.flag, w.flag, n, w.off, w.pos, w.bsum_p, w.bsum_v, w.zero,
                          slot.r->dev, s, tag));
-  HRF_HIP(hipEventRecord(slot.r->ev, s));
   hipLaunchKernelGGL(k_pre_compact, grid, dim3(kPreThreads), 0, s, w.flag, w.pos, w.key, n,
                      w.ckey, w.cidx);
   HRF_LAUNCH_CHECK();
-  HRF_TRY(readback_wait(slot.r, tag));
+  HRF_TRY(readback_wait(slot.r, tag, s));
   const uint64_t kept = slot.r->host[1];
   if (kept > static_cast<uint64_t>(n)) {
     set_error("internal: selection count read-back incomplete (%llu)",

@@ -238,6 +238,24 @@ def test_bad_channels_raise(hrf):
                            8.0, 8.0, torch.eye(3, device=d), (16, 16), (16, 16), 1.0, 1000.0)
 
 
+def test_count_readback_stream_fallback(hrf, oracle_mod, monkeypatch):
+    """The pair / visible counts reach the host through pinned words that
+    the scan kernel tags last; with the poll disabled
+    (HRF_READBACK_SPIN_US=0) the host takes the stream-synchronisation
+    fallback, and both paths give the oracle's lists."""
+    sc = _scene(*CASES[1])
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    for spin in ("0", "20000"):
+        monkeypatch.setenv("HRF_READBACK_SPIN_US", spin)
+        t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+        print(f"spin={spin} K={pl.numel()}", flush=True)
+        np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+        np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+        np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+        assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 def test_forward_parity_wide_keys(hrf, oracle_mod):
     """Tile id and gaussian index need more than 32 bits together (16384
     tiles, 270k Gaussians): the binning takes the separate key/value sort
