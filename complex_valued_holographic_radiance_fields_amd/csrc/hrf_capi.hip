@@ -425,6 +425,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // scan writes [K, V, flag] straight into the pinned read-back words.
   {
     HRF_STAGE("scan", s);
+    slot.pending = true;
     HRF_TRY(launch_partials_scan(w.part_t, w.part_v, n, w.sort_flag, slot.r->dev, s, tag));
   }
   // The tile ranges need only the rectangles: they run while the host waits
@@ -434,6 +435,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
     HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s));
   }
   HRF_TRY(readback_wait(slot.r, tag, s));
+  slot.pending = false;
   const uint64_t host_tot[3] = {slot.r->host[0], slot.r->host[1], slot.r->host[2]};
   if (host_tot[1] > static_cast<uint64_t>(n) || host_tot[2] > 1) {
     set_error("internal: count read-back incomplete (V %llu, flag %llu)",

@@ -86,13 +86,18 @@ uint64_t readback_arm(Readback* r);
 // it arrived.
 int readback_wait(Readback* r, uint64_t tag, hipStream_t s);
 void readback_release(Readback* r);
+// Holds a slot for one call.  `pending` is set once the writing kernel is
+// queued and cleared by a successful wait: a slot left pending (an error
+// between the two) is never handed out again, since that kernel may still
+// write to it.
 struct ReadbackSlot {
   Readback* r = nullptr;
+  bool pending = false;
   ReadbackSlot() = default;
   ReadbackSlot(const ReadbackSlot&) = delete;
   ReadbackSlot& operator=(const ReadbackSlot&) = delete;
   ~ReadbackSlot() {
-    if (r) readback_release(r);
+    if (r && !pending) readback_release(r);
   }
 };
 

@@ -435,12 +435,14 @@ int hrf_preprocess_select(const hrf_scene_params* sp, const float* R, const floa
   // Exclusive positions of the kept Gaussians (the binning's offsets scan,
   // with the flags as both of its inputs); totals[1] = kept count, written
   // into the pinned read-back words, read while the compaction runs.
+  slot.pending = true;
   HRF_TRY(launch_offsets(nullptr, w.flag, w.flag, n, w.off, w.pos, w.bsum_p, w.bsum_v, w.zero,
                          slot.r->dev, s, tag));
   hipLaunchKernelGGL(k_pre_compact, grid, dim3(kPreThreads), 0, s, w.flag, w.pos, w.key, n,
                      w.ckey, w.cidx);
   HRF_LAUNCH_CHECK();
   HRF_TRY(readback_wait(slot.r, tag, s));
+  slot.pending = false;
   const uint64_t kept = slot.r->host[1];
   if (kept > static_cast<uint64_t>(n)) {
     set_error("internal: selection count read-back incomplete (%llu)",
