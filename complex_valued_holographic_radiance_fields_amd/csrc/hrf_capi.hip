@@ -530,7 +530,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_packed(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
-                                 f.gx, vbits, b.keys_a, s));
+                                 f.gx, vbits, b.keys_a, s, w.vis, w.part_v,
+                                 num_visible > 0 ? visible : nullptr));
     }
     bool in_b = false;
     // The last sort pass writes the gaussian bits straight into point_list;
@@ -554,7 +555,8 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
-                                num_pairs, f.gx, b.keys_a, vals_a, s));
+                                num_pairs, f.gx, b.keys_a, vals_a, s, w.vis, w.part_v,
+                                num_visible > 0 ? visible : nullptr));
     }
     bool in_b = false;
     {
@@ -600,7 +602,6 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     if (order_out)
       HRF_TRY(launch_order_by_cost(rp.sub_cnt_out, f.ntiles * g->planes, order_out, s));
   }
-  if (num_visible > 0) HRF_TRY(launch_compact_visible(w.vis, w.part_v, n, visible, s));
   return HRF_OK;
 }
 

@@ -266,8 +266,6 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
                    int64_t n, uint64_t* off, uint32_t* vis_off, uint64_t* bsum_p,
                    uint32_t* bsum_v, const uint32_t* sort_flag, uint64_t* totals,
                    hipStream_t s, uint64_t tag = 0);
-// The depth-order permutation used by the emit kernels is order[] when
-// *sorted_flag != 0 and the identity otherwise.
 // Count partials: part_t / part_v hold per-kProjThreads-block sums (from
 // k_project, index order, part_v with the kPartFlag bits); launch_partials_scan
 // turns them, in place, into exclusive block bases (part_t[nb] = K), writes
@@ -280,22 +278,26 @@ int launch_rank_partials(const uint32_t* order, const uint32_t* tiles, int64_t n
                          uint64_t* part_r, hipStream_t s);
 // The emit kernels take the scanned bases: part_t (index order) or, when
 // *sorted_flag, part_r (rank order), and form each block's pair offsets
-// from the tile counts themselves.
+// from the tile counts themselves; the depth-order permutation they use is
+// order[] when *sorted_flag != 0 and the identity otherwise.  With
+// `visible`, the emit launch also writes the visible compaction (the
+// indices with vis set, in order: index block b of 256 from vis and the
+// scanned bases part_v; same grid as the emission).
 int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s);
+                      hipStream_t s, const uint32_t* vis = nullptr,
+                      const uint32_t* part_v = nullptr, int64_t* visible = nullptr);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s);
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       const uint32_t* vis = nullptr, const uint32_t* part_v = nullptr,
+                       int64_t* visible = nullptr);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
-// visible = indices with vis set, in order; part_v = scanned block bases.
-int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t n,
-                           int64_t* visible, hipStream_t s);
 int64_t partial_elems(int64_t n);  // kProjThreads-blocks + 1
 int launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t s);
 int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);

@@ -473,6 +473,26 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
 // [off[r_begin], off[r_end]).  Tile order inside a Gaussian is y outer, x
 // inner (rasterizer_splat.cu:162-173).
 constexpr int kEmitThreads = kProjThreads;
+// Visible compaction of index block blockIdx.x (indices [256 b, 256 b +
+// 256), the block base part_v[b] from the scan), done by the emission
+// launch, whose grid has the same blocks: every thread of the block calls
+// it.
+struct VisibleOut {
+  const uint32_t* vis;
+  const uint32_t* part_v;
+  int64_t* visible;  // nullptr: nothing to write
+};
+
+__device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int64_t n) {
+  if (!vo.visible) return;
+  __shared__ uint32_t s_vw[kEmitThreads / 64];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kEmitThreads + threadIdx.x;
+  const uint32_t v = i < n ? vo.vis[i] : 0u;
+  uint32_t total;
+  const uint32_t ex = block_exclusive_scan<uint32_t>(v, &total, s_vw);
+  if (v) vo.visible[vo.part_v[blockIdx.x] + ex] = i;
+}
+
 __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ part_t,
                                                       const uint64_t* __restrict__ part_r,
                                                       const uint32_t* __restrict__ tiles,
@@ -480,7 +500,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
                                                       const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
                                                       int gx, uint32_t* __restrict__ keys,
-                                                      uint32_t* __restrict__ vals) {
+                                                      uint32_t* __restrict__ vals, VisibleOut vo) {
+  compact_visible_block(vo, n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -536,7 +557,9 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
                                                              const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
                                                              int64_t n, int gx, int vbits,
-                                                             uint32_t* __restrict__ words) {
+                                                             uint32_t* __restrict__ words,
+                                                             VisibleOut vo) {
+  compact_visible_block(vo, n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -722,17 +745,6 @@ __global__ __launch_bounds__(kDiffThreads) void k_ranges_from_diff(const int32_t
   }
 }
 
-__global__ __launch_bounds__(kProjThreads) void k_compact_visible(
-    const uint32_t* __restrict__ vis, const uint32_t* __restrict__ part_v, int64_t n,
-    int64_t* __restrict__ visible) {
-  __shared__ uint32_t s_wave[kProjThreads / 64];
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kProjThreads + threadIdx.x;
-  const uint32_t v = i < n ? vis[i] : 0u;
-  uint32_t total;
-  const uint32_t ex = block_exclusive_scan<uint32_t>(v, &total, s_wave);
-  if (v) visible[part_v[blockIdx.x] + ex] = i;
-}
-
 }  // namespace
 
 size_t scan_scratch_elems(int64_t n) {
@@ -914,20 +926,24 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
-                      hipStream_t s) {
+                      hipStream_t s, const uint32_t* vis, const uint32_t* part_v,
+                      int64_t* visible) {
   if (k <= 0 || n <= 0) return HRF_OK;
+  const VisibleOut vo{vis, part_v, visible};
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, part_t,
-                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals);
+                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals, vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s) {
+                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       const uint32_t* vis, const uint32_t* part_v, int64_t* visible) {
   if (n <= 0) return HRF_OK;
+  const VisibleOut vo{vis, part_v, visible};
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words);
+                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words, vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -975,15 +991,6 @@ int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges, int nti
   if (k <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_tile_ranges, dim3(blocks_for(k, 256)), dim3(256), 0, s, keys, k,
                      ranges);
-  HRF_LAUNCH_CHECK();
-  return HRF_OK;
-}
-
-int launch_compact_visible(const uint32_t* vis, const uint32_t* part_v, int64_t n,
-                           int64_t* visible, hipStream_t s) {
-  if (n <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_compact_visible, dim3(blocks_for(n, kProjThreads)), dim3(kProjThreads), 0,
-                     s, vis, part_v, n, visible);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
