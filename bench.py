@@ -56,6 +56,29 @@ def profiled_traffic(config, stage, C, M):
     return None, None
 
 
+# One wave64 VALU instruction per SIMD every 4 cycles: 256 CUs x 4 SIMDs x
+# 2.4 GHz / 4.
+VALU_PEAK_WAVE_INSTR_PER_S = 256 * 4 * 2.4e9 / 4
+
+
+def profiled_valu(config, stage, C, M):
+    """VALU wave-instructions per dispatch of `stage`'s kernel from the
+    committed rocprofv3 SQ_INSTS_VALU summary of this workload, or None."""
+    path = os.path.join(REPO, "profiles", f"valu_{config}.txt")
+    name = STAGE_KERNEL.get(stage, "").format(C=C, M=M)
+    if not name or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("#") or not line.startswith(name + " "):
+                continue
+            rest = line[len(name):].split()
+            # columns after the name: n, waves, valu, lds, salu, valu_us
+            if len(rest) >= 3:
+                return int(float(rest[2]))
+    return None
+
+
 def algorithmic_bytes(N, K, P, C, W, H, S, T):
     """Compulsory-dataflow byte model per frame and per stage launch.
 
@@ -507,6 +530,20 @@ def main():
                 "avg_launch_ms": round(dom_live, 4),
                 "bytes_per_launch": int(B["per_launch"][dom]), "traffic_source": src}
 
+    # Diagnostic: the render kernels are VALU-bound, so their issue time at
+    # the FP32 vector peak (instruction counts from the committed profile)
+    # against the measured launch time is the fraction that matters there.
+    valu = {}
+    for st in ("render_fwd", "render_bwd"):
+        instr = profiled_valu(spec.name, st, C, 2 * S)
+        t_ms = dom_live if (st == dom and dom_live) else stages.get(st, {}).get("avg_launch_ms")
+        if instr and t_ms:
+            issue_ms = instr / VALU_PEAK_WAVE_INSTR_PER_S * 1e3
+            valu[st] = {"wave_instructions": instr, "issue_ms_at_peak": round(issue_ms, 4),
+                        "measured_ms": round(t_ms, 4), "frac": round(issue_ms / t_ms, 3)}
+    if valu:
+        valu["source"] = f"profiles/valu_{spec.name}.txt"
+
     pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
     opt_step = measure_optimizer(spec, dev, args.no_cpu_baseline)
     recon = measure_reconstruction(spec, dev, args.no_cpu_baseline)
@@ -555,6 +592,7 @@ def main():
         "stages_ms_per_frame": {s: round(v["ms_per_frame"], 4) for s, v in stages.items()},
         "stages_from": f"stage-traced pass of {prof_steps} frames",
         "roofline": roof,
+        "valu": valu or None,
         "cpu_baseline": cpu,
         "preprocess": pre,
         "optimizer": opt_step,
