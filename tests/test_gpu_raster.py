@@ -256,6 +256,47 @@ def test_count_readback_stream_fallback(hrf, oracle_mod, monkeypatch):
         assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
+def test_concurrent_forwards_on_two_streams(hrf, oracle_mod):
+    """Two host threads rasterize different scenes at the same time, each on
+    its own stream: the count read-backs use separate pinned slots and every
+    result matches the oracle."""
+    import threading
+
+    import torch
+
+    scs = [_scene(*CASES[1]), _scene(*CASES[3])]
+    refs = []
+    for sc in scs:
+        g, cam = oracle_inputs(sc)
+        refs.append(oracle_mod.rasterize_forward(g, cam))
+    errors, outs = [], [[], []]
+
+    def worker(i):
+        try:
+            st = torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                for _ in range(4):
+                    _, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(scs[i])
+                    outs[i].append((pl.cpu().numpy(), ranges.cpu().numpy(),
+                                    field.cpu().numpy()))
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=100)
+    print(f"threads done, errors={errors}", flush=True)
+    assert not errors
+    for i in range(2):
+        assert len(outs[i]) == 4
+        for pl, ranges, field in outs[i]:
+            np.testing.assert_array_equal(ranges, refs[i]["ranges"])
+            np.testing.assert_array_equal(pl, refs[i]["point_list"])
+            assert rel_l2(field, refs[i]["field"]) < TOL
+
+
 def test_forward_parity_wide_keys(hrf, oracle_mod):
     """Tile id and gaussian index need more than 32 bits together (16384
     tiles, 270k Gaussians): the binning takes the separate key/value sort
