@@ -333,7 +333,9 @@ def bench_cfg3(args, dev):
     """Config 3, the propagation-only microbench: a (3, 2048, 2048) field to
     8 distances on the 4096 grid, forward (D*C outputs) + adjoint (sum over
     distances back to the field) per step, through the multi-distance entry
-    points.  Byte model: the one SURVEY gives for config 3."""
+    points.  Byte model: every 2-D transform is one read and one write of
+    its M x M complex64 grid, plus the S x S inputs and outputs (the same
+    compulsory-dataflow model as the headline frame)."""
     import numpy as np
     import torch
 
