@@ -107,6 +107,31 @@ struct Dft<8, INV> {
   }
 };
 
+// DFT-8 of inputs that are zero at t = 0, 1, 6, 7 (the first stage of a
+// transform whose nonzero input lies in [N/4, 3N/4)): the two DFT-4 halves
+// of (0, a, c, 0) reduce to sums and differences of a and c.
+template <bool INV>
+__device__ __forceinline__ void dft8_half(float2 (&x)[8]) {
+  const float2 a = x[2], b = x[3], c = x[4], d = x[5];
+  const float2 ma = mul_mi<INV>(a), mb = mul_mi<INV>(b);
+  float2 e[4] = {cadd(c, a), csub(ma, c), csub(c, a), csub(make_float2(-c.x, -c.y), ma)};
+  float2 o[4] = {cadd(d, b), csub(mb, d), csub(d, b), csub(make_float2(-d.x, -d.y), mb)};
+  constexpr float k = 0.70710678118654752f;
+  const float2 o1 = INV ? make_float2((o[1].x - o[1].y) * k, (o[1].x + o[1].y) * k)
+                        : make_float2((o[1].x + o[1].y) * k, (o[1].y - o[1].x) * k);
+  const float2 o3 = INV ? make_float2(-(o[3].x + o[3].y) * k, (o[3].x - o[3].y) * k)
+                        : make_float2((o[3].y - o[3].x) * k, -(o[3].x + o[3].y) * k);
+  const float2 o2 = mul_mi<INV>(o[2]);
+  x[0] = cadd(e[0], o[0]);
+  x[4] = csub(e[0], o[0]);
+  x[1] = cadd(e[1], o1);
+  x[5] = csub(e[1], o1);
+  x[2] = cadd(e[2], o2);
+  x[6] = csub(e[2], o2);
+  x[3] = cadd(e[3], o3);
+  x[7] = csub(e[3], o3);
+}
+
 // Odd radix by symmetric pairing: X_m = x0 + sum_j cos(2 pi jm/R)(x_j+x_{R-j})
 //   -/+ i sum_j sin(2 pi jm/R)(x_j-x_{R-j}),  X_{R-m} with the opposite sign.
 template <int R>
@@ -208,8 +233,11 @@ constexpr int kCopyIters = (kFftBatch * N + T - 1) / T;
 // k < NS, 1 <= t < R (OFF = sum of NS (R - 1) over the earlier stages; N - 1
 // entries in all).  A butterfly then reads its R - 1 twiddles at one base
 // address plus constant offsets.
-template <int N, int R, int NS, bool INV, int OFF, int T>
+// HALF (first stage only, R = 8): the inputs at t = 0, 1, 6, 7 are zero and
+// are neither read nor stored by the caller.
+template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF = false>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
+  static_assert(!HALF || (R == 8 && NS == 1), "pruned first stage is radix 8");
   constexpr int B = kFftBatch;
   constexpr int NR = N / R;
   constexpr int NB = B * NR;
@@ -241,10 +269,12 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
       if (lin_load) {
         const int base = pad(q);
 #pragma unroll
-        for (int t = 0; t < R; ++t) x[t] = lds[base + t * LSP];
+        for (int t = 0; t < R; ++t)
+          if (!HALF || (t >= 2 && t <= 5)) x[t] = lds[base + t * LSP];
       } else {
 #pragma unroll
-        for (int t = 0; t < R; ++t) x[t] = lds[pad(q + t * LS)];
+        for (int t = 0; t < R; ++t)
+          if (!HALF || (t >= 2 && t <= 5)) x[t] = lds[pad(q + t * LS)];
       }
       if (NS > 1) {
         const float2* wk = tw + (twoff + OFF + k * (R - 1) - 1);
@@ -255,7 +285,10 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
           x[t] = cmulf(x[t], w);
         }
       }
-      Dft<R, INV>::run(x);
+      if constexpr (HALF)
+        dft8_half<INV>(x);
+      else
+        Dft<R, INV>::run(x);
 #pragma unroll
       for (int t = 0; t < R; ++t) y[u][t] = x[t];
       // Stockham output position (j/NS)*NS*R + k + t*NS, interleaved.
@@ -279,11 +312,11 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   __syncthreads();
 }
 
-template <int T, int N, bool INV, int NS, int OFF, int R, int... Rest>
+template <int T, int N, bool INV, bool HALF, int NS, int OFF, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, R, NS, INV, OFF, T>(lds, tw);
+  fft_stage<N, R, NS, INV, OFF, T, HALF && NS == 1>(lds, tw);
   if constexpr (sizeof...(Rest) > 0)
-    run_stages<T, N, INV, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
+    run_stages<T, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
 
 // The plans (radix sequence per length), shared by the device transforms
@@ -303,9 +336,9 @@ struct Plan;
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct Plan<NN> {                                                                 \
-    template <bool INV, int T = kFftThreads>                                        \
+    template <bool INV, int T = kFftThreads, bool HALF = false>                     \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<T, NN, INV, 1, 0, __VA_ARGS__>(lds, tw);                           \
+      run_stages<T, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                     \
     }                                                                               \
   };
 HRF_FFT_PLANS(HRF_FFT_PLAN)
@@ -394,7 +427,9 @@ __device__ __forceinline__ int64_t tile_off(int img, int ncb, int cb, int h, int
 
 // A / A': forward FFT of B rows of a plain (nimg, h, w_in) image placed at
 // column c_in of the zero-padded N-length row -> tiled (nimg, h, N).
-template <int N>
+// HALF: [c_in, c_in + w_in) lies in [N/4, 3N/4); only that half is staged
+// and the first stage is pruned.
+template <int N, bool HALF>
 __global__ __launch_bounds__(kRowThreads) void k_rows_in(const float2* __restrict__ src,
                                                          float2* __restrict__ dst, int nimg,
                                                          int h, int w_in, int c_in,
@@ -409,25 +444,28 @@ __global__ __launch_bounds__(kRowThreads) void k_rows_in(const float2* __restric
   const int r0 = (blockIdx.x - img * blocks_per_img) * B;
   {
     // All of a thread's loads are issued before the first LDS write.
-    float2 v[kCopyIters<N, kRowThreads>];
+    constexpr int E0 = HALF ? B * N / 4 : 0;
+    constexpr int EN = HALF ? B * N / 2 : B * N;
+    constexpr int IT = (EN + kRowThreads - 1) / kRowThreads;
+    float2 v[IT];
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
+    for (int it = 0; it < IT; ++it) {
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * kRowThreads;
       const int rr = e & 3, i = e >> 2;  // 16 lanes per row: 128-byte runs
       const int r = r0 + rr;
       const int col = i - c_in;
       v[it] = make_float2(0.0f, 0.0f);
-      if (e < B * N && r < h && col >= 0 && col < w_in)
+      if (e < E0 + EN && r < h && col >= 0 && col < w_in)
         v[it] = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
     }
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
-      if (e < B * N) lds[pad(e)] = v[it];
+    for (int it = 0; it < IT; ++it) {
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * kRowThreads;
+      if (e < E0 + EN) lds[pad(e)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<false, kRowThreads>(lds, twp);
+  Plan<N>::template run<false, kRowThreads, HALF>(lds, twp);
   for (int e = threadIdx.x; e < B * N; e += kRowThreads) {
     const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
     const int r = r0 + rr;
@@ -494,7 +532,9 @@ __device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb
 // (P*C, H, N) row spectra of the fields (rows r_pad..r_pad+H of the padded
 // grid; the other rows are zero); Z tiled (C, S, N) receives rows
 // [s_crop, s_crop+S) of iFFTcol(sum_p FFTcol(X[p,c]) * T[p,c] * A).
-template <int N>
+// HALF: the field rows lie in [N/4, 3N/4); only that half is staged and the
+// forward transforms' first stage is pruned.
+template <int N, bool HALF>
 __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(const float2* __restrict__ X,
                                                          float2* __restrict__ Z, int P, int C,
                                                          int H, int r_pad, int S, int s_crop,
@@ -533,14 +573,16 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
     const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
     // (kz and acc are live here, so the copy is not unrolled: its load
     // buffer would not fit the register budget.)
-    for (int e = threadIdx.x; e < B * N; e += kFftThreads) {
+    constexpr int E0 = HALF ? B * N / 4 : 0;
+    constexpr int E1 = HALF ? 3 * B * N / 4 : B * N;
+    for (int e = E0 + static_cast<int>(threadIdx.x); e < E1; e += kFftThreads) {
       const int r = e / B - r_pad;
       float2 v = make_float2(0.0f, 0.0f);
       if (r >= 0 && r < H) v = src[e - r_pad * B];
       lds[pad(e)] = v;
     }
     __syncthreads();
-    Plan<N>::template run<false>(lds, twp);
+    Plan<N>::template run<false, kFftThreads, HALF>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -581,7 +623,9 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
 // B': adjoint column pass.  X tiled (C, S, N) row spectra of the padded
 // hologram gradient (rows s_pad..s_pad+S of the grid); Z tiled (P*C, H, N)
 // receives rows [r_crop, r_crop+H) of iFFTcol(FFTcol(X[c]) conj(T[p,c]) A).
-template <int N>
+// HALF: the S gradient rows lie in [N/4, 3N/4) (always, with N = 2S); only
+// that half is staged and the forward transform's first stage is pruned.
+template <int N, bool HALF>
 __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(const float2* __restrict__ X,
                                                          float2* __restrict__ Z, int P, int C,
                                                          int S, int s_pad, int H, int r_crop,
@@ -599,22 +643,25 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
 
   const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, B);
   {
-    float2 v[kCopyIters<N>];
+    constexpr int E0 = HALF ? B * N / 4 : 0;
+    constexpr int EN = HALF ? B * N / 2 : B * N;
+    constexpr int IT = (EN + kFftThreads - 1) / kFftThreads;
+    float2 v[IT];
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
+    for (int it = 0; it < IT; ++it) {
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * kFftThreads;
       const int r = e / B - s_pad;
       v[it] = make_float2(0.0f, 0.0f);
-      if (e < B * N && r >= 0 && r < S) v[it] = src[e - s_pad * B];
+      if (e < E0 + EN && r >= 0 && r < S) v[it] = src[e - s_pad * B];
     }
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kFftThreads;
-      if (e < B * N) lds[pad(e)] = v[it];
+    for (int it = 0; it < IT; ++it) {
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * kFftThreads;
+      if (e < E0 + EN) lds[pad(e)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<false>(lds, twp);
+  Plan<N>::template run<false, kFftThreads, HALF>(lds, twp);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
@@ -743,14 +790,22 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   {
     HRF_STAGE("asm_rows_in", s);
     const int nimg = P * C;
-    hipLaunchKernelGGL((k_rows_in<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads), 0, s,
-                       fields, X, nimg, H, W, N / 2 - W / 2, tw);
+    if (2 * W <= N)
+      hipLaunchKernelGGL((k_rows_in<N, true>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads),
+                         0, s, fields, X, nimg, H, W, N / 2 - W / 2, tw);
+    else
+      hipLaunchKernelGGL((k_rows_in<N, false>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads),
+                         0, s, fields, X, nimg, H, W, N / 2 - W / 2, tw);
     HRF_LAUNCH_CHECK();
   }
   {
     HRF_STAGE("asm_col_fwd", s);
-    hipLaunchKernelGGL((k_col_fwd<N>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P, C, H,
-                       N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
+    if (2 * H <= N)
+      hipLaunchKernelGGL((k_col_fwd<N, true>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P,
+                         C, H, N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
+    else
+      hipLaunchKernelGGL((k_col_fwd<N, false>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z,
+                         P, C, H, N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
     HRF_LAUNCH_CHECK();
   }
   {
@@ -774,14 +829,15 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
   const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
   {
     HRF_STAGE("asm_rows_in", s);
-    hipLaunchKernelGGL((k_rows_in<N>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s,
+    // S rows of width S = N/2 at column N/4: always the pruned variant
+    hipLaunchKernelGGL((k_rows_in<N, true>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s,
                        gholo, X, C, S, S, N / 2 - S / 2, tw);
     HRF_LAUNCH_CHECK();
   }
   {
     HRF_STAGE("asm_col_adj", s);
-    hipLaunchKernelGGL((k_col_adj<N>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P, C, S,
-                       N / 2 - S / 2, H, N / 2 - H / 2, sfreq, ap, mc, tw);
+    hipLaunchKernelGGL((k_col_adj<N, true>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P,
+                       C, S, N / 2 - S / 2, H, N / 2 - H / 2, sfreq, ap, mc, tw);
     HRF_LAUNCH_CHECK();
   }
   {
