@@ -69,6 +69,30 @@ def test_forward_matches_oracle(hrf, oracle_mod, near, far, P, C):
         np.testing.assert_allclose(got[k], ref[k], rtol=3e-7, err_msg=k)
 
 
+@pytest.mark.parametrize("depths", ["equal", "narrow"])
+def test_forward_depth_sort_bit_range(hrf, oracle_mod, depths):
+    """Depth keys that are all equal (index order must stay) or differ only
+    in their low 16 bits, with many ties: the stable depth order still
+    matches the oracle's."""
+    prm = list(_params(n=4000, P=3, C=3, seed=5))
+    prm[7] = np.eye(3, dtype=np.float32)
+    prm[8] = np.zeros(3, np.float32)
+    rng = np.random.default_rng(6)
+    means = prm[0].copy()
+    if depths == "equal":
+        means[:, 2] = 3.0
+    else:
+        means[:, 2] = (3.0 + rng.integers(0, 300, size=len(means)) * 2.0 ** -20).astype(np.float32)
+    means[::7, 2] = 0.5  # some rows in front of the near plane
+    prm[0] = means
+    ref = oracle_mod.preprocess_forward(*prm, near=1.0, far=1000.0)
+    out = _run(prm, 1.0, 1000.0)
+    print(f"depths={depths} selected={len(ref['idxs'])}", flush=True)
+    assert len(ref["idxs"]) > 1000
+    np.testing.assert_array_equal(out[-1].cpu().numpy(), ref["idxs"])
+    np.testing.assert_array_equal(out[1].cpu().numpy(), ref["z"])
+
+
 @pytest.mark.parametrize("near,far,P,C", [(1.0, 1000.0, 3, 3), (1.0, 4.0, 5, 2)])
 def test_backward_matches_oracle(hrf, oracle_mod, near, far, P, C):
     from complex_valued_holographic_radiance_fields_amd import preprocess
