@@ -585,7 +585,6 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.pprobs = g->plane_probs;
   rp.n = n;
   rp.num_pairs = num_pairs;
-  int32_t* order_out = nullptr;
   if (plane_lists) {
     HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
                      hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
@@ -594,13 +593,10 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
     rp.sub_out = sw.entries;
     rp.sub_cnt_out = sw.counts;
-    order_out = sw.order;
   }
   {
     HRF_STAGE("render_fwd", s);
     HRF_TRY(launch_render_forward(rp, s));
-    if (order_out)
-      HRF_TRY(launch_order_by_cost(rp.sub_cnt_out, f.ntiles * g->planes, order_out, s));
   }
   return HRF_OK;
 }
@@ -609,7 +605,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
                         const float* final_T, const int32_t* n_contrib,
                         const int32_t* point_list, const int32_t* ranges, int64_t num_pairs,
                         void* ws, size_t ws_bytes, const void* fwd_geom_ws,
-                        size_t fwd_geom_ws_bytes, const void* plane_lists,
+                        size_t fwd_geom_ws_bytes, void* plane_lists,
                         size_t plane_lists_bytes, float* grad_cam, float* grad_z,
                         float* grad_quats, float* grad_scales, float* grad_colours,
                         float* grad_phase, float* grad_opacities, float* grad_plane_probs,
@@ -650,6 +646,18 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     rec = fw.rec;
     pmask = fw.pmask;
   }
+  // Plane member lists from the forward: the render backward walks them, in
+  // the block order the prologue forms from their counts (written into the
+  // lists' order words).
+  SubWs sw{};
+  const bool use_sub = plane_lists && num_pairs > 0;
+  if (use_sub) {
+    HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
+                     hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
+                     "plane lists"));
+    Carver cs(plane_lists);
+    sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
+  }
   {
     HRF_STAGE("project", s);
     if (!fwd_geom_ws) {
@@ -662,7 +670,8 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
       pp.vis = w.vis;
       HRF_TRY(launch_project(pp, s));
     }
-    HRF_TRY(launch_fill_f32(w.acc, 0.0f, n * acc_stride(g->channels, g->planes), s));
+    HRF_TRY(launch_bwd_prologue(w.acc, n * acc_stride(g->channels, g->planes), sw.counts,
+                                use_sub ? f.ntiles * g->planes : 0, sw.order, s));
   }
 
   if (num_pairs > 0) {
@@ -684,13 +693,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     rp.final_T_in = final_T;
     rp.n_contrib_in = n_contrib;
     rp.acc = w.acc;
-    if (plane_lists) {
-      HRF_TRY(check_ws(const_cast<void*>(plane_lists), plane_lists_bytes,
-                       hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height,
-                                                   g->planes),
-                       "plane lists"));
-      Carver cs(const_cast<void*>(plane_lists));
-      const SubWs sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
+    if (use_sub) {
       rp.sub = sw.entries;
       rp.sub_cnt = sw.counts;
       rp.order = sw.order;

@@ -340,9 +340,11 @@ struct RenderParams {
 int launch_render_forward(const RenderParams& p, hipStream_t s);
 int launch_render_empty(const RenderParams& p, hipStream_t s);
 int launch_render_backward(const RenderParams& p, hipStream_t s);
-// order[0..m) = the ids 0..m-1 sorted by cnt[id] descending (in logarithmic
-// buckets, 8 per octave; arbitrary order inside a bucket).
-int launch_order_by_cost(const int32_t* cnt, int m, int32_t* order, hipStream_t s);
+// Backward prologue, one launch: acc[0, n) = 0 and, when order != nullptr
+// and m > 0, order[0..m) = the ids 0..m-1 sorted by cnt[id] descending (in
+// logarithmic buckets, 8 per octave; arbitrary order inside a bucket).
+int launch_bwd_prologue(float* acc, int64_t n, const int32_t* cnt, int m, int32_t* order,
+                        hipStream_t s);
 
 // ASM (band-limited angular spectrum).
 struct AsmConsts {

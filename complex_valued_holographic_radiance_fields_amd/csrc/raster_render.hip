@@ -593,8 +593,9 @@ __device__ __forceinline__ int cost_bucket(int c) {
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderBins = 256;
 
-__global__ __launch_bounds__(kOrderThreads) void k_order_by_cost(const int32_t* cnt, int m,
-                                                                 int32_t* order) {
+// order[0..m) = the ids sorted by cost bucket, highest first; one block of
+// kOrderThreads threads.
+__device__ __forceinline__ void order_by_cost_block(const int32_t* cnt, int m, int32_t* order) {
   __shared__ int s_bin[kOrderBins];
   for (int i = threadIdx.x; i < kOrderBins; i += kOrderThreads) s_bin[i] = 0;
   __syncthreads();
@@ -628,6 +629,25 @@ __global__ __launch_bounds__(kOrderThreads) void k_order_by_cost(const int32_t* 
     const int pos = atomicAdd(&s_bin[cost_bucket(cnt[i])], 1);
     order[pos] = i;
   }
+}
+
+// Backward prologue: block 0 forms the backward's (tile, plane) block order
+// from the forward's member counts (when `order` is given) while the other
+// blocks clear the accumulator records (n4 float4s, then `tail` floats).
+__global__ __launch_bounds__(kOrderThreads) void k_bwd_prologue(float4* __restrict__ acc4,
+                                                                int64_t n4,
+                                                                float* __restrict__ tail,
+                                                                int ntail, const int32_t* cnt,
+                                                                int m, int32_t* order) {
+  if (blockIdx.x == 0) {
+    if (order) order_by_cost_block(cnt, m, order);
+    return;
+  }
+  const int64_t stride = static_cast<int64_t>(gridDim.x - 1) * kOrderThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x - 1) * kOrderThreads + threadIdx.x; i < n4;
+       i += stride)
+    acc4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (blockIdx.x == 1 && static_cast<int>(threadIdx.x) < ntail) tail[threadIdx.x] = 0.0f;
 }
 
 __global__ void k_render_empty(float2* field, float* final_T, int32_t* n_contrib,
@@ -687,9 +707,20 @@ int launch_render_backward(const RenderParams& p, hipStream_t s) {
   return HRF_OK;
 }
 
-int launch_order_by_cost(const int32_t* cnt, int m, int32_t* order, hipStream_t s) {
-  if (m <= 0) return HRF_OK;
-  hipLaunchKernelGGL(k_order_by_cost, dim3(1), dim3(kOrderThreads), 0, s, cnt, m, order);
+int launch_bwd_prologue(float* acc, int64_t n, const int32_t* cnt, int m, int32_t* order,
+                        hipStream_t s) {
+  if (reinterpret_cast<uintptr_t>(acc) & 15) {
+    set_error("internal: accumulator records not 16-byte aligned");
+    return HRF_ERR_INVALID;
+  }
+  const int64_t n4 = n / 4;
+  const int ntail = static_cast<int>(n - 4 * n4);
+  const int64_t per = static_cast<int64_t>(kOrderThreads) * 4;  // float4s per block
+  int64_t fill_blocks = (n4 + per - 1) / per;
+  if (fill_blocks < 1) fill_blocks = 1;
+  hipLaunchKernelGGL(k_bwd_prologue, dim3(static_cast<unsigned>(1 + fill_blocks)),
+                     dim3(kOrderThreads), 0, s, reinterpret_cast<float4*>(acc), n4,
+                     acc + 4 * n4, ntail, cnt, m, (m > 0 ? order : nullptr));
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

@@ -102,10 +102,12 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
  * with P planes: P*K (gaussian, list position) int32 pairs (plane q's list
  * of tile t starts at q*K + ranges[t][0]), then, each from the next
  * 256-byte boundary, T*P int32 counts (tile-major) and the T*P (tile, plane)
- * ids t*P + q ordered by count, largest first (the backward's block order).  hrf_raster_forward_render fills them (plane_lists non-NULL)
- * with each (tile, plane)'s members, in list order, over the entries its
- * compositing visited; hrf_raster_backward given the same buffer walks
- * those lists instead of filtering every tile list once per plane.  No
+ * ids t*P + q ordered by count, largest first (the backward's block order).
+ * hrf_raster_forward_render fills the lists and counts (plane_lists
+ * non-NULL) with each (tile, plane)'s members, in list order, over the
+ * entries its compositing visited; hrf_raster_backward given the same
+ * buffer writes the block order from the counts and walks those lists
+ * instead of filtering every tile list once per plane.  No
  * counterpart in the reference (its backward re-reads the whole tile list
  * per plane, backward_splat.cu:148-306). */
 size_t hrf_raster_plane_lists_size(int64_t num_pairs, int32_t width, int32_t height,
@@ -124,7 +126,9 @@ size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t p
  * reused instead of recomputing the projection (the reference recomputes
  * means2D and cov2D, rasterizer_splat.cu:606-617).
  * plane_lists (optional, may be NULL): the plane member lists the forward of
- * these same inputs wrote (same point_list, ranges and n_contrib).
+ * these same inputs wrote (same point_list, ranges and n_contrib); the
+ * backward writes their block-order words (the lists and counts are only
+ * read).
  * Replaces Rasterizer::backward (rasterizer_splat.cu:551-684),
  * backward_splat.cu:78-417 and backward.cu. */
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
@@ -133,7 +137,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
                         const int32_t* ranges, int64_t num_pairs,
                         void* ws, size_t ws_bytes,
                         const void* fwd_geom_ws, size_t fwd_geom_ws_bytes,
-                        const void* plane_lists, size_t plane_lists_bytes,
+                        void* plane_lists, size_t plane_lists_bytes,
                         float* grad_cam, float* grad_z, float* grad_quats,
                         float* grad_scales, float* grad_colours, float* grad_phase,
                         float* grad_opacities, float* grad_plane_probs,

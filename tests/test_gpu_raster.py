@@ -364,8 +364,9 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     """The forward's plane member lists (kept for the backward): each
     (tile, plane) list is exactly that plane's members of the tile list, in
     list order, cut after the last batch the forward composited (never before
-    any pixel's n_contrib); the block order is a permutation sorted by list
-    length; the backward walking them matches the oracle's
+    any pixel's n_contrib); the block order the backward writes into the
+    same buffer is a permutation sorted by list length; the backward walking
+    them matches the oracle's
     backward on the same forward state and the backward that filters the tile
     lists itself (both sum float atomics, so to rounding: rel-L2 < 1e-6)."""
     import torch
@@ -396,15 +397,7 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     ent = buf[:P * K * 8].view(np.int32).reshape(P, K, 2)
     c0 = (P * K * 8 + 255) // 256 * 256
     cnt = buf[c0:c0 + ntiles * P * 4].view(np.int32).reshape(ntiles, P)
-    # Then the backward's block order: a permutation of the (tile, plane)
-    # ids, counts non-increasing at the granularity of 8 buckets per octave.
     o0 = (c0 + ntiles * P * 4 + 255) // 256 * 256
-    order = buf[o0:o0 + ntiles * P * 4].view(np.int32)
-    np.testing.assert_array_equal(np.sort(order), np.arange(ntiles * P))
-    v = np.maximum(cnt.reshape(-1)[order].astype(np.int64), 0) + 1
-    e = np.floor(np.log2(v)).astype(np.int64)
-    mant = np.where(e >= 3, v >> np.maximum(e - 3, 0), v << np.maximum(3 - e, 0)) & 7
-    assert np.all(np.diff(e * 8 + mant) <= 0)
     pl_np, r_np, nc_np = pl.cpu().numpy(), ranges.cpu().numpy(), nc.cpu().numpy()
     member = g.pprobs >= np.float32(1e-6)
     # float64 alpha of a Gaussian over a tile's pixel centres
@@ -457,6 +450,16 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     with_lists = rasterizer.backward(gft, *args, (W, H), (16, 16), fT, nc, pl, ranges, 1.0, 1000.0,
                                      geometry=geom)
     filtered = rasterizer.backward(gft, *args, (W, H), (16, 16), fT, nc, pl, ranges, 1.0, 1000.0)
+    # The block order the backward wrote after the counts: a permutation of
+    # the (tile, plane) ids, counts non-increasing at the granularity of 8
+    # buckets per octave.
+    torch.cuda.synchronize()
+    order = geom.plane_lists.cpu().numpy()[o0:o0 + ntiles * P * 4].view(np.int32)
+    np.testing.assert_array_equal(np.sort(order), np.arange(ntiles * P))
+    v = np.maximum(cnt.reshape(-1)[order].astype(np.int64), 0) + 1
+    e = np.floor(np.log2(v)).astype(np.int64)
+    mant = np.where(e >= 3, v >> np.maximum(e - 3, 0), v << np.maximum(3 - e, 0)) & 7
+    assert np.all(np.diff(e * 8 + mant) <= 0)
     state = dict(ref, final_T=fT.cpu().numpy(), n_contrib=nc_np, point_list=pl_np, ranges=r_np)
     rb = oracle_mod.rasterize_backward(g, cam, state, gf)
     names = ["cam", "z", "quats", "scales", "colours", "phase", "opac", "plane"]
