@@ -571,15 +571,26 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   for (int p = 0; p < P; ++p) {
     __syncthreads();
     const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
-    // (kz and acc are live here, so the copy is not unrolled: its load
-    // buffer would not fit the register budget.)
     constexpr int E0 = HALF ? B * N / 4 : 0;
     constexpr int E1 = HALF ? 3 * B * N / 4 : B * N;
-    for (int e = E0 + static_cast<int>(threadIdx.x); e < E1; e += kFftThreads) {
-      const int r = e / B - r_pad;
-      float2 v = make_float2(0.0f, 0.0f);
-      if (r >= 0 && r < H) v = src[e - r_pad * B];
-      lds[pad(e)] = v;
+    // kz and acc are live here, so the copy keeps only kPlaneLoads loads in
+    // flight per thread (a whole-tile register buffer would not fit).
+    constexpr int kPlaneLoads = 4;
+    for (int e0 = E0 + static_cast<int>(threadIdx.x); e0 < E1;
+         e0 += kPlaneLoads * kFftThreads) {
+      float2 v[kPlaneLoads];
+#pragma unroll
+      for (int u = 0; u < kPlaneLoads; ++u) {
+        const int e = e0 + u * kFftThreads;
+        const int r = e / B - r_pad;
+        v[u] = make_float2(0.0f, 0.0f);
+        if (e < E1 && r >= 0 && r < H) v[u] = src[e - r_pad * B];
+      }
+#pragma unroll
+      for (int u = 0; u < kPlaneLoads; ++u) {
+        const int e = e0 + u * kFftThreads;
+        if (e < E1) lds[pad(e)] = v[u];
+      }
     }
     __syncthreads();
     Plan<N>::template run<false, kFftThreads, HALF>(lds, twp);
