@@ -121,9 +121,14 @@ def test_odd_size_rejected(hrf):
 # 1600, 2016, 2048) run the fused row/column kernels; other sizes (M = 96
 # above) run the hipFFT path.  The headline grid (800 -> 1600) and every
 # large plan are checked against the oracle, forward and adjoint.
+# Fields wider and/or taller than half the padded grid (up to 2S is allowed)
+# take the transforms whose first stage is not pruned.
 @pytest.mark.parametrize("P,C,H,W,S", [(3, 3, 800, 800, 800), (1, 2, 100, 60, 512),
-                                       (2, 1, 64, 64, 1008), (1, 1, 128, 96, 1024)],
-                         ids=["headline1600", "m1024", "m2016", "m2048"])
+                                       (2, 1, 64, 64, 1008), (1, 1, 128, 96, 1024),
+                                       (1, 2, 96, 100, 64), (2, 1, 48, 120, 64),
+                                       (1, 1, 110, 40, 80)],
+                         ids=["headline1600", "m1024", "m2016", "m2048", "wide_tall_m128",
+                              "wide_m128", "tall_m160"])
 def test_multiplane_fused_grids(hrf, oracle_mod, P, C, H, W, S):
     import torch
     from complex_valued_holographic_radiance_fields_amd import propagation
