@@ -194,6 +194,11 @@ def test_single_gaussian_closed_form(hrf):
     assert abs(v - expect) < 1e-6
     assert abs(info[0][0, 12, 20].item() - 0.3) < 1e-6
     assert int(info[1][0, 12, 20]) == 1
+    # one pair (its 3-pixel radius stays inside tile (1, 0) of the 2 x 2
+    # grid): point_list [0], that tile's range [0, 1), the others empty
+    np.testing.assert_array_equal(info[2].cpu().numpy(), [0])
+    np.testing.assert_array_equal(info[3].cpu().numpy(), [[0, 0], [0, 1], [0, 0], [0, 0]])
+    np.testing.assert_array_equal(info[4].cpu().numpy(), [0])
 
 
 def test_autograd_dropin(hrf):
@@ -312,6 +317,7 @@ def test_forward_parity_wide_keys(hrf, oracle_mod):
     t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
     np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
     np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
