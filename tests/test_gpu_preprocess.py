@@ -69,6 +69,18 @@ def test_forward_matches_oracle(hrf, oracle_mod, near, far, P, C):
         np.testing.assert_allclose(got[k], ref[k], rtol=3e-7, err_msg=k)
 
 
+def test_selection_count_stream_fallback(hrf, oracle_mod, monkeypatch):
+    """The kept count reaches the host through the same tagged pinned words
+    as the rasterizer's; with the poll disabled (HRF_READBACK_SPIN_US=0) the
+    stream-synchronisation fallback gives the same selection."""
+    prm = _params(P=3, C=3, seed=9)
+    ref = oracle_mod.preprocess_forward(*prm, near=1.0, far=1000.0)
+    monkeypatch.setenv("HRF_READBACK_SPIN_US", "0")
+    out = _run(prm, 1.0, 1000.0)
+    print(f"fallback selected={len(ref['idxs'])}", flush=True)
+    np.testing.assert_array_equal(out[-1].cpu().numpy(), ref["idxs"])
+
+
 @pytest.mark.parametrize("depths", ["equal", "narrow"])
 def test_forward_depth_sort_bit_range(hrf, oracle_mod, depths):
     """Depth keys that are all equal (index order must stay) or differ only
