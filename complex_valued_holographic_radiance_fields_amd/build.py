@@ -41,6 +41,7 @@ SOURCES = [
     "preprocess.hip",
     "optim.hip",
     "recon.hip",
+    "ssim.hip",
     "hrf_trace.hip",
 ]
 

@@ -110,6 +110,51 @@ void readback_release(Readback* r) {
 }
 
 namespace {
+// The counts hrf_raster_forward_prepare returned, per geometry workspace
+// (the last prepare on each), so hrf_raster_forward_render can reject counts
+// that differ from them before anything is enqueued.  Bounded: past
+// kMaxPrepared workspaces the oldest record is dropped (the render then has
+// only the kernels' own output bounds to rely on).
+struct Prepared {
+  const void* ws;
+  int64_t n, k, v;
+};
+constexpr size_t kMaxPrepared = 256;
+std::mutex g_prep_mu;
+std::vector<Prepared> g_prep;
+}  // namespace
+
+void prepared_record(const void* ws, int64_t n, int64_t k, int64_t v) {
+  std::lock_guard<std::mutex> lk(g_prep_mu);
+  for (auto& e : g_prep) {
+    if (e.ws == ws) {
+      e = Prepared{ws, n, k, v};
+      return;
+    }
+  }
+  if (g_prep.size() >= kMaxPrepared) g_prep.erase(g_prep.begin());
+  g_prep.push_back(Prepared{ws, n, k, v});
+}
+
+int prepared_check(const void* ws, int64_t n, int64_t k, int64_t v) {
+  std::lock_guard<std::mutex> lk(g_prep_mu);
+  for (const auto& e : g_prep) {
+    if (e.ws != ws) continue;
+    if (e.n != n || e.k != k || e.v != v) {
+      set_error("forward render: counts (N %lld, K %lld, V %lld) differ from what "
+                "hrf_raster_forward_prepare returned for this geometry workspace "
+                "(N %lld, K %lld, V %lld)",
+                static_cast<long long>(n), static_cast<long long>(k),
+                static_cast<long long>(v), static_cast<long long>(e.n),
+                static_cast<long long>(e.k), static_cast<long long>(e.v));
+      return HRF_ERR_INVALID;
+    }
+    return HRF_OK;
+  }
+  return HRF_OK;
+}
+
+namespace {
 
 // ------------------------------------------------------------ validation --
 int check_raster_args(const hrf_gaussians* g, const hrf_camera* cam) {
@@ -305,6 +350,21 @@ int bits_for(int ntiles) {
   return b;
 }
 
+// Pair counts index the reference's int32 point_list / ranges outputs
+// (rasterizer_splat.cu:430 holds the count in an int).
+int check_pair_count(int64_t k) {
+  if (k < 0) {
+    set_error("invalid pair count %lld", static_cast<long long>(k));
+    return HRF_ERR_INVALID;
+  }
+  if (k > 0x7FFFFFFFLL) {
+    set_error("pair count %lld exceeds the int32 point_list/ranges format",
+              static_cast<long long>(k));
+    return HRF_ERR_OVERFLOW;
+  }
+  return HRF_OK;
+}
+
 int check_ws(void* ws, size_t have, size_t need, const char* what) {
   if (need > 0 && (!ws || have < need)) {
     set_error("%s workspace too small: %zu bytes given, %zu needed", what, have, need);
@@ -467,6 +527,7 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   }
   *num_pairs = static_cast<int64_t>(host_tot[0]);
   *num_visible = static_cast<int64_t>(host_tot[1]);
+  prepared_record(geom_ws, n, *num_pairs, *num_visible);
   return HRF_OK;
 }
 
@@ -477,15 +538,17 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
                               int32_t* ranges, int64_t* visible, void* plane_lists,
                               size_t plane_lists_bytes, void* stream) {
   HRF_TRY(check_raster_args(g, cam));
-  if (num_pairs < 0 || num_pairs > 0x7FFFFFFFLL || num_visible < 0 || num_visible > g->n) {
-    set_error("invalid pair/visible counts (%lld, %lld)", static_cast<long long>(num_pairs),
-              static_cast<long long>(num_visible));
+  HRF_TRY(check_pair_count(num_pairs));
+  if (num_visible < 0 || num_visible > g->n) {
+    set_error("invalid visible count %lld for %lld Gaussians",
+              static_cast<long long>(num_visible), static_cast<long long>(g->n));
     return HRF_ERR_INVALID;
   }
   if (!field || !final_T || !n_contrib || !ranges) {
     set_error("null output pointer");
     return HRF_ERR_INVALID;
   }
+  if (g->n > 0) HRF_TRY(prepared_check(geom_ws, g->n, num_pairs, num_visible));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const Frame f = frame_of(cam);
   RenderParams rp{};
@@ -530,13 +593,15 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_packed(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
-                                 f.gx, vbits, b.keys_a, s, w.vis, w.part_v,
-                                 num_visible > 0 ? visible : nullptr));
+                                 num_pairs, f.gx, vbits, b.keys_a, s, w.vis, w.part_v,
+                                 num_visible > 0 ? visible : nullptr, num_visible));
     }
     bool in_b = false;
     // The last sort pass writes the gaussian bits straight into point_list;
-    // otherwise the sorted words are unpacked.
-    const bool fused = num_pairs > 1 && diff_ranges;
+    // otherwise the sorted words are unpacked.  A one-tile image has no
+    // tile bits to sort (end_bit 0): the emitted depth-rank order is already
+    // the sorted order and the unpack writes it.
+    const bool fused = num_pairs > 1 && diff_ranges && end_bit > 0;
     {
       HRF_STAGE("tile_sort", s);
       HRF_TRY(radix_sort_keys(b.keys_a, b.keys_b, num_pairs, vbits, end_bit, b.radix, &in_b, s,
@@ -556,7 +621,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
                                 num_pairs, f.gx, b.keys_a, vals_a, s, w.vis, w.part_v,
-                                num_visible > 0 ? visible : nullptr));
+                                num_visible > 0 ? visible : nullptr, num_visible));
     }
     bool in_b = false;
     {
@@ -618,10 +683,7 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
     set_error("null gradient output pointer");
     return HRF_ERR_INVALID;
   }
-  if (num_pairs < 0 || num_pairs > 0x7FFFFFFFLL) {
-    set_error("invalid pair count %lld", static_cast<long long>(num_pairs));
-    return HRF_ERR_INVALID;
-  }
+  HRF_TRY(check_pair_count(num_pairs));
   if (num_pairs > 0 && (!grad_field || !final_T || !n_contrib || !point_list || !ranges)) {
     set_error("null forward-state pointer");
     return HRF_ERR_INVALID;

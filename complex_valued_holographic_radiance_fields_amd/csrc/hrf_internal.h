@@ -287,15 +287,16 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
                       hipStream_t s, const uint32_t* vis = nullptr,
-                      const uint32_t* part_v = nullptr, int64_t* visible = nullptr);
+                      const uint32_t* part_v = nullptr, int64_t* visible = nullptr,
+                      int64_t vmax = 0);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       int64_t n, int64_t k, int gx, int vbits, uint32_t* words, hipStream_t s,
                        const uint32_t* vis = nullptr, const uint32_t* part_v = nullptr,
-                       int64_t* visible = nullptr);
+                       int64_t* visible = nullptr, int64_t vmax = 0);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
 int64_t partial_elems(int64_t n);  // kProjThreads-blocks + 1

@@ -275,6 +275,38 @@ int for_tensor_groups(int nt, const int64_t* numels, Fill fill, Launch launch) {
   return HRF_OK;
 }
 
+
+// Sparse Adam over the visible rows (spadam.cu:8-36, the `adamUpdate` behind
+// python_import.py:457-460): param, exp_avg, exp_avg_sq are (B, N, D), grad
+// (B, V, D) holds the gradients of the V visible rows, visible (V) their row
+// indices.  No bias correction, as the reference.  One thread per element of
+// (B, V, D) in row-major order, so a row's D elements are contiguous in both
+// the gathered gradient and the parameter tensors.  Rows outside [0, N) are
+// skipped (the reference writes out of bounds); duplicate rows race, as in
+// the reference.
+__global__ __launch_bounds__(kOptThreads) void k_sparse_adam(
+    float* __restrict__ param, const float* __restrict__ grad, float* __restrict__ exp_avg,
+    float* __restrict__ exp_avg_sq, const int64_t* __restrict__ visible, int64_t B, int64_t N,
+    int64_t V, int64_t D, float lr, float b1, float b2, float eps) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kOptThreads + threadIdx.x;
+  const int64_t total = B * V * D;
+  if (i >= total) return;
+  const int64_t d = i % D;
+  const int64_t bv = i / D;
+  const int64_t v = bv % V, b = bv / V;
+  const int64_t row = visible[v];
+  if (row < 0 || row >= N) return;
+  const int64_t at = (b * N + row) * D + d;
+  const float gr = grad[i];
+  float m = exp_avg[at];
+  float s2 = exp_avg_sq[at];
+  m = b1 * m + (1.0f - b1) * gr;
+  s2 = b2 * s2 + (1.0f - b2) * gr * gr;
+  const float step = -lr * m / (sqrtf(s2) + eps);
+  param[at] += step;
+  exp_avg[at] = m;
+  exp_avg_sq[at] = s2;
+}
 }  // namespace
 }  // namespace hrf
 
@@ -408,6 +440,34 @@ int hrf_adan_step(const hrf_adan_tensor* tensors, int32_t num_tensors,
         HRF_LAUNCH_CHECK();
         return HRF_OK;
       });
+}
+
+int hrf_sparse_adam_update(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
+                           const int64_t* visible, int64_t batch, int64_t rows, int64_t cols,
+                           int64_t num_visible, float lr, float beta1, float beta2, float eps,
+                           void* stream) {
+  if (batch < 0 || rows < 0 || cols < 0 || num_visible < 0) {
+    set_error("sparse adam: negative shape (%lld, %lld, %lld, %lld)",
+              static_cast<long long>(batch), static_cast<long long>(rows),
+              static_cast<long long>(cols), static_cast<long long>(num_visible));
+    return HRF_ERR_INVALID;
+  }
+  const int64_t total = batch * num_visible * cols;
+  if (total == 0) return HRF_OK;
+  if (!param || !grad || !exp_avg || !exp_avg_sq || !visible) {
+    set_error("sparse adam: null pointer");
+    return HRF_ERR_INVALID;
+  }
+  if (total / kOptThreads >= 0x7FFFFFFFLL) {
+    set_error("sparse adam: too many elements (%lld)", static_cast<long long>(total));
+    return HRF_ERR_INVALID;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_sparse_adam, dim3(blocks_for(total, kOptThreads)), dim3(kOptThreads), 0,
+                     s, param, grad, exp_avg, exp_avg_sq, visible, batch, rows, num_visible,
+                     cols, lr, beta1, beta2, eps);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
 }
 
 }  // extern "C"

@@ -69,12 +69,22 @@ __device__ __forceinline__ bool project_one(const ProjectParams& p, int64_t g) {
       det_cov = ax * aw - ay * az;
       if (fabsf(det_cov) < 1e-8f) culled = true;
     }
+    float radius_f = 0.0f;
     if (!culled) {
       const float mid = 0.5f * (ax + aw);
       const float disc = fmaxf(0.1f, mid * mid - det_cov);
       const float lambda1 = mid + sqrtf(disc);
       const float lambda2 = mid - sqrtf(disc);
-      const float radius_f = ceilf(3.0f * sqrtf(fmaxf(lambda1, lambda2)));
+      radius_f = ceilf(3.0f * sqrtf(fmaxf(lambda1, lambda2)));
+      // A NaN or non-positive radius (a degenerate covariance: zero
+      // quaternion, NaN or infinite scale; undefined in the reference)
+      // culls the Gaussian, so it reaches no tile list; so does a NaN 2-D
+      // mean (NaN camera-space x or y, whose covariance the Jacobian's clamp
+      // keeps finite), which would otherwise land in tile 0 and composite
+      // with alpha fminf(0.99, NaN) = 0.99.
+      if (!(radius_f > 0.0f) || isnan(mx) || isnan(my)) culled = true;
+    }
+    if (!culled) {
       const int rad_i = radius_f < 2147483520.0f ? static_cast<int>(radius_f) : 2147483520;
       const int radius = rad_i > 1 ? rad_i : 1;
       const float rf = static_cast<float>(radius);

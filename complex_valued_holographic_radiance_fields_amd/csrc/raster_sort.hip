@@ -481,6 +481,7 @@ struct VisibleOut {
   const uint32_t* vis;
   const uint32_t* part_v;
   int64_t* visible;  // nullptr: nothing to write
+  int64_t vmax;      // length of `visible`: positions at or past it are not written
 };
 
 __device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int64_t n) {
@@ -490,7 +491,8 @@ __device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int6
   const uint32_t v = i < n ? vo.vis[i] : 0u;
   uint32_t total;
   const uint32_t ex = block_exclusive_scan<uint32_t>(v, &total, s_vw);
-  if (v) vo.visible[vo.part_v[blockIdx.x] + ex] = i;
+  const int64_t at = static_cast<int64_t>(vo.part_v[blockIdx.x]) + ex;
+  if (v && at < vo.vmax) vo.visible[at] = i;
 }
 
 __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ part_t,
@@ -499,7 +501,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
                                                       const uint32_t* __restrict__ order,
                                                       const uint32_t* __restrict__ sorted_flag,
                                                       const uint2* __restrict__ rect, int64_t n,
-                                                      int gx, uint32_t* __restrict__ keys,
+                                                      int64_t k, int gx,
+                                                      uint32_t* __restrict__ keys,
                                                       uint32_t* __restrict__ vals, VisibleOut vo) {
   compact_visible_block(vo, n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
@@ -516,7 +519,9 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restric
     s_rect[threadIdx.x] = rect[g];
   }
   __syncthreads();
-  const uint64_t e0 = s_off[0], e1 = s_off[nr];
+  // Pairs at or past k (the output length) are not written.
+  const uint64_t uk = static_cast<uint64_t>(k);
+  const uint64_t e0 = s_off[0], e1 = s_off[nr] < uk ? s_off[nr] : uk;
   for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
     int lo = 0, hi = nr;  // s_off[lo] <= e < s_off[hi]
     while (hi - lo > 1) {
@@ -556,7 +561,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
                                                              const uint32_t* __restrict__ order,
                                                              const uint32_t* __restrict__ sorted_flag,
                                                              const uint2* __restrict__ rect,
-                                                             int64_t n, int gx, int vbits,
+                                                             int64_t n, int64_t k, int gx,
+                                                             int vbits,
                                                              uint32_t* __restrict__ words,
                                                              VisibleOut vo) {
   compact_visible_block(vo, n);
@@ -575,7 +581,9 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
     s_rect[threadIdx.x] = rect[g];
   }
   __syncthreads();
-  const uint64_t e0 = s_off[0], e1 = s_off[nr];
+  // Pairs at or past k (the output length) are not written.
+  const uint64_t uk = static_cast<uint64_t>(k);
+  const uint64_t e0 = s_off[0], e1 = s_off[nr] < uk ? s_off[nr] : uk;
   const uint32_t ugx = static_cast<uint32_t>(gx);
   for (uint64_t c0 = e0; c0 < e1; c0 += kEmitChunk) {
     const int clen = static_cast<int>(e1 - c0 < kEmitChunk ? e1 - c0 : kEmitChunk);
@@ -627,12 +635,14 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
 
 // Sorted packed words -> point_list (the gaussian field) and tile ranges.
 __global__ void k_unpack_ranges(const uint32_t* __restrict__ words, int64_t k, int vbits,
-                                int32_t* __restrict__ point_list, int32_t* __restrict__ ranges) {
+                                int32_t* __restrict__ point_list, int32_t* __restrict__ ranges,
+                                uint32_t ntiles) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= k) return;
   const uint32_t w = words[i];
   const uint32_t t = w >> vbits;
   point_list[i] = static_cast<int32_t>(w & ((1u << vbits) - 1u));
+  if (t >= ntiles) return;  // only a word the emission never wrote
   if (i == 0 || (words[i - 1] >> vbits) != t)
     ranges[2 * static_cast<int64_t>(t)] = static_cast<int32_t>(i);
   if (i == k - 1 || (words[i + 1] >> vbits) != t)
@@ -640,10 +650,11 @@ __global__ void k_unpack_ranges(const uint32_t* __restrict__ words, int64_t k, i
 }
 
 __global__ void k_tile_ranges(const uint32_t* __restrict__ keys, int64_t k,
-                              int32_t* __restrict__ ranges) {
+                              int32_t* __restrict__ ranges, uint32_t ntiles) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= k) return;
   const uint32_t t = keys[i];
+  if (t >= ntiles) return;  // only a key the emission never wrote
   if (i == 0 || keys[i - 1] != t) ranges[2 * static_cast<int64_t>(t)] = static_cast<int32_t>(i);
   if (i == k - 1 || keys[i + 1] != t)
     ranges[2 * static_cast<int64_t>(t) + 1] = static_cast<int32_t>(i + 1);
@@ -927,23 +938,25 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
                       hipStream_t s, const uint32_t* vis, const uint32_t* part_v,
-                      int64_t* visible) {
+                      int64_t* visible, int64_t vmax) {
   if (k <= 0 || n <= 0) return HRF_OK;
-  const VisibleOut vo{vis, part_v, visible};
+  const VisibleOut vo{vis, part_v, visible, vmax};
   hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, part_t,
-                     part_r, tiles, order, sorted_flag, rect, n, gx, keys, vals, vo);
+                     part_r, tiles, order, sorted_flag, rect, n, k, gx, keys, vals, vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
 int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
-                       int64_t n, int gx, int vbits, uint32_t* words, hipStream_t s,
-                       const uint32_t* vis, const uint32_t* part_v, int64_t* visible) {
+                       int64_t n, int64_t k, int gx, int vbits, uint32_t* words, hipStream_t s,
+                       const uint32_t* vis, const uint32_t* part_v, int64_t* visible,
+                       int64_t vmax) {
   if (n <= 0) return HRF_OK;
-  const VisibleOut vo{vis, part_v, visible};
+  const VisibleOut vo{vis, part_v, visible, vmax};
   hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     part_t, part_r, tiles, order, sorted_flag, rect, n, gx, vbits, words, vo);
+                     part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, vbits, words,
+                     vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -980,7 +993,7 @@ int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* p
   HRF_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2 * int64_t(ntiles), s));
   if (k <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_unpack_ranges, dim3(blocks_for(k, 256)), dim3(256), 0, s, words, k,
-                     vbits, point_list, ranges);
+                     vbits, point_list, ranges, static_cast<uint32_t>(ntiles));
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -990,7 +1003,7 @@ int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges, int nti
   HRF_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2 * int64_t(ntiles), s));
   if (k <= 0) return HRF_OK;
   hipLaunchKernelGGL(k_tile_ranges, dim3(blocks_for(k, 256)), dim3(256), 0, s, keys, k,
-                     ranges);
+                     ranges, static_cast<uint32_t>(ntiles));
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }

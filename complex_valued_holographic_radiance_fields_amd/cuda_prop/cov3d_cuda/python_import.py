@@ -6,7 +6,10 @@ pybind class interface (binding.cpp:31-36, rasterizer_splat.h:255-293).
 The geometry operators ``compute_cov3d_cuda``, ``compute_jacobian_cuda``,
 ``compute_cov2d_cuda``, ``compute_means2d_cuda`` and ``invert_cov2d_cuda``
 (python_import.py:53-281,343-419) are here too: ``model.py:16-19`` imports
-them in the same statement as ``splat_tile_cuda``.
+them in the same statement as ``splat_tile_cuda``.  So are ``fast_ssim``
+(with ``FusedSSIMMap``, ``C1``, ``C2``; python_import.py:43-58,449-454) and
+``sparse_adam_update`` (:457-460), which ``utils/data_utils.py:20`` and
+``utils/optimizer.py:21`` import, both on HIP kernels.
 Unlike the reference nothing is built at import time (python_import.py:9-16),
 the forward state travels in the autograd context instead of a process-wide
 singleton (so two forwards before one backward are safe), and every error
@@ -18,6 +21,8 @@ from torch.autograd import Function
 
 from ... import geometry as _geom
 from ... import rasterizer as _rast
+from ...optim import sparse_adam_update  # noqa: F401  (python_import.py:457-460)
+from ...ssim import FusedSSIMMap  # noqa: F401  (python_import.py:43-58)
 
 
 class Rasterizer:
@@ -221,3 +226,15 @@ def compute_means2d_cuda(cam_means_3D, fx, fy, px, py, near_plane, far_plane):
 def invert_cov2d_cuda(cov_2D):
     """(N,2,2) -> (N,2,2)."""
     return InvertCov2DFunction.apply(cov_2D)
+
+
+# SSIM constants and loss of python_import.py:449-454.
+C1 = 0.01 ** 2
+C2 = 0.03 ** 2
+
+
+def fast_ssim(img1, img2):
+    """Mean of the fused SSIM map of two (C, H, W) images."""
+    ssim_map = FusedSSIMMap.apply(C1, C2, img1, img2)
+    return ssim_map.mean()
+

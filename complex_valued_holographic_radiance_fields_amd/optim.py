@@ -214,3 +214,34 @@ def training_step_update(optimizer: Adan, parameters: Iterable[torch.Tensor],
     total, coef = grad_norm_clip_coef(params, max_norm)
     optimizer.step(grad_scale=coef if coef.is_cuda else None)
     return total
+
+
+def sparse_adam_update(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+                       exp_avg_sq: torch.Tensor, visible_chunk: torch.Tensor, lr: float,
+                       b1: float, b2: float, eps: float) -> None:
+    """Adam step of the visible rows, in place (spadam.cu:8-55 behind
+    python_import.py:457-460): param, exp_avg, exp_avg_sq (B, N, D); grad
+    (B, V, D) the visible rows' gradients; visible_chunk (V) int64 row
+    indices.  No bias correction; the scalars are used in float32, as the
+    reference's kernel arguments.  Rows outside [0, N) are skipped."""
+    ts = {"param": param, "exp_avg": exp_avg, "exp_avg_sq": exp_avg_sq, "grad": grad}
+    for name, t in ts.items():
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError(f"{name} must be a CUDA tensor (the HIP optimizer has no CPU path)")
+        if t.dtype != torch.float32 or t.dim() != 3 or not t.is_contiguous():
+            raise RuntimeError(f"{name} must be a contiguous 3-D float32 tensor; got "
+                               f"{t.dtype} {tuple(t.shape)}")
+    if exp_avg.shape != param.shape or exp_avg_sq.shape != param.shape:
+        raise RuntimeError("exp_avg and exp_avg_sq must have the shape of param")
+    if not isinstance(visible_chunk, torch.Tensor) or not visible_chunk.is_cuda or \
+            visible_chunk.dtype != torch.int64 or visible_chunk.dim() != 1:
+        raise RuntimeError("visible_chunk must be a 1-D int64 CUDA tensor")
+    B, N, D = param.shape
+    V = visible_chunk.shape[0]
+    if tuple(grad.shape) != (B, V, D):
+        raise RuntimeError(f"grad must have shape ({B}, {V}, {D}); got {tuple(grad.shape)}")
+    vis = visible_chunk.contiguous()
+    _lib.check(_lib.load().hrf_sparse_adam_update(
+        param.data_ptr(), grad.data_ptr(), exp_avg.data_ptr(), exp_avg_sq.data_ptr(),
+        vis.data_ptr(), B, N, D, V, float(lr), float(b1), float(b2), float(eps),
+        _lib.stream_ptr(param.device)))

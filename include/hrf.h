@@ -88,6 +88,13 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam,
  * ranges (T,2) and visible (V).  With K == 0 it writes the reference's
  * empty-scene outputs (rasterizer_splat.cu:434-449): zero field, final_T=1,
  * n_contrib=0, ranges=0; point_list and visible are not touched.
+ * num_pairs and num_visible must be the counts hrf_raster_forward_prepare
+ * returned for this geometry workspace (point_list holds num_pairs entries,
+ * visible num_visible).  Other counts are rejected with HRF_ERR_INVALID
+ * before anything is enqueued (the library keeps the counts of the last
+ * prepare per workspace, for up to 256 workspaces); past that record, no
+ * kernel writes more than num_pairs / num_visible entries whatever the
+ * counts.  A count beyond 2^31 - 1 returns HRF_ERR_OVERFLOW.
  * Replaces rasterizer_splat.cu:451-547 and forward_splat.cu:101-289. */
 int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
                               void* geom_ws, size_t geom_ws_bytes,
@@ -459,6 +466,36 @@ typedef struct hrf_adan_config {
  * folds clip_grad_norm_'s rescaling into this pass. */
 int hrf_adan_step(const hrf_adan_tensor* tensors, int32_t num_tensors,
                   const hrf_adan_config* cfg, const float* grad_scale, void* stream);
+
+/* ---------------- training-loop helpers of the cov3d_cuda module ----------
+ * The two remaining names python_import.py exports (utils/data_utils.py:20
+ * and utils/optimizer.py:21 import them). */
+
+/* SSIM map of two (C,H,W) float images, 11x11 Gaussian window (sigma 1.5)
+ * with zero padding, written to ssim_map (C,H,W); c1, c2 the stabilising
+ * constants (0.01^2, 0.03^2 in the reference).  Replaces fusedssim
+ * (cuda_prop/cov3d_cuda/conv.cu:935-1002,1138-1166) behind fast_ssim
+ * (python_import.py:43-58,449-454), which supports C = 3 only. */
+int hrf_ssim_map(const float* img1, const float* img2, int32_t channels, int32_t height,
+                 int32_t width, float c1, float c2, float* ssim_map, void* stream);
+
+/* grad_img1 (C,H,W) = d(sum grad_map * ssim_map)/d img1 (img2 gets no
+ * gradient, as in the reference).  Replaces fusedssim_backward
+ * (conv.cu:1011-1135,1168-1197). */
+int hrf_ssim_backward(const float* img1, const float* img2, const float* grad_map,
+                      int32_t channels, int32_t height, int32_t width, float c1, float c2,
+                      float* grad_img1, void* stream);
+
+/* Sparse Adam step over the visible rows, no bias correction: param,
+ * exp_avg, exp_avg_sq (batch, rows, cols); grad (batch, num_visible, cols),
+ * the visible rows' gradients in the order of visible (num_visible) int64
+ * row indices.  Rows outside [0, rows) are skipped.  Replaces adamUpdate
+ * (cuda_prop/cov3d_cuda/spadam.cu:8-55) behind sparse_adam_update
+ * (python_import.py:457-460). */
+int hrf_sparse_adam_update(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
+                           const int64_t* visible, int64_t batch, int64_t rows, int64_t cols,
+                           int64_t num_visible, float lr, float beta1, float beta2, float eps,
+                           void* stream);
 
 /* ---------------- stage tracing (no counterpart in the reference, which
  * prints per-phase CUDA event times from train.py:263-344) ---------------- */

@@ -199,7 +199,7 @@ static uint32_t to_u32_sat(float f) {
 /* preprocessGaussiansKernel (forward_splat.cu:17-98) + getRect
  * (auxiliary.h:119-137).  rect = (minx, miny, maxx, maxy) per Gaussian.
  * A non-positive or NaN radius (degenerate covariance; undefined in the
- * reference) culls the Gaussian. */
+ * reference) or a NaN 2-D mean culls the Gaussian. */
 void oracle_preprocess(int64_t n, const float* means2d, const float* cov2d, const float* z,
                        int W, int H, float near_p, float far_p, int32_t* radii,
                        uint32_t* tiles, uint32_t* rect) {
@@ -225,6 +225,10 @@ void oracle_preprocess(int64_t n, const float* means2d, const float* cov2d, cons
     const float lambda2 = mid - sqrtf(disc);
     const float radius_f = ceilf(3.0f * sqrtf(fmaxf(lambda1, lambda2)));
     if (!(radius_f > 0.0f)) continue;
+    /* A NaN 2-D mean (NaN camera-space x or y: the Jacobian's clamp keeps
+     * the covariance finite) would fall in tile 0 and composite with alpha
+     * fminf(0.99, NaN) = 0.99; it is culled like a NaN radius. */
+    if (isnan(means2d[g * 2 + 0]) || isnan(means2d[g * 2 + 1])) continue;
     const int rad_i = radius_f < 2147483520.0f ? (int)radius_f : 2147483520;
     radii[g] = rad_i;
     const int radius = rad_i > 1 ? rad_i : 1;
@@ -312,18 +316,22 @@ void oracle_bin(int64_t n, const float* z, const uint32_t* tiles, const uint32_t
 /* renderTileKernel (forward_splat.cu:101-289), defined semantics: every
  * pixel of a partial edge tile sees the full batch (the reference leaves
  * LDS slots of out-of-image threads unloaded).  field is (P,C,H,W) complex
- * interleaved (re, im); final_T and n_contrib (P,H,W). */
+ * interleaved (re, im); final_T and n_contrib (P,H,W).  tile_mask (one byte
+ * per tile, may be NULL = every tile): pixels of tiles whose byte is 0 are
+ * skipped and their outputs left as they are. */
 void oracle_render_forward(int W, int H, int P, int C, const int32_t* ranges,
                            const int32_t* point_list, const float* means2d, const float* cov2d,
                            const float* z, const float* colours, const float* phase,
                            const float* opac, const float* pprobs, float near_p, float far_p,
-                           float* field, float* final_T, int32_t* n_contrib) {
+                           float* field, float* final_T, int32_t* n_contrib,
+                           const uint8_t* tile_mask) {
   const int gx = (W + TILE - 1) / TILE;
   const int64_t HW = (int64_t)W * H;
 #pragma omp parallel for schedule(dynamic, 4)
   for (int64_t pix = 0; pix < HW; ++pix) {
     const int py = (int)(pix / W), px = (int)(pix % W);
     const int tile = (py / TILE) * gx + (px / TILE);
+    if (tile_mask && !tile_mask[tile]) continue;
     const int r0 = ranges[2 * tile], r1 = ranges[2 * tile + 1];
     const float pxf = (float)px, pyf = (float)py;
     for (int p = 0; p < P; ++p) {
@@ -382,14 +390,15 @@ void oracle_render_forward(int W, int H, int P, int C, const int32_t* ranges,
 /* renderBackwardTileKernel (backward_splat.cu:78-307).  grad_field (P,C,H,W)
  * complex interleaved.  Outputs (double accumulators, zeroed here):
  * g_means2d (N,2), g_cov2d (N,4), g_col (N,C), g_phase (N,C), g_opac (N),
- * g_plane (N,P). */
+ * g_plane (N,P).  tile_mask as in oracle_render_forward: only the pixels of
+ * the selected tiles contribute. */
 void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t* ranges,
                             const int32_t* point_list, const float* means2d,
                             const float* cov2d, const float* colours, const float* phase,
                             const float* opac, const float* pprobs, const float* final_T,
                             const int32_t* n_contrib, const float* grad_field,
                             double* g_means2d, double* g_cov2d, double* g_col, double* g_phase,
-                            double* g_opac, double* g_plane) {
+                            double* g_opac, double* g_plane, const uint8_t* tile_mask) {
   const int gx = (W + TILE - 1) / TILE;
   const int64_t HW = (int64_t)W * H;
   memset(g_means2d, 0, sizeof(double) * 2 * n);
@@ -403,6 +412,7 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
   for (int64_t pix = 0; pix < HW; ++pix) {
     const int py = (int)(pix / W), px = (int)(pix % W);
     const int tile = (py / TILE) * gx + (px / TILE);
+    if (tile_mask && !tile_mask[tile]) continue;
     const int r0 = ranges[2 * tile], r1 = ranges[2 * tile + 1];
     const float pxf = (float)px, pyf = (float)py;
     for (int p = 0; p < P; ++p) {

@@ -24,6 +24,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle_hrf.so")
+# HRF_ORACLE_LIB selects another build of the same source (the sanitizer
+# build, `make sanitized`); the default is the optimised library.
+_ALT_LIB = os.environ.get("HRF_ORACLE_LIB")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
@@ -46,11 +49,18 @@ def lib():
     if _lib is not None:
         return _lib
     src = os.path.join(_HERE, "hrf_oracle.c")
+    if _ALT_LIB:
+        _lib = _bind(ctypes.CDLL(_ALT_LIB))
+        return _lib
     if not os.path.exists(_LIB_PATH) or (
         os.path.exists(src) and os.path.getmtime(src) > os.path.getmtime(_LIB_PATH)
     ):
         build()
-    L = ctypes.CDLL(_LIB_PATH)
+    _lib = _bind(ctypes.CDLL(_LIB_PATH))
+    return _lib
+
+
+def _bind(L):
     L.oracle_cov3d.argtypes = [_f32p, _f32p, _f32p]
     L.oracle_project.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _flt, _flt, _flt, _flt,
                                  _int, _int, _flt, _flt, _f32p, _f32p, _f32p, _f32p, _f32p]
@@ -61,10 +71,11 @@ def lib():
     L.oracle_bin.argtypes = [_i64, _f32p, _u32p, _u32p, _int, _int, _i64, _i32p, _i32p]
     L.oracle_render_forward.argtypes = [_int, _int, _int, _int, _i32p, _i32p, _f32p, _f32p,
                                         _f32p, _f32p, _f32p, _f32p, _f32p, _flt, _flt,
-                                        _f32p, _f32p, _i32p]
+                                        _f32p, _f32p, _i32p, ctypes.c_void_p]
     L.oracle_render_backward.argtypes = [_i64, _int, _int, _int, _int, _i32p, _i32p, _f32p,
                                          _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p,
-                                         _f32p, _f64p, _f64p, _f64p, _f64p, _f64p, _f64p]
+                                         _f32p, _f64p, _f64p, _f64p, _f64p, _f64p, _f64p,
+                                         ctypes.c_void_p]
     L.oracle_geom_backward.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p, _flt, _flt, _int,
                                        _int, _flt, _flt, _f32p, _f32p, _f32p, _f32p, _f32p,
                                        _f32p, _f32p]
@@ -80,7 +91,6 @@ def lib():
     L.oracle_asm_spectral.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _int, _int,
                                       _flt, _flt, _flt, _flt, _int]
     L.oracle_asm_consts.argtypes = [_flt, _flt, _flt, _int, _f32p]
-    _lib = L
     return L
 
 
@@ -178,8 +188,23 @@ def bin_pairs(z, tiles, rect, cam: Camera):
     return pl[:k], ranges
 
 
-def render_forward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges):
+def _tile_mask(mask, cam: Camera):
+    """(uint8 array kept alive, its address) for an optional per-tile mask."""
+    if mask is None:
+        return None, None
+    T = ((cam.width + 15) // 16) * ((cam.height + 15) // 16)
+    m = np.ascontiguousarray(mask, dtype=np.uint8)
+    if m.shape != (T,):
+        raise ValueError(f"tile mask must have {T} entries, got {m.shape}")
+    return m, m.ctypes.data
+
+
+def render_forward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges,
+                   tile_mask=None):
+    """Field (P,C,H,W), final_T and n_contrib (P,H,W); with tile_mask only the
+    selected tiles' pixels are rendered (the rest stay 0)."""
     L = lib()
+    keep, mptr = _tile_mask(tile_mask, cam)
     P, C, H, W = g.P, g.C, cam.height, cam.width
     field = np.zeros((P, C, H, W, 2), np.float32)
     fT = np.zeros((P, H, W), np.float32)
@@ -188,13 +213,17 @@ def render_forward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges
     L.oracle_render_forward(W, H, P, C, np.ascontiguousarray(ranges, np.int32), pl,
                             _f32(means2d), _f32(cov2d), _f32(g.z), _f32(g.colours),
                             _f32(g.phase), _f32(g.opac), _f32(g.pprobs), cam.near, cam.far,
-                            field, fT, nc)
+                            field, fT, nc, mptr)
+    del keep
     return field[..., 0] + 1j * field[..., 1], fT, nc
 
 
 def render_backward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, ranges, final_T,
-                    n_contrib, grad_field):
+                    n_contrib, grad_field, tile_mask=None):
+    """Render-backward accumulators (float64); with tile_mask only the
+    selected tiles' pixels contribute."""
     L = lib()
+    keep, mptr = _tile_mask(tile_mask, cam)
     n, P, C, H, W = g.n, g.P, g.C, cam.height, cam.width
     gf = np.ascontiguousarray(
         np.stack([grad_field.real, grad_field.imag], axis=-1), dtype=np.float32)
@@ -206,7 +235,8 @@ def render_backward(g: Gaussians, cam: Camera, means2d, cov2d, point_list, range
                              _f32(g.opac), _f32(g.pprobs), _f32(final_T),
                              np.ascontiguousarray(n_contrib, np.int32), gf, out["means2d"],
                              out["cov2d"], out["colours"], out["phase"], out["opac"],
-                             out["plane"])
+                             out["plane"], mptr)
+    del keep
     return out
 
 
@@ -668,3 +698,92 @@ def reconstruct_backward(grad, phases, amplitude, wavelengths, pitch, distances,
             g_amp[c] += w * t.real
             g_ph[f] += scales[c] * w * amplitude[c] * t.imag
     return g_ph, g_amp
+
+
+# ----------------------------------------------------------- SSIM (fast_ssim)
+# Restates the reference's fused SSIM (cuda_prop/cov3d_cuda/conv.cu:935-1135)
+# in float64: the 11x11 window as the outer product of the normalised 1-D
+# Gaussian (sigma 1.5; the reference's 2-D constants G_000..G_120 are those
+# products rounded to 1e-10), zero padding, the map's four factors and the
+# image-1 gradient through the window statistics.
+
+def ssim_window_1d() -> np.ndarray:
+    k = np.arange(11, dtype=np.float64) - 5.0
+    w = np.exp(-k * k / (2.0 * 1.5 * 1.5))
+    return w / w.sum()
+
+
+def _window_sum(a: np.ndarray) -> np.ndarray:
+    """sum over the 11x11 window (weights w_i w_j) of a zero-padded (..., H, W)."""
+    w = ssim_window_1d()
+    H, W = a.shape[-2:]
+    p = np.zeros(a.shape[:-2] + (H + 10, W + 10), dtype=np.float64)
+    p[..., 5:5 + H, 5:5 + W] = a
+    out = np.zeros(a.shape, dtype=np.float64)
+    for i in range(11):
+        for j in range(11):
+            out += w[i] * w[j] * p[..., i:i + H, j:j + W]
+    return out
+
+
+def _ssim_terms(x, y, C1, C2):
+    mu1, mu2 = _window_sum(x), _window_sum(y)
+    s11 = _window_sum(x * x) - mu1 * mu1
+    s22 = _window_sum(y * y) - mu2 * mu2
+    s12 = _window_sum(x * y) - mu1 * mu2
+    C = 2.0 * mu1 * mu2 + C1
+    D = 2.0 * s12 + C2
+    A = mu1 * mu1 + mu2 * mu2 + C1
+    B = s11 + s22 + C2
+    return mu1, mu2, A, B, C, D
+
+
+def ssim_map(img1, img2, C1=0.01 ** 2, C2=0.03 ** 2) -> np.ndarray:
+    """SSIM map (C, H, W) in float64 (conv.cu:993-1001)."""
+    x = np.asarray(img1, dtype=np.float64)
+    y = np.asarray(img2, dtype=np.float64)
+    _, _, A, B, C, D = _ssim_terms(x, y, C1, C2)
+    return (C * D) / (A * B)
+
+
+def ssim_backward(img1, img2, grad_map, C1=0.01 ** 2, C2=0.03 ** 2) -> np.ndarray:
+    """d(sum grad_map * map)/d img1 in float64 (conv.cu:1075-1130): the map's
+    partials with respect to mu1, window(x^2) and window(xy), pulled back
+    through the (symmetric) window."""
+    x = np.asarray(img1, dtype=np.float64)
+    y = np.asarray(img2, dtype=np.float64)
+    g = np.asarray(grad_map, dtype=np.float64)
+    mu1, mu2, A, B, C, D = _ssim_terms(x, y, C1, C2)
+    AB = A * B
+    d_mu1 = g * ((mu2 * 2.0 * D) / AB - (mu2 * 2.0 * C) / AB - (mu1 * 2.0 * C * D) / (A * A * B)
+                 + (mu1 * 2.0 * C * D) / (AB * B))
+    d_s11 = g * ((-C * D) / (AB * B))
+    d_s12 = g * ((2.0 * C) / AB)
+    return _window_sum(d_mu1) + 2.0 * x * _window_sum(d_s11) + y * _window_sum(d_s12)
+
+
+# ----------------------------------------------------- sparse Adam (spadam.cu)
+
+def sparse_adam_update(param, grad, exp_avg, exp_avg_sq, visible, lr, b1, b2, eps):
+    """Restates sparse_adam_kernel (cuda_prop/cov3d_cuda/spadam.cu:8-36) in
+    float32, op for op: returns updated copies of (param, exp_avg,
+    exp_avg_sq).  param/exp_avg/exp_avg_sq (B, N, D), grad (B, V, D),
+    visible (V) row indices; rows outside [0, N) are skipped."""
+    p = np.array(param, dtype=np.float32, copy=True)
+    m = np.array(exp_avg, dtype=np.float32, copy=True)
+    s = np.array(exp_avg_sq, dtype=np.float32, copy=True)
+    g = np.asarray(grad, dtype=np.float32)
+    lr, b1, b2, eps = (np.float32(v) for v in (lr, b1, b2, eps))
+    one = np.float32(1.0)
+    N = p.shape[1]
+    for v, row in enumerate(np.asarray(visible, dtype=np.int64)):
+        if row < 0 or row >= N:
+            continue
+        gr = g[:, v, :]
+        mm = b1 * m[:, row, :] + (one - b1) * gr
+        ss = b2 * s[:, row, :] + (one - b2) * gr * gr
+        step = (-lr * mm) / (np.sqrt(ss) + eps)
+        p[:, row, :] = p[:, row, :] + step
+        m[:, row, :] = mm
+        s[:, row, :] = ss
+    return p, m, s

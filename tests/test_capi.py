@@ -96,6 +96,14 @@ def test_reference_import_statements_resolve():
     from complex_valued_holographic_radiance_fields_amd.cuda_prop.cov3d_cuda.python_import \
         import (compute_cov2d_cuda, compute_cov3d_cuda, compute_jacobian_cuda,  # noqa: F401
                 compute_means2d_cuda, invert_cov2d_cuda, splat_tile_cuda)
+    # utils/data_utils.py:20 and utils/optimizer.py:21
+    from complex_valued_holographic_radiance_fields_amd.cuda_prop.cov3d_cuda.python_import \
+        import fast_ssim  # noqa: F401
+    from complex_valued_holographic_radiance_fields_amd.cuda_prop.cov3d_cuda.python_import \
+        import sparse_adam_update  # noqa: F401
+    from complex_valued_holographic_radiance_fields_amd.cuda_prop.cov3d_cuda import \
+        python_import as pi
+    assert (pi.C1, pi.C2) == (0.01 ** 2, 0.03 ** 2)
 
 
 def test_geometry_operators_reject_host_tensors():
@@ -111,3 +119,135 @@ def test_geometry_operators_reject_host_tensors():
         pi.invert_cov2d_cuda(torch.eye(2).expand(3, 2, 2))
     with pytest.raises(ValueError):
         pi.compute_means2d_cuda(torch.ones(3, 3), 1.0, 1.0, 0.0, 0.0, 1.0, 100.0)
+    with pytest.raises(ValueError):
+        pi.fast_ssim(torch.zeros(3, 8, 8), torch.zeros(3, 8, 8))
+    z = torch.zeros(1, 4, 2)
+    with pytest.raises(ValueError):
+        pi.sparse_adam_update(z, z[:, :1], z, z, torch.zeros(1, dtype=torch.int64), 1e-3, 0.9,
+                              0.999, 1e-15)
+
+
+def _bind(lib, name):
+    from complex_valued_holographic_radiance_fields_amd import _lib as L
+
+    f = getattr(lib, name)
+    f.restype, f.argtypes = L.SIGNATURES[name]
+    return f
+
+
+def _descriptors(n, C=3, P=3, W=64, H=48):
+    """Descriptors with placeholder (never dereferenced) input addresses: the
+    checks under test run on the host before any HIP call."""
+    from complex_valued_holographic_radiance_fields_amd import _lib as L
+
+    fake = 0x1000
+    g = L.HrfGaussians(fake, fake, fake, fake, fake, fake, fake, fake, n, C, P)
+    c = L.HrfCamera(100.0, 100.0, W / 2, H / 2, fake, W, H, 1.0, 1000.0)
+    return g, c
+
+
+def _err(lib):
+    lib.hrf_last_error.restype = ctypes.c_char_p
+    return lib.hrf_last_error().decode()
+
+
+def test_prepare_with_no_gaussians_returns_zero_counts(lib):
+    """N = 0: K = V = 0 and no device work (the reference reads
+    point_offsets[N-1] here, rasterizer_splat.cu:431)."""
+    f = _bind(lib, "hrf_raster_forward_prepare")
+    g, c = _descriptors(0)
+    k, v = ctypes.c_int64(-1), ctypes.c_int64(-1)
+    assert f(ctypes.byref(g), ctypes.byref(c), None, 0, None, ctypes.byref(k),
+             ctypes.byref(v)) == 0
+    assert (k.value, v.value) == (0, 0)
+
+
+def test_backward_with_no_gaussians_is_a_no_op(lib):
+    f = _bind(lib, "hrf_raster_backward")
+    g, c = _descriptors(0)
+    st = f(ctypes.byref(g), ctypes.byref(c), None, None, None, None, None, 0, None, 0, None, 0,
+           None, 0, None, None, None, None, None, None, None, None, None)
+    assert st == 0
+
+
+def test_pair_count_beyond_int32_raises_overflow(lib):
+    """K >= 2^31 cannot index the int32 point_list / ranges outputs
+    (rasterizer_splat.cu:430 keeps K in an int): HRF_ERR_OVERFLOW, checked on
+    the host before anything is enqueued."""
+    fake = 0x1000
+    render = _bind(lib, "hrf_raster_forward_render")
+    g, c = _descriptors(1000)
+    for k in (2 ** 31, 2 ** 40):
+        st = render(ctypes.byref(g), ctypes.byref(c), fake, 1 << 40, fake, 1 << 40, k, 10, fake,
+                    fake, fake, fake, fake, fake, None, 0, None)
+        assert st == 4, (k, st, _err(lib))
+        assert "int32" in _err(lib)
+    bwd = _bind(lib, "hrf_raster_backward")
+    st = bwd(ctypes.byref(g), ctypes.byref(c), fake, fake, fake, fake, fake, 2 ** 31, fake,
+             1 << 40, None, 0, None, 0, fake, fake, fake, fake, fake, fake, fake, fake, None)
+    assert st == 4, _err(lib)
+    st = render(ctypes.byref(g), ctypes.byref(c), fake, 1 << 40, fake, 1 << 40, -1, 10, fake,
+                fake, fake, fake, fake, fake, None, 0, None)
+    assert st == 1
+
+
+def test_undersized_workspaces_rejected(lib):
+    """A workspace smaller than its *_workspace_size: HRF_ERR_WORKSPACE with
+    the sizes in the message, before any HIP call."""
+    fake = 0x1000
+    n, C, P, W, H = 5000, 3, 3, 64, 48
+    g, c = _descriptors(n, C, P, W, H)
+    geom = _bind(lib, "hrf_raster_geom_workspace_size")(n, C, P)
+    prep = _bind(lib, "hrf_raster_forward_prepare")
+    k, v = ctypes.c_int64(0), ctypes.c_int64(0)
+    st = prep(ctypes.byref(g), ctypes.byref(c), fake, geom - 1, None, ctypes.byref(k),
+              ctypes.byref(v))
+    assert st == 3 and "geometry workspace too small" in _err(lib)
+    st = prep(ctypes.byref(g), ctypes.byref(c), None, geom, None, ctypes.byref(k),
+              ctypes.byref(v))
+    assert st == 3
+    K = 70000
+    binb = _bind(lib, "hrf_raster_binning_workspace_size")(K, W, H)
+    render = _bind(lib, "hrf_raster_forward_render")
+    st = render(ctypes.byref(g), ctypes.byref(c), fake, geom, fake, binb - 1, K, 100, fake, fake,
+                fake, fake, fake, fake, None, 0, None)
+    assert st == 3 and "binning workspace too small" in _err(lib)
+    plb = _bind(lib, "hrf_raster_plane_lists_size")(K, W, H, P)
+    bw = _bind(lib, "hrf_raster_backward_workspace_size")(n, C, P)
+    bwd = _bind(lib, "hrf_raster_backward")
+    st = bwd(ctypes.byref(g), ctypes.byref(c), fake, fake, fake, fake, fake, K, fake, bw - 1,
+             None, 0, None, 0, fake, fake, fake, fake, fake, fake, fake, fake, None)
+    assert st == 3 and "backward workspace too small" in _err(lib)
+    st = bwd(ctypes.byref(g), ctypes.byref(c), fake, fake, fake, fake, fake, K, fake, bw,
+             fake, geom - 1, None, 0, fake, fake, fake, fake, fake, fake, fake, fake, None)
+    assert st == 3 and "forward geometry workspace too small" in _err(lib)
+    st = bwd(ctypes.byref(g), ctypes.byref(c), fake, fake, fake, fake, fake, K, fake, bw,
+             fake, geom, fake, plb - 1, fake, fake, fake, fake, fake, fake, fake, fake, None)
+    assert st == 3 and "plane lists workspace too small" in _err(lib)
+    asm = _bind(lib, "hrf_asm_workspace_size")(3, 3, 800)
+    mp = _bind(lib, "hrf_asm_multiplane_forward")
+    wl = (ctypes.c_float * 3)(639e-9, 515e-9, 473e-9)
+    ds = (ctypes.c_float * 3)(-1e-3, 0.0, 1e-3)
+    st = mp(fake, 3, 3, 800, 800, 800, wl, ds, 3.74e-6, 800.0, fake, fake, asm - 1, None)
+    assert st == 3, _err(lib)
+
+
+def test_invalid_shapes_rejected_without_gpu(lib):
+    """Planes outside 1..32, non-positive image sizes, odd propagation sizes
+    and null inputs are rejected on the host."""
+    prep = _bind(lib, "hrf_raster_forward_prepare")
+    k, v = ctypes.c_int64(0), ctypes.c_int64(0)
+    for kw in ({"P": 0}, {"P": 33}, {"W": 0}, {"H": -4}):
+        args = dict(n=10, C=3, P=3, W=64, H=48)
+        args.update(kw)
+        g, c = _descriptors(**args)
+        assert prep(ctypes.byref(g), ctypes.byref(c), None, 0, None, ctypes.byref(k),
+                    ctypes.byref(v)) == 1, kw
+    g, c = _descriptors(10)
+    g.quats = None
+    assert prep(ctypes.byref(g), ctypes.byref(c), None, 0, None, ctypes.byref(k),
+                ctypes.byref(v)) == 1
+    assert "null input" in _err(lib)
+    fwd = _bind(lib, "hrf_asm_forward")
+    st = fwd(0x1000, 101, 100, 100, 515e-9, 3.74e-6, 0.0, 100.0, 0x1000, 0x1000, 1 << 30, None)
+    assert st == 1 and "even" in _err(lib)

@@ -1,0 +1,186 @@
+"""Oracle parity of the rasterizer at the BASELINE configurations' full size.
+
+The oracle's full-image render is too slow at 1M Gaussians, so each config
+is checked on a seeded set of tiles that includes the densest tiles, the
+image corners and edges (and, at cfg2's 1008x756, the partial bottom tile
+row), plus random non-empty tiles:
+
+* each selected tile's list (point_list over its range) is recomputed from
+  the oracle's tile rectangles and depth keys: every Gaussian whose rectangle
+  covers the tile, ordered by (depth key, index) — bit-exact;
+* the oracle renders those tiles from the HIP lists (tile mask) and its
+  field, final_T and n_contrib are compared pixel by pixel there;
+* the backward runs with an upstream gradient that is CN(0,1) on those
+  tiles and zero elsewhere, so every Gaussian gradient comes from them only:
+  the HIP backward (on the benchmark's path: forward records and plane
+  member lists reused) against the oracle's tile-masked render backward and
+  its geometry backward over all Gaussians.
+
+Config 0 (10k Gaussians at 256x256, P = C = 1) is small enough for the
+oracle's full render: whole-image forward and backward parity, and the
+frame's hologram through the multi-plane ASM.
+
+Bars: lists bit-exact; fields, final_T and all 8 gradients rel-L2 < 1e-4;
+n_contrib may differ only where the two sides' float exp straddles the
+T < 1e-4 termination (< 1e-3 of the compared pixels)."""
+import numpy as np
+import pytest
+
+from conftest import oracle_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+NAMES = ["cam", "z", "quats", "scales", "colours", "phase", "opac", "plane"]
+
+
+def _depth_key(z):
+    b = np.asarray(z, np.float32).view(np.uint32).astype(np.uint64)
+    return np.where(b & 0x80000000, b & 0x7FFFFFFF, b | 0x80000000)
+
+
+def _select_tiles(ranges, gx, gy, seed, n_dense=4, n_random=8):
+    lens = ranges[:, 1].astype(np.int64) - ranges[:, 0]
+    nonempty = np.nonzero(lens > 0)[0]
+    dense = list(np.argsort(-lens, kind="stable")[:n_dense])
+    border = [0, gx - 1, (gy - 1) * gx, gy * gx - 1,  # corners
+              (gy // 2) * gx, (gy // 2) * gx + gx - 1,  # left / right edge
+              gx // 2, (gy - 1) * gx + gx // 2]  # top / bottom edge
+    rng = np.random.default_rng(seed)
+    rand = list(rng.choice(nonempty, size=min(n_random, len(nonempty)), replace=False))
+    sel = sorted(set(int(t) for t in dense + border + rand))
+    return sel
+
+
+def _check_tile_lists(sel, pl_of, ranges, rect, key, gx):
+    """Each selected tile's list == the Gaussians whose rect covers it, by
+    (depth key, index)."""
+    for t in sel:
+        tx, ty = t % gx, t // gx
+        cover = np.nonzero((rect[:, 0] <= tx) & (tx < rect[:, 2]) & (rect[:, 1] <= ty) &
+                           (ty < rect[:, 3]))[0]
+        order = cover[np.lexsort((cover, key[cover]))]
+        got = pl_of(t)
+        assert got.shape == order.shape, (t, got.shape, order.shape)
+        np.testing.assert_array_equal(got, order, err_msg=f"tile {t}")
+        if len(order) == 0:
+            assert ranges[t, 0] == 0 and ranges[t, 1] == 0
+
+
+def _pixel_mask(sel, gx, gy, W, H):
+    tm = np.zeros(gx * gy, np.uint8)
+    tm[sel] = 1
+    pm = np.repeat(np.repeat(tm.reshape(gy, gx), 16, 0), 16, 1)[:H, :W].astype(bool)
+    return tm, pm
+
+
+@pytest.mark.parametrize("name", ["headline", "cfg1", "cfg2"])
+def test_config_tiles_forward_backward_parity(hrf, oracle_mod, name):
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import rasterizer, scenes
+
+    spec = scenes.config(name)
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    W, H, P, C = spec.width, spec.height, g.P, g.C
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    t = scenes.to_torch(sc)
+    field, info, geom = rasterizer.forward(
+        t["cam_means"], t["z"], t["quats"], t["scales"], t["colours"], t["phase"], t["opac"],
+        t["pprobs"], sc.fx, sc.fy, sc.px, sc.py, t["view"], (W, H), (16, 16), 1.0, 1000.0,
+        keep_geometry=True)
+    fT, nc, pl, ranges, vis = info
+    torch.cuda.synchronize()
+    ranges_h = ranges.cpu().numpy()
+    sel = _select_tiles(ranges_h, gx, gy, seed=len(name))
+    K = int(pl.numel())
+    print(f"{name}: N={g.n} K={K} tiles={sel}", flush=True)
+    assert 16 <= len(sel)
+    if name == "cfg2":
+        assert H % 16 != 0 and any(tt // gx == gy - 1 for tt in sel)  # partial bottom row
+
+    pr = oracle_mod.project(g, cam)
+    _, tiles_ref, rect_ref = oracle_mod.preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
+    assert K == int(tiles_ref.astype(np.int64).sum())
+    pl_h = pl.cpu().numpy()
+    _check_tile_lists(sel, lambda tt: pl_h[ranges_h[tt, 0]:ranges_h[tt, 1]], ranges_h,
+                      rect_ref.astype(np.int64), _depth_key(g.z), gx)
+
+    tm, pm = _pixel_mask(sel, gx, gy, W, H)
+    rf, rT, rn = oracle_mod.render_forward(g, cam, pr["means2d"], pr["cov2d"], pl_h, ranges_h,
+                                           tile_mask=tm)
+    f_h = field.cpu().numpy()
+    assert rel_l2(f_h[:, :, pm], rf[:, :, pm]) < TOL
+    assert rel_l2(fT.cpu().numpy()[:, pm], rT[:, pm]) < TOL
+    mism = np.mean(nc.cpu().numpy()[:, pm] != rn[:, pm])
+    assert mism < 1e-3, mism
+
+    rng = np.random.default_rng(17)
+    gf = ((rng.normal(size=(P, C, H, W)) + 1j * rng.normal(size=(P, C, H, W))) *
+          np.sqrt(0.5)).astype(np.complex64)
+    gf[:, :, ~pm] = 0
+    grads = rasterizer.backward(torch.from_numpy(gf).cuda(), t["cam_means"], t["z"], t["quats"],
+                                t["scales"], t["colours"], t["phase"], t["opac"], t["pprobs"],
+                                sc.fx, sc.fy, sc.px, sc.py, t["view"], (W, H), (16, 16), fT, nc,
+                                pl, ranges, 1.0, 1000.0, geometry=geom)
+    torch.cuda.synchronize()
+    rb = oracle_mod.render_backward(g, cam, pr["means2d"], pr["cov2d"], pl_h, ranges_h, rT, rn,
+                                    gf, tile_mask=tm)
+    gc, gq, gs = oracle_mod.geom_backward(g, cam, rb["means2d"].astype(np.float32),
+                                          rb["cov2d"].astype(np.float32))
+    ref = dict(cam=gc, quats=gq, scales=gs, colours=rb["colours"], phase=rb["phase"],
+               opac=rb["opac"], plane=rb["plane"])
+    touched = int(np.count_nonzero(np.any(rb["colours"] != 0, axis=1)))
+    print(f"{name}: {touched} Gaussians with nonzero colour gradients", flush=True)
+    assert touched > 100
+    for nm, gg in zip(NAMES, grads):
+        got = gg.cpu().numpy()
+        if nm == "z":
+            assert not got.any()
+            continue
+        e = rel_l2(got, ref[nm])
+        assert e < TOL, (nm, e)
+    del field, info, geom, grads
+    torch.cuda.empty_cache()
+
+
+def test_config0_full_parity(hrf, oracle_mod):
+    """Config 0 (10k Gaussians, 256x256, 1 plane, 1 wavelength): whole-image
+    forward (lists, visible, field, final_T, n_contrib) and backward parity,
+    and the hologram of the frame through the ASM (M = 512)."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from complex_valued_holographic_radiance_fields_amd.frame import Frame
+
+    spec = scenes.config("cfg0")
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    assert (g.n, spec.width, spec.height, g.P, g.C) == (10_000, 256, 256, 1, 1)
+    t = scenes.to_torch(sc)
+    fr = Frame(t, spec, sc.fx, sc.fy, sc.px, sc.py)
+    holo = fr.forward()
+    grads = fr.backward(t["grad_holo"])
+    torch.cuda.synchronize()
+    fT, nc, pl, ranges, vis = fr.fwd_state
+    ref = oracle_mod.rasterize_forward(g, cam)
+    print(f"cfg0: K={ref['K']}", flush=True)
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+    assert rel_l2(fr.fields.cpu().numpy(), ref["field"]) < TOL
+    assert rel_l2(fT.cpu().numpy(), ref["final_T"]) < TOL
+    assert np.mean(nc.cpu().numpy() != ref["n_contrib"]) < 1e-3
+    S = spec.size
+    prop = [-d for d in spec.distances]
+    ref_holo = oracle_mod.multiplane_forward(ref["field"], spec.wavelengths, prop, scenes.PITCH,
+                                             S, float(S))
+    assert rel_l2(holo.cpu().numpy(), ref_holo) < TOL
+    gfield = oracle_mod.multiplane_adjoint(sc.grad_holo, spec.height, spec.width,
+                                           spec.wavelengths, prop, scenes.PITCH, S, float(S))
+    rb = oracle_mod.rasterize_backward(g, cam, ref, gfield.astype(np.complex64))
+    for nm, gg in zip(NAMES, grads):
+        got = gg.cpu().numpy()
+        if nm == "z":
+            assert not got.any()
+            continue
+        assert rel_l2(got, rb[nm]) < TOL, nm

@@ -964,3 +964,170 @@ def test_reconstruct_backward_finite_differences(oracle_mod):
         e[c, i, j] = h
         fd = (loss(phases, amp + e) - loss(phases, amp - e)) / (2 * h)
         assert abs(fd - g_amp[c, i, j]) <= 2e-3 * max(1.0, abs(fd)), (c, i, j, fd, g_amp[c, i, j])
+
+
+# ------------------------------------------------------------ SSIM oracle pins
+
+def test_ssim_window_is_the_normalised_gaussian(oracle_mod):
+    """The 1-D window: 11 taps, sum 1, symmetric, neighbour ratios
+    exp((2k+1)/(2 sigma^2)) with sigma 1.5, and the reference's listed
+    centre and end values (conv.cu:8-18: G_05 = 0.26601171493530273,
+    G_00 = 0.001028380123898387)."""
+    w = oracle_mod.ssim_window_1d()
+    assert w.shape == (11,) and abs(w.sum() - 1.0) < 1e-15
+    np.testing.assert_array_equal(w, w[::-1])
+    for k in range(5):
+        d0, d1 = 5 - k, 4 - k
+        np.testing.assert_allclose(w[k + 1] / w[k], math.exp((d0 * d0 - d1 * d1) / 4.5),
+                                   rtol=1e-13)
+    # the reference lists float32 values
+    assert np.float32(w[5]) == np.float32(0.26601171493530273)
+    assert np.float32(w[0]) == np.float32(0.001028380123898387)
+
+
+def _ssim_brute(x, y, C1, C2):
+    """Pure-Python loops over the 11x11 window of every pixel (zero outside
+    the image): an independent restatement of the map for tiny images."""
+    w1 = [math.exp(-((k - 5) ** 2) / 4.5) for k in range(11)]
+    s = sum(w1)
+    w1 = [v / s for v in w1]
+    Cn, H, W = x.shape
+    out = np.zeros(x.shape)
+    for c in range(Cn):
+        for i in range(H):
+            for j in range(W):
+                m1 = m2 = e11 = e22 = e12 = 0.0
+                for a in range(11):
+                    for b in range(11):
+                        ii, jj = i + a - 5, j + b - 5
+                        if 0 <= ii < H and 0 <= jj < W:
+                            wt = w1[a] * w1[b]
+                            u, v = float(x[c, ii, jj]), float(y[c, ii, jj])
+                            m1 += wt * u
+                            m2 += wt * v
+                            e11 += wt * u * u
+                            e22 += wt * v * v
+                            e12 += wt * u * v
+                num = (2 * m1 * m2 + C1) * (2 * (e12 - m1 * m2) + C2)
+                den = (m1 * m1 + m2 * m2 + C1) * ((e11 - m1 * m1) + (e22 - m2 * m2) + C2)
+                out[c, i, j] = num / den
+    return out
+
+
+def test_ssim_map_brute_force_and_closed_forms(oracle_mod):
+    rng = np.random.default_rng(31)
+    C1, C2 = 0.01 ** 2, 0.03 ** 2
+    x = rng.uniform(size=(2, 6, 7))
+    y = rng.uniform(size=(2, 6, 7))
+    np.testing.assert_allclose(oracle_mod.ssim_map(x, y, C1, C2), _ssim_brute(x, y, C1, C2),
+                               rtol=1e-12, atol=1e-14)
+    # identical images: 1 everywhere
+    np.testing.assert_allclose(oracle_mod.ssim_map(x, x, C1, C2), 1.0, rtol=0, atol=1e-13)
+    # constant images a, b: at pixels whose window lies inside the image the
+    # variances vanish and the map is (2ab + C1) / (a^2 + b^2 + C1)
+    a, b = 0.3, 0.7
+    xa = np.full((1, 24, 26), a)
+    yb = np.full((1, 24, 26), b)
+    m = oracle_mod.ssim_map(xa, yb, C1, C2)
+    np.testing.assert_allclose(m[0, 5:-5, 5:-5], (2 * a * b + C1) / (a * a + b * b + C1),
+                               rtol=1e-12)
+    assert np.all(m <= 1.0 + 1e-12)
+
+
+def test_ssim_backward_finite_differences(oracle_mod):
+    """The image-1 gradient of sum(g * map): float64 central differences at
+    interior, edge and corner pixels; zero at img1 == img2 (every map entry
+    is at its maximum 1 there)."""
+    rng = np.random.default_rng(32)
+    C1, C2 = 0.01 ** 2, 0.03 ** 2
+    x = rng.uniform(size=(2, 14, 16))
+    y = np.clip(x + 0.2 * rng.normal(size=x.shape), 0, 1)
+    g = rng.normal(size=x.shape)
+    grad = oracle_mod.ssim_backward(x, y, g, C1, C2)
+
+    def loss(xx):
+        return float(np.sum(g * oracle_mod.ssim_map(xx, y, C1, C2)))
+
+    h = 1e-6
+    for idx in [(0, 7, 8), (1, 0, 0), (0, 13, 5), (1, 6, 15), (0, 2, 3)]:
+        e = np.zeros_like(x)
+        e[idx] = h
+        fd = (loss(x + e) - loss(x - e)) / (2 * h)
+        assert abs(fd - grad[idx]) <= 1e-6 * max(1.0, abs(fd)), (idx, fd, grad[idx])
+    np.testing.assert_allclose(oracle_mod.ssim_backward(x, x, g, C1, C2), 0.0, atol=1e-12)
+
+
+# ------------------------------------------------------- sparse Adam oracle pins
+
+def test_sparse_adam_closed_forms(oracle_mod):
+    """From zero state the first step is m = (1-b1) g, s = (1-b2) g^2,
+    p' = p - lr (1-b1) g / (sqrt(1-b2) |g| + eps); rows not listed, and rows
+    outside [0, N), are untouched; a second step follows the recurrence."""
+    rng = np.random.default_rng(33)
+    B, N, D = 2, 9, 5
+    lr, b1, b2, eps = 1e-2, 0.9, 0.999, 1e-15
+    p0 = rng.normal(size=(B, N, D)).astype(np.float32)
+    z = np.zeros_like(p0)
+    vis = np.array([4, 1, 7, -1, 9], dtype=np.int64)  # two out of range
+    g = rng.normal(size=(B, len(vis), D)).astype(np.float32)
+    p1, m1, s1 = oracle_mod.sparse_adam_update(p0, g, z, z, vis, lr, b1, b2, eps)
+    # the kernel's scalars are float32: 1 - b in float32 (1 - 0.999 rounds to
+    # 0.0010000467)
+    ob1 = float(np.float32(1) - np.float32(b1))
+    ob2 = float(np.float32(1) - np.float32(b2))
+    for v, row in enumerate(vis[:3]):
+        gv = g[:, v, :].astype(np.float64)
+        np.testing.assert_allclose(m1[:, row], ob1 * gv, rtol=1e-6)
+        np.testing.assert_allclose(s1[:, row], ob2 * gv * gv, rtol=1e-6)
+        exp_p = p0[:, row] - lr * ob1 * gv / (math.sqrt(ob2) * np.abs(gv) + eps)
+        np.testing.assert_allclose(p1[:, row], exp_p, rtol=1e-5, atol=1e-7)
+    others = [r for r in range(N) if r not in (4, 1, 7)]
+    np.testing.assert_array_equal(p1[:, others], p0[:, others])
+    assert not m1[:, others].any() and not s1[:, others].any()
+    g2 = rng.normal(size=g.shape).astype(np.float32)
+    p2, m2, s2 = oracle_mod.sparse_adam_update(p1, g2, m1, s1, vis, lr, b1, b2, eps)
+    row = 7
+    gv = g2[:, 2].astype(np.float64)
+    mm = float(np.float32(b1)) * m1[:, row] + ob1 * gv
+    ss = float(np.float32(b2)) * s1[:, row] + ob2 * gv * gv
+    np.testing.assert_allclose(m2[:, row], mm, rtol=1e-6)
+    np.testing.assert_allclose(p2[:, row], p1[:, row] - lr * mm / (np.sqrt(ss) + eps),
+                               rtol=1e-5, atol=1e-7)
+
+
+def test_tile_masked_render_matches_full_render(oracle_mod):
+    """The tile-subset entry the full-size GPU parity uses: a masked render
+    equals the full render on the selected tiles (and leaves the rest at
+    0); a masked backward equals the full backward when the upstream
+    gradient vanishes outside them; and the per-tile lists rebuilt from the
+    rectangles and (depth key, index) order equal the oracle's binning."""
+    from test_gpu_config_parity import _check_tile_lists, _depth_key, _pixel_mask, _select_tiles
+
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    sc = scenes.generate(scenes.small("mask", 6000, 120, 72, 2, 3, "object", seed=5))
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    W, H = cam.width, cam.height
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    sel = _select_tiles(ref["ranges"], gx, gy, seed=3, n_random=5)
+    pl = ref["point_list"]
+    _check_tile_lists(sel, lambda t: pl[ref["ranges"][t, 0]:ref["ranges"][t, 1]], ref["ranges"],
+                      ref["rect"].astype(np.int64), _depth_key(g.z), gx)
+    tm, pm = _pixel_mask(sel, gx, gy, W, H)
+    pr = ref["proj"]
+    f, T, n = oracle_mod.render_forward(g, cam, pr["means2d"], pr["cov2d"], pl, ref["ranges"],
+                                        tile_mask=tm)
+    np.testing.assert_array_equal(f[:, :, pm], ref["field"][:, :, pm])
+    np.testing.assert_array_equal(T[:, pm], ref["final_T"][:, pm])
+    np.testing.assert_array_equal(n[:, pm], ref["n_contrib"][:, pm])
+    assert not f[:, :, ~pm].any() and not T[:, ~pm].any()
+    rng = np.random.default_rng(2)
+    gf = (rng.normal(size=f.shape) + 1j * rng.normal(size=f.shape)).astype(np.complex64)
+    gf[:, :, ~pm] = 0
+    full = oracle_mod.render_backward(g, cam, pr["means2d"], pr["cov2d"], pl, ref["ranges"],
+                                      ref["final_T"], ref["n_contrib"], gf)
+    part = oracle_mod.render_backward(g, cam, pr["means2d"], pr["cov2d"], pl, ref["ranges"],
+                                      ref["final_T"], ref["n_contrib"], gf, tile_mask=tm)
+    for k in full:
+        np.testing.assert_array_equal(part[k], full[k])
