@@ -147,9 +147,81 @@ def asm_torch(field, wavelength, pitch, distance, S, aperture):
     return out[s0:s0 + S, s0:s0 + S]
 
 
+def _cpu_params(sc, grad: bool):
+    t = lambda a: torch.from_numpy(a.copy()).requires_grad_(grad)  # noqa: E731
+    return [t(sc.cam_means), t(sc.quats), t(sc.scales), t(sc.colours), t(sc.phase), t(sc.opac),
+            t(sc.pprobs)]
+
+
+def run_frame(sc, backward: bool = True, cap_s: float = 600.0):
+    """The whole CPU frame of scene ``sc``, not sampled: every 64x64 tile of
+    the Python splat, every (plane, wavelength) pure-torch propagation and
+    the sum over planes (Scene.splat, model.py:1194-1272), then (backward)
+    autograd of Re<hologram, g> with the scene's upstream gradient g.
+    Stops once ``cap_s`` seconds of wall time have passed (the protocol's
+    did-not-finish cap).  Returns dict(finished, fwd_ms, bwd_ms, elapsed_s,
+    tiles_done, tiles)."""
+    spec = sc.spec
+    W, H, P, C, S = spec.width, spec.height, spec.planes, len(spec.wavelengths), spec.size
+    params = _cpu_params(sc, backward)
+    R = torch.from_numpy(sc.view.copy())
+    fx, fy, px, py = sc.fx, sc.fy, sc.px, sc.py
+    tile = 64
+    xt, yt = math.ceil(W / tile), math.ceil(H / tile)
+    t0 = time.perf_counter()
+    res = dict(finished=False, fwd_ms=None, bwd_ms=None, tiles=xt * yt, tiles_done=0)
+    with torch.set_grad_enabled(backward):
+        with torch.no_grad():
+            m = means_2d(params[0], fx, fy, px, py)
+            c2 = cov_2d(params[0], params[1], params[2], fx, fy, R, W, H)
+            bounds = gaussian_bounds(m, c2, W, H)
+        rows = []
+        for yi in range(yt):
+            row = []
+            for xi in range(xt):
+                x, y = xi * tile, yi * tile
+                tw, th = min(tile, W - x), min(tile, H - y)
+                sel = ((bounds[:, 0] <= x + tw - 1) & (bounds[:, 2] >= x) &
+                       (bounds[:, 1] <= y + th - 1) & (bounds[:, 3] >= y))
+                row.append(splat_tile(params, torch.where(sel)[0], x, y, tw, th, fx, fy, px, py,
+                                      R, W, H, P, C))
+                res["tiles_done"] += 1
+                if time.perf_counter() - t0 > cap_s:
+                    res["elapsed_s"] = time.perf_counter() - t0
+                    return res
+            rows.append(torch.cat(row, dim=3))
+        field = torch.cat(rows, dim=2)  # (P, C, H, W)
+        holo = []
+        for c in range(C):
+            acc = None
+            for p in range(P):
+                o = asm_torch(field[p, c], spec.wavelengths[c], 3.74e-6, -spec.distances[p], S,
+                              float(S))
+                acc = o if acc is None else acc + o
+            holo.append(acc)
+            if time.perf_counter() - t0 > cap_s:
+                res["elapsed_s"] = time.perf_counter() - t0
+                return res
+        holo = torch.stack(holo, 0)
+    t1 = time.perf_counter()
+    res["fwd_ms"] = (t1 - t0) * 1e3
+    if backward:
+        g = torch.from_numpy(sc.grad_holo.copy())
+        (holo.real * g.real + holo.imag * g.imag).sum().backward()
+        res["bwd_ms"] = (time.perf_counter() - t1) * 1e3
+    res["elapsed_s"] = time.perf_counter() - t0
+    res["finished"] = res["elapsed_s"] <= cap_s
+    return res
+
+
 def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
-    """Time the CPU path on a bounded sample of one frame of scene ``sc``
-    (package Scene).  Returns (ms_per_frame_estimate, sample description)."""
+    """ESTIMATE of the CPU path's time for one frame of scene ``sc`` from a
+    bounded sample (for frames far beyond the did-not-finish cap): random
+    64x64 tiles forward+backward until the budget is spent, scaled by the
+    ratio of all tiles' selected-Gaussian counts to the sampled tiles'
+    counts (the tile cost grows with the Gaussians it evaluates), plus the
+    per-frame projection setup and one propagation forward+backward scaled
+    by P*C.  Returns (ms_per_frame_estimate, sample description)."""
     torch.manual_seed(seed)
     spec = sc.spec
     W, H, P, C = spec.width, spec.height, spec.planes, len(spec.wavelengths)
@@ -170,8 +242,18 @@ def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
         c2 = cov_2d(params[0], params[1], params[2], fx, fy, R, W, H)
         bounds = gaussian_bounds(m, c2, W, H)
     setup_s = time.perf_counter() - t0
+    # Gaussians each tile evaluates (tile pixels x selected Gaussians)
+    work = []
+    for ti in range(xt * yt):
+        yi, xi = divmod(ti, xt)
+        x, y = xi * tile, yi * tile
+        tw, th = min(tile, W - x), min(tile, H - y)
+        sel = ((bounds[:, 0] <= x + tw - 1) & (bounds[:, 2] >= x) & (bounds[:, 1] <= y + th - 1) &
+               (bounds[:, 3] >= y))
+        work.append(float(sel.sum()) * tw * th)
     done = 0
     raster_s = 0.0
+    work_done = 0.0
     for ti in order:
         yi, xi = divmod(ti, xt)
         x, y = xi * tile, yi * tile
@@ -179,6 +261,7 @@ def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
         sel = ((bounds[:, 0] <= x + tw - 1) & (bounds[:, 2] >= x) & (bounds[:, 1] <= y + th - 1) &
                (bounds[:, 3] >= y))
         idx = torch.where(sel)[0]
+        work_done += work[ti]
         t1 = time.perf_counter()
         out = splat_tile(params, idx, x, y, tw, th, fx, fy, px, py, R, W, H, P, C)
         if out.requires_grad:
@@ -188,7 +271,7 @@ def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
         done += 1
         if raster_s > budget_s * 0.7:
             break
-    raster_frame_s = raster_s * (xt * yt) / done
+    raster_frame_s = raster_s * (sum(work) / work_done if work_done > 0 else (xt * yt) / done)
     # ASM: one (plane, wavelength) propagation forward+backward, times P*C.
     f = torch.randn((H, W), dtype=torch.complex64).requires_grad_(True)
     S = spec.size
@@ -198,9 +281,11 @@ def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
     (o.real * g.real + o.imag * g.imag).sum().backward()
     asm_one_s = time.perf_counter() - t2
     total_s = setup_s + raster_frame_s + asm_one_s * P * C
-    desc = (f"reference CPU PyTorch path restated (oracle/cpu_baseline.py): {done} of {xt * yt} "
-            f"64x64 tiles fwd+bwd (random sample, scaled by tile count) + 1 of {P * C} ASM "
-            f"fwd+bwd (scaled by P*C) + projection setup; {spec.name} N={sc.cam_means.shape[0]}")
+    desc = (f"ESTIMATE from a sample: reference CPU PyTorch path restated "
+            f"(oracle/cpu_baseline.py), {done} of {xt * yt} random 64x64 tiles fwd+bwd scaled "
+            f"by the tiles' selected-Gaussian work ({work_done / max(sum(work), 1):.1%} of the "
+            f"frame's), 1 of {P * C} ASM fwd+bwd scaled by P*C, projection setup; "
+            f"{spec.name} N={sc.cam_means.shape[0]}")
     return total_s * 1000.0, desc
 
 

@@ -629,7 +629,9 @@ def test_render_rejects_counts_other_than_prepared(hrf):
 
     for k, v in ((K - 1, V), (K + 1, V), (K, V - 1), (K, V + 1)):
         assert render(k, v) == 1, (k, v)
-        assert b"differ" in lib.hrf_last_error()
+        err = lib.hrf_last_error()
+        # V + 1 can exceed N (every Gaussian visible): the count check fires first
+        assert b"differ" in err or (v > n and b"invalid visible count" in err), err
     assert render(K, V) == 0
     torch.cuda.synchronize()
     ref, _, (_, _, pl_ref, rg_ref, vis_ref) = _run_gpu_forward(sc)
