@@ -104,6 +104,7 @@ SIGNATURES = {
     "hrf_grad_norm": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "hrf_scale_grads": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _vp, _vp]),
     "hrf_adan_step": (ctypes.c_int, [_P(HrfAdanTensor), _i32, _P(HrfAdanConfig), _vp, _vp]),
+    "hrf_grad_norm_static": (ctypes.c_int, [_P(_vp), _P(_i64), _i32, _f32, _vp, _vp, _vp]),
     "hrf_ssim_map": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _f32, _vp, _vp]),
     "hrf_ssim_backward": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _f32, _f32, _vp, _vp]),
     "hrf_sparse_adam_update": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

@@ -14,11 +14,22 @@
 // (and the scaled gradient written back), so the separate rescaling pass of
 // clip_grad_norm_ is optional.
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "hrf_internal.h"
 
 namespace hrf {
+
+// Scratch of hrf_grad_norm_static: the per-chunk partial sums of squares,
+// one float per 2048 gradient elements, in a file-scope device array instead
+// of a caller workspace (each GPU the library runs on holds its own copy,
+// 256 KiB, until the process ends).  In host code this name is only a
+// stand-in for the symbol: the device address comes from
+// hipGetSymbolAddress, once per device (static_norm_scratch below).
+constexpr int kStaticNormPartials = 65536;
+static __device__ __align__(256) float scratch[kStaticNormPartials];
+
 namespace {
 
 constexpr int kOptThreads = 256;
@@ -219,6 +230,40 @@ __global__ __launch_bounds__(kOptThreads) void k_scale(GradTable t, const float*
 
 int64_t chunks_of(int64_t numel) { return (numel + kOptChunk - 1) / kOptChunk; }
 
+int64_t total_elems(const int64_t* numels, int nt) {
+  int64_t c = 0;
+  for (int i = 0; i < nt; ++i) c += numels[i];
+  return c;
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (each device holds its own copy of the array at its own address).
+// Host code passes this address, never the array's name, to the kernels.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int static_norm_scratch(float** out) {
+  int dev = 0;
+  HRF_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("grad norm (static scratch): device %d out of range", dev);
+    return HRF_ERR_INVALID;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HRF_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) {
+      set_error("grad norm (static scratch): no device address for the scratch array");
+      return HRF_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return HRF_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Blocks of all tensors, the norm's partial-sum count.
@@ -227,6 +272,10 @@ int64_t total_chunks(const int64_t* numels, int nt) {
   for (int i = 0; i < nt; ++i) c += chunks_of(numels[i]);
   return c;
 }
+
+int launch_grad_norm(const float* const* grads, const int64_t* numels, int num_tensors,
+                     float max_norm, float* total_norm, float* clip_coef, float* partial,
+                     hipStream_t s);
 
 int check_grad_list(const float* const* grads, const int64_t* numels, int nt) {
   if (nt < 0 || (nt > 0 && (!grads || !numels))) {
@@ -332,8 +381,41 @@ int hrf_grad_norm(const float* const* grads, const int64_t* numels, int32_t num_
     set_error("grad norm workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
     return HRF_ERR_WORKSPACE;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  float* partial = static_cast<float*>(ws);
+  return launch_grad_norm(grads, numels, num_tensors, max_norm, total_norm, clip_coef,
+                          static_cast<float*>(ws), static_cast<hipStream_t>(stream));
+}
+
+int hrf_grad_norm_static(const float* const* grads, const int64_t* numels, int32_t num_tensors,
+                         float max_norm, float* total_norm, float* clip_coef, void* stream) {
+  HRF_TRY(check_grad_list(grads, numels, num_tensors));
+  if (!total_norm && !clip_coef) {
+    set_error("grad norm: no output");
+    return HRF_ERR_INVALID;
+  }
+  const int64_t chunks = total_chunks(numels, num_tensors);
+  if (chunks > kStaticNormPartials) {
+    set_error("grad norm (static scratch): %lld gradient elements need %lld partial sums; the "
+              "static scratch holds %d (at most %lld elements); use hrf_grad_norm with a "
+              "workspace",
+              static_cast<long long>(total_elems(numels, num_tensors)),
+              static_cast<long long>(chunks), kStaticNormPartials,
+              static_cast<long long>(kStaticNormPartials) * kOptChunk);
+    return HRF_ERR_WORKSPACE;
+  }
+  float* partial = nullptr;
+  HRF_TRY(static_norm_scratch(&partial));
+  return launch_grad_norm(grads, numels, num_tensors, max_norm, total_norm, clip_coef, partial,
+                          static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace hrf {
+namespace {
+
+int launch_grad_norm(const float* const* grads, const int64_t* numels, int num_tensors,
+                     float max_norm, float* total_norm, float* clip_coef, float* partial,
+                     hipStream_t s) {
   HRF_STAGE("grad_norm", s);
   HRF_TRY(for_tensor_groups<GradTable>(
       num_tensors, numels, [&](GradTable& t, int slot, int i) { t.g[slot] = grads[i]; },
@@ -349,6 +431,11 @@ int hrf_grad_norm(const float* const* grads, const int64_t* numels, int32_t num_
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
+
+}  // namespace
+}  // namespace hrf
+
+extern "C" {
 
 int hrf_scale_grads(float* const* grads, const int64_t* numels, int32_t num_tensors,
                     const float* coef, void* stream) {

@@ -434,6 +434,19 @@ int hrf_grad_norm(const float* const* grads, const int64_t* numels, int32_t num_
                   float max_norm, float* total_norm, float* clip_coef, void* ws,
                   size_t ws_bytes, void* stream);
 
+/* hrf_grad_norm without a workspace: the partial sums live in a static
+ * device array of the library (65536 floats, 256 KiB per GPU, held until the
+ * process ends), so this entry point allocates nothing and calls no
+ * allocating routine.  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight training or
+ * serving loops, harnesses that forbid allocation).  At most 65536 * 2048 =
+ * 134217728 gradient elements in total (HRF_ERR_WORKSPACE beyond).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams or host threads) race and must be ordered by the caller.
+ * Same results as hrf_grad_norm (same kernels, same summation order). */
+int hrf_grad_norm_static(const float* const* grads, const int64_t* numels, int32_t num_tensors,
+                         float max_norm, float* total_norm, float* clip_coef, void* stream);
+
 /* grads *= *coef (device scalar): the rescaling half of clip_grad_norm_. */
 int hrf_scale_grads(float* const* grads, const int64_t* numels, int32_t num_tensors,
                     const float* coef, void* stream);

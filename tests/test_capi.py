@@ -251,3 +251,19 @@ def test_invalid_shapes_rejected_without_gpu(lib):
     fwd = _bind(lib, "hrf_asm_forward")
     st = fwd(0x1000, 101, 100, 100, 515e-9, 3.74e-6, 0.0, 100.0, 0x1000, 0x1000, 1 << 30, None)
     assert st == 1 and "even" in _err(lib)
+
+
+def test_grad_norm_static_rejects_inputs_beyond_its_scratch(lib):
+    """The allocation-free norm holds 65536 partial sums (2048 elements
+    each): larger inputs get HRF_ERR_WORKSPACE on the host, before any HIP
+    call."""
+    f = _bind(lib, "hrf_grad_norm_static")
+    fake = 0x1000
+    n = 2
+    ptrs = (ctypes.c_void_p * n)(fake, fake)
+    numels = (ctypes.c_int64 * n)(65536 * 2048, 1)
+    st = f(ptrs, numels, n, 1.0, fake, fake, None)
+    assert st == 3, _err(lib)
+    assert "static scratch" in _err(lib) and "134217728" in _err(lib)
+    st = f(ptrs, numels, n, 1.0, None, None, None)
+    assert st == 1 and "no output" in _err(lib)
