@@ -1131,3 +1131,182 @@ def test_tile_masked_render_matches_full_render(oracle_mod):
                                       ref["final_T"], ref["n_contrib"], gf, tile_mask=tm)
     for k in full:
         np.testing.assert_array_equal(part[k], full[k])
+
+
+# ------------------------------------ gradient formulas that are not derivatives
+# The reference computes three gradients literally from formulas that are not
+# the derivatives of its forward; mathematics still fixes what each formula
+# is, so each is pinned against an independent float64 computation.
+
+def _rot_glm(q):
+    """The quaternion polynomial in GLM [column][row] layout (as the
+    reference builds its mat3), not normalised."""
+    r, x, y, z = q
+    return np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - r * z), 2 * (x * z + r * y)],
+                     [2 * (x * y + r * z), 1 - 2 * (x * x + z * z), 2 * (y * z - r * x)],
+                     [2 * (x * z - r * y), 2 * (y * z + r * x), 1 - 2 * (x * x + y * y)]])
+
+
+def _sigma_glm(q, s):
+    """Sigma in the oracle's output layout: out[c][r] = sum_k s_k^2 R[c][k] R[r][k]
+    with R = _rot_glm(q / |q|)."""
+    R = _rot_glm(q / np.linalg.norm(q))
+    return np.einsum("k,ck,rk->cr", s * s, R, R)
+
+
+def _cov3d_bwd_case(seed=40, n=24):
+    rng = np.random.default_rng(seed)
+    q = rng.normal(size=(n, 4))
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    s = np.exp(rng.normal(-1, 0.3, size=(n, 3)))
+    G = rng.normal(size=(n, 3, 3))
+    return q, s, G
+
+
+def test_sigma_restatement_matches_oracle(oracle_mod):
+    q, s, _ = _cov3d_bwd_case()
+    got = oracle_mod.cov3d_forward(q.astype(np.float32), s.astype(np.float32))
+    for i in range(len(q)):
+        ref = _sigma_glm(q[i], s[i])
+        np.testing.assert_allclose(got[i], ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+
+
+def test_quaternion_gradient_is_derivative_of_hadamard_form(oracle_mod):
+    """backward.cu:161-187 sums G .* (S dR/dq_m)^T-products elementwise
+    (Hadamard) without the chain through the normalisation.  With S diagonal
+    that sum is exactly d/dq_m of h(q) = sum_ij G_ij s_i s_j R[j][i] R[i][j]
+    (R the un-normalised polynomial in GLM layout; backward.cu:31-73 are its
+    partial derivatives): checked by float64 central differences of h at
+    unit quaternions."""
+    q, s, G = _cov3d_bwd_case()
+    gq, _ = oracle_mod.cov3d_backward(G.astype(np.float32), q.astype(np.float32),
+                                      s.astype(np.float32))
+
+    def h(qq, Gi, si):
+        R = _rot_glm(qq)
+        return float(np.sum(Gi * np.outer(si, si) * R.T * R))
+
+    e = 1e-6
+    for i in range(len(q)):
+        num = np.array([(h(q[i] + e * np.eye(4)[m], G[i], s[i]) -
+                         h(q[i] - e * np.eye(4)[m], G[i], s[i])) / (2 * e) for m in range(4)])
+        np.testing.assert_allclose(gq[i], num, rtol=2e-5, atol=2e-5 * np.abs(num).max())
+
+
+def test_scale_gradient_is_derivative_at_conjugate_rotation(oracle_mod):
+    """backward.cu:139-142 forms grad_s = (2 R^T G R)_kk s_k with R in GLM
+    layout; that is the true derivative of <G, Sigma(q_bar, s)> over s at
+    the conjugate quaternion q_bar = (r, -x, -y, -z), not at q (float64
+    central differences; at q itself it is off by O(1) for a general
+    rotation, so a transposed R fails)."""
+    q, s, G = _cov3d_bwd_case(seed=41)
+    _, gs = oracle_mod.cov3d_backward(G.astype(np.float32), q.astype(np.float32),
+                                      s.astype(np.float32))
+    e = 1e-6
+    worst_at_q = 0.0
+    for i in range(len(q)):
+        qb = q[i] * np.array([1.0, -1.0, -1.0, -1.0])
+
+        def f(ss, qq):
+            return float(np.sum(G[i] * _sigma_glm(qq, ss)))
+
+        num = np.array([(f(s[i] + e * np.eye(3)[k], qb) - f(s[i] - e * np.eye(3)[k], qb)) /
+                        (2 * e) for k in range(3)])
+        np.testing.assert_allclose(gs[i], num, rtol=2e-5, atol=2e-5 * np.abs(num).max())
+        at_q = np.array([(f(s[i] + e * np.eye(3)[k], q[i]) - f(s[i] - e * np.eye(3)[k], q[i])) /
+                         (2 * e) for k in range(3)])
+        worst_at_q = max(worst_at_q, float(np.abs(at_q - gs[i]).max() / np.abs(at_q).max()))
+    assert worst_at_q > 0.1
+
+
+def _conic_case(oracle_mod, on_axes):
+    """Big faint Gaussians (every alpha in [1/255, 0.99)), so dL/dconic is a
+    true derivative; on_axes puts every mean on x = 0 or y = 0, where the
+    identity-rotation covariance projects to a diagonal cov2D."""
+    g, cam = _fd_scene()
+    if on_axes:
+        g.cam_means[0::2, 0] = 0.0
+        g.cam_means[1::2, 1] = 0.0
+    else:
+        # rotated about the view axis and anisotropic: the conic's
+        # off-diagonal entry is comparable to its diagonal
+        th = np.linspace(0.3, 2.8, g.n)
+        g.quats[:] = np.stack([np.cos(th / 2), 0 * th, 0 * th, np.sin(th / 2)], 1)
+        g.scales[:] = np.array([1.6, 0.8, 1.0], np.float32)
+    # every alpha of every Gaussian at every pixel in [1/255, 0.99): the
+    # backward's skips and clamp never apply, so dL/dconic is a derivative
+    pr = oracle_mod.project(g, cam)
+    ys, xs = np.mgrid[0:cam.height, 0:cam.width]
+    for i in range(g.n):
+        A = np.linalg.inv(pr["cov2d"][i].astype(np.float64).reshape(2, 2))
+        d = np.stack([pr["means2d"][i, 0] - xs, pr["means2d"][i, 1] - ys], -1)
+        q = np.einsum("...i,ij,...j->...", d, A, d)
+        a = g.opac[i] * np.exp(-0.5 * q) * g.pprobs[i].min()
+        assert a.min() > 1.2 / 255 and a.max() < 0.99
+    rng = np.random.default_rng(6)
+    shape = (g.P, g.C, cam.height, cam.width)
+    gf = rng.normal(size=shape) + 1j * rng.normal(size=shape)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    rb = oracle_mod.render_backward(g, cam, ref["proj"]["means2d"], ref["proj"]["cov2d"],
+                                    ref["point_list"], ref["ranges"], ref["final_T"],
+                                    ref["n_contrib"], gf.astype(np.complex64))
+    return g, cam, gf, ref, rb
+
+
+def _dL_dconic(oracle_mod, g, cam, gf, ref):
+    """Central differences of the compositor's loss with respect to each
+    Gaussian's conic entries (a = conic_xx, b = one off-diagonal entry,
+    c = conic_yy), the covariance passed as the inverse of the perturbed
+    conic (the perturbation keeps it symmetric, so d/db is half the
+    symmetric difference)."""
+    m = ref["proj"]["means2d"]
+    cov = ref["proj"]["cov2d"].astype(np.float64).reshape(-1, 2, 2)
+
+    def loss(cv):
+        f, _, _ = oracle_mod.render_forward(g, cam, m, cv.reshape(-1, 4).astype(np.float32),
+                                            ref["point_list"], ref["ranges"])
+        return float(np.sum(f.real.astype(np.float64) * gf.real + f.imag * gf.imag))
+
+    out = np.zeros((g.n, 3))
+    for i in range(g.n):
+        A = np.linalg.inv(cov[i])
+        h = 2e-3 * np.abs(A).max()
+        for k, E in enumerate((np.array([[1, 0], [0, 0]]), np.array([[0, 1], [1, 0]]),
+                               np.array([[0, 0], [0, 1]]))):
+            cp, cm = cov.copy(), cov.copy()
+            cp[i] = np.linalg.inv(A + h * E)
+            cm[i] = np.linalg.inv(A - h * E)
+            out[i, k] = (loss(cp) - loss(cm)) / (2 * h) * (0.5 if k == 1 else 1.0)
+    return out, cov
+
+
+def test_cov2d_gradient_map_diagonal_closed_form(oracle_mod):
+    """backward_splat.cu:279-296 maps dL/dconic to cov2D with a non-exact
+    formula; for a diagonal cov2D it reduces to xx = dL/da / c_xx^2,
+    xy = -dL/db / (c_xx c_yy), yy = dL/dc / c_yy^2, with dL/dconic taken as
+    true derivatives (finite differences of the compositor)."""
+    g, cam, gf, ref, rb = _conic_case(oracle_mod, on_axes=True)
+    dc, cov = _dL_dconic(oracle_mod, g, cam, gf, ref)
+    assert np.abs(cov[:, 0, 1]).max() == 0 and np.abs(cov[:, 1, 0]).max() == 0
+    cxx, cyy = cov[:, 0, 0], cov[:, 1, 1]
+    exp = np.stack([dc[:, 0] / cxx ** 2, -dc[:, 1] / (cxx * cyy), -dc[:, 1] / (cxx * cyy),
+                    dc[:, 2] / cyy ** 2], 1)
+    assert rel_l2(rb["cov2d"], exp) < 3e-3, rel_l2(rb["cov2d"], exp)
+
+
+def test_cov2d_gradient_map_in_conic_form(oracle_mod):
+    """For a general cov2D the reference's map, written in the conic entries
+    (a, b, c) = inverse(cov2D) instead of the covariance and 1/det, is
+    xx = da a^2 + dc b^2, xy = da a b - db (a c - b^2) + dc b c,
+    yy = da b^2 + dc c^2, applied to dL/dconic from finite differences of
+    the compositor."""
+    g, cam, gf, ref, rb = _conic_case(oracle_mod, on_axes=False)
+    dc, cov = _dL_dconic(oracle_mod, g, cam, gf, ref)
+    A = np.linalg.inv(cov)
+    assert np.all(np.abs(A[:, 0, 1]) > 0.2 * np.minimum(A[:, 0, 0], A[:, 1, 1]))
+    A = np.linalg.inv(cov)
+    a, b, c = A[:, 0, 0], A[:, 0, 1], A[:, 1, 1]
+    da, db, dcc = dc[:, 0], dc[:, 1], dc[:, 2]
+    xy = da * a * b - db * (a * c - b * b) + dcc * b * c
+    exp = np.stack([da * a * a + dcc * b * b, xy, xy, da * b * b + dcc * c * c], 1)
+    assert rel_l2(rb["cov2d"], exp) < 3e-3, rel_l2(rb["cov2d"], exp)
