@@ -159,12 +159,65 @@ __device__ __forceinline__ float invisible_threshold(float ow) {
   return fmaxf(thr, 0.0f) * 1.001f + 0.01f;
 }
 
+// A staged conic whose exponent cannot round to a positive value at any
+// pixel: positive definite with |correlation| below 0.99995.  The exponent
+// dx (A dx + B dy) + C dy^2 is then a sum whose rounding error (a few ulps
+// of its terms) stays below its true, non-positive value, so the reference's
+// "power > 0: skip" test can never fire and the member loop omits it.
+__device__ __forceinline__ bool conic_safe(float a, float b, float b2, float c) {
+  return a > 0.0f && c > 0.0f && a * c - b * b2 > 1e-4f * (a * c);
+}
+
+// Forward staged record: full quads only (a 12-byte LDS read occupies the
+// LDS longer than a 16-byte one), and no list position (the loop tracks
+// the batch-local index instead):
+//   quad 0: (mx, my, kc*i00, kc*(i01 + i10))
+//   quad 1: (kc*i11, log2(o w), re0, im0)
+//   quad 2: (re1, im1, re2, im2)            (C >= 2)
+// with kc = -log2(e)/2.
+__host__ __device__ constexpr int fwd_quads(int C) { return C == 1 ? 2 : 3; }
+
+// Forward member evaluation.  Exponent in base 2 with log2(o w) folded in:
+// pw = dx (A dx + B dy) + (C dy) dy + log2(o w), so alpha = min(0.99,
+// exp2(pw)) needs no multiply by the opacity; at the mean (dx = dy = 0) pw
+// is log2(o w) exactly.  A lane is done exactly when T < 1e-4 (T changes
+// only on composited members, and a lane stops at the member that takes T
+// below 1e-4; lanes outside the image start at T = 0), so no separate flag
+// is carried.  Branch-free: lanes that are done (or, in the exact variant,
+// where the reference's power > 0 test skips the member) take alpha = 0,
+// which leaves T and the field exactly unchanged.  `lastj` becomes the
+// member's batch index j (a scalar) where the lane composites it; `real`
+// (scalar) is false for padding members.
+template <int C, bool kExact>
+__device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
+                                           float pxf, float pyf, float& T,
+                                           float (&acc)[2 * C], int& lastj, int j, bool real) {
+  const float dx = a.x - pxf, dy = a.y - pyf;
+  const float t = fmaf(a.z, dx, a.w * dy);
+  const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
+  const bool live = !(T < kTermT);
+  // NaN passes the power test (alpha 0.99), as in the reference; only
+  // batches holding a conic that is not safe evaluate the test.
+  const bool ok = kExact ? (live && !(pw > b.y)) : live;
+  const float alpha = ok ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
+  const float sT = alpha * T;
+  const float amp[6] = {b.z, b.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    acc[2 * k] = fmaf(sT, amp[2 * k], acc[2 * k]);
+    acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
+  }
+  T = T - sT;  // T (1 - alpha), reusing alpha T
+  lastj = (ok && (!kExact || real)) ? j : lastj;
+}
+
 template <int C>
-__global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
-  constexpr int NQ = rec_quads(C);
+__global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderParams p) {
+  constexpr int NQ = fwd_quads(C);
   constexpr int RS = rec_stride(C);
   constexpr int kUnroll = 8;
   __shared__ float4 s_rec[kBlock * NQ];
+  __shared__ int s_pos[kBlock];  // list position + 1 of each staged member
   __shared__ int s_wt[kBlock / 64];
   __shared__ int s_kcull;  // 1 + the largest list position culled as invisible
 
@@ -180,12 +233,12 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     p.ranges_out[2 * tile + threadIdx.x] = p.ranges[2 * tile + threadIdx.x];
   const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
 
-  float T = 1.0f;
+  // Lanes outside the image start done (T = 0 < 1e-4) and write nothing.
+  float T = inside ? 1.0f : 0.0f;
   float acc[2 * C];
 #pragma unroll
   for (int i = 0; i < 2 * C; ++i) acc[i] = 0.0f;
   int last = 0;
-  bool done = !inside;
   int listed = 0;  // plane members of the batches composited so far
   int2* const sub_out =
       p.sub_out ? p.sub_out + static_cast<int64_t>(plane) * p.num_pairs + r0 : nullptr;
@@ -193,11 +246,12 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
   if (threadIdx.x == 0) s_kcull = 0;
   for (int base = 0; base < n; base += kBlock) {
-    if (__syncthreads_and(done)) break;
+    if (__syncthreads_and(T < kTermT)) break;
     const int k = base + static_cast<int>(threadIdx.x);
     bool mem = false;
     int g = 0;
-    float4 rq[2];  // geometry quads; the amplitude quads load at the LDS write
+    // geometry quads; the amplitude quads load at the LDS write
+    float4 rq[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
     float w = 0.0f;
     const float4* src = nullptr;
     if (k < n) {
@@ -219,66 +273,69 @@ __global__ __launch_bounds__(kBlock) void k_render_fwd(RenderParams p) {
     }
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
+    // Any staged conic that is not safe: this batch runs the exact loop.
+    const bool exact = __syncthreads_or(mem && !conic_safe(rq[0].z, rq[0].w, rq[1].x, rq[1].y));
     if (mem) {
       if (sub_out) sub_out[listed + pos] = make_int2(g, k);
-      // quad 0: (mx, my, kc*i00, kc*i01); quad 1: (kc*i10, kc*i11, o*w, -),
-      // kc = -log2(e)/2: the exponent of G = exp2(.) is then a quadratic
-      // form with the -1/2 and the change of base folded in.
+      const float4 am = src[2];  // (re0, im0, re1, im1)
       s_rec[pos * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
-                                    kBwdConicScale * rq[0].w);
-      s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].x, kBwdConicScale * rq[1].y,
-                                        rq[1].z * w, __int_as_float(k + 1));
-#pragma unroll
-      for (int q = 2; q < NQ; ++q) s_rec[pos * NQ + q] = src[q];
+                                    kBwdConicScale * (rq[0].w + rq[1].x));
+      s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].y,
+                                        __builtin_amdgcn_logf(rq[1].z * w), am.x, am.y);
+      if (NQ > 2) {
+        const float4 am2 = rec_quads(C) > 3 ? src[3] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_rec[pos * NQ + (NQ > 2 ? 2 : 0)] = make_float4(am.z, am.w, am2.x, am2.y);
+      }
+      s_pos[pos] = k + 1;
     }
     // Pad the staged batch to a multiple of kUnroll with members no pixel
-    // can use: a positive-definite exponent 1e12 (power > 0), so they never
-    // contribute or count.
+    // can use: log2(o w) = -inf (alpha 0, T unchanged).
     listed += cnt;
     const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
     if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
       const int q0 = static_cast<int>(threadIdx.x) * NQ;
-      s_rec[q0] = make_float4(1e6f, 1e6f, 1.0f, 0.0f);
-      s_rec[q0 + 1] = make_float4(0.0f, 1.0f, 0.0f, __int_as_float(0));
+      s_rec[q0] = make_float4(1e6f, 1e6f, 0.0f, 0.0f);
+      s_rec[q0 + 1] = make_float4(0.0f, -__builtin_inff(), 0.0f, 0.0f);
 #pragma unroll
       for (int q = 2; q < NQ; ++q) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     __syncthreads();
-    // Branch-free per member: lanes that are done or outside the Gaussian's
-    // support (power > 0) take alpha = 0, which leaves T and the field
-    // exactly unchanged; a wave leaves the batch once all its lanes are done.
-    for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
-      if (__all(done)) break;
+    // Branch-free per member; a wave leaves the batch once all its lanes
+    // are done.
+    const bool live0 = !(T < kTermT);
+    int lastj = -1;
+    if (!exact) {
+      for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
+        if (__all(T < kTermT)) break;
 #pragma unroll
-      for (int jj = 0; jj < kUnroll; ++jj) {
-        const int j = j0 + jj;
-        const float4 a = s_rec[j * NQ];
-        const float4 b = s_rec[j * NQ + 1];
-        const float dx = a.x - pxf, dy = a.y - pyf;
-        const float pw = fmaf(dx, fmaf(a.z, dx, b.x * dy), dy * fmaf(a.w, dx, b.y * dy));
-        const float G = __builtin_amdgcn_exp2f(pw);
-        const bool ok = !done && !(pw > 0.0f);  // NaN passes, as the reference
-        const float alpha = ok ? fminf(kMaxAlpha, b.z * G) : 0.0f;
-        const float sT = alpha * T;
-        const float4 c0 = s_rec[j * NQ + 2];
-        const float4 c1 = s_rec[j * NQ + (NQ > 3 ? 3 : 2)];
-        const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-          acc[2 * c] = fmaf(sT, amp[2 * c], acc[2 * c]);
-          acc[2 * c + 1] = fmaf(sT, amp[2 * c + 1], acc[2 * c + 1]);
+        for (int jj = 0; jj < kUnroll; ++jj) {
+          const int j = j0 + jj;
+          fwd_member<C, false>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf,
+                               pyf, T, acc, lastj, j, j < cnt);
         }
-        T = T - sT;  // T (1 - alpha), reusing alpha T
-        last = ok ? __float_as_int(b.w) : last;
-        done = done || (ok && T < kTermT);
+      }
+      // A lane still running composited every member of the batch (no
+      // power test could fail): the batch's last member is its last
+      // contributor.  One that terminated here did so at member lastj.
+      if (!(T < kTermT) && cnt > 0) lastj = cnt - 1;
+    } else {
+      for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
+        if (__all(T < kTermT)) break;
+#pragma unroll
+        for (int jj = 0; jj < kUnroll; ++jj) {
+          const int j = j0 + jj;
+          fwd_member<C, true>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf,
+                              pyf, T, acc, lastj, j, j < cnt);
+        }
       }
     }
+    if (live0 && lastj >= 0) last = s_pos[lastj];
   }
 
   if (sub_out && threadIdx.x == 0) p.sub_cnt_out[tile * p.P + plane] = listed;
   __syncthreads();
   // A pixel that never terminated composited every member, culled ones too.
-  if (!done) last = max(last, s_kcull);
+  if (!(T < kTermT)) last = max(last, s_kcull);
   if (inside) {
     const int64_t HW = static_cast<int64_t>(p.W) * p.H;
     const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
@@ -529,8 +586,10 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         last_alpha = ok ? alpha : last_alpha;
         const float Q = ok ? Gv * ((S - R) * T) : 0.0f;
         const float Qdx = Q * dx, Qdy = Q * dy;
-        buf[m * NV + 0] = Q * u;
-        buf[m * NV + 1] = Q * v;
+        // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v: the
+        // flush forms them from these two sums and the member's conic
+        buf[m * NV + 0] = Qdx;
+        buf[m * NV + 1] = Qdy;
         buf[m * NV + 2] = Qdx * dx;
         buf[m * NV + 3] = Qdx * dy;
         buf[m * NV + 4] = Qdy * dy;
@@ -554,14 +613,21 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     }
     __syncthreads();
     for (int e = threadIdx.x; e < cnt * NV; e += kBlock) {
-      const float val = s_acc[e];
-      if (val == 0.0f) continue;
       const int j = e / NV, i = e - j * NV;
+      float val = s_acc[e];
+      if (i < 2) {
+        // sum Q u = kc cxx sum Q dx + kc cxy sum Q dy; sum Q v = kc cxy
+        // sum Q dx + kc czz sum Q dy (the staged conic is scaled by kc)
+        const float4 a = s_rec[j * NQ];
+        const float sx = s_acc[j * NV], sy = s_acc[j * NV + 1];
+        val = i == 0 ? fmaf(a.z, sx, a.w * sy) : fmaf(a.w, sx, s_rec[j * NQ + 1].x * sy);
+      }
+      if (val == 0.0f) continue;
       const int gg = s_g[j];
       const float ow = s_rec[j * NQ + 1].y;
       int slot;
       float scale;
-      if (i == 0) {  // partials carry u = kc*(cxx dx + cxy dy)
+      if (i == 0) {  // sum Q u, u = kc*(cxx dx + cxy dy)
         slot = 0;
         scale = -half_w * ow / kBwdConicScale;
       } else if (i == 1) {

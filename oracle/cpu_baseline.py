@@ -214,6 +214,26 @@ def run_frame(sc, backward: bool = True, cap_s: float = 600.0):
     return res
 
 
+def time_propagations(jobs, S, aperture, pitch=3.74e-6, seed=0):
+    """Every pure-torch propagation of ``jobs`` (a list of (field (H, W)
+    complex64, wavelength, distance)) forward, then its backward by autograd
+    with a seeded CN(0,1) upstream gradient, one after another (not
+    sampled).  Returns (forward ms, backward ms) summed over the jobs."""
+    gen = torch.Generator().manual_seed(seed)
+    fwd = bwd = 0.0
+    for field, wl, d in jobs:
+        f = field.detach().clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        o = asm_torch(f, wl, pitch, d, S, aperture)
+        t1 = time.perf_counter()
+        g = torch.complex(torch.randn(o.shape, generator=gen), torch.randn(o.shape, generator=gen))
+        (o.real * g.real + o.imag * g.imag).sum().backward()
+        t2 = time.perf_counter()
+        fwd += (t1 - t0) * 1e3
+        bwd += (t2 - t1) * 1e3
+    return fwd, bwd
+
+
 def time_frame(sc, budget_s: float = 12.0, seed: int = 0):
     """ESTIMATE of the CPU path's time for one frame of scene ``sc`` from a
     bounded sample (for frames far beyond the did-not-finish cap): random

@@ -1,0 +1,46 @@
+"""Calibration kernels of known VALU work (tests/hip/wave_reduce_test.hip):
+8192 waves, each issuing exactly 8 * iters v_fma_f32 (k_calib_fma) or
+8 * iters v_exp_f32 + 8 * iters v_mul_f32 (k_calib_exp).  Run under
+rocprofv3 --pmc, their SQ_INSTS_VALU / SQ_INSTS_VALU_TRANS_F32 /
+SQ_ACTIVE_INST_VALU readings against these known counts calibrate the
+counters the render kernels' VALU figures use; the printed issue rates
+(wave-instructions per second, timed with hipEvents) give the measured
+VALU and transcendental throughput of the card."""
+import ctypes
+import os
+
+import pytest
+
+from conftest import REPO
+
+pytestmark = pytest.mark.gpu
+
+LIB = os.path.join(REPO, "tests", "hip", "libwave_test.so")
+BLOCKS = 2048  # x 4 waves = 8192 waves: 8 per SIMD on 256 CUs
+ITERS = 4096
+
+
+@pytest.mark.parametrize("kind", ["fma", "exp"])
+def test_calibration_kernel_rates(hrf, kind):
+    import torch
+
+    lib = ctypes.CDLL(LIB)
+    f = getattr(lib, f"calib_valu_{kind}")
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    out = torch.empty(BLOCKS * 256, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    assert f(out.data_ptr(), BLOCKS, 16, 0.5, stream) == 0  # warm-up
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    assert f(out.data_ptr(), BLOCKS, ITERS, 0.5, stream) == 0
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    waves = BLOCKS * 4
+    per_wave = 8 * ITERS * (1 if kind == "fma" else 2)
+    rate = waves * per_wave / (ms * 1e-3)
+    print(f"calib {kind}: {waves} waves x {per_wave} VALU instructions in {ms:.4f} ms = "
+          f"{rate / 1e9:.1f} G wave-instructions/s", flush=True)
+    assert bool(torch.isfinite(out).all())
+    assert rate > 1e11

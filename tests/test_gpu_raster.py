@@ -637,3 +637,27 @@ def test_render_rejects_counts_other_than_prepared(hrf):
     ref, _, (_, _, pl_ref, rg_ref, vis_ref) = _run_gpu_forward(sc)
     assert torch.equal(pl[:K], pl_ref) and torch.equal(rg, rg_ref)
     assert torch.equal(vis[:V], vis_ref)
+
+
+def test_forward_parity_dense_terminations(hrf, oracle_mod):
+    """Opaque, large Gaussians (the "dense" plane-list scene): about 40% of
+    the pixels stop at T < 1e-4, many in the middle of a 256-entry batch or
+    of an 8-member group of the member loop.  The field, final_T and
+    n_contrib of terminated pixels (the list position of the member that
+    took T below 1e-4) match the oracle."""
+    sc = _plane_list_scene("dense")
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    fT_h, nc_h = fT.cpu().numpy(), nc.cpu().numpy()
+    term = ref["final_T"] < 1e-4
+    print(f"dense: K={ref['K']} terminated {term.mean():.2f}", flush=True)
+    assert term.mean() > 0.2
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+    assert rel_l2(fT_h, ref["final_T"]) < TOL
+    mism = nc_h != ref["n_contrib"]
+    assert mism.mean() < 1e-3, (mism.mean(), np.argwhere(mism)[:5])
+    # where the two sides terminate at the same member, n_contrib is equal
+    both = term & (fT_h < 1e-4)
+    assert np.mean(nc_h[both] != ref["n_contrib"][both]) < 1e-3
