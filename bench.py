@@ -595,9 +595,13 @@ def main():
     if valu:
         valu["source"] = f"profiles/valu_{spec.name}.txt"
 
-    pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
-    opt_step = measure_optimizer(spec, dev, args.no_cpu_baseline)
-    recon = measure_reconstruction(spec, dev, args.no_cpu_baseline)
+    # The training-loop rows around the frame are measured on the headline
+    # scene only (their own workloads, reported beside the frame).
+    pre = opt_step = recon = None
+    if spec.name == "headline":
+        pre = measure_preprocess(spec, dev, args.no_cpu_baseline)
+        opt_step = measure_optimizer(spec, dev, args.no_cpu_baseline)
+        recon = measure_reconstruction(spec, dev, args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
