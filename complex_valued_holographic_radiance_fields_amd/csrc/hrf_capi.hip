@@ -626,8 +626,9 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
     bool in_b = false;
     {
       HRF_STAGE("tile_sort", s);
+      // The sorted tile ids are only needed to form the ranges from them.
       HRF_TRY(radix_sort_pairs(b.keys_a, vals_a, b.keys_b, vals_b, num_pairs, end_bit, b.radix,
-                               &in_b, s));
+                               &in_b, s, nullptr, false, !diff_ranges));
     }
     const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
     // The sorted values must end in point_list whatever the pass count did

@@ -230,16 +230,18 @@ size_t scan_scratch_elems(int64_t n);
 // passes do nothing on the device while *run_flag == 0 (callers use an even
 // pass count then, so the data stays in (ka,va) either way).
 size_t radix_scratch_elems(int64_t n);
-// With index_values, the values are taken to be 0..n-1 (va is only used as
-// a buffer).
+// ceil(end_bit/8) passes, digit widths differing by at most one (the wider
+// ones last).  With index_values, the values are taken to be 0..n-1 (va is
+// only used as a buffer).  keys_needed == false: the last pass writes only
+// the values (the sorted keys are then left nowhere).
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
                      hipStream_t s, const uint32_t* run_flag = nullptr,
-                     bool index_values = false);
+                     bool index_values = false, bool keys_needed = true);
 int radix_passes(int end_bit);
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
-// (the other bits ride along unsorted), in ceil(nbits/8) passes of equal
-// digit width; same scratch and ping-pong convention as radix_sort_pairs.
+// (the other bits ride along unsorted), in ceil(nbits/8) passes with the
+// digit widths of radix_sort_pairs; same scratch and ping-pong convention.
 // final_out != nullptr (needs n > 1, nbits > 0): the last pass writes
 // word & final_mask there instead of into the ping-pong buffers.
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,

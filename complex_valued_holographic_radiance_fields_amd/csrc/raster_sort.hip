@@ -22,6 +22,10 @@ constexpr int kRadixWaves = kRadixThreads / 64;
 constexpr int kRadixItems = 8;  // per thread
 constexpr int kRadixTile = kRadixThreads * kRadixItems;
 constexpr int kRadixBins = 256;
+// Partitioning of the radix passes: one tile per block up to
+// kRadixTargetParts tiles, beyond that up to kRadixMaxSub tiles per block.
+constexpr int kRadixTargetParts = 4096;
+constexpr int kRadixMaxSub = 64;
 
 constexpr int kDiffThreads = 1024;
 constexpr int kDiffItems = 4;    // Gaussians per thread per step, loads issued together
@@ -55,177 +59,237 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
 
 // ----------------------------------------------------------- radix sort --
 
-// Digit histogram of each block's kRadixTile keys: digit = (key >> shift) &
-// mask with at most 2^RB values; hist is digit-major ([digit][block]): a
-// scan along each digit's row plus the totals of the lower digits give
-// every (digit, block) output offset.
+// The keys are cut into partitions of `sub` consecutive kRadixTile tiles
+// (sub grows with n so that the partition count stays near
+// kRadixTargetParts): the histogram spine is [digit][partition], small
+// enough that its scan is a few coalesced block scans, and the scatter
+// block of a partition walks its tiles in order carrying each digit's
+// running output offset.
+
+// Digit histogram of each partition: digit = (key >> shift) & mask with at
+// most 2^RB values; one LDS histogram per wave (fewer same-address atomic
+// collisions between the waves), summed at the end.  hist is digit-major
+// ([digit][partition]): a scan along each digit's row plus the totals of
+// the lower digits give every (digit, partition) output offset.
 template <int RB>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
                                                               uint32_t mask,
                                                               uint32_t* __restrict__ hist,
-                                                              int nblocks,
+                                                              int nparts, int sub,
                                                               const uint32_t* __restrict__ run_flag) {
   constexpr int kBins = 1 << RB;
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_hist[kBins];
-  if (threadIdx.x < kBins) s_hist[threadIdx.x] = 0;
+  __shared__ uint32_t s_hist[kRadixWaves][kBins];
+  for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
+    s_hist[e / kBins][e % kBins] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kRadixTile;
+  const int wave = threadIdx.x >> 6;
+  const int64_t pbase = static_cast<int64_t>(blockIdx.x) * sub * kRadixTile;
+  for (int t = 0; t < sub; ++t) {
+    const int64_t base = pbase + static_cast<int64_t>(t) * kRadixTile;
+    if (base >= n) break;
+    uint32_t k[kRadixItems];
 #pragma unroll
-  for (int i = 0; i < kRadixItems; ++i) {
-    const int64_t idx = base + i * kRadixThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&s_hist[(keys[idx] >> shift) & mask], 1u);
+    for (int i = 0; i < kRadixItems; ++i) {
+      const int64_t idx = base + i * kRadixThreads + threadIdx.x;
+      k[i] = idx < n ? keys[idx] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kRadixItems; ++i) {
+      const int64_t idx = base + i * kRadixThreads + threadIdx.x;
+      if (idx < n) atomicAdd(&s_hist[wave][(k[i] >> shift) & mask], 1u);
+    }
   }
   __syncthreads();
-  if (threadIdx.x < kBins)
-    hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = s_hist[threadIdx.x];
+  for (int d = threadIdx.x; d < kBins; d += kRadixThreads) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int w = 0; w < kRadixWaves; ++w) c += s_hist[w][d];
+    hist[static_cast<int64_t>(d) * nparts + blockIdx.x] = c;
+  }
 }
 
-// Per digit (one block each): exclusive scan of the digit's per-block
-// counts across the blocks, in place, and the digit's total.  The scatter
-// adds the totals of the lower digits itself.
+// Per digit (one block each): exclusive scan of the digit's per-partition
+// counts across the partitions, in place, and the digit's total.  The row
+// is scanned in chunks of kRowScanItems * kRowScanThreads (each thread
+// kRowScanItems consecutive counts) with a running carry.  The scatter adds
+// the totals of the lower digits itself.
 constexpr int kRowScanThreads = 1024;
+constexpr int kRowScanItems = 4;
 __global__ __launch_bounds__(kRowScanThreads) void k_radix_rowscan(
-    uint32_t* __restrict__ hist, int nblocks, uint32_t* __restrict__ totals,
+    uint32_t* __restrict__ hist, int nparts, uint32_t* __restrict__ totals,
     const uint32_t* __restrict__ run_flag) {
   if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_wave[kRowScanThreads / 64];
-  uint32_t* row = hist + static_cast<int64_t>(blockIdx.x) * nblocks;
-  const int per = (nblocks + kRowScanThreads - 1) / kRowScanThreads;
-  const int b0 = threadIdx.x * per;
-  const int b1 = b0 + per < nblocks ? b0 + per : nblocks;
-  uint32_t local = 0;
-  for (int b = b0; b < b1; ++b) local += row[b];
-  uint32_t total;
-  uint32_t run = block_exclusive_scan(local, &total, s_wave);
-  for (int b = b0; b < b1; ++b) {
-    const uint32_t c = row[b];
-    row[b] = run;
-    run += c;
+  uint32_t* row = hist + static_cast<int64_t>(blockIdx.x) * nparts;
+  uint32_t carry = 0;
+  for (int c0 = 0; c0 < nparts; c0 += kRowScanItems * kRowScanThreads) {
+    const int b = c0 + kRowScanItems * static_cast<int>(threadIdx.x);
+    uint32_t v[kRowScanItems];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kRowScanItems; ++j) {
+      v[j] = b + j < nparts ? row[b + j] : 0u;
+      sum += v[j];
+    }
+    uint32_t total;
+    uint32_t run = carry + block_exclusive_scan(sum, &total, s_wave);
+#pragma unroll
+    for (int j = 0; j < kRowScanItems; ++j) {
+      if (b + j < nparts) row[b + j] = run;
+      run += v[j];
+    }
+    carry += total;
+    __syncthreads();  // s_wave is rewritten by the next chunk's scan
   }
-  if (threadIdx.x == 0) totals[blockIdx.x] = total;
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
-// Stable scatter.  Wave w owns the contiguous sub-range
-// [base + w*512, base + (w+1)*512) processed as 8 iterations of 64 keys;
-// the rank of a key among equal digits before it is found with a ballot
-// match (RB ballots) plus per-wave LDS digit counters.  The block's keys are
-// then reordered by digit in LDS (stable: digit, wave, rank), and written
-// out from there in order: consecutive threads store consecutive elements
-// of each digit's output run, so the global stores coalesce instead of
-// spreading every wave-wide store over up to 2^RB runs.
+// Stable scatter of one partition, tile by tile.  In a tile, wave w owns
+// the contiguous sub-range [base + w*512, base + (w+1)*512) processed as 8
+// iterations of 64 keys; the rank of a key among equal digits before it is
+// found with a ballot match (RB ballots) plus per-wave LDS digit counters.
+// The tile's keys are then reordered by digit in LDS (stable: digit, wave,
+// rank), and written out from there in order: consecutive threads store
+// consecutive elements of each digit's output run, so the global stores
+// coalesce instead of spreading every wave-wide store over up to 2^RB runs.
+// Thread d < 2^RB holds digit d's next output position in the partition
+// (`run`), advanced by the digit's count after each tile.  kout == nullptr
+// with VALS: only the values are written (the caller needs no sorted keys).
 template <int RB, bool VALS>
 __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
     uint32_t mask, const uint32_t* __restrict__ hist_scan,
-    const uint32_t* __restrict__ digit_totals, int nblocks,
+    const uint32_t* __restrict__ digit_totals, int nparts, int sub,
     const uint32_t* __restrict__ run_flag, uint32_t out_mask) {
   constexpr int kBins = 1 << RB;
+  static_assert(kBins <= kRadixThreads, "one thread per digit");
   if (run_flag && *run_flag == 0u) return;
   __shared__ uint32_t s_cnt[kRadixWaves][kBins];
-  __shared__ uint32_t s_delta[kBins];  // global offset of the digit minus its local offset
+  __shared__ uint32_t s_delta[kBins];  // output offset of the digit minus its local offset
   __shared__ uint32_t s_wsum[kRadixWaves];
-  __shared__ uint32_t s_gsum[kRadixWaves];
   __shared__ uint32_t s_key[kRadixTile];
   __shared__ uint32_t s_val[VALS ? kRadixTile : 1];
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
-    s_cnt[e / kBins][e % kBins] = 0;
-  __syncthreads();
+  const bool write_keys = !VALS || kout != nullptr;
 
-  const int64_t bbase = static_cast<int64_t>(blockIdx.x) * kRadixTile;
-  const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
-  const int nvalid = static_cast<int>(n - bbase < kRadixTile ? n - bbase : kRadixTile);
+  // Digit d's first output position in this partition: the global totals
+  // of the lower digits plus the partition's offset along digit d's row.
+  uint32_t run = 0;
+  {
+    const uint32_t gtot = threadIdx.x < kBins ? digit_totals[threadIdx.x] : 0u;
+    uint32_t gincl = gtot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t gy = __shfl_up(gincl, o, 64);
+      if (lane >= o) gincl += gy;
+    }
+    if (lane == 63) s_wsum[wave] = gincl;
+    __syncthreads();
+    if (threadIdx.x < kBins) {
+      const int d = threadIdx.x;
+      uint32_t gbase = gincl - gtot;
+      for (int w = 0; w < wave; ++w) gbase += s_wsum[w];
+      run = gbase + hist_scan[static_cast<int64_t>(d) * nparts + blockIdx.x];
+    }
+  }
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
-  int dig[kRadixItems];
+
+  for (int t = 0; t < sub; ++t) {
+    const int64_t bbase = (static_cast<int64_t>(blockIdx.x) * sub + t) * kRadixTile;
+    if (bbase >= n) break;  // same for every thread of the block
+    // Also orders the previous tile's reads of s_key/s_delta/s_wsum before
+    // this tile's writes.
+    __syncthreads();
+    for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
+      s_cnt[e / kBins][e % kBins] = 0;
+    __syncthreads();
+
+    const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
+    const int nvalid = static_cast<int>(n - bbase < kRadixTile ? n - bbase : kRadixTile);
+    uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
+    int dig[kRadixItems];
 #pragma unroll
-  for (int it = 0; it < kRadixItems; ++it) {
-    const int64_t idx = wbase + it * 64 + lane;
-    const bool valid = idx < n;
-    key[it] = valid ? kin[idx] : 0u;
-    // vin == nullptr: the values are the element indices (first pass of a
-    // sort whose payload is the identity permutation).
-    if (VALS) val[it] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
-    const int d = valid ? static_cast<int>((key[it] >> shift) & mask) : 0;
-    dig[it] = valid ? d : -1;
-    uint64_t peers = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < RB; ++b) {
-      const bool bit = (d >> b) & 1;
-      const uint64_t bb = __ballot(bit);
-      peers &= bit ? bb : ~bb;
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int64_t idx = wbase + it * 64 + lane;
+      const bool valid = idx < n;
+      key[it] = valid ? kin[idx] : 0u;
+      // vin == nullptr: the values are the element indices (first pass of a
+      // sort whose payload is the identity permutation).
+      if (VALS) val[it] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
     }
-    const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
-    uint32_t prev = 0;
-    if (valid) prev = s_cnt[wave][d];
-    rank[it] = prev + before;
-    if (valid && before == 0) s_cnt[wave][d] = prev + static_cast<uint32_t>(__popcll(peers));
-  }
-  __syncthreads();
-  // Per digit: the counts of the lower waves (s_cnt becomes each wave's
-  // local start), the block total, and exclusive scans over the digits of
-  // the block totals (the digit's local start in the reordered block) and
-  // of the global digit totals (the digit's first output position).
-  uint32_t tot = 0, gtot = 0;
-  if (threadIdx.x < kBins) {
-    const int d = threadIdx.x;
 #pragma unroll
-    for (int w = 0; w < kRadixWaves; ++w) tot += s_cnt[w][d];
-    gtot = digit_totals[d];
-  }
-  uint32_t incl = tot, gincl = gtot;
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int64_t idx = wbase + it * 64 + lane;
+      const bool valid = idx < n;
+      const int d = valid ? static_cast<int>((key[it] >> shift) & mask) : 0;
+      dig[it] = valid ? d : -1;
+      uint64_t peers = __ballot(valid);
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(incl, o, 64);
-    const uint32_t gy = __shfl_up(gincl, o, 64);
-    if (lane >= o) {
-      incl += y;
-      gincl += gy;
+      for (int b = 0; b < RB; ++b) {
+        const bool bit = (d >> b) & 1;
+        const uint64_t bb = __ballot(bit);
+        peers &= bit ? bb : ~bb;
+      }
+      const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
+      uint32_t prev = 0;
+      if (valid) prev = s_cnt[wave][d];
+      rank[it] = prev + before;
+      if (valid && before == 0) s_cnt[wave][d] = prev + static_cast<uint32_t>(__popcll(peers));
     }
-  }
-  if (lane == 63) {
-    s_wsum[wave] = incl;
-    s_gsum[wave] = gincl;
-  }
-  __syncthreads();
-  if (threadIdx.x < kBins) {
-    const int d = threadIdx.x;
-    uint32_t loc = incl - tot, gbase = gincl - gtot;
-    for (int w = 0; w < wave; ++w) {
-      loc += s_wsum[w];
-      gbase += s_gsum[w];
-    }
-    s_delta[d] = gbase + hist_scan[static_cast<int64_t>(d) * nblocks + blockIdx.x] - loc;
-    uint32_t run = loc;
+    __syncthreads();
+    // Per digit: the counts of the lower waves (s_cnt becomes each wave's
+    // local start), the tile total, and the exclusive scan over the digits
+    // of the tile totals (the digit's local start in the reordered tile).
+    uint32_t tot = 0;
+    if (threadIdx.x < kBins) {
 #pragma unroll
-    for (int w = 0; w < kRadixWaves; ++w) {
-      const uint32_t c = s_cnt[w][d];
-      s_cnt[w][d] = run;
-      run += c;
+      for (int w = 0; w < kRadixWaves; ++w) tot += s_cnt[w][threadIdx.x];
     }
-  }
-  __syncthreads();
+    uint32_t incl = tot;
 #pragma unroll
-  for (int it = 0; it < kRadixItems; ++it) {
-    if (dig[it] >= 0) {
-      const uint32_t lp = s_cnt[wave][dig[it]] + rank[it];
-      s_key[lp] = key[it];
-      if (VALS) s_val[lp] = val[it];
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
     }
-  }
-  __syncthreads();
+    if (lane == 63) s_wsum[wave] = incl;
+    __syncthreads();
+    if (threadIdx.x < kBins) {
+      const int d = threadIdx.x;
+      uint32_t loc = incl - tot;
+      for (int w = 0; w < wave; ++w) loc += s_wsum[w];
+      s_delta[d] = run - loc;
+      run += tot;
+      uint32_t r = loc;
 #pragma unroll
-  for (int it = 0; it < kRadixItems; ++it) {
-    const int i = it * kRadixThreads + static_cast<int>(threadIdx.x);
-    if (i < nvalid) {
-      const uint32_t k = s_key[i];
-      const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
-      kout[pos] = k & out_mask;
-      if (VALS) vout[pos] = s_val[i];
+      for (int w = 0; w < kRadixWaves; ++w) {
+        const uint32_t c = s_cnt[w][d];
+        s_cnt[w][d] = r;
+        r += c;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      if (dig[it] >= 0) {
+        const uint32_t lp = s_cnt[wave][dig[it]] + rank[it];
+        s_key[lp] = key[it];
+        if (VALS) s_val[lp] = val[it];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int i = it * kRadixThreads + static_cast<int>(threadIdx.x);
+      if (i < nvalid) {
+        const uint32_t k = s_key[i];
+        const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
+        if (write_keys) kout[pos] = k & out_mask;
+        if (VALS) vout[pos] = s_val[i];
+      }
     }
   }
 }
@@ -779,50 +843,112 @@ size_t radix_scratch_elems(int64_t n) {
 
 namespace {
 
+// Partitioning of n keys: `sub` tiles of kRadixTile per partition, `np`
+// partitions.  sub stays 1 below 2*kRadixTargetParts tiles (every tile its
+// own block) and grows beyond, capped at kRadixMaxSub; np <= tiles, so the
+// spine fits the scratch that radix_scratch_elems sizes for one row per tile.
+struct RadixParts {
+  int np;
+  int sub;
+};
+
+int radix_parts(int64_t n, RadixParts* p) {
+  const int64_t tiles = (n + kRadixTile - 1) / kRadixTile;
+  int64_t sub = tiles / kRadixTargetParts;
+  if (sub < 1) sub = 1;
+  if (sub > kRadixMaxSub) sub = kRadixMaxSub;
+  const int64_t np = (tiles + sub - 1) / sub;
+  if (np > 0x7FFFFFFF) {
+    set_error("radix sort: too many keys (%lld)", static_cast<long long>(n));
+    return HRF_ERR_INVALID;
+  }
+  p->np = static_cast<int>(np);
+  p->sub = static_cast<int>(sub);
+  return HRF_OK;
+}
+
 template <int RB, bool VALS>
 int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
-               int64_t n, int nb, int shift, uint32_t mask, uint32_t* scratch,
+               int64_t n, const RadixParts& rp, int shift, uint32_t mask, uint32_t* scratch,
                const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu) {
-  const int64_t hist_n = static_cast<int64_t>(nb) << RB;
+  const int64_t hist_n = static_cast<int64_t>(rp.np) << RB;
   uint32_t* hist = scratch;
   uint32_t* totals = scratch + hist_n;
-  hipLaunchKernelGGL(k_radix_hist<RB>, dim3(nb), dim3(kRadixThreads), 0, s, src_k, n, shift,
-                     mask, hist, nb, run_flag);
+  hipLaunchKernelGGL(k_radix_hist<RB>, dim3(rp.np), dim3(kRadixThreads), 0, s, src_k, n, shift,
+                     mask, hist, rp.np, rp.sub, run_flag);
   HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, nb,
+  hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, rp.np,
                      totals, run_flag);
   HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(nb), dim3(kRadixThreads), 0, s, src_k,
-                     src_v, dst_k, dst_v, n, shift, mask, hist, totals, nb, run_flag, out_mask);
+  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(rp.np), dim3(kRadixThreads), 0, s,
+                     src_k, src_v, dst_k, dst_v, n, shift, mask, hist, totals, rp.np, rp.sub,
+                     run_flag, out_mask);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
 
-int block_count(int64_t n, int* nb) {
-  const int64_t nb64 = (n + kRadixTile - 1) / kRadixTile;
-  if (nb64 > 0x7FFFFFFF) {
-    set_error("radix sort: too many keys (%lld)", static_cast<long long>(n));
-    return HRF_ERR_INVALID;
+// Digit width of pass `pass` of `passes` over nbits key bits: widths differ
+// by at most one and the wider digits come last (13 bits: 6 then 7).  The
+// first pass moves the most bytes per element (the later ones may write
+// less), and fewer digits there mean fewer, longer output runs per tile.
+int digit_bits(int nbits, int passes, int pass) {
+  const int base = nbits / passes, extra = nbits % passes;
+  return base + (pass >= passes - extra ? 1 : 0);
+}
+
+// Pass over digit bits [shift, shift + bits) with the narrowest digit
+// template that holds them (bits <= 8).
+template <bool VALS>
+int radix_pass_bits(int bits, const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k,
+                    uint32_t* dst_v, int64_t n, const RadixParts& rp, int shift,
+                    uint32_t* scratch, const uint32_t* run_flag, hipStream_t s,
+                    uint32_t out_mask = 0xFFFFFFFFu) {
+  const uint32_t mask = (1u << bits) - 1u;
+  switch (bits) {
+    case 1: case 2: case 3: case 4:
+      return radix_pass<4, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
+                                 run_flag, s, out_mask);
+    case 5:
+      return radix_pass<5, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
+                                 run_flag, s, out_mask);
+    case 6:
+      return radix_pass<6, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
+                                 run_flag, s, out_mask);
+    case 7:
+      return radix_pass<7, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
+                                 run_flag, s, out_mask);
+    case 8:
+      return radix_pass<8, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
+                                 run_flag, s, out_mask);
+    default:
+      set_error("internal: radix digit of %d bits", bits);
+      return HRF_ERR_INVALID;
   }
-  *nb = static_cast<int>(nb64);
-  return HRF_OK;
 }
 
 }  // namespace
 
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
                      int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s,
-                     const uint32_t* run_flag, bool index_values) {
+                     const uint32_t* run_flag, bool index_values, bool keys_needed) {
   *result_in_b = false;
   if (n <= 1) return HRF_OK;
+  if (end_bit < 1 || end_bit > 32) {
+    set_error("internal: radix sort over %d key bits", end_bit);
+    return HRF_ERR_INVALID;
+  }
   const int passes = radix_passes(end_bit);
-  int nb = 0;
-  HRF_TRY(block_count(n, &nb));
+  RadixParts rp{};
+  HRF_TRY(radix_parts(n, &rp));
   uint32_t *src_k = ka, *src_v = va, *dst_k = kb, *dst_v = vb;
+  int done = 0;
   for (int pass = 0; pass < passes; ++pass) {
+    const int bits = digit_bits(end_bit, passes, pass);
     const uint32_t* vin = (pass == 0 && index_values) ? nullptr : src_v;
-    HRF_TRY((radix_pass<8, true>(src_k, vin, dst_k, dst_v, n, nb, pass * 8, 0xFFu, scratch,
-                                 run_flag, s)));
+    uint32_t* kout = (pass == passes - 1 && !keys_needed) ? nullptr : dst_k;
+    HRF_TRY(radix_pass_bits<true>(bits, src_k, vin, kout, dst_v, n, rp, done, scratch, run_flag,
+                                  s));
+    done += bits;
     uint32_t* tk = src_k;
     uint32_t* tv = src_v;
     src_k = dst_k;
@@ -845,43 +971,18 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
     }
     return HRF_OK;
   }
-  const int passes = (nbits + 7) / 8;
-  const int rb = (nbits + passes - 1) / passes;  // digit bits, <= 8
-  int nb = 0;
-  HRF_TRY(block_count(n, &nb));
+  const int passes = radix_passes(nbits);
+  RadixParts rp{};
+  HRF_TRY(radix_parts(n, &rp));
   uint32_t *src = ka, *dst = kb;
   int done = 0;
   for (int pass = 0; pass < passes; ++pass) {
-    const int bits = nbits - done < rb ? nbits - done : rb;
-    const uint32_t mask = (1u << bits) - 1u;
-    const int shift = lo_bit + done;
+    const int bits = digit_bits(nbits, passes, pass);
     const bool last = pass == passes - 1 && final_out;
     uint32_t* out = last ? final_out : dst;
     const uint32_t om = last ? final_mask : 0xFFFFFFFFu;
-    int rc;
-    switch (rb) {
-      case 1: case 2: case 3: case 4:
-        rc = radix_pass<4, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s, om);
-        break;
-      case 5:
-        rc = radix_pass<5, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s, om);
-        break;
-      case 6:
-        rc = radix_pass<6, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s, om);
-        break;
-      case 7:
-        rc = radix_pass<7, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s, om);
-        break;
-      default:
-        rc = radix_pass<8, false>(src, nullptr, out, nullptr, n, nb, shift, mask, scratch,
-                                  nullptr, s, om);
-        break;
-    }
-    HRF_TRY(rc);
+    HRF_TRY(radix_pass_bits<false>(bits, src, nullptr, out, nullptr, n, rp, lo_bit + done,
+                                   scratch, nullptr, s, om));
     done += bits;
     uint32_t* t = src;
     src = dst;

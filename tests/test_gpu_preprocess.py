@@ -105,6 +105,27 @@ def test_forward_depth_sort_bit_range(hrf, oracle_mod, depths):
     np.testing.assert_array_equal(out[1].cpu().numpy(), ref["z"])
 
 
+def test_forward_depth_sort_partitioned(hrf, oracle_mod):
+    """~21.8M selected rows: past 8192 radix tiles, so each block of the
+    depth sort's passes walks a partition of several tiles (the last one
+    partial).  Depths on a 2^-12 grid give long runs of ties, whose index
+    order the stable passes must keep."""
+    n = 24_000_000
+    rng = np.random.default_rng(21)
+    means = rng.uniform(-4, 4, size=(n, 3)).astype(np.float32)
+    means[:, 2] = np.round(rng.uniform(0.5, 6.0, size=n) * 4096.0).astype(np.float32) / 4096.0
+    R = np.eye(3, dtype=np.float32)
+    T = np.zeros(3, np.float32)
+    ref = oracle_mod.preprocess_select(means, R, T, 1.0, 1000.0)
+    prm = (means, np.tile(np.float32([1, 0, 0, 0]), (n, 1)), np.zeros((n, 3), np.float32),
+           np.zeros((n, 1), np.float32), np.zeros((n, 1), np.float32), np.zeros(n, np.float32),
+           np.zeros((n, 1), np.float32), R, T)
+    print(f"partitioned depth sort n={n} selected={len(ref)}", flush=True)
+    assert len(ref) > 2 * 4096 * 2048
+    out = _run(prm, 1.0, 1000.0)
+    np.testing.assert_array_equal(out[-1].cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("near,far,P,C", [(1.0, 1000.0, 3, 3), (1.0, 4.0, 5, 2)])
 def test_backward_matches_oracle(hrf, oracle_mod, near, far, P, C):
     from complex_valued_holographic_radiance_fields_amd import preprocess
