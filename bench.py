@@ -416,6 +416,17 @@ def bench_cfg3(args, dev):
     fwd_b = C * (8 * S * S + 16 * M * M) + D * C * (32 * M * M + 8 * S * S)
     adj_b = D * C * (8 * S * S + 32 * M * M) + C * (16 * M * M + 8 * S * S)
     ach = (fwd_b + adj_b) / (ms * 1e-3) / 1e9
+    # What the fused passes move (the multi-distance workspace holds the
+    # column results of G = 2 distances at a time): forward = field in, row
+    # spectra (C,S,M) out once and in once per group, (D,C,S,M) column results
+    # out and in, (D,C,S,S) out; the adjoint mirrors it with the (C,S,M)
+    # column sum written per group and read back by the next group and by the
+    # inverse rows pass.
+    groups = (D + 1) // 2
+    row_b, col_b = 8 * C * S * M, 8 * D * C * S * M
+    fused_b = (8 * C * S * S + row_b * (1 + groups) + 2 * col_b + 8 * D * C * S * S +
+               8 * D * C * S * S + 2 * col_b + row_b * 2 * groups + 8 * C * S * S)
+    fused_gbs = fused_b / (ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import cpu_baseline
@@ -438,8 +449,11 @@ def bench_cfg3(args, dev):
                       "fft_grid": M, "parallelism": "single-gpu"},
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                        "traffic": None, "kernel": "whole step (hipFFT transforms + MAC/pad/crop)",
+                        "traffic": None,
+                        "kernel": "whole step (fused LDS-FFT row and column passes)",
                         "bytes_per_step": int(fwd_b + adj_b)},
+           "fused_dataflow_bytes": int(fused_b),
+           "fused_dataflow_frac": round(fused_gbs / HBM_PEAK_GBS, 4),
            "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
 

@@ -22,8 +22,8 @@
 // batch of B rows or columns held in LDS: each stage reads all butterfly
 // inputs into registers, applies table twiddles (double-precision table,
 // rounded to float), does the R-point DFT, and writes the outputs back to
-// their Stockham positions between two barriers.  Transform lengths with
-// other prime factors (or longer than 2048) use the hipFFT path.
+// their Stockham positions between two barriers.  Transform lengths
+// without a plan here use the hipFFT path.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -40,6 +40,14 @@ namespace {
 constexpr int kFftThreads = 512;   // column passes
 constexpr int kRowThreads = 1024;  // row passes (same LDS batch, twice the waves)
 constexpr int kFftBatch = 4;  // rows / columns per block
+// Column-pass threads and the occupancy they are compiled for: the longest
+// transforms (N >= 3840: a 138-147 KB LDS batch, one block per CU) run
+// twice the waves per block, which also halves each thread's share of the
+// per-element transfer state.
+template <int N>
+constexpr int kColThreads = N >= 3840 ? 1024 : kFftThreads;
+template <int N>
+constexpr int kColMinBlocks = N <= 1600 ? 4 : (N <= 2048 ? 2 : 1);
 constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
 
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
@@ -329,7 +337,9 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   X(1024, 8, 8, 4, 4)    \
   X(1600, 8, 8, 5, 5)    \
   X(2016, 8, 4, 7, 3, 3) \
-  X(2048, 8, 8, 8, 4)
+  X(2048, 8, 8, 8, 4)    \
+  X(3840, 8, 8, 4, 5, 3) \
+  X(4096, 8, 8, 8, 8)
 
 template <int N>
 struct Plan;
@@ -531,21 +541,22 @@ __device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb
 // B: forward column pass for one channel and one column tile.  X tiled
 // (P*C, H, N) row spectra of the fields (rows r_pad..r_pad+H of the padded
 // grid; the other rows are zero); Z tiled (C, S, N) receives rows
-// [s_crop, s_crop+S) of iFFTcol(sum_p FFTcol(X[p,c]) * T[p,c] * A).
+// [s_crop, s_crop+S) of iFFTcol(sum_p FFTcol(X[p,c]) * T[p,c] * A), or
+// adds them to what Z holds (accumulate != 0).
 // HALF: the field rows lie in [N/4, 3N/4); only that half is staged and the
 // forward transforms' first stage is pruned.
 template <int N, bool HALF>
-__global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(const float2* __restrict__ X,
-                                                         float2* __restrict__ Z, int P, int C,
-                                                         int H, int r_pad, int S, int s_crop,
-                                                         float sfreq, float ap, AsmFftConsts mc,
-                                                         const float2* __restrict__ tw) {
+__global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
+    const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int H, int r_pad, int S,
+    int s_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw,
+    int accumulate) {
   constexpr int B = kFftBatch;
+  constexpr int T = kColThreads<N>;
   constexpr int ncb = N / B;
-  constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
+  constexpr int EPT = (B * N + T - 1) / T;
   __shared__ float2 lds[lds_elems<N>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N>(s_tw, tw);
+  const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
@@ -556,7 +567,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   float2 acc[EPT];
 #pragma unroll
   for (int u = 0; u < EPT; ++u) {
-    const int q = threadIdx.x + u * kFftThreads;
+    const int q = threadIdx.x + u * T;
     acc[u] = make_float2(0.0f, 0.0f);
     kz[u] = -1.0f;
     if (q < B * N) {
@@ -577,29 +588,29 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
     // flight per thread (a whole-tile register buffer would not fit).
     constexpr int kPlaneLoads = 4;
     for (int e0 = E0 + static_cast<int>(threadIdx.x); e0 < E1;
-         e0 += kPlaneLoads * kFftThreads) {
+         e0 += kPlaneLoads * T) {
       float2 v[kPlaneLoads];
 #pragma unroll
       for (int u = 0; u < kPlaneLoads; ++u) {
-        const int e = e0 + u * kFftThreads;
+        const int e = e0 + u * T;
         const int r = e / B - r_pad;
         v[u] = make_float2(0.0f, 0.0f);
         if (e < E1 && r >= 0 && r < H) v[u] = src[e - r_pad * B];
       }
 #pragma unroll
       for (int u = 0; u < kPlaneLoads; ++u) {
-        const int e = e0 + u * kFftThreads;
+        const int e = e0 + u * T;
         if (e < E1) lds[pad(e)] = v[u];
       }
     }
     __syncthreads();
-    Plan<N>::template run<false, kFftThreads, HALF>(lds, twp);
+    Plan<N>::template run<false, T, HALF>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-      const int q = threadIdx.x + u * kFftThreads;
+      const int q = threadIdx.x + u * T;
       if (q < B * N && kz[u] >= 0.0f) {
         bool within = band_all;
         if (!within) {
@@ -622,13 +633,17 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < EPT; ++u) {
-    const int q = threadIdx.x + u * kFftThreads;
+    const int q = threadIdx.x + u * T;
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<true>(lds, twp);
+  Plan<N>::template run<true, T>(lds, twp);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, B);
-  for (int e = threadIdx.x; e < B * S; e += kFftThreads) dst[e] = lds[pad(e + s_crop * B)];
+  if (accumulate) {
+    for (int e = threadIdx.x; e < B * S; e += T) dst[e] = cadd(dst[e], lds[pad(e + s_crop * B)]);
+  } else {
+    for (int e = threadIdx.x; e < B * S; e += T) dst[e] = lds[pad(e + s_crop * B)];
+  }
 }
 
 // B': adjoint column pass.  X tiled (C, S, N) row spectra of the padded
@@ -637,17 +652,16 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_fwd(co
 // HALF: the S gradient rows lie in [N/4, 3N/4) (always, with N = 2S); only
 // that half is staged and the forward transform's first stage is pruned.
 template <int N, bool HALF>
-__global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(const float2* __restrict__ X,
-                                                         float2* __restrict__ Z, int P, int C,
-                                                         int S, int s_pad, int H, int r_crop,
-                                                         float sfreq, float ap, AsmFftConsts mc,
-                                                         const float2* __restrict__ tw) {
+__global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
+    const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int S, int s_pad, int H,
+    int r_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw) {
   constexpr int B = kFftBatch;
+  constexpr int T = kColThreads<N>;
   constexpr int ncb = N / B;
-  constexpr int EPT = (B * N + kFftThreads - 1) / kFftThreads;
+  constexpr int EPT = (B * N + T - 1) / T;
   __shared__ float2 lds[lds_elems<N>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N>(s_tw, tw);
+  const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   int c, cb;
   map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
   const int k0 = cb * B;
@@ -656,28 +670,28 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
   {
     constexpr int E0 = HALF ? B * N / 4 : 0;
     constexpr int EN = HALF ? B * N / 2 : B * N;
-    constexpr int IT = (EN + kFftThreads - 1) / kFftThreads;
+    constexpr int IT = (EN + T - 1) / T;
     float2 v[IT];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
       const int r = e / B - s_pad;
       v[it] = make_float2(0.0f, 0.0f);
       if (e < E0 + EN && r >= 0 && r < S) v[it] = src[e - s_pad * B];
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * kFftThreads;
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
       if (e < E0 + EN) lds[pad(e)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<false, kFftThreads, HALF>(lds, twp);
+  Plan<N>::template run<false, T, HALF>(lds, twp);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
   for (int u = 0; u < EPT; ++u) {
-    const int q = threadIdx.x + u * kFftThreads;
+    const int q = threadIdx.x + u * T;
     kz[u] = -1.0f;
     gs[u] = make_float2(0.0f, 0.0f);
     if (q < B * N) {
@@ -697,7 +711,7 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
     const float nd = -mc.d[p];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-      const int q = threadIdx.x + u * kFftThreads;
+      const int q = threadIdx.x + u * T;
       if (q < B * N) {
         float2 r = make_float2(0.0f, 0.0f);
         if (kz[u] >= 0.0f) {
@@ -719,9 +733,9 @@ __global__ __launch_bounds__(kFftThreads, (N <= 1600 ? 4 : 2)) void k_col_adj(co
       }
     }
     __syncthreads();
-    Plan<N>::template run<true>(lds, twp);
+    Plan<N>::template run<true, T>(lds, twp);
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
-    for (int e = threadIdx.x; e < B * H; e += kFftThreads) dst[e] = lds[pad(e + r_crop * B)];
+    for (int e = threadIdx.x; e < B * H; e += T) dst[e] = lds[pad(e + r_crop * B)];
   }
 }
 
@@ -789,42 +803,103 @@ AsmFftConsts fft_consts(int P, int C, int M, double pitch, const float* wl, cons
   return mc;
 }
 
+// Launches of the four passes for a length-N plan.  Inputs of width w (or
+// height h) sit centred in the padded length-N line, at N/2 - w/2; when
+// 2w <= N they lie in [N/4, 3N/4) and the pruned first stage is taken.
+template <int N>
+int pass_rows_in(const float2* src, float2* X, int nimg, int h, int w, const float2* tw,
+                 hipStream_t s) {
+  const int B = kFftBatch;
+  const dim3 grid(nimg * ((h + B - 1) / B));
+  if (2 * w <= N)
+    hipLaunchKernelGGL((k_rows_in<N, true>), grid, dim3(kRowThreads), 0, s, src, X, nimg, h, w,
+                       N / 2 - w / 2, tw);
+  else
+    hipLaunchKernelGGL((k_rows_in<N, false>), grid, dim3(kRowThreads), 0, s, src, X, nimg, h, w,
+                       N / 2 - w / 2, tw);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+// Keeps rows [N/2 - h/2, +h) and columns [N/2 - w/2, +w), times 1/N^2.
+template <int N>
+int pass_rows_out(const float2* Z, float2* dst, int nimg, int h, int w, const float2* tw,
+                  hipStream_t s) {
+  const int B = kFftBatch;
+  const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
+  hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((h + B - 1) / B)), dim3(kRowThreads), 0, s, Z,
+                     dst, nimg, h, w, N / 2 - w / 2, scale, tw);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+// B with P transfer functions summed: X (P*C, h_in, N) -> Z (C, h_out, N).
+template <int N>
+int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
+                 float ap, const AsmFftConsts& mc, const float2* tw, bool accumulate,
+                 hipStream_t s) {
+  const dim3 grid(C * (N / kFftBatch)), block(kColThreads<N>);
+  if (2 * h_in <= N)
+    hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,
+                       accumulate ? 1 : 0);
+  else
+    hipLaunchKernelGGL((k_col_fwd<N, false>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,
+                       accumulate ? 1 : 0);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+// B' with P transfer functions applied one by one: X (C, h_in, N) ->
+// Z (P*C, h_out, N).
+template <int N>
+int pass_col_adj(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
+                 float ap, const AsmFftConsts& mc, const float2* tw, hipStream_t s) {
+  const dim3 grid(C * (N / kFftBatch)), block(kColThreads<N>);
+  if (2 * h_in <= N)
+    hipLaunchKernelGGL((k_col_adj<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw);
+  else
+    hipLaunchKernelGGL((k_col_adj<N, false>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw);
+  HRF_LAUNCH_CHECK();
+  return HRF_OK;
+}
+
+float freq_step_of(int N, double pitch) {
+  return static_cast<float>(1.0 / (static_cast<double>(N) * pitch));
+}
+
+// The transfer constants with the propagation direction reversed: k_col_fwd
+// applies exp(+i d kz) and k_col_adj exp(-i d kz), so negated distances give
+// the conjugate transfer function in the one and the plain one in the other.
+// The band limits depend on d^2 and stay those of the given distances.
+AsmFftConsts fft_consts_reversed(int P, int C, int M, double pitch, const float* wl,
+                                 const float* dist) {
+  AsmFftConsts mc = fft_consts(P, C, M, pitch, wl, dist);
+  for (int p = 0; p < P; ++p) mc.d[p] = -mc.d[p];
+  return mc;
+}
+
 template <int N>
 int run_forward(const float2* fields, int P, int C, int H, int W, int S, double pitch,
                 const float* wl, const float* dist, float ap, float2* holo, float2* X, float2* Z,
                 hipStream_t s) {
   const float2* tw = nullptr;
   HRF_TRY(twiddles(N, &tw));
-  const int B = kFftBatch;
-  const float sfreq = static_cast<float>(1.0 / (static_cast<double>(N) * pitch));
   const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
   {
     HRF_STAGE("asm_rows_in", s);
-    const int nimg = P * C;
-    if (2 * W <= N)
-      hipLaunchKernelGGL((k_rows_in<N, true>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads),
-                         0, s, fields, X, nimg, H, W, N / 2 - W / 2, tw);
-    else
-      hipLaunchKernelGGL((k_rows_in<N, false>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads),
-                         0, s, fields, X, nimg, H, W, N / 2 - W / 2, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_rows_in<N>(fields, X, P * C, H, W, tw, s));
   }
   {
     HRF_STAGE("asm_col_fwd", s);
-    if (2 * H <= N)
-      hipLaunchKernelGGL((k_col_fwd<N, true>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P,
-                         C, H, N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
-    else
-      hipLaunchKernelGGL((k_col_fwd<N, false>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z,
-                         P, C, H, N / 2 - H / 2, S, N / 2 - S / 2, sfreq, ap, mc, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, tw, false, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
-    const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
-    hipLaunchKernelGGL((k_rows_out<N>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s, Z,
-                       holo, C, S, S, N / 2 - S / 2, scale, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_rows_out<N>(Z, holo, C, S, S, tw, s));
   }
   return HRF_OK;
 }
@@ -835,29 +910,77 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
                 float2* Z, hipStream_t s) {
   const float2* tw = nullptr;
   HRF_TRY(twiddles(N, &tw));
-  const int B = kFftBatch;
-  const float sfreq = static_cast<float>(1.0 / (static_cast<double>(N) * pitch));
   const AsmFftConsts mc = fft_consts(P, C, N, pitch, wl, dist);
   {
     HRF_STAGE("asm_rows_in", s);
-    // S rows of width S = N/2 at column N/4: always the pruned variant
-    hipLaunchKernelGGL((k_rows_in<N, true>), dim3(C * ((S + B - 1) / B)), dim3(kRowThreads), 0, s,
-                       gholo, X, C, S, S, N / 2 - S / 2, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_rows_in<N>(gholo, X, C, S, S, tw, s));
   }
   {
     HRF_STAGE("asm_col_adj", s);
-    hipLaunchKernelGGL((k_col_adj<N, true>), dim3(C * (N / B)), dim3(kFftThreads), 0, s, X, Z, P,
-                       C, S, N / 2 - S / 2, H, N / 2 - H / 2, sfreq, ap, mc, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_col_adj<N>(X, Z, P, C, S, H, freq_step_of(N, pitch), ap, mc, tw, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
-    const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
-    const int nimg = P * C;
-    hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((H + B - 1) / B)), dim3(kRowThreads), 0, s,
-                       Z, gfields, nimg, H, W, N / 2 - W / 2, scale, tw);
-    HRF_LAUNCH_CHECK();
+    HRF_TRY(pass_rows_out<N>(Z, gfields, P * C, H, W, tw, s));
+  }
+  return HRF_OK;
+}
+
+// Multi-distance forward, (C,H,W) -> (D,C,S,S): the structure of the
+// adjoint above with the plain transfer function, one forward column
+// transform per group of distances.  X holds (C,H,N); Z holds `group`
+// distances' (C,S,N) spectra.
+template <int N>
+int run_md_forward(const float2* field, int D, int C, int H, int W, int S, double pitch,
+                   const float* wl, const float* dist, float ap, float2* out, float2* X,
+                   float2* Z, int group, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw));
+  const int64_t SS = static_cast<int64_t>(S) * S;
+  {
+    HRF_STAGE("asm_rows_in", s);
+    HRF_TRY(pass_rows_in<N>(field, X, C, H, W, tw, s));
+  }
+  for (int d0 = 0; d0 < D; d0 += group) {
+    const int g = D - d0 < group ? D - d0 : group;
+    const AsmFftConsts mc = fft_consts_reversed(g, C, N, pitch, wl, dist + d0);
+    {
+      HRF_STAGE("asm_col_adj", s);
+      HRF_TRY(pass_col_adj<N>(X, Z, g, C, H, S, freq_step_of(N, pitch), ap, mc, tw, s));
+    }
+    {
+      HRF_STAGE("asm_rows_out", s);
+      HRF_TRY(pass_rows_out<N>(Z, out + d0 * C * SS, g * C, S, S, tw, s));
+    }
+  }
+  return HRF_OK;
+}
+
+// Multi-distance adjoint, (D,C,S,S) -> (C,H,W): the structure of the forward
+// above with the conjugate transfer function, summed over the distances;
+// each group of distances adds its column-pass result into Z (C,H,N).
+template <int N>
+int run_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double pitch,
+                   const float* wl, const float* dist, float ap, float2* gfield, float2* X,
+                   float2* Z, int group, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw));
+  const int64_t SS = static_cast<int64_t>(S) * S;
+  for (int d0 = 0; d0 < D; d0 += group) {
+    const int g = D - d0 < group ? D - d0 : group;
+    const AsmFftConsts mc = fft_consts_reversed(g, C, N, pitch, wl, dist + d0);
+    {
+      HRF_STAGE("asm_rows_in", s);
+      HRF_TRY(pass_rows_in<N>(gout + d0 * C * SS, X, g * C, S, S, tw, s));
+    }
+    {
+      HRF_STAGE("asm_col_fwd", s);
+      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, tw, d0 > 0, s));
+    }
+  }
+  {
+    HRF_STAGE("asm_rows_out", s);
+    HRF_TRY(pass_rows_out<N>(Z, gfield, C, H, W, tw, s));
   }
   return HRF_OK;
 }
@@ -865,45 +988,91 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
 }  // namespace
 
 bool fused_fft_supported(int M) {
-  return M == 128 || M == 160 || M == 192 || M == 512 || M == 1024 || M == 1600 ||
-         M == 2016 || M == 2048;
+#define HRF_FFT_SUPPORTED(NN, ...) \
+  if (M == NN) return true;
+  HRF_FFT_PLANS(HRF_FFT_SUPPORTED)
+#undef HRF_FFT_SUPPORTED
+  return false;
 }
+
+// One case per plan: `case NN: return RUNNER<NN> ARGS;` (RUNNER and ARGS
+// are defined around each use).
+#define HRF_FFT_CASE(NN, ...) \
+  case NN:                    \
+    return RUNNER<NN> ARGS;
 
 int fused_asm_forward(const float2* fields, int P, int C, int H, int W, int S, double pitch,
                       const float* wl, const float* dist, float ap, float2* holo, float2* X,
                       float2* Z, hipStream_t s) {
+#define RUNNER run_forward
+#define ARGS (fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s)
   switch (2 * S) {
-    case 128: return run_forward<128>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 160: return run_forward<160>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 192: return run_forward<192>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 512: return run_forward<512>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 1024: return run_forward<1024>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 1600: return run_forward<1600>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 2016: return run_forward<2016>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
-    case 2048: return run_forward<2048>(fields, P, C, H, W, S, pitch, wl, dist, ap, holo, X, Z, s);
+    HRF_FFT_PLANS(HRF_FFT_CASE)
     default:
-      set_error("fused ASM: unsupported grid %d", 2 * S);
-      return HRF_ERR_INVALID;
+      break;
   }
+#undef ARGS
+#undef RUNNER
+  set_error("fused ASM: unsupported grid %d", 2 * S);
+  return HRF_ERR_INVALID;
 }
 
 int fused_asm_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double pitch,
                       const float* wl, const float* dist, float ap, float2* gfields, float2* X,
                       float2* Z, hipStream_t s) {
+#define RUNNER run_adjoint
+#define ARGS (gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s)
   switch (2 * S) {
-    case 128: return run_adjoint<128>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 160: return run_adjoint<160>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 192: return run_adjoint<192>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 512: return run_adjoint<512>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 1024: return run_adjoint<1024>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 1600: return run_adjoint<1600>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 2016: return run_adjoint<2016>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
-    case 2048: return run_adjoint<2048>(gholo, P, C, H, W, S, pitch, wl, dist, ap, gfields, X, Z, s);
+    HRF_FFT_PLANS(HRF_FFT_CASE)
     default:
-      set_error("fused ASM: unsupported grid %d", 2 * S);
-      return HRF_ERR_INVALID;
+      break;
   }
+#undef ARGS
+#undef RUNNER
+  set_error("fused ASM: unsupported grid %d", 2 * S);
+  return HRF_ERR_INVALID;
 }
+
+int fused_md_forward(const float2* field, int D, int C, int H, int W, int S, double pitch,
+                     const float* wl, const float* dist, float ap, float2* out, float2* X,
+                     float2* Z, int group, hipStream_t s) {
+  if (group < 1) {
+    set_error("internal: multi-distance group of %d", group);
+    return HRF_ERR_INVALID;
+  }
+#define RUNNER run_md_forward
+#define ARGS (field, D, C, H, W, S, pitch, wl, dist, ap, out, X, Z, group, s)
+  switch (2 * S) {
+    HRF_FFT_PLANS(HRF_FFT_CASE)
+    default:
+      break;
+  }
+#undef ARGS
+#undef RUNNER
+  set_error("fused ASM: unsupported grid %d", 2 * S);
+  return HRF_ERR_INVALID;
+}
+
+int fused_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double pitch,
+                     const float* wl, const float* dist, float ap, float2* gfield, float2* X,
+                     float2* Z, int group, hipStream_t s) {
+  if (group < 1) {
+    set_error("internal: multi-distance group of %d", group);
+    return HRF_ERR_INVALID;
+  }
+#define RUNNER run_md_adjoint
+#define ARGS (gout, D, C, H, W, S, pitch, wl, dist, ap, gfield, X, Z, group, s)
+  switch (2 * S) {
+    HRF_FFT_PLANS(HRF_FFT_CASE)
+    default:
+      break;
+  }
+#undef ARGS
+#undef RUNNER
+  set_error("fused ASM: unsupported grid %d", 2 * S);
+  return HRF_ERR_INVALID;
+}
+#undef HRF_FFT_CASE
 
 void fused_fft_release_all() {
   std::lock_guard<std::mutex> lock(g_tw_mu);

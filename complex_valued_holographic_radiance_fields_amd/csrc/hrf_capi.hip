@@ -976,6 +976,13 @@ int hrf_asm_multidistance_forward(const void* field, int32_t num_distances, int3
   Carver cv(ws);
   float2* spec = cv.take<float2>(static_cast<size_t>(channels) * MM);
   float2* buf = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  if (fused_fft_supported(M)) {
+    // X = spec holds the C row spectra (H <= M rows); buf holds the column
+    // results of M / size = 2 distances at a time (C * size * M each).
+    return fused_md_forward(static_cast<const float2*>(field), num_distances, channels, height,
+                            width, size, pixel_pitch, wavelengths, distances, aperture,
+                            static_cast<float2*>(out), spec, buf, M / size, s);
+  }
   // The C channel spectra are computed once and shared by every distance.
   {
     HRF_STAGE("asm_pad", s);
@@ -1025,6 +1032,13 @@ int hrf_asm_multidistance_adjoint(const void* grad_out, int32_t num_distances, i
   Carver cv(ws);
   float2* acc = cv.take<float2>(static_cast<size_t>(channels) * MM);
   float2* buf = cv.take<float2>(static_cast<size_t>(channels) * MM);
+  if (fused_fft_supported(M)) {
+    // X = acc holds the row spectra of 2 distances' gradients at a time
+    // (C * size * M each); buf holds the (C, H, M) column-pass sum.
+    return fused_md_adjoint(static_cast<const float2*>(grad_out), num_distances, channels,
+                            height, width, size, pixel_pitch, wavelengths, distances, aperture,
+                            static_cast<float2*>(grad_field), acc, buf, M / size, s);
+  }
   // sum_d conj(T_d) FFT(pad g_d) in the spectral domain, one inverse FFT.
   for (int d = 0; d < num_distances; ++d) {
     {

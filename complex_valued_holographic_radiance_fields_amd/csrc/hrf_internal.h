@@ -391,6 +391,15 @@ int fused_asm_forward(const float2* fields, int P, int C, int H, int W, int S, d
 int fused_asm_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double pitch,
                       const float* wl, const float* dist, float ap, float2* gfields, float2* X,
                       float2* Z, hipStream_t s);
+// Multi-distance forward (C,H,W) -> (D,C,S,S) and adjoint (D,C,S,S) ->
+// (C,H,W), `group` distances per column pass.  Forward: X needs C*H*M and Z
+// group*C*S*M elements; adjoint: X group*C*S*M and Z C*H*M.
+int fused_md_forward(const float2* field, int D, int C, int H, int W, int S, double pitch,
+                     const float* wl, const float* dist, float ap, float2* out, float2* X,
+                     float2* Z, int group, hipStream_t s);
+int fused_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double pitch,
+                     const float* wl, const float* dist, float ap, float2* gfield, float2* X,
+                     float2* Z, int group, hipStream_t s);
 void fused_fft_release_all();
 
 }  // namespace hrf

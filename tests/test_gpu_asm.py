@@ -118,17 +118,20 @@ def test_odd_size_rejected(hrf):
 
 
 # Grids with a hand-written LDS-FFT plan (M = 2S in 128, 160, 192, 512, 1024,
-# 1600, 2016, 2048) run the fused row/column kernels; other sizes (M = 96
-# above) run the hipFFT path.  The headline grid (800 -> 1600) and every
-# large plan are checked against the oracle, forward and adjoint.
+# 1600, 2016, 2048, 3840, 4096) run the fused row/column kernels; other sizes
+# (M = 96 above) run the hipFFT path.  The headline grid (800 -> 1600) and
+# every large plan are checked against the oracle, forward and adjoint.
 # Fields wider and/or taller than half the padded grid (up to 2S is allowed)
 # take the transforms whose first stage is not pruned.
 @pytest.mark.parametrize("P,C,H,W,S", [(3, 3, 800, 800, 800), (1, 2, 100, 60, 512),
                                        (2, 1, 64, 64, 1008), (1, 1, 128, 96, 1024),
+                                       (2, 1, 120, 200, 1920), (1, 2, 96, 128, 2048),
+                                       (1, 1, 40, 2300, 2048), (1, 1, 2000, 24, 1920),
                                        (1, 2, 96, 100, 64), (2, 1, 48, 120, 64),
                                        (1, 1, 110, 40, 80)],
-                         ids=["headline1600", "m1024", "m2016", "m2048", "wide_tall_m128",
-                              "wide_m128", "tall_m160"])
+                         ids=["headline1600", "m1024", "m2016", "m2048", "m3840", "m4096",
+                              "wide_m4096", "tall_m3840", "wide_tall_m128", "wide_m128",
+                              "tall_m160"])
 def test_multiplane_fused_grids(hrf, oracle_mod, P, C, H, W, S):
     import torch
     from complex_valued_holographic_radiance_fields_amd import propagation
@@ -213,23 +216,27 @@ def test_multidistance_matches_oracle(hrf, oracle_mod):
         assert rel_l2(got_adj[c], ref) < TOL, c
 
 
-def test_multidistance_autograd_and_single_calls(hrf):
+@pytest.mark.parametrize("S,D", [(48, 2), (64, 3), (96, 5)],
+                         ids=["hipfft_m96", "fused_m128", "fused_m192"])
+def test_multidistance_autograd_and_single_calls(hrf, S, D):
     """MultiDistancePropagation's backward is multidistance_adjoint, and every
-    output equals the single-call propagation of the same field."""
+    output equals the single-call propagation of the same field.  On the
+    fused grids the distances go through the column passes two at a time
+    (an odd count leaves a group of one)."""
     import torch
     from complex_valued_holographic_radiance_fields_amd import propagation
 
     rng = np.random.default_rng(22)
-    C, H, W, S = 3, 32, 32, 48
+    C, H, W = 3, 32, 32
     wl = [639e-9, 515e-9, 473e-9]
-    dist = [2e-3, 5e-4]
+    dist = [2e-3, 5e-4, -1e-3, 3e-3, -2.5e-4][:D]
     f = torch.from_numpy(_field(rng, (C, H, W))).cuda().requires_grad_(True)
     out = propagation.MultiDistancePropagation.apply(f, wl, PITCH, dist, (S, S), float(S))
     for d, dv in enumerate(dist):
         for c in range(C):
             single = propagation.propagate(f.detach()[c], wl[c], PITCH, dv, (S, S), float(S))
             assert rel_l2(out.detach()[d, c].cpu().numpy(), single.cpu().numpy()) < 1e-6
-    g = torch.from_numpy(_field(rng, (2, C, S, S))).cuda()
+    g = torch.from_numpy(_field(rng, (D, C, S, S))).cuda()
     (out.real * g.real + out.imag * g.imag).sum().backward()
     adj = propagation.multidistance_adjoint(g, (H, W), wl, PITCH, dist, (S, S), float(S))
     assert rel_l2(f.grad.cpu().numpy(), adj.cpu().numpy()) < 1e-6

@@ -9,7 +9,7 @@ do not need the oracle's full render (which is too slow at these sizes):
 * render: fields and gradients finite, final_T in (0, 1], n_contrib no
   larger than the tile's list;
 * propagation at the configuration's grid: the adjoint identity
-  <A x, y> = <x, A^H y> (cfg4's 3840 grid runs the hipFFT path).
+  <A x, y> = <x, A^H y> (cfg4's 3840 grid runs the fused LDS-FFT passes).
 
 cfg4 (3M Gaussians at 1920x1080, ~8.7e8 pairs) also exercises the key/value
 sort path (tile and gaussian bits do not fit one 32-bit word)."""
@@ -124,7 +124,7 @@ def test_config_propagation_adjoint(hrf, name):
 
 def test_cfg3_propagation_microbench(hrf, oracle_mod):
     """Config 3 at full size: (3, 2048, 2048) fields to 8 log-spaced
-    distances on the 4096 grid (hipFFT transforms), forward and adjoint.
+    distances on the 4096 grid (fused LDS-FFT passes), forward and adjoint.
     One (distance, channel) output is checked against the oracle (numpy
     double-precision FFT); the full operator through the adjoint identity."""
     import torch
