@@ -57,27 +57,30 @@ def profiled_traffic(config, stage, C, M):
     return None, None
 
 
-# One wave64 VALU instruction per SIMD every 4 cycles: 256 CUs x 4 SIMDs x
-# 2.4 GHz / 4.
-VALU_PEAK_WAVE_INSTR_PER_S = 256 * 4 * 2.4e9 / 4
-
-
 def profiled_valu(config, stage, C, M):
-    """VALU wave-instructions per dispatch of `stage`'s kernel from the
-    committed rocprofv3 SQ_INSTS_VALU summary of this workload, or None."""
+    """(VALU wave-instructions, transcendental wave-instructions, issue peak
+    in wave-instructions/s) per dispatch of `stage`'s kernel from the
+    committed rocprofv3 summary of this workload, or None.  The peak is one
+    wave64 instruction per SIMD every 4 cycles at the shader clock the
+    summary measured on its calibration kernels (1024 SIMDs); a
+    transcendental holds its SIMD for two of those slots."""
     path = os.path.join(REPO, "profiles", f"valu_{config}.txt")
     name = STAGE_KERNEL.get(stage, "").format(C=C, M=M)
     if not name or not os.path.exists(path):
         return None
+    row, clock = None, None
     with open(path) as f:
         for line in f:
-            if line.startswith("#") or not line.startswith(name + " "):
-                continue
-            rest = line[len(name):].split()
-            # columns after the name: n, waves, valu, lds, salu, valu_us
-            if len(rest) >= 3:
-                return int(float(rest[2]))
-    return None
+            if line.startswith("clock_ghz "):
+                clock = float(line.split()[1])
+            elif not line.startswith("#") and line.startswith(name + " "):
+                # columns after the name: n, waves, valu, trans, salu, lds, ...
+                rest = line[len(name):].split()
+                if len(rest) >= 4:
+                    row = (int(float(rest[2])), int(float(rest[3])))
+    if row is None or clock is None:
+        return None
+    return row[0], row[1], 1024 * clock * 1e9 / 4
 
 
 def algorithmic_bytes(N, K, P, C, W, H, S, T):
@@ -600,11 +603,13 @@ def main():
     # against the measured launch time is the fraction that matters there.
     valu = {}
     for st in ("render_fwd", "render_bwd"):
-        instr = profiled_valu(spec.name, st, C, 2 * S)
+        prof = profiled_valu(spec.name, st, C, 2 * S)
         t_ms = dom_live if (st == dom and dom_live) else stages.get(st, {}).get("avg_launch_ms")
-        if instr and t_ms:
-            issue_ms = instr / VALU_PEAK_WAVE_INSTR_PER_S * 1e3
-            valu[st] = {"wave_instructions": instr, "issue_ms_at_peak": round(issue_ms, 4),
+        if prof and t_ms:
+            instr, trans, peak = prof
+            issue_ms = (instr + trans) / peak * 1e3
+            valu[st] = {"wave_instructions": instr, "transcendental": trans,
+                        "issue_ms_at_peak": round(issue_ms, 4), "peak_wave_instr_per_s": peak,
                         "measured_ms": round(t_ms, 4), "frac": round(issue_ms / t_ms, 3)}
     if valu:
         valu["source"] = f"profiles/valu_{spec.name}.txt"
