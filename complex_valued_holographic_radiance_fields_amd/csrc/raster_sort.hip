@@ -146,6 +146,61 @@ __global__ __launch_bounds__(kRowScanThreads) void k_radix_rowscan(
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+// Loads one wave's kRadixItems x 64 consecutive keys (and values) from
+// wbase on and ranks them: rank = the number of keys with the same digit
+// before it in the wave's range (the wave's LDS digit counters `cnt` carry
+// the count across the items), dig = its digit, or -1 past the end.  FULL:
+// the whole range is in bounds (no per-item tests).  The lanes holding the
+// same digit are found from one ballot per digit bit: ANDed over the bits,
+// the ballot where this lane's bit is set, its complement where it is clear
+// — b & ~(a ^ c) with a the ballot, b the running mask and c all ones or
+// zeros, one three-input bitwise instruction per 32-bit half (truth table
+// 0x84, symmetric in a and c).
+template <int RB, bool VALS, bool FULL>
+__device__ __forceinline__ void load_rank(const uint32_t* __restrict__ kin,
+                                          const uint32_t* __restrict__ vin, int64_t wbase,
+                                          int64_t n, int lane, uint64_t lt_mask, int shift,
+                                          uint32_t mask, uint32_t* cnt,
+                                          uint32_t (&key)[kRadixItems],
+                                          uint32_t (&val)[kRadixItems],
+                                          uint32_t (&rank)[kRadixItems],
+                                          int (&dig)[kRadixItems]) {
+  const uint32_t* kw = kin + wbase;
+  const uint32_t* vw = vin ? vin + wbase : nullptr;
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    const int o = it * 64 + lane;
+    const bool valid = FULL || wbase + o < n;
+    key[it] = valid ? kw[o] : 0u;
+    // vin == nullptr: the values are the element indices (first pass of a
+    // sort whose payload is the identity permutation).
+    if (VALS) val[it] = valid ? (vw ? vw[o] : static_cast<uint32_t>(wbase + o)) : 0u;
+  }
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    const int o = it * 64 + lane;
+    const bool valid = FULL || wbase + o < n;
+    const uint32_t d = valid ? (key[it] >> shift) & mask : 0u;
+    dig[it] = valid ? static_cast<int>(d) : -1;
+    const uint64_t vb = FULL ? ~0ull : __ballot(valid);
+    uint32_t lo = static_cast<uint32_t>(vb), hi = static_cast<uint32_t>(vb >> 32);
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const uint32_t bit = (d >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      const uint32_t m = 0u - bit;
+      lo = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(bb), lo, m, 0x84);
+      hi = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(bb >> 32), hi, m, 0x84);
+    }
+    const uint64_t peers = (static_cast<uint64_t>(hi) << 32) | lo;
+    const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
+    uint32_t prev = 0;
+    if (valid) prev = cnt[d];
+    rank[it] = prev + before;
+    if (valid && before == 0) cnt[d] = prev + static_cast<uint32_t>(__popcll(peers));
+  }
+}
+
 // Stable scatter of one partition, tile by tile.  In a tile, wave w owns
 // the contiguous sub-range [base + w*512, base + (w+1)*512) processed as 8
 // iterations of 64 keys; the rank of a key among equal digits before it is
@@ -212,34 +267,12 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const int nvalid = static_cast<int>(n - bbase < kRadixTile ? n - bbase : kRadixTile);
     uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
     int dig[kRadixItems];
-#pragma unroll
-    for (int it = 0; it < kRadixItems; ++it) {
-      const int64_t idx = wbase + it * 64 + lane;
-      const bool valid = idx < n;
-      key[it] = valid ? kin[idx] : 0u;
-      // vin == nullptr: the values are the element indices (first pass of a
-      // sort whose payload is the identity permutation).
-      if (VALS) val[it] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
-    }
-#pragma unroll
-    for (int it = 0; it < kRadixItems; ++it) {
-      const int64_t idx = wbase + it * 64 + lane;
-      const bool valid = idx < n;
-      const int d = valid ? static_cast<int>((key[it] >> shift) & mask) : 0;
-      dig[it] = valid ? d : -1;
-      uint64_t peers = __ballot(valid);
-#pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        const bool bit = (d >> b) & 1;
-        const uint64_t bb = __ballot(bit);
-        peers &= bit ? bb : ~bb;
-      }
-      const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
-      uint32_t prev = 0;
-      if (valid) prev = s_cnt[wave][d];
-      rank[it] = prev + before;
-      if (valid && before == 0) s_cnt[wave][d] = prev + static_cast<uint32_t>(__popcll(peers));
-    }
+    if (nvalid == kRadixTile)
+      load_rank<RB, VALS, true>(kin, vin, wbase, n, lane, lt_mask, shift, mask, s_cnt[wave], key,
+                                val, rank, dig);
+    else
+      load_rank<RB, VALS, false>(kin, vin, wbase, n, lane, lt_mask, shift, mask, s_cnt[wave], key,
+                                 val, rank, dig);
     __syncthreads();
     // Per digit: the counts of the lower waves (s_cnt becomes each wave's
     // local start), the tile total, and the exclusive scan over the digits
