@@ -185,9 +185,12 @@ __host__ __device__ constexpr int fwd_quads(int C) { return C == 1 ? 2 : 3; }
 // below 1e-4; lanes outside the image start at T = 0), so no separate flag
 // is carried.  Branch-free: lanes that are done (or, in the exact variant,
 // where the reference's power > 0 test skips the member) take alpha = 0,
-// which leaves T and the field exactly unchanged.  `lastj` becomes the
-// member's batch index j (a scalar) where the lane composites it; `real`
-// (scalar) is false for padding members.
+// which leaves T and the field exactly unchanged.  Exact variant: `lastj`
+// becomes the member's batch index j (a scalar) where the lane composites
+// it; `real` (scalar) is false for padding members.  Fast variant: `lastj`
+// counts the members evaluated while the lane was live (one add of the
+// live mask, no index select): a lane composites every member until the
+// one that ends it, so the count minus one is that member's index.
 template <int C, bool kExact>
 __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
                                            float pxf, float pyf, float& T,
@@ -208,7 +211,10 @@ __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const
     acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
   }
   T = T - sT;  // T (1 - alpha), reusing alpha T
-  lastj = (ok && (!kExact || real)) ? j : lastj;
+  if (kExact)
+    lastj = (ok && real) ? j : lastj;
+  else
+    lastj += ok ? 1 : 0;
 }
 
 template <int C>
@@ -305,19 +311,22 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     const bool live0 = !(T < kTermT);
     int lastj = -1;
     if (!exact) {
+      int evaluated = 0;
       for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
         if (__all(T < kTermT)) break;
 #pragma unroll
         for (int jj = 0; jj < kUnroll; ++jj) {
           const int j = j0 + jj;
           fwd_member<C, false>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf,
-                               pyf, T, acc, lastj, j, j < cnt);
+                               pyf, T, acc, evaluated, j, j < cnt);
         }
       }
       // A lane still running composited every member of the batch (no
       // power test could fail): the batch's last member is its last
-      // contributor.  One that terminated here did so at member lastj.
-      if (!(T < kTermT) && cnt > 0) lastj = cnt - 1;
+      // contributor.  One that terminated here composited members
+      // 0..evaluated-1 (padding follows every real member, so it ended on
+      // a real one).
+      lastj = !(T < kTermT) ? cnt - 1 : evaluated - 1;
     } else {
       for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
         if (__all(T < kTermT)) break;

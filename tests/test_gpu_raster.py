@@ -661,3 +661,28 @@ def test_forward_parity_dense_terminations(hrf, oracle_mod):
     # where the two sides terminate at the same member, n_contrib is equal
     both = term & (fT_h < 1e-4)
     assert np.mean(nc_h[both] != ref["n_contrib"][both]) < 1e-3
+
+
+def test_allocation_failure_then_recovery(hrf, oracle_mod):
+    """An allocation that cannot be satisfied (a 200000 x 200000 image: the
+    (P,C,H,W) field alone would be petabytes) raises RuntimeError at the
+    boundary before any kernel runs, as the reference's buffer resizes do
+    (rasterizer_splat.cu:217-222); the next, ordinary frame on the same
+    device is still exact."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import rasterizer, scenes
+
+    sc = _scene("small", 400, 64, 48, 2, 3, "object")
+    t = scenes.to_torch(sc)
+    print("allocation failure: 200000 x 200000 request", flush=True)
+    with pytest.raises(RuntimeError):
+        rasterizer.forward(t["cam_means"], t["z"], t["quats"], t["scales"], t["colours"],
+                           t["phase"], t["opac"], t["pprobs"], sc.fx, sc.fy, sc.px, sc.py,
+                           t["view"], (200_000, 200_000), (16, 16), 1.0, 1000.0)
+    torch.cuda.synchronize()
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    _, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
