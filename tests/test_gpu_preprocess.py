@@ -157,7 +157,8 @@ def test_autograd_function(hrf):
     leaves = [_t(a).requires_grad_(True) for a in prm[:7]]
     R, T = _t(prm[7]), _t(prm[8])
     out = preprocess.render_preprocess(*leaves, R, T, 1.0, 1000.0)
-    gs = [torch.randn_like(o) for o in out[:-1]]
+    gen = torch.Generator(device="cuda").manual_seed(14)
+    gs = [torch.randn(o.shape, device="cuda", generator=gen) for o in out[:-1]]
     sum((o * g).sum() for o, g in zip(out[:-1], gs)).backward()
     direct = preprocess.backward(gs, *[x.detach() for x in leaves], R, out[-1])
     for leaf, d in zip(leaves, direct):

@@ -221,7 +221,8 @@ def test_autograd_dropin(hrf):
     field, vis = pi.splat_tile_cuda(*leaves, sc.fx, sc.fy, sc.px, sc.py, t["view"], (64, 64),
                                     1.0, 1000.0)
     assert vis.dtype == torch.int64
-    g = torch.randn_like(field)
+    g = torch.randn(field.shape, dtype=field.dtype, device="cuda",
+                    generator=torch.Generator(device="cuda").manual_seed(15))
     (field.real * g.real + field.imag * g.imag).sum().backward()
     ras = pi.Rasterizer()
     out, info = ras.forward(*[x.detach() for x in leaves], sc.fx, sc.fy, sc.px, sc.py, t["view"],
