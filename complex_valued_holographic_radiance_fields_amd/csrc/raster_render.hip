@@ -93,56 +93,61 @@ __device__ __forceinline__ float alpha_threshold(float ow) {
   return 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
 }
 
-// min of q over x1 = mx - px in [xlo, xhi] at a fixed x2 = my - py (or the
-// same with the roles swapped): the 1-D minimiser of the convex quadratic,
-// clamped to the interval.  r11 = 1/a11 (hardware reciprocal): q at any
-// point of the interval bounds the minimum from above, and the minimiser's
-// rounding moves q by a11 (dx)^2, far inside the threshold's margin.
-__device__ __forceinline__ float edge_min(float a11, float a12, float a22, float r11, float x2,
-                                          float lo, float hi) {
-  const float x1 = fminf(fmaxf(-a12 * x2 * r11, lo), hi);
-  return x1 * (a11 * x1 + 2.0f * a12 * x2) + a22 * x2 * x2;
-}
-
-// A Gaussian's cull region q(d) <= thr: conic, reciprocals of its diagonal,
-// and the half-extents of the region's bounding box (widened by 0.01% +
-// 1e-3 px).  pd = false (not positive definite, or NaN): never culled.
+// Cull tests.  q(d) = cxx dx^2 + 2 cxy dx dy + czz dy^2 with d = mean -
+// pixel centre: a convex quadratic when the conic is positive definite.
+// CullShape holds the conic with 2 cxy and the two 1-D minimiser slopes
+// -cxy/cxx and -cxy/czz (hardware reciprocals).  pd = false (not positive
+// definite, or NaN): never culled.
 struct CullShape {
-  float cxx, cxy, czz, rxx, rzz, ex, ey;
+  float cxx, czz, t12, nx, nz;
   bool pd;
 };
 
-__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz, float thr) {
+__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz) {
   CullShape c;
   c.cxx = cxx;
-  c.cxy = cxy;
   c.czz = czz;
-  const float det = cxx * czz - cxy * cxy;
-  c.pd = cxx > 0.0f && czz > 0.0f && det > 0.0f;
-  const float rdet = __builtin_amdgcn_rcpf(det);
-  c.rxx = __builtin_amdgcn_rcpf(cxx);
-  c.rzz = __builtin_amdgcn_rcpf(czz);
-  c.ex = sqrtf(fmaxf(thr * czz * rdet, 0.0f)) * 1.0001f + 1e-3f;
-  c.ey = sqrtf(fmaxf(thr * cxx * rdet, 0.0f)) * 1.0001f + 1e-3f;
+  c.t12 = 2.0f * cxy;
+  c.pd = cxx > 0.0f && czz > 0.0f && cxx * czz - cxy * cxy > 0.0f;
+  c.nx = -cxy * __builtin_amdgcn_rcpf(cxx);
+  c.nz = -cxy * __builtin_amdgcn_rcpf(czz);
   return c;
 }
 
-// Exact test: does q(d) <= thr hold anywhere in the box of pixel centres
-// [x0, x0+ext] x [y0, y0+ext]?  Boxes outside the region's bounding box are
-// rejected first; q is convex, so if the mean is outside the box the
-// minimum over the box lies on one of its four edges.
+// min of q(u, v) = a u^2 + t u v + b v^2 over u in [lo, hi] at a fixed v:
+// the 1-D minimiser n v (n = -t / 2a), clamped to the interval.  q at any
+// point of the interval bounds the minimum from above, and the minimiser's
+// rounding moves q by a (du)^2, far inside the thresholds' margins.
+__device__ __forceinline__ float seg_min(float a, float b, float t, float n, float v, float lo,
+                                         float hi) {
+  const float u = fminf(fmaxf(n * v, lo), hi);
+  return fmaf(u, fmaf(a, u, t * v), (b * v) * v);
+}
+
+// Minimum of q over the box of pixel centres [x0, x0+ext] x [y0, y0+ext]
+// (0 when the mean lies in it).  A convex function's minimum over a box is
+// reached on the faces the mean lies beyond: the segment from the mean (q's
+// minimum) to any point of the box enters the box through one of them, and
+// q along it never exceeds its value at that point.  So it is the smaller
+// of the minima over the face x = clamp(mx, x0, x1) (over the box's dy
+// range) and the face y = clamp(my, y0, y1) (over its dx range); when the
+// mean lies within the box's range of a coordinate, that "face" is a line
+// through the box, whose minimum only bounds the box's from above.
+__device__ __forceinline__ float box_min(float mx, float my, const CullShape& c, float x0,
+                                         float y0, float ext) {
+  const float dxl = mx - (x0 + ext), dxh = mx - x0;
+  const float dyl = my - (y0 + ext), dyh = my - y0;
+  const float dxn = fminf(fmaxf(0.0f, dxl), dxh);  // mx - clamp(mx, x0, x1)
+  const float dyn = fminf(fmaxf(0.0f, dyl), dyh);
+  const float mv = seg_min(c.czz, c.cxx, c.t12, c.nz, dxn, dyl, dyh);
+  const float mh = seg_min(c.cxx, c.czz, c.t12, c.nx, dyn, dxl, dxh);
+  return fminf(mv, mh);
+}
+
+// Exact test: does q(d) <= thr hold at some point of that box?
 __device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape& c, float thr,
                                             float x0, float y0, float ext) {
-  if (!c.pd) return true;
-  const float x1 = x0 + ext, y1 = y0 + ext;
-  if (mx + c.ex < x0 || mx - c.ex > x1 || my + c.ey < y0 || my - c.ey > y1) return false;
-  if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return true;
-  const float dxl = mx - x1, dxh = mx - x0, dyl = my - y1, dyh = my - y0;
-  float m = edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyl, dxl, dxh);
-  m = fminf(m, edge_min(c.cxx, c.cxy, c.czz, c.rxx, dyh, dxl, dxh));
-  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxl, dyl, dyh));
-  m = fminf(m, edge_min(c.czz, c.cxy, c.cxx, c.rzz, dxh, dyl, dyh));
-  return m <= thr;
+  return !c.pd || box_min(mx, my, c, x0, y0, ext) <= thr;
 }
 
 // Forward members without effect.  A Gaussian whose alpha stays below 2^-26
@@ -271,7 +276,7 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       rq[1] = src[1];
       w = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
       const float thr = invisible_threshold(rq[1].z * w);
-      const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y, thr);
+      const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y);
       if (!box_reaches(rq[0].x, rq[0].y, cs, thr, tx0, ty0, static_cast<float>(kTile - 1))) {
         mem = false;
         atomicMax(&s_kcull, k + 1);
@@ -398,7 +403,10 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
   }
   const int tx = tile % p.gx, ty = tile / p.gx;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave is the same in every lane; read it as a scalar so that what is
+  // derived from it (and from the per-wave LDS counts below) stays scalar.
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int pxi = tx * kTile + (wave & 1) * 8 + (lane & 7);
   const int pyi = ty * kTile + (wave >> 1) * 8 + (lane >> 3);
   const bool inside = pxi < p.W && pyi < p.H;
@@ -484,7 +492,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
         const float thr = alpha_threshold(rq[1].z * wpl);
         if (thr >= 0.0f) {
-          const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y, thr);
+          const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float x0 = tx0 + (w & 1) * 8, y0 = ty0 + (w >> 1) * 8;
@@ -510,7 +518,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       tot[f] = 0;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const int c = s_cnt[w][f];
+        const int c = __builtin_amdgcn_readfirstlane(s_cnt[w][f]);  // same in every lane
         off[f] += (w < wave) ? c : 0;
         tot[f] += c;
       }
