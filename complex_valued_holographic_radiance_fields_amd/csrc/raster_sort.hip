@@ -592,81 +592,33 @@ __device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int6
   if (v && at < vo.vmax) vo.visible[at] = i;
 }
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit(const uint64_t* __restrict__ part_t,
-                                                      const uint64_t* __restrict__ part_r,
-                                                      const uint32_t* __restrict__ tiles,
-                                                      const uint32_t* __restrict__ order,
-                                                      const uint32_t* __restrict__ sorted_flag,
-                                                      const uint2* __restrict__ rect, int64_t n,
-                                                      int64_t k, int gx,
-                                                      uint32_t* __restrict__ keys,
-                                                      uint32_t* __restrict__ vals, VisibleOut vo) {
-  compact_visible_block(vo, n);
-  __shared__ uint64_t s_off[kEmitThreads + 1];
-  __shared__ uint32_t s_g[kEmitThreads];
-  __shared__ uint2 s_rect[kEmitThreads];
-  __shared__ uint64_t s_wave[kEmitThreads / 64];
-  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
-  const int64_t r = rb + threadIdx.x;
-  const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
-  block_offsets(part_t, part_r, tiles, order, sorted_flag, rb, nr, s_off, s_wave);
-  if (threadIdx.x < nr) {
-    const uint32_t g = ordered(order, sorted_flag, r);
-    s_g[threadIdx.x] = g;
-    s_rect[threadIdx.x] = rect[g];
-  }
-  __syncthreads();
-  // Pairs at or past k (the output length) are not written.
-  const uint64_t uk = static_cast<uint64_t>(k);
-  const uint64_t e0 = s_off[0], e1 = s_off[nr] < uk ? s_off[nr] : uk;
-  for (uint64_t e = e0 + threadIdx.x; e < e1; e += kEmitThreads) {
-    int lo = 0, hi = nr;  // s_off[lo] <= e < s_off[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= e)
-        lo = mid;
-      else
-        hi = mid;
-    }
-    const uint2 rc = s_rect[lo];
-    const uint32_t minx = rc.x & 0xFFFF, miny = rc.x >> 16, maxx = rc.y & 0xFFFF;
-    const uint32_t w = maxx - minx;
-    const uint32_t i = static_cast<uint32_t>(e - s_off[lo]);
-    const uint32_t ty = miny + i / w, tx = minx + i % w;
-    keys[e] = ty * static_cast<uint32_t>(gx) + tx;
-    vals[e] = s_g[lo];
-  }
-}
-
-// Packed emission: one word (tile << vbits) | gaussian per pair, in the same
-// order as k_emit.
-// Packed emission.  The block's pairs [e0, e1) (those of its kEmitThreads
-// Gaussians in rank order) are produced in chunks of kEmitChunk: each thread
-// takes kEmitPer consecutive pairs, finds the Gaussian and tile of its first
-// one (one binary search over the block's offsets, one division by the rect
-// width), then walks on (next tile in the rect, next Gaussian with pairs)
-// and stores the words in LDS (one pad word per kEmitPer, so the lanes'
-// strided stores hit distinct banks); the chunk then leaves in coalesced
-// stores.
+// The block's pairs [e0, e1) (those of its kEmitThreads Gaussians in rank
+// order) are produced in chunks of kEmitChunk: each thread takes kEmitPer
+// consecutive pairs, finds the Gaussian and tile of its first one (one
+// binary search over the block's offsets, one division by the rect width),
+// then walks on (next tile in the rect, next Gaussian with pairs) and stores
+// the pairs in LDS (one pad word per kEmitPer, so the lanes' strided stores
+// hit distinct banks); the chunk then leaves in coalesced stores.
+// kWide == false: one word (tile << vbits) | gaussian per pair into
+// `words`.  kWide: the tile id into `words` and the gaussian into `vals`
+// (tile and gaussian bits do not fit one word).
 constexpr int kEmitPer = 16;
 constexpr int kEmitChunk = kEmitThreads * kEmitPer;
 __device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
 
-__global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __restrict__ part_t,
-                                                             const uint64_t* __restrict__ part_r,
-                                                             const uint32_t* __restrict__ tiles,
-                                                             const uint32_t* __restrict__ order,
-                                                             const uint32_t* __restrict__ sorted_flag,
-                                                             const uint2* __restrict__ rect,
-                                                             int64_t n, int64_t k, int gx,
-                                                             int vbits,
-                                                             uint32_t* __restrict__ words,
-                                                             VisibleOut vo) {
+template <bool kWide>
+__global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
+    const uint64_t* __restrict__ part_t, const uint64_t* __restrict__ part_r,
+    const uint32_t* __restrict__ tiles, const uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ sorted_flag, const uint2* __restrict__ rect, int64_t n,
+    int64_t k, int gx, int vbits, uint32_t* __restrict__ words, uint32_t* __restrict__ vals,
+    VisibleOut vo) {
   compact_visible_block(vo, n);
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
   __shared__ uint32_t s_words[kEmitChunk + kEmitChunk / kEmitPer];
+  __shared__ uint32_t s_vals[kWide ? kEmitChunk + kEmitChunk / kEmitPer : 1];
   __shared__ uint64_t s_wave[kEmitThreads / 64];
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
   const int64_t r = rb + threadIdx.x;
@@ -717,7 +669,12 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
           ty = rc.x >> 16;
           gb = s_g[lo];
         }
-        s_words[emit_pad(j0 + j)] = ((ty * ugx + tx) << vbits) | gb;
+        if (kWide) {
+          s_words[emit_pad(j0 + j)] = ty * ugx + tx;
+          s_vals[emit_pad(j0 + j)] = gb;
+        } else {
+          s_words[emit_pad(j0 + j)] = ((ty * ugx + tx) << vbits) | gb;
+        }
         if (++tx == maxx) {
           tx = minx;
           ++ty;
@@ -725,7 +682,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(const uint64_t* __
       }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < clen; i += kEmitThreads) words[c0 + i] = s_words[emit_pad(i)];
+    for (int i = threadIdx.x; i < clen; i += kEmitThreads) {
+      words[c0 + i] = s_words[emit_pad(i)];
+      if (kWide) vals[c0 + i] = s_vals[emit_pad(i)];
+    }
     __syncthreads();
   }
 }
@@ -1075,8 +1035,9 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
                       int64_t* visible, int64_t vmax) {
   if (k <= 0 || n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
-  hipLaunchKernelGGL(k_emit, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s, part_t,
-                     part_r, tiles, order, sorted_flag, rect, n, k, gx, keys, vals, vo);
+  hipLaunchKernelGGL(k_emit_packed<true>, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads),
+                     0, s, part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, 0, keys,
+                     vals, vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1088,9 +1049,9 @@ int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uin
                        int64_t vmax) {
   if (n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
-  hipLaunchKernelGGL(k_emit_packed, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads), 0, s,
-                     part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, vbits, words,
-                     vo);
+  hipLaunchKernelGGL(k_emit_packed<false>, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads),
+                     0, s, part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, vbits, words,
+                     nullptr, vo);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
