@@ -12,7 +12,9 @@ do not need the oracle's full render (which is too slow at these sizes):
   <A x, y> = <x, A^H y> (cfg4's 3840 grid runs the fused LDS-FFT passes).
 
 cfg4 (3M Gaussians at 1920x1080, ~8.7e8 pairs) also exercises the key/value
-sort path (tile and gaussian bits do not fit one 32-bit word)."""
+sort path (tile and gaussian bits do not fit one 32-bit word); the headline
+geometry with larger Gaussians (2.4e7 pairs) runs the packed sort with several
+key tiles per scatter block."""
 import numpy as np
 import pytest
 
@@ -148,4 +150,36 @@ def test_cfg3_propagation_microbench(hrf, oracle_mod):
     rhs = torch.vdot(x.reshape(-1).to(torch.complex128), Ahy.reshape(-1).to(torch.complex128))
     assert float(abs(lhs - rhs) / abs(lhs)) < 1e-5
     del out, y, Ahy
+    torch.cuda.empty_cache()
+
+
+def test_packed_sort_partitioned(hrf, oracle_mod):
+    """The headline geometry with larger Gaussians (log-scale mean -3.5): K
+    above 2^24 pairs with tile and gaussian still in one 32-bit word, so the
+    packed sort's passes run with several 2048-key tiles per block and the
+    last pass writes point_list; binning checked exactly as above."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from complex_valued_holographic_radiance_fields_amd.frame import Frame
+
+    base = scenes.config("headline")
+    spec = scenes.SceneSpec("packed_big", 9, base.n, base.width, base.height, base.planes,
+                            base.wavelengths, base.distances, "object", log_scale_mean=-3.5)
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    pr = oracle_mod.project(g, cam)
+    _, tiles_ref, rect_ref = oracle_mod.preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
+    K = int(tiles_ref.astype(np.int64).sum())
+    print(f"packed_big: N={g.n} K={K}", flush=True)
+    assert K > (1 << 24)
+    t = scenes.to_torch(sc)
+    fr = Frame(t, spec, sc.fx, sc.fy, sc.px, sc.py)
+    fr.forward()
+    torch.cuda.synchronize()
+    fT, nc, pl, ranges, vis = fr.fwd_state
+    W, H = spec.width, spec.height
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    _check_binning(t, pl, ranges, tiles_ref, rect_ref, gx, gx * gy)
+    assert bool(((fT > 0) & (fT <= 1)).all())
+    del fr
     torch.cuda.empty_cache()
