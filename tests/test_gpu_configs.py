@@ -14,7 +14,8 @@ do not need the oracle's full render (which is too slow at these sizes):
 cfg4 (3M Gaussians at 1920x1080, ~8.7e8 pairs) also exercises the key/value
 sort path (tile and gaussian bits do not fit one 32-bit word); the headline
 geometry with larger Gaussians (2.4e7 pairs) runs the packed sort with several
-key tiles per scatter block."""
+key tiles per scatter block; a 160 x 125-tile grid with 150k Gaussians runs the
+key/value sort with ranges formed from the sorted tiles."""
 import numpy as np
 import pytest
 
@@ -179,6 +180,36 @@ def test_packed_sort_partitioned(hrf, oracle_mod):
     fT, nc, pl, ranges, vis = fr.fwd_state
     W, H = spec.width, spec.height
     gx, gy = (W + 15) // 16, (H + 15) // 16
+    _check_binning(t, pl, ranges, tiles_ref, rect_ref, gx, gx * gy)
+    assert bool(((fT > 0) & (fT <= 1)).all())
+    del fr
+    torch.cuda.empty_cache()
+
+
+def test_wide_sort_path_large_grid(hrf, oracle_mod):
+    """A tile grid beyond the difference array's bound (160 x 125 tiles) with
+    150k Gaussians: tile (15) and gaussian (18) bits exceed one word, so the
+    pairs go through the key/value sort and the ranges are formed from the
+    sorted tiles (the path the direct binning does not take); binning checked
+    exactly as above."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from complex_valued_holographic_radiance_fields_amd.frame import Frame
+
+    spec = scenes.SceneSpec("wide_grid", 11, 150_000, 2560, 2000, 1, [515e-9], [-2e-3],
+                            "uniform")
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    pr = oracle_mod.project(g, cam)
+    _, tiles_ref, rect_ref = oracle_mod.preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
+    print(f"wide_grid: N={g.n} K={int(tiles_ref.astype(np.int64).sum())}", flush=True)
+    t = scenes.to_torch(sc)
+    fr = Frame(t, spec, sc.fx, sc.fy, sc.px, sc.py)
+    fr.forward()
+    torch.cuda.synchronize()
+    fT, nc, pl, ranges, vis = fr.fwd_state
+    gx, gy = (spec.width + 15) // 16, (spec.height + 15) // 16
+    assert (gx + 1) * (gy + 1) > 16000
     _check_binning(t, pl, ranges, tiles_ref, rect_ref, gx, gx * gy)
     assert bool(((fT > 0) & (fT <= 1)).all())
     del fr
