@@ -448,7 +448,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     maxlast = max(maxlast, wmax[w]);
   }
 
-  float R = 0.0f, S_last = 0.0f, last_alpha = 0.0f;
+  float R = 0.0f, pend = 0.0f;
   const float half_w = 0.5f * static_cast<float>(p.W);
   const float half_h = 0.5f * static_cast<float>(p.H);
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
@@ -579,8 +579,11 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         const float alpha = fminf(kMaxAlpha, b.y * Gv);
         const bool ok = kk < last && !(pw > 0.0f) && alpha >= kMinAlphaBwd;
         any = any || ok;
-        T = ok ? T * __builtin_amdgcn_rcpf(1.0f - alpha) : T;
-        const float dcol = ok ? alpha * T : 0.0f;
+        // A member that does not contribute at this pixel takes alpha = 0:
+        // T * rcp(1) and 0 * x leave T and the partials exactly unchanged.
+        const float ae = ok ? alpha : 0.0f;
+        T = T * __builtin_amdgcn_rcpf(1.0f - ae);
+        const float dcol = ae * T;
         // Re(colour * conj(g)) summed over channels; the reference's complex
         // recurrence acc = la*last + (1-la)*acc is linear, so only its
         // projection R = sum_c Re(acc_c conj(g_c)) is carried.
@@ -597,11 +600,13 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
             S = fmaf(amp[2 * c + 1], gim[c], S);
           }
         }
-        const float Rn = fmaf(last_alpha, S_last - R, R);
-        R = ok ? Rn : R;
-        S_last = ok ? S : S_last;
-        last_alpha = ok ? alpha : last_alpha;
-        const float Q = ok ? Gv * ((S - R) * T) : 0.0f;
+        // The reference's recurrence acc = a_l S_l + (1 - a_l) acc over the
+        // contributing members: R advances by the pending a_l (S_l - R) of
+        // the previous contributor, and this member's becomes pending.
+        R += ok ? pend : 0.0f;
+        const float dS = S - R;
+        pend = ok ? alpha * dS : pend;
+        const float Q = (ok ? Gv : 0.0f) * (dS * T);
         const float Qdx = Q * dx, Qdy = Q * dy;
         // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v: the
         // flush forms them from these two sums and the member's conic
