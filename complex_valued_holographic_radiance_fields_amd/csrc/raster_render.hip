@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   if (threadIdx.x < NQ) {
     s_rec[kDummy * NQ + threadIdx.x] =
         threadIdx.x == 0   ? make_float4(1e6f, 1e6f, kBwdConicScale, 0.0f)
-        : threadIdx.x == 1 ? make_float4(kBwdConicScale, 0.0f, __int_as_float(0x7FFFFFFF), 0.0f)
+        : threadIdx.x == 1 ? make_float4(kBwdConicScale, 0.0f, __int_as_float(0x7FFFFFFF), 1.0f)
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
 
@@ -527,14 +527,17 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     const int cnt = tot[0];
     if (qm != 0u) {
       const int slot = off[0];
-      // quad 0: (mx, my, kc*cxx, kc*cxy); quad 1: (kc*czz, o*w, k, -) with
-      // kc = -log2(e)/2, so the exponent of G = exp2(.) is dx*u + dy*v with
-      // u = kc*(cxx dx + cxy dy) and v = kc*(cxy dx + czz dy).
+      // quad 0: (mx, my, kc*cxx, 2 kc*cxy); quad 1: (kc*czz, log2(o*w), k,
+      // o*w) with kc = -log2(e)/2, so pw = dx (kc cxx dx + 2 kc cxy dy) +
+      // kc czz dy^2 + log2(o w) is log2(e) * power + log2(o w) and
+      // exp2(pw) = o w G (the reference's backward exponent: one
+      // off-diagonal, doubled, backward_splat.cu:208-210).  Quad 1 also
+      // carries the list position (int bits) for the n_contrib test.
+      const float ow = rq[1].z * wpl;
       s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
-                                     kBwdConicScale * rq[0].w);
-      // quad 1 also carries the list position (int bits) for the n_contrib test
-      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, rq[1].z * wpl,
-                                         __int_as_float(k), 0.0f);
+                                     2.0f * kBwdConicScale * rq[0].w);
+      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, __builtin_amdgcn_logf(ow),
+                                         __int_as_float(k), ow);
       // Amplitude quads only for members that survived the cull (same
       // 64-byte record as quads 0-1, so the loads hit the cache).
 #pragma unroll
@@ -572,12 +575,11 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         const float4 b = s_rec[slot * NQ + 1];
         const int kk = __float_as_int(b.z);
         const float dx = a.x - pxf, dy = a.y - pyf;
-        const float u = fmaf(a.z, dx, a.w * dy);
-        const float v = fmaf(b.x, dy, a.w * dx);
-        const float pw = fmaf(dx, u, dy * v);  // = log2(e) * power
-        const float Gv = __builtin_amdgcn_exp2f(pw);
-        const float alpha = fminf(kMaxAlpha, b.y * Gv);
-        const bool ok = kk < last && !(pw > 0.0f) && alpha >= kMinAlphaBwd;
+        const float t = fmaf(a.z, dx, a.w * dy);
+        const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));  // log2(e) power + log2(o w)
+        const float Ga = __builtin_amdgcn_exp2f(pw);             // o w G
+        const float alpha = fminf(kMaxAlpha, Ga);
+        const bool ok = kk < last && !(pw > b.y) && alpha >= kMinAlphaBwd;
         any = any || ok;
         // A member that does not contribute at this pixel takes alpha = 0:
         // T * rcp(1) and 0 * x leave T and the partials exactly unchanged.
@@ -606,7 +608,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         R += ok ? pend : 0.0f;
         const float dS = S - R;
         pend = ok ? alpha * dS : pend;
-        const float Q = (ok ? Gv : 0.0f) * (dS * T);
+        const float Q = (ok ? Ga : 0.0f) * (dS * T);  // o w times dL/dG
         const float Qdx = Q * dx, Qdy = Q * dy;
         // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v: the
         // flush forms them from these two sums and the member's conic
@@ -639,28 +641,33 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       float val = s_acc[e];
       if (i < 2) {
         // sum Q u = kc cxx sum Q dx + kc cxy sum Q dy; sum Q v = kc cxy
-        // sum Q dx + kc czz sum Q dy (the staged conic is scaled by kc)
+        // sum Q dx + kc czz sum Q dy (the staged conic is scaled by kc, the
+        // off-diagonal doubled)
         const float4 a = s_rec[j * NQ];
         const float sx = s_acc[j * NV], sy = s_acc[j * NV + 1];
-        val = i == 0 ? fmaf(a.z, sx, a.w * sy) : fmaf(a.w, sx, s_rec[j * NQ + 1].x * sy);
+        const float kxy = 0.5f * a.w;
+        val = i == 0 ? fmaf(a.z, sx, kxy * sy) : fmaf(kxy, sx, s_rec[j * NQ + 1].x * sy);
       }
       if (val == 0.0f) continue;
       const int gg = s_g[j];
-      const float ow = s_rec[j * NQ + 1].y;
+      // The partials carry o w (Q = o w dL/dG): the mean and conic terms
+      // need exactly that factor, the o w term (sum G dL/dalpha) its
+      // removal.
+      const float ow = s_rec[j * NQ + 1].w;
       int slot;
       float scale;
       if (i == 0) {  // sum Q u, u = kc*(cxx dx + cxy dy)
         slot = 0;
-        scale = -half_w * ow / kBwdConicScale;
+        scale = -half_w / kBwdConicScale;
       } else if (i == 1) {
         slot = 1;
-        scale = -half_h * ow / kBwdConicScale;
+        scale = -half_h / kBwdConicScale;
       } else if (i < 5) {
         slot = i;
-        scale = -0.5f * ow;
+        scale = -0.5f;
       } else if (i == 5) {
         slot = 5 + 2 * C + plane;
-        scale = 1.0f;
+        scale = 1.0f / ow;
       } else {
         slot = i - 1;  // A_c at 5+c (i = 6+c), B_c at 5+C+c (i = 6+C+c)
         scale = 1.0f;
