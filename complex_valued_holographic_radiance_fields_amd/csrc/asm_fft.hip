@@ -38,8 +38,14 @@ namespace hrf {
 namespace {
 
 constexpr int kFftThreads = 512;   // column passes
-constexpr int kRowThreads = 1024;  // row passes (same LDS batch, twice the waves)
-constexpr int kFftBatch = 4;  // rows / columns per block
+constexpr int kFftBatch = 4;  // columns per column-pass block; columns of an intermediate tile
+// Rows per row-pass block and its threads: four rows in 1024 threads, two
+// in 512 for the longest transforms (N >= 3840), whose four-row batch
+// (147 KB of LDS) would leave one block per CU.
+template <int N>
+constexpr int kRowBatch = N >= 3840 ? 2 : 4;
+template <int N>
+constexpr int kRowThreads = 256 * kRowBatch<N>;
 // Column-pass threads and the occupancy they are compiled for: the longest
 // transforms (N >= 3840: a 138-147 KB LDS batch, one block per CU) run
 // twice the waves per block, which also halves each thread's share of the
@@ -227,13 +233,13 @@ struct Dft<7, INV> : DftOdd<7, INV> {};
 // first stage's loads at N = 160, 2016) the padded addresses stay a base
 // plus a compile-time offset.
 __device__ __forceinline__ constexpr int pad(int a) { return a + ((a >> 5) << 2); }
-template <int N>
+template <int N, int B = kFftBatch>
 constexpr int lds_elems() {
-  return pad(kFftBatch * N - 1) + 1;
+  return pad(B * N - 1) + 1;
 }
 // Elements per thread when a block copies its B x N batch.
-template <int N, int T = kFftThreads>
-constexpr int kCopyIters = (kFftBatch * N + T - 1) / T;
+template <int N, int T = kFftThreads, int B = kFftBatch>
+constexpr int kCopyIters = (B * N + T - 1) / T;
 
 // Twiddles are stored per stage, in the order the butterflies use them:
 // the stage with radix R after NS points have been combined holds
@@ -243,10 +249,10 @@ constexpr int kCopyIters = (kFftBatch * N + T - 1) / T;
 // address plus constant offsets.
 // HALF (first stage only, R = 8): the inputs at t = 0, 1, 6, 7 are zero and
 // are neither read nor stored by the caller.
-template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF = false>
+template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF, int B>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
   static_assert(!HALF || (R == 8 && NS == 1), "pruned first stage is radix 8");
-  constexpr int B = kFftBatch;
+  static_assert(B > 0 && (B & (B - 1)) == 0, "the batch is a power of two");
   constexpr int NR = N / R;
   constexpr int NB = B * NR;
   constexpr int BPT = (NB + T - 1) / T;
@@ -271,7 +277,7 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
     const int q = tid + u * T;
     ob[u] = -1;
     if (BPT * T == NB || q < NB) {
-      const int j = q >> 2;  // butterfly index within its transform
+      const int j = q / B;  // butterfly index within its transform
       const int k = j % NS;
       float2 x[R];
       if (lin_load) {
@@ -320,11 +326,11 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   __syncthreads();
 }
 
-template <int T, int N, bool INV, bool HALF, int NS, int OFF, int R, int... Rest>
+template <int T, int B, int N, bool INV, bool HALF, int NS, int OFF, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, R, NS, INV, OFF, T, HALF && NS == 1>(lds, tw);
+  fft_stage<N, R, NS, INV, OFF, T, HALF && NS == 1, B>(lds, tw);
   if constexpr (sizeof...(Rest) > 0)
-    run_stages<T, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
+    run_stages<T, B, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
 
 // The plans (radix sequence per length), shared by the device transforms
@@ -346,9 +352,9 @@ struct Plan;
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct Plan<NN> {                                                                 \
-    template <bool INV, int T = kFftThreads, bool HALF = false>                     \
+    template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<T, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                     \
+      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
     }                                                                               \
   };
 HRF_FFT_PLANS(HRF_FFT_PLAN)
@@ -435,33 +441,35 @@ __device__ __forceinline__ int64_t tile_off(int img, int ncb, int cb, int h, int
   return ((static_cast<int64_t>(img) * ncb + cb) * h + r) * B + b;
 }
 
-// A / A': forward FFT of B rows of a plain (nimg, h, w_in) image placed at
-// column c_in of the zero-padded N-length row -> tiled (nimg, h, N).
-// HALF: [c_in, c_in + w_in) lies in [N/4, 3N/4); only that half is staged
-// and the first stage is pruned.
+// A / A': forward FFT of kRowBatch rows of a plain (nimg, h, w_in) image
+// placed at column c_in of the zero-padded N-length row -> tiled (nimg, h,
+// N).  HALF: [c_in, c_in + w_in) lies in [N/4, 3N/4); only that half is
+// staged and the first stage is pruned.
 template <int N, bool HALF>
-__global__ __launch_bounds__(kRowThreads) void k_rows_in(const float2* __restrict__ src,
+__global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __restrict__ src,
                                                          float2* __restrict__ dst, int nimg,
                                                          int h, int w_in, int c_in,
                                                          const float2* __restrict__ tw) {
-  constexpr int B = kFftBatch;
-  constexpr int ncb = N / B;
-  __shared__ float2 lds[lds_elems<N>()];
+  constexpr int RB = kRowBatch<N>;  // rows (transforms) of this block
+  constexpr int T = kRowThreads<N>;
+  constexpr int TB = kFftBatch;     // columns of an intermediate tile
+  constexpr int ncb = N / TB;
+  __shared__ float2 lds[lds_elems<N, RB>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N, kRowThreads>(s_tw, tw);
-  const int blocks_per_img = (h + B - 1) / B;
+  const float2* twp = stage_twiddles<N, T>(s_tw, tw);
+  const int blocks_per_img = (h + RB - 1) / RB;
   const int img = blockIdx.x / blocks_per_img;
-  const int r0 = (blockIdx.x - img * blocks_per_img) * B;
+  const int r0 = (blockIdx.x - img * blocks_per_img) * RB;
   {
     // All of a thread's loads are issued before the first LDS write.
-    constexpr int E0 = HALF ? B * N / 4 : 0;
-    constexpr int EN = HALF ? B * N / 2 : B * N;
-    constexpr int IT = (EN + kRowThreads - 1) / kRowThreads;
+    constexpr int E0 = HALF ? RB * N / 4 : 0;
+    constexpr int EN = HALF ? RB * N / 2 : RB * N;
+    constexpr int IT = (EN + T - 1) / T;
     float2 v[IT];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * kRowThreads;
-      const int rr = e & 3, i = e >> 2;  // 16 lanes per row: 128-byte runs
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
+      const int rr = e % RB, i = e / RB;  // 64/RB lanes per row: 512/RB-byte runs
       const int r = r0 + rr;
       const int col = i - c_in;
       v[it] = make_float2(0.0f, 0.0f);
@@ -470,59 +478,64 @@ __global__ __launch_bounds__(kRowThreads) void k_rows_in(const float2* __restric
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * kRowThreads;
+      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
       if (e < E0 + EN) lds[pad(e)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<false, kRowThreads, HALF>(lds, twp);
-  for (int e = threadIdx.x; e < B * N; e += kRowThreads) {
-    const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
+  Plan<N>::template run<false, T, HALF, RB>(lds, twp);
+  // Tile cb's rows r0 .. r0 + RB - 1 are RB * TB consecutive words.
+  for (int e = threadIdx.x; e < RB * N; e += T) {
+    const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
     const int r = r0 + rr;
-    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, B)] = lds[pad(4 * (4 * cb + bc) + rr)];
+    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, TB)] = lds[pad(RB * (TB * cb + bc) + rr)];
   }
 }
 
-// C / C': inverse FFT of B rows of a tiled (nimg, h, N) spectrum; keeps
-// columns [c_out, c_out + w_out) times `scale` -> plain (nimg, h, w_out).
+// C / C': inverse FFT of kRowBatch rows of a tiled (nimg, h, N) spectrum;
+// keeps columns [c_out, c_out + w_out) times `scale` -> plain (nimg, h,
+// w_out).
 template <int N>
-__global__ __launch_bounds__(kRowThreads) void k_rows_out(const float2* __restrict__ src,
+__global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __restrict__ src,
                                                           float2* __restrict__ dst, int nimg,
                                                           int h, int w_out, int c_out,
                                                           float scale,
                                                           const float2* __restrict__ tw) {
-  constexpr int B = kFftBatch;
-  constexpr int ncb = N / B;
-  __shared__ float2 lds[lds_elems<N>()];
+  constexpr int RB = kRowBatch<N>;
+  constexpr int T = kRowThreads<N>;
+  constexpr int TB = kFftBatch;
+  constexpr int ncb = N / TB;
+  constexpr int IT = kCopyIters<N, T, RB>;
+  __shared__ float2 lds[lds_elems<N, RB>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
-  const float2* twp = stage_twiddles<N, kRowThreads>(s_tw, tw);
-  const int blocks_per_img = (h + B - 1) / B;
+  const float2* twp = stage_twiddles<N, T>(s_tw, tw);
+  const int blocks_per_img = (h + RB - 1) / RB;
   const int img = blockIdx.x / blocks_per_img;
-  const int r0 = (blockIdx.x - img * blocks_per_img) * B;
+  const int r0 = (blockIdx.x - img * blocks_per_img) * RB;
   {
-    float2 v[kCopyIters<N, kRowThreads>];
+    float2 v[IT];
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
-      const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
+    for (int it = 0; it < IT; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * T;
+      const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
       const int r = r0 + rr;
       v[it] = make_float2(0.0f, 0.0f);
-      if (e < B * N && r < h) v[it] = src[tile_off(img, ncb, cb, h, r, bc, B)];
+      if (e < RB * N && r < h) v[it] = src[tile_off(img, ncb, cb, h, r, bc, TB)];
     }
 #pragma unroll
-    for (int it = 0; it < kCopyIters<N, kRowThreads>; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * kRowThreads;
-      const int cb = e >> 4, rr = (e >> 2) & 3, bc = e & 3;
-      if (e < B * N) lds[pad(4 * (4 * cb + bc) + rr)] = v[it];
+    for (int it = 0; it < IT; ++it) {
+      const int e = static_cast<int>(threadIdx.x) + it * T;
+      const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
+      if (e < RB * N) lds[pad(RB * (TB * cb + bc) + rr)] = v[it];
     }
   }
   __syncthreads();
-  Plan<N>::template run<true, kRowThreads>(lds, twp);
-  for (int e = threadIdx.x; e < B * w_out; e += kRowThreads) {
-    const int rr = e & 3, i = e >> 2;
+  Plan<N>::template run<true, T, false, RB>(lds, twp);
+  for (int e = threadIdx.x; e < RB * w_out; e += T) {
+    const int rr = e % RB, i = e / RB;
     const int r = r0 + rr;
     if (r < h) {
-      const float2 v = lds[pad(4 * (c_out + i) + rr)];
+      const float2 v = lds[pad(RB * (c_out + i) + rr)];
       dst[(static_cast<int64_t>(img) * h + r) * w_out + i] = cscale(v, scale);
     }
   }
@@ -809,13 +822,13 @@ AsmFftConsts fft_consts(int P, int C, int M, double pitch, const float* wl, cons
 template <int N>
 int pass_rows_in(const float2* src, float2* X, int nimg, int h, int w, const float2* tw,
                  hipStream_t s) {
-  const int B = kFftBatch;
+  const int B = kRowBatch<N>;
   const dim3 grid(nimg * ((h + B - 1) / B));
   if (2 * w <= N)
-    hipLaunchKernelGGL((k_rows_in<N, true>), grid, dim3(kRowThreads), 0, s, src, X, nimg, h, w,
+    hipLaunchKernelGGL((k_rows_in<N, true>), grid, dim3(kRowThreads<N>), 0, s, src, X, nimg, h, w,
                        N / 2 - w / 2, tw);
   else
-    hipLaunchKernelGGL((k_rows_in<N, false>), grid, dim3(kRowThreads), 0, s, src, X, nimg, h, w,
+    hipLaunchKernelGGL((k_rows_in<N, false>), grid, dim3(kRowThreads<N>), 0, s, src, X, nimg, h, w,
                        N / 2 - w / 2, tw);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
@@ -825,9 +838,9 @@ int pass_rows_in(const float2* src, float2* X, int nimg, int h, int w, const flo
 template <int N>
 int pass_rows_out(const float2* Z, float2* dst, int nimg, int h, int w, const float2* tw,
                   hipStream_t s) {
-  const int B = kFftBatch;
+  const int B = kRowBatch<N>;
   const float scale = static_cast<float>(1.0 / (static_cast<double>(N) * N));
-  hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((h + B - 1) / B)), dim3(kRowThreads), 0, s, Z,
+  hipLaunchKernelGGL((k_rows_out<N>), dim3(nimg * ((h + B - 1) / B)), dim3(kRowThreads<N>), 0, s, Z,
                      dst, nimg, h, w, N / 2 - w / 2, scale, tw);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
