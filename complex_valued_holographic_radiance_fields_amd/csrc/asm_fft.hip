@@ -52,8 +52,13 @@ constexpr int kRowThreads = 256 * kRowBatch<N>;
 // per-element transfer state.
 template <int N>
 constexpr int kColThreads = N >= 3840 ? 1024 : kFftThreads;
+// Columns per column-pass block: two (half an intermediate tile) for the
+// longest transforms, whose four-column batch would take 147 KB of LDS
+// (one block per CU) and 16 spectrum and transfer entries per thread.
 template <int N>
-constexpr int kColMinBlocks = N <= 1600 ? 4 : (N <= 2048 ? 2 : 1);
+constexpr int kColBatch = N >= 3840 ? 2 : kFftBatch;
+template <int N>
+constexpr int kColMinBlocks = N <= 1600 ? 4 : 2;
 constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
 
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
@@ -563,16 +568,18 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int H, int r_pad, int S,
     int s_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw,
     int accumulate) {
-  constexpr int B = kFftBatch;
+  constexpr int B = kColBatch<N>;  // columns of this block
+  constexpr int TB = kFftBatch;    // columns of an intermediate tile
   constexpr int T = kColThreads<N>;
-  constexpr int ncb = N / B;
+  constexpr int ncb = N / TB;
   constexpr int EPT = (B * N + T - 1) / T;
-  __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 lds[lds_elems<N, B>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
-  int c, cb;
-  map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
-  const int k0 = cb * B;
+  int c, hb;
+  map_cblock(blockIdx.x, gridDim.x, &c, &hb, N / B);
+  const int cb = hb / (TB / B), col0 = (hb % (TB / B)) * B;  // tile, first column in it
+  const int k0 = hb * B;
 
   // kz of each owned element, or -1 where the aperture or the evanescent
   // cut zeroes the transfer function for every plane.
@@ -594,7 +601,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   }
   for (int p = 0; p < P; ++p) {
     __syncthreads();
-    const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
+    const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
     constexpr int E0 = HALF ? B * N / 4 : 0;
     constexpr int E1 = HALF ? 3 * B * N / 4 : B * N;
     // kz and acc are live here, so the copy keeps only kPlaneLoads loads in
@@ -608,7 +615,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
         const int e = e0 + u * T;
         const int r = e / B - r_pad;
         v[u] = make_float2(0.0f, 0.0f);
-        if (e < E1 && r >= 0 && r < H) v[u] = src[e - r_pad * B];
+        if (e < E1 && r >= 0 && r < H) v[u] = src[r * TB + e % B];
       }
 #pragma unroll
       for (int u = 0; u < kPlaneLoads; ++u) {
@@ -617,7 +624,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
       }
     }
     __syncthreads();
-    Plan<N>::template run<false, T, HALF>(lds, twp);
+    Plan<N>::template run<false, T, HALF, B>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -650,12 +657,15 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<true, T>(lds, twp);
-  float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, B);
+  Plan<N>::template run<true, T, false, B>(lds, twp);
+  float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
   if (accumulate) {
-    for (int e = threadIdx.x; e < B * S; e += T) dst[e] = cadd(dst[e], lds[pad(e + s_crop * B)]);
+    for (int e = threadIdx.x; e < B * S; e += T) {
+      const int o = (e / B) * TB + e % B;
+      dst[o] = cadd(dst[o], lds[pad(e + s_crop * B)]);
+    }
   } else {
-    for (int e = threadIdx.x; e < B * S; e += T) dst[e] = lds[pad(e + s_crop * B)];
+    for (int e = threadIdx.x; e < B * S; e += T) dst[(e / B) * TB + e % B] = lds[pad(e + s_crop * B)];
   }
 }
 
@@ -668,18 +678,20 @@ template <int N, bool HALF>
 __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
     const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int S, int s_pad, int H,
     int r_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw) {
-  constexpr int B = kFftBatch;
+  constexpr int B = kColBatch<N>;
+  constexpr int TB = kFftBatch;
   constexpr int T = kColThreads<N>;
-  constexpr int ncb = N / B;
+  constexpr int ncb = N / TB;
   constexpr int EPT = (B * N + T - 1) / T;
-  __shared__ float2 lds[lds_elems<N>()];
+  __shared__ float2 lds[lds_elems<N, B>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
-  int c, cb;
-  map_cblock(blockIdx.x, gridDim.x, &c, &cb, ncb);
-  const int k0 = cb * B;
+  int c, hb;
+  map_cblock(blockIdx.x, gridDim.x, &c, &hb, N / B);
+  const int cb = hb / (TB / B), col0 = (hb % (TB / B)) * B;
+  const int k0 = hb * B;
 
-  const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, B);
+  const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
   {
     constexpr int E0 = HALF ? B * N / 4 : 0;
     constexpr int EN = HALF ? B * N / 2 : B * N;
@@ -690,7 +702,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
       const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
       const int r = e / B - s_pad;
       v[it] = make_float2(0.0f, 0.0f);
-      if (e < E0 + EN && r >= 0 && r < S) v[it] = src[e - s_pad * B];
+      if (e < E0 + EN && r >= 0 && r < S) v[it] = src[r * TB + e % B];
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
@@ -699,7 +711,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
     }
   }
   __syncthreads();
-  Plan<N>::template run<false, T, HALF>(lds, twp);
+  Plan<N>::template run<false, T, HALF, B>(lds, twp);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
@@ -746,9 +758,9 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
       }
     }
     __syncthreads();
-    Plan<N>::template run<true, T>(lds, twp);
-    float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, B);
-    for (int e = threadIdx.x; e < B * H; e += T) dst[e] = lds[pad(e + r_crop * B)];
+    Plan<N>::template run<true, T, false, B>(lds, twp);
+    float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
+    for (int e = threadIdx.x; e < B * H; e += T) dst[(e / B) * TB + e % B] = lds[pad(e + r_crop * B)];
   }
 }
 
@@ -851,7 +863,7 @@ template <int N>
 int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
                  float ap, const AsmFftConsts& mc, const float2* tw, bool accumulate,
                  hipStream_t s) {
-  const dim3 grid(C * (N / kFftBatch)), block(kColThreads<N>);
+  const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
                        N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,
@@ -869,7 +881,7 @@ int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, 
 template <int N>
 int pass_col_adj(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
                  float ap, const AsmFftConsts& mc, const float2* tw, hipStream_t s) {
-  const dim3 grid(C * (N / kFftBatch)), block(kColThreads<N>);
+  const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_adj<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
                        N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw);
