@@ -52,11 +52,13 @@ constexpr int kRowThreads = 256 * kRowBatch<N>;
 // per-element transfer state.
 template <int N>
 constexpr int kColThreads = N >= 3840 ? 1024 : kFftThreads;
-// Columns per column-pass block: two (half an intermediate tile) for the
-// longest transforms, whose four-column batch would take 147 KB of LDS
-// (one block per CU) and 16 spectrum and transfer entries per thread.
+// Columns per column-pass block: two (half an intermediate tile) above
+// 1600 points, where a four-column batch takes 73-147 KB of LDS (one or two
+// blocks per CU) and, at 3840/4096, 16 spectrum and transfer entries per
+// thread (spilled); four at 1600 and below (two columns measured no faster
+// at 1600).
 template <int N>
-constexpr int kColBatch = N >= 3840 ? 2 : kFftBatch;
+constexpr int kColBatch = N > 1600 ? 2 : kFftBatch;
 template <int N>
 constexpr int kColMinBlocks = N <= 1600 ? 4 : 2;
 constexpr double kTwoPiD = 2.0 * 3.14159265358979323846;
