@@ -39,11 +39,11 @@ namespace {
 
 constexpr int kFftThreads = 512;   // column passes
 constexpr int kFftBatch = 4;  // columns per column-pass block; columns of an intermediate tile
-// Rows per row-pass block and its threads: four rows in 1024 threads, two
-// in 512 for the longest transforms (N >= 3840), whose four-row batch
-// (147 KB of LDS) would leave one block per CU.
+// Rows per row-pass block and its threads: four rows in 1024 threads up to
+// 1600 points, two in 512 above, where a four-row batch takes 73-147 KB of
+// LDS (two or one blocks per CU; two-row blocks measured slower at 1600).
 template <int N>
-constexpr int kRowBatch = N >= 3840 ? 2 : 4;
+constexpr int kRowBatch = N > 1600 ? 2 : 4;
 template <int N>
 constexpr int kRowThreads = 256 * kRowBatch<N>;
 // Column-pass threads and the occupancy they are compiled for: the longest
