@@ -588,13 +588,20 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   // rectangles in the geometry workspace (no pass over the sorted pairs);
   // the forward render copies them into `ranges`.
   const bool diff_ranges = tile_diff_fits(f.gx, f.gy);
+  // Large pair counts per Gaussian block: the emission also takes the first
+  // sort pass's histogram over its blocks.
+  SortFirstPass first{};
+  const int first_bits = radix_first_bits(end_bit);  // 0 without tile bits (one tile)
+  const bool first_fused =
+      first_bits > 0 && emit_first_pass(n, num_pairs, first_bits, b.radix, &first);
   if (end_bit + vbits <= 32) {
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_packed(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
                                  num_pairs, f.gx, vbits, b.keys_a, s, w.vis, w.part_v,
-                                 num_visible > 0 ? visible : nullptr, num_visible));
+                                 num_visible > 0 ? visible : nullptr, num_visible, b.radix,
+                                 first_fused ? &first : nullptr, vbits, first_bits));
     }
     bool in_b = false;
     // The last sort pass writes the gaussian bits straight into point_list;
@@ -606,7 +613,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
       HRF_STAGE("tile_sort", s);
       HRF_TRY(radix_sort_keys(b.keys_a, b.keys_b, num_pairs, vbits, end_bit, b.radix, &in_b, s,
                               fused ? reinterpret_cast<uint32_t*>(point_list) : nullptr,
-                              (1u << vbits) - 1u));
+                              (1u << vbits) - 1u, first_fused ? &first : nullptr));
     }
     if (!fused) {
       HRF_STAGE("ranges", s);
@@ -621,14 +628,16 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
       HRF_STAGE("emit", s);
       HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
                                 num_pairs, f.gx, b.keys_a, vals_a, s, w.vis, w.part_v,
-                                num_visible > 0 ? visible : nullptr, num_visible));
+                                num_visible > 0 ? visible : nullptr, num_visible, b.radix,
+                                first_fused ? &first : nullptr, 0, first_bits));
     }
     bool in_b = false;
     {
       HRF_STAGE("tile_sort", s);
       // The sorted tile ids are only needed to form the ranges from them.
       HRF_TRY(radix_sort_pairs(b.keys_a, vals_a, b.keys_b, vals_b, num_pairs, end_bit, b.radix,
-                               &in_b, s, nullptr, false, !diff_ranges));
+                               &in_b, s, nullptr, false, !diff_ranges,
+                               first_fused ? &first : nullptr));
     }
     const uint32_t* sorted_keys = in_b ? b.keys_b : b.keys_a;
     // The sorted values must end in point_list whatever the pass count did

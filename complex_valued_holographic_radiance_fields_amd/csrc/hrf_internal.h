@@ -234,10 +234,18 @@ size_t radix_scratch_elems(int64_t n);
 // ones last).  With index_values, the values are taken to be 0..n-1 (va is
 // only used as a buffer).  keys_needed == false: the last pass writes only
 // the values (the sorted keys are then left nowhere).
+// A first sort pass whose histogram the pair emission took: np partitions
+// (the emission blocks), partition b being pairs [bounds[b], bounds[b + 1]),
+// the counts already in the sort scratch (digit-major, np columns).
+struct SortFirstPass {
+  int np;
+  const int64_t* bounds;
+};
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
                      hipStream_t s, const uint32_t* run_flag = nullptr,
-                     bool index_values = false, bool keys_needed = true);
+                     bool index_values = false, bool keys_needed = true,
+                     const SortFirstPass* first = nullptr);
 int radix_passes(int end_bit);
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
 // (the other bits ride along unsorted), in ceil(nbits/8) passes with the
@@ -246,7 +254,17 @@ int radix_passes(int end_bit);
 // word & final_mask there instead of into the ping-pong buffers.
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s,
-                    uint32_t* final_out = nullptr, uint32_t final_mask = 0xFFFFFFFFu);
+                    uint32_t* final_out = nullptr, uint32_t final_mask = 0xFFFFFFFFu,
+                    const SortFirstPass* first = nullptr);
+// Whether the pair emission of n Gaussians and k pairs takes the first
+// tile-sort pass's histogram (of `bits` digit bits): only when its blocks
+// average many sort tiles of pairs (with ~1-2 tiles per block the partial
+// tiles of such partitions would cost the scatter what the histogram
+// saves) and the spine and partition bounds fit `scratch` (radix scratch
+// for k keys).  Fills *first (its bounds inside the scratch) when so.
+bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirstPass* first);
+// Digit bits of the first pass of a sort over nbits bits (the narrowest).
+int radix_first_bits(int nbits);
 
 // Tile ranges from the Gaussians' tile rectangles (tiles[g] > 0 marks a
 // rectangle) instead of the sorted pairs: a 2-D difference array of
@@ -290,7 +308,9 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
                       hipStream_t s, const uint32_t* vis = nullptr,
                       const uint32_t* part_v = nullptr, int64_t* visible = nullptr,
-                      int64_t vmax = 0);
+                      int64_t vmax = 0, uint32_t* scratch = nullptr,
+                      const SortFirstPass* first = nullptr, int first_shift = 0,
+                      int first_bits = 0);
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.
@@ -298,7 +318,9 @@ int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uin
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                        int64_t n, int64_t k, int gx, int vbits, uint32_t* words, hipStream_t s,
                        const uint32_t* vis = nullptr, const uint32_t* part_v = nullptr,
-                       int64_t* visible = nullptr, int64_t vmax = 0);
+                       int64_t* visible = nullptr, int64_t vmax = 0,
+                       uint32_t* scratch = nullptr, const SortFirstPass* first = nullptr,
+                       int first_shift = 0, int first_bits = 0);
 int launch_unpack_ranges(const uint32_t* words, int64_t k, int vbits, int32_t* point_list,
                          int32_t* ranges, int ntiles, hipStream_t s);
 int64_t partial_elems(int64_t n);  // kProjThreads-blocks + 1

@@ -218,7 +218,8 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
     uint32_t mask, const uint32_t* __restrict__ hist_scan,
     const uint32_t* __restrict__ digit_totals, int nparts, int sub,
-    const uint32_t* __restrict__ run_flag, uint32_t out_mask) {
+    const uint32_t* __restrict__ run_flag, uint32_t out_mask,
+    const int64_t* __restrict__ bounds) {
   constexpr int kBins = 1 << RB;
   static_assert(kBins <= kRadixThreads, "one thread per digit");
   if (run_flag && *run_flag == 0u) return;
@@ -253,9 +254,19 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
   }
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-  for (int t = 0; t < sub; ++t) {
-    const int64_t bbase = (static_cast<int64_t>(blockIdx.x) * sub + t) * kRadixTile;
-    if (bbase >= n) break;  // same for every thread of the block
+  // This block's partition [pstart, pend): sub tiles from blockIdx.x * sub,
+  // or the range `bounds` gives (the emission block's pairs).
+  int64_t pstart, pend;
+  if (bounds) {
+    pstart = bounds[blockIdx.x] < n ? bounds[blockIdx.x] : n;
+    pend = bounds[blockIdx.x + 1] < n ? bounds[blockIdx.x + 1] : n;
+  } else {
+    pstart = static_cast<int64_t>(blockIdx.x) * sub * kRadixTile;
+    pend = pstart + static_cast<int64_t>(sub) * kRadixTile < n
+               ? pstart + static_cast<int64_t>(sub) * kRadixTile
+               : n;
+  }
+  for (int64_t bbase = pstart; bbase < pend; bbase += kRadixTile) {  // uniform
     // Also orders the previous tile's reads of s_key/s_delta/s_wsum before
     // this tile's writes.
     __syncthreads();
@@ -264,15 +275,15 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     __syncthreads();
 
     const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
-    const int nvalid = static_cast<int>(n - bbase < kRadixTile ? n - bbase : kRadixTile);
+    const int nvalid = static_cast<int>(pend - bbase < kRadixTile ? pend - bbase : kRadixTile);
     uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
     int dig[kRadixItems];
     if (nvalid == kRadixTile)
-      load_rank<RB, VALS, true>(kin, vin, wbase, n, lane, lt_mask, shift, mask, s_cnt[wave], key,
-                                val, rank, dig);
+      load_rank<RB, VALS, true>(kin, vin, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave],
+                                key, val, rank, dig);
     else
-      load_rank<RB, VALS, false>(kin, vin, wbase, n, lane, lt_mask, shift, mask, s_cnt[wave], key,
-                                 val, rank, dig);
+      load_rank<RB, VALS, false>(kin, vin, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave],
+                                 key, val, rank, dig);
     __syncthreads();
     // Per digit: the counts of the lower waves (s_cnt becomes each wave's
     // local start), the tile total, and the exclusive scan over the digits
@@ -606,14 +617,33 @@ constexpr int kEmitPer = 16;
 constexpr int kEmitChunk = kEmitThreads * kEmitPer;
 __device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
 
-template <bool kWide>
+// Optional first sort pass histogram taken by the emission: each emission
+// block is then one partition of that pass (its pairs [e0, e1)).  hist
+// (digit-major, gridDim.x columns) receives the block's counts of digit
+// (key >> shift) & mask; bounds[b] the block's first pair, bounds[gridDim.x]
+// the pair count.
+struct EmitHist {
+  uint32_t* hist;  // nullptr: no histogram
+  int64_t* bounds;
+  int shift;
+  uint32_t mask;
+  int rows;  // digit rows of the pass's histogram (2^RB >= mask + 1; the rest are zero)
+};
+
+template <bool kWide, bool kHist>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
     const uint64_t* __restrict__ part_t, const uint64_t* __restrict__ part_r,
     const uint32_t* __restrict__ tiles, const uint32_t* __restrict__ order,
     const uint32_t* __restrict__ sorted_flag, const uint2* __restrict__ rect, int64_t n,
     int64_t k, int gx, int vbits, uint32_t* __restrict__ words, uint32_t* __restrict__ vals,
-    VisibleOut vo) {
+    VisibleOut vo, EmitHist eh) {
   compact_visible_block(vo, n);
+  __shared__ uint32_t s_dh[kHist ? kEmitThreads / 64 : 1][kHist ? kRadixBins : 1];
+  const int wave = threadIdx.x >> 6;
+  if (kHist) {
+    for (int e = threadIdx.x; e < (kEmitThreads / 64) * kRadixBins; e += kEmitThreads)
+      s_dh[e / kRadixBins][e % kRadixBins] = 0u;
+  }
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
@@ -683,10 +713,26 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
     }
     __syncthreads();
     for (int i = threadIdx.x; i < clen; i += kEmitThreads) {
-      words[c0 + i] = s_words[emit_pad(i)];
+      const uint32_t w = s_words[emit_pad(i)];
+      words[c0 + i] = w;
       if (kWide) vals[c0 + i] = s_vals[emit_pad(i)];
+      if (kHist) atomicAdd(&s_dh[wave][(w >> eh.shift) & eh.mask], 1u);
     }
     __syncthreads();
+  }
+  if (kHist) {
+    for (int d = threadIdx.x; d < eh.rows; d += kEmitThreads) {
+      uint32_t c = 0;
+      if (d <= static_cast<int>(eh.mask)) {
+#pragma unroll
+        for (int w = 0; w < kEmitThreads / 64; ++w) c += s_dh[w][d];
+      }
+      eh.hist[static_cast<int64_t>(d) * gridDim.x + blockIdx.x] = c;
+    }
+    if (threadIdx.x == 0) {
+      eh.bounds[blockIdx.x] = static_cast<int64_t>(e0);
+      if (blockIdx.x == gridDim.x - 1) eh.bounds[gridDim.x] = k;
+    }
   }
 }
 
@@ -863,19 +909,25 @@ int radix_parts(int64_t n, RadixParts* p) {
 template <int RB, bool VALS>
 int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
                int64_t n, const RadixParts& rp, int shift, uint32_t mask, uint32_t* scratch,
-               const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu) {
-  const int64_t hist_n = static_cast<int64_t>(rp.np) << RB;
+               const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu,
+               const SortFirstPass* fp = nullptr) {
+  // fp: the histogram is in the scratch already (taken by the pair
+  // emission over its blocks, which are this pass's partitions).
+  const int np = fp ? fp->np : rp.np;
+  const int64_t hist_n = static_cast<int64_t>(np) << RB;
   uint32_t* hist = scratch;
   uint32_t* totals = scratch + hist_n;
-  hipLaunchKernelGGL(k_radix_hist<RB>, dim3(rp.np), dim3(kRadixThreads), 0, s, src_k, n, shift,
-                     mask, hist, rp.np, rp.sub, run_flag);
-  HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, rp.np,
+  if (!fp) {
+    hipLaunchKernelGGL(k_radix_hist<RB>, dim3(rp.np), dim3(kRadixThreads), 0, s, src_k, n, shift,
+                       mask, hist, rp.np, rp.sub, run_flag);
+    HRF_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, np,
                      totals, run_flag);
   HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(rp.np), dim3(kRadixThreads), 0, s,
-                     src_k, src_v, dst_k, dst_v, n, shift, mask, hist, totals, rp.np, rp.sub,
-                     run_flag, out_mask);
+  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(np), dim3(kRadixThreads), 0, s, src_k,
+                     src_v, dst_k, dst_v, n, shift, mask, hist, totals, np, rp.sub, run_flag,
+                     out_mask, fp ? fp->bounds : nullptr);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -895,24 +947,24 @@ template <bool VALS>
 int radix_pass_bits(int bits, const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k,
                     uint32_t* dst_v, int64_t n, const RadixParts& rp, int shift,
                     uint32_t* scratch, const uint32_t* run_flag, hipStream_t s,
-                    uint32_t out_mask = 0xFFFFFFFFu) {
+                    uint32_t out_mask = 0xFFFFFFFFu, const SortFirstPass* fp = nullptr) {
   const uint32_t mask = (1u << bits) - 1u;
   switch (bits) {
     case 1: case 2: case 3: case 4:
       return radix_pass<4, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask);
+                                 run_flag, s, out_mask, fp);
     case 5:
       return radix_pass<5, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask);
+                                 run_flag, s, out_mask, fp);
     case 6:
       return radix_pass<6, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask);
+                                 run_flag, s, out_mask, fp);
     case 7:
       return radix_pass<7, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask);
+                                 run_flag, s, out_mask, fp);
     case 8:
       return radix_pass<8, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask);
+                                 run_flag, s, out_mask, fp);
     default:
       set_error("internal: radix digit of %d bits", bits);
       return HRF_ERR_INVALID;
@@ -923,7 +975,8 @@ int radix_pass_bits(int bits, const uint32_t* src_k, const uint32_t* src_v, uint
 
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int64_t n,
                      int end_bit, uint32_t* scratch, bool* result_in_b, hipStream_t s,
-                     const uint32_t* run_flag, bool index_values, bool keys_needed) {
+                     const uint32_t* run_flag, bool index_values, bool keys_needed,
+                     const SortFirstPass* first) {
   *result_in_b = false;
   if (n <= 1) return HRF_OK;
   if (end_bit < 1 || end_bit > 32) {
@@ -940,7 +993,7 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
     const uint32_t* vin = (pass == 0 && index_values) ? nullptr : src_v;
     uint32_t* kout = (pass == passes - 1 && !keys_needed) ? nullptr : dst_k;
     HRF_TRY(radix_pass_bits<true>(bits, src_k, vin, kout, dst_v, n, rp, done, scratch, run_flag,
-                                  s));
+                                  s, 0xFFFFFFFFu, pass == 0 ? first : nullptr));
     done += bits;
     uint32_t* tk = src_k;
     uint32_t* tv = src_v;
@@ -955,7 +1008,7 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
 
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s, uint32_t* final_out,
-                    uint32_t final_mask) {
+                    uint32_t final_mask, const SortFirstPass* first) {
   *result_in_b = false;
   if (n <= 1 || nbits <= 0) {
     if (final_out) {
@@ -975,7 +1028,7 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
     uint32_t* out = last ? final_out : dst;
     const uint32_t om = last ? final_mask : 0xFFFFFFFFu;
     HRF_TRY(radix_pass_bits<false>(bits, src, nullptr, out, nullptr, n, rp, lo_bit + done,
-                                   scratch, nullptr, s, om));
+                                   scratch, nullptr, s, om, pass == 0 ? first : nullptr));
     done += bits;
     uint32_t* t = src;
     src = dst;
@@ -1028,16 +1081,53 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
   return HRF_OK;
 }
 
+namespace {
+// Minimum average pairs per emission block for the emission to take the
+// first sort pass's histogram: 16 sort tiles.
+constexpr int64_t kFirstPassMinPairs = 16 * static_cast<int64_t>(kRadixTile);
+int digit_template_bits(int bits) { return bits <= 4 ? 4 : bits; }
+// Offset of the partition bounds in the sort scratch: after the spine and
+// the digit totals (at most kRadixBins), 8-byte aligned.
+int64_t first_bounds_off(int64_t np, int bits) {
+  return ((np << digit_template_bits(bits)) + kRadixBins + 1) & ~int64_t(1);
+}
+EmitHist emit_hist_of(uint32_t* scratch, const SortFirstPass* first, int shift, int bits) {
+  if (!first) return EmitHist{nullptr, nullptr, 0, 0u, 0};
+  return EmitHist{scratch, const_cast<int64_t*>(first->bounds), shift, (1u << bits) - 1u,
+                  1 << digit_template_bits(bits)};
+}
+}  // namespace
+
+int radix_first_bits(int nbits) { return nbits > 0 ? nbits / radix_passes(nbits) : 0; }
+
+bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirstPass* first) {
+  if (n <= 0 || k <= 1 || bits < 1 || bits > 8 || !scratch) return false;
+  const int64_t np = blocks_for(n, kEmitThreads);
+  if (k / np < kFirstPassMinPairs || np > 0x7FFFFFFF) return false;
+  const int64_t need = first_bounds_off(np, bits) + 2 * (np + 1);
+  if (need > static_cast<int64_t>(radix_scratch_elems(k))) return false;
+  first->np = static_cast<int>(np);
+  first->bounds = reinterpret_cast<const int64_t*>(scratch + first_bounds_off(np, bits));
+  return true;
+}
+
 int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint32_t* tiles,
                       const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                       int64_t n, int64_t k, int gx, uint32_t* keys, uint32_t* vals,
                       hipStream_t s, const uint32_t* vis, const uint32_t* part_v,
-                      int64_t* visible, int64_t vmax) {
+                      int64_t* visible, int64_t vmax, uint32_t* scratch,
+                      const SortFirstPass* first, int first_shift, int first_bits) {
   if (k <= 0 || n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
-  hipLaunchKernelGGL(k_emit_packed<true>, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads),
-                     0, s, part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, 0, keys,
-                     vals, vo);
+  const EmitHist eh = emit_hist_of(scratch, first, first_shift, first_bits);
+  if (eh.hist)
+    hipLaunchKernelGGL((k_emit_packed<true, true>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, 0, keys, vals, vo, eh);
+  else
+    hipLaunchKernelGGL((k_emit_packed<true, false>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, 0, keys, vals, vo, eh);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1046,12 +1136,19 @@ int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uin
                        const uint32_t* order, const uint32_t* sorted_flag, const uint2* rect,
                        int64_t n, int64_t k, int gx, int vbits, uint32_t* words, hipStream_t s,
                        const uint32_t* vis, const uint32_t* part_v, int64_t* visible,
-                       int64_t vmax) {
+                       int64_t vmax, uint32_t* scratch, const SortFirstPass* first,
+                       int first_shift, int first_bits) {
   if (n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
-  hipLaunchKernelGGL(k_emit_packed<false>, dim3(blocks_for(n, kEmitThreads)), dim3(kEmitThreads),
-                     0, s, part_t, part_r, tiles, order, sorted_flag, rect, n, k, gx, vbits, words,
-                     nullptr, vo);
+  const EmitHist eh = emit_hist_of(scratch, first, first_shift, first_bits);
+  if (eh.hist)
+    hipLaunchKernelGGL((k_emit_packed<false, true>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, vbits, words, nullptr, vo, eh);
+  else
+    hipLaunchKernelGGL((k_emit_packed<false, false>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, vbits, words, nullptr, vo, eh);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
