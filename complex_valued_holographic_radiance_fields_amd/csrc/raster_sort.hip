@@ -8,6 +8,8 @@
 // stable-sorted once by depth' (4 passes over N), pairs are emitted in that
 // rank order, and a stable sort by tile id alone (ceil(log2 T / 8) passes,
 // 2 for T <= 65536) finishes the job: same order, far fewer bytes moved.
+#include <type_traits>
+
 #include "hrf_internal.h"
 
 namespace hrf {
@@ -17,10 +19,16 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanThreads * kScanItems;  // elements per block
 
+constexpr int kRadixItems = 8;  // keys per thread and tile
+// Block size of the radix kernels: 256 threads (2048-key tiles), or 1024
+// (8192-key tiles) for sorts of at least kRadixLargeMinKeys keys.  Longer
+// tiles give longer output runs per digit, which memory writes more
+// efficiently (8.7e8 pairs: 9.6 -> 7.9 ms for the two passes), but fewer,
+// longer blocks cost the smaller sorts (1.1e7 pairs: 101 -> 116 us).
 constexpr int kRadixThreads = 256;
-constexpr int kRadixWaves = kRadixThreads / 64;
-constexpr int kRadixItems = 8;  // per thread
-constexpr int kRadixTile = kRadixThreads * kRadixItems;
+constexpr int kRadixThreadsLarge = 1024;
+constexpr int64_t kRadixLargeMinKeys = int64_t{1} << 26;
+constexpr int kRadixTile = kRadixThreads * kRadixItems;  // the smaller tile
 constexpr int kRadixBins = 256;
 // Partitioning of the radix passes: one tile per block up to
 // kRadixTargetParts tiles, beyond that up to kRadixMaxSub tiles per block.
@@ -32,6 +40,12 @@ constexpr int kDiffItems = 4;    // Gaussians per thread per step, loads issued 
 constexpr int kDiffBlocks = 256;
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+// A value that is the same in every lane, moved to scalar registers.
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 // Exclusive block scan of one value per thread (wave64 shuffles + LDS).
 template <typename T>
@@ -59,53 +73,54 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
 
 // ----------------------------------------------------------- radix sort --
 
-// The keys are cut into partitions of `sub` consecutive kRadixTile tiles
-// (sub grows with n so that the partition count stays near
-// kRadixTargetParts): the histogram spine is [digit][partition], small
-// enough that its scan is a few coalesced block scans, and the scatter
-// block of a partition walks its tiles in order carrying each digit's
-// running output offset.
+// The keys are cut into partitions of `sub` consecutive tiles of
+// kRadixItems keys per thread of the block (sub grows with n so that the
+// partition count stays near kRadixTargetParts): the histogram spine is
+// [digit][partition], small enough that its scan is a few coalesced block
+// scans, and the scatter block of a partition walks its tiles in order
+// carrying each digit's running output offset.
 
 // Digit histogram of each partition: digit = (key >> shift) & mask with at
 // most 2^RB values; one LDS histogram per wave (fewer same-address atomic
 // collisions between the waves), summed at the end.  hist is digit-major
 // ([digit][partition]): a scan along each digit's row plus the totals of
 // the lower digits give every (digit, partition) output offset.
-template <int RB>
-__global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
+template <int RB, int TH>
+__global__ __launch_bounds__(TH) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
                                                               uint32_t mask,
                                                               uint32_t* __restrict__ hist,
                                                               int nparts, int sub,
                                                               const uint32_t* __restrict__ run_flag) {
   constexpr int kBins = 1 << RB;
+  constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_hist[kRadixWaves][kBins];
-  for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
+  __shared__ uint32_t s_hist[kWaves][kBins];
+  for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
     s_hist[e / kBins][e % kBins] = 0;
   __syncthreads();
   const int wave = threadIdx.x >> 6;
-  const int64_t pbase = static_cast<int64_t>(blockIdx.x) * sub * kRadixTile;
+  const int64_t pbase = static_cast<int64_t>(blockIdx.x) * sub * kTile;
   for (int t = 0; t < sub; ++t) {
-    const int64_t base = pbase + static_cast<int64_t>(t) * kRadixTile;
+    const int64_t base = pbase + static_cast<int64_t>(t) * kTile;
     if (base >= n) break;
     uint32_t k[kRadixItems];
 #pragma unroll
     for (int i = 0; i < kRadixItems; ++i) {
-      const int64_t idx = base + i * kRadixThreads + threadIdx.x;
+      const int64_t idx = base + i * TH + threadIdx.x;
       k[i] = idx < n ? keys[idx] : 0u;
     }
 #pragma unroll
     for (int i = 0; i < kRadixItems; ++i) {
-      const int64_t idx = base + i * kRadixThreads + threadIdx.x;
+      const int64_t idx = base + i * TH + threadIdx.x;
       if (idx < n) atomicAdd(&s_hist[wave][(k[i] >> shift) & mask], 1u);
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < kBins; d += kRadixThreads) {
+  for (int d = threadIdx.x; d < kBins; d += TH) {
     uint32_t c = 0;
 #pragma unroll
-    for (int w = 0; w < kRadixWaves; ++w) c += s_hist[w][d];
+    for (int w = 0; w < kWaves; ++w) c += s_hist[w][d];
     hist[static_cast<int64_t>(d) * nparts + blockIdx.x] = c;
   }
 }
@@ -147,35 +162,58 @@ __global__ __launch_bounds__(kRowScanThreads) void k_radix_rowscan(
 }
 
 // Loads one wave's kRadixItems x 64 consecutive keys (and values) from
-// wbase on and ranks them: rank = the number of keys with the same digit
-// before it in the wave's range (the wave's LDS digit counters `cnt` carry
-// the count across the items), dig = its digit, or -1 past the end.  FULL:
-// the whole range is in bounds (no per-item tests).  The lanes holding the
-// same digit are found from one ballot per digit bit: ANDed over the bits,
-// the ballot where this lane's bit is set, its complement where it is clear
-// — b & ~(a ^ c) with a the ballot, b the running mask and c all ones or
-// zeros, one three-input bitwise instruction per 32-bit half (truth table
-// 0x84, symmetric in a and c).
-template <int RB, bool VALS, bool FULL>
-__device__ __forceinline__ void load_rank(const uint32_t* __restrict__ kin,
+// wbase on (wbase and n the same in every lane).  Every lane issues every
+// load (indices past n read element n - 1, n > 0): the number of loads in
+// flight is then the same on every path, so a wait for them can leave
+// later stores outstanding.  The entries past n are never ranked or
+// written (rank_tile tests the index).
+template <bool VALS>
+__device__ __forceinline__ void load_tile(const uint32_t* __restrict__ kin,
                                           const uint32_t* __restrict__ vin, int64_t wbase,
-                                          int64_t n, int lane, uint64_t lt_mask, int shift,
-                                          uint32_t mask, uint32_t* cnt,
-                                          uint32_t (&key)[kRadixItems],
-                                          uint32_t (&val)[kRadixItems],
-                                          uint32_t (&rank)[kRadixItems],
-                                          int (&dig)[kRadixItems]) {
-  const uint32_t* kw = kin + wbase;
-  const uint32_t* vw = vin ? vin + wbase : nullptr;
+                                          int64_t n, int lane, uint32_t (&key)[kRadixItems],
+                                          uint32_t (&val)[kRadixItems]) {
+  // Scalar base and last valid offset: past the end the whole wave reads
+  // element n - 1.
+  const int64_t rem = n - wbase;
+  const int64_t b = rem > 0 ? wbase : n - 1;
+  const uint32_t lim =
+      rem > 0 ? static_cast<uint32_t>(rem < kRadixItems * 64 ? rem : kRadixItems * 64) - 1u : 0u;
+  const uint32_t* kw = kin + b;
+  if (VALS && vin) {
+    const uint32_t* vw = vin + b;
 #pragma unroll
-  for (int it = 0; it < kRadixItems; ++it) {
-    const int o = it * 64 + lane;
-    const bool valid = FULL || wbase + o < n;
-    key[it] = valid ? kw[o] : 0u;
+    for (int it = 0; it < kRadixItems; ++it) {
+      const uint32_t o = static_cast<uint32_t>(it * 64 + lane);
+      const uint32_t src = o < lim ? o : lim;
+      key[it] = kw[src];
+      val[it] = vw[src];
+    }
+  } else {
     // vin == nullptr: the values are the element indices (first pass of a
     // sort whose payload is the identity permutation).
-    if (VALS) val[it] = valid ? (vw ? vw[o] : static_cast<uint32_t>(wbase + o)) : 0u;
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const uint32_t o = static_cast<uint32_t>(it * 64 + lane);
+      key[it] = kw[o < lim ? o : lim];
+      if (VALS) val[it] = static_cast<uint32_t>(wbase) + o;
+    }
   }
+}
+
+// Ranks one wave's loaded keys: rank = the number of keys with the same
+// digit before it in the wave's range (the wave's LDS digit counters `cnt`
+// carry the count across the items), dig = its digit, or -1 past the end.
+// The lanes holding the same digit are found from one ballot per digit bit:
+// ANDed over the bits, the ballot where this lane's bit is set, its
+// complement where it is clear — b & ~(a ^ c) with a the ballot, b the
+// running mask and c all ones or zeros, one three-input bitwise instruction
+// per 32-bit half (truth table 0x84, symmetric in a and c).
+template <int RB, bool FULL>
+__device__ __forceinline__ void rank_tile(const uint32_t (&key)[kRadixItems], int64_t wbase,
+                                          int64_t n, int lane, uint64_t lt_mask, int shift,
+                                          uint32_t mask, uint32_t* cnt,
+                                          uint32_t (&rank)[kRadixItems],
+                                          int (&dig)[kRadixItems]) {
 #pragma unroll
   for (int it = 0; it < kRadixItems; ++it) {
     const int o = it * 64 + lane;
@@ -212,8 +250,8 @@ __device__ __forceinline__ void load_rank(const uint32_t* __restrict__ kin,
 // Thread d < 2^RB holds digit d's next output position in the partition
 // (`run`), advanced by the digit's count after each tile.  kout == nullptr
 // with VALS: only the values are written (the caller needs no sorted keys).
-template <int RB, bool VALS>
-__global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
+template <int RB, bool VALS, int TH>
+__global__ __launch_bounds__(TH) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n, int shift,
     uint32_t mask, const uint32_t* __restrict__ hist_scan,
@@ -221,15 +259,16 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     const uint32_t* __restrict__ run_flag, uint32_t out_mask,
     const int64_t* __restrict__ bounds) {
   constexpr int kBins = 1 << RB;
-  static_assert(kBins <= kRadixThreads, "one thread per digit");
+  constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
+  static_assert(kBins <= TH, "one thread per digit");
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_cnt[kRadixWaves][kBins];
+  __shared__ uint32_t s_cnt[kWaves][kBins];
   __shared__ uint32_t s_delta[kBins];  // output offset of the digit minus its local offset
-  __shared__ uint32_t s_wsum[kRadixWaves];
-  __shared__ uint32_t s_key[kRadixTile];
-  __shared__ uint32_t s_val[VALS ? kRadixTile : 1];
+  __shared__ uint32_t s_wsum[kWaves];
+  __shared__ uint32_t s_key[kTile];
+  __shared__ uint32_t s_val[VALS ? kTile : 1];
   const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const bool write_keys = !VALS || kout != nullptr;
 
   // Digit d's first output position in this partition: the global totals
@@ -261,29 +300,27 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     pstart = bounds[blockIdx.x] < n ? bounds[blockIdx.x] : n;
     pend = bounds[blockIdx.x + 1] < n ? bounds[blockIdx.x + 1] : n;
   } else {
-    pstart = static_cast<int64_t>(blockIdx.x) * sub * kRadixTile;
-    pend = pstart + static_cast<int64_t>(sub) * kRadixTile < n
-               ? pstart + static_cast<int64_t>(sub) * kRadixTile
+    pstart = static_cast<int64_t>(blockIdx.x) * sub * kTile;
+    pend = pstart + static_cast<int64_t>(sub) * kTile < n
+               ? pstart + static_cast<int64_t>(sub) * kTile
                : n;
   }
-  for (int64_t bbase = pstart; bbase < pend; bbase += kRadixTile) {  // uniform
-    // Also orders the previous tile's reads of s_key/s_delta/s_wsum before
-    // this tile's writes.
-    __syncthreads();
-    for (int e = threadIdx.x; e < kRadixWaves * kBins; e += kRadixThreads)
-      s_cnt[e / kBins][e % kBins] = 0;
-    __syncthreads();
+  // The same in every lane: held as scalars, so the tile loop and its
+  // full/partial choice are scalar branches.
+  pstart = uniform_i64(pstart);
+  pend = uniform_i64(pend);
 
+  // One tile at bbase whose keys and values are loaded; FULL: all
+  // kTile of them are in the partition.
+  auto tile = [&](auto full, int64_t bbase, const uint32_t(&key)[kRadixItems],
+                  const uint32_t(&val)[kRadixItems]) {
+    constexpr bool FULL = decltype(full)::value;
     const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
-    const int nvalid = static_cast<int>(pend - bbase < kRadixTile ? pend - bbase : kRadixTile);
-    uint32_t key[kRadixItems], val[kRadixItems], rank[kRadixItems];
+    const int nvalid =
+        FULL ? kTile : static_cast<int>(pend - bbase < kTile ? pend - bbase : kTile);
+    uint32_t rank[kRadixItems];
     int dig[kRadixItems];
-    if (nvalid == kRadixTile)
-      load_rank<RB, VALS, true>(kin, vin, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave],
-                                key, val, rank, dig);
-    else
-      load_rank<RB, VALS, false>(kin, vin, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave],
-                                 key, val, rank, dig);
+    rank_tile<RB, FULL>(key, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave], rank, dig);
     __syncthreads();
     // Per digit: the counts of the lower waves (s_cnt becomes each wave's
     // local start), the tile total, and the exclusive scan over the digits
@@ -291,7 +328,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
     uint32_t tot = 0;
     if (threadIdx.x < kBins) {
 #pragma unroll
-      for (int w = 0; w < kRadixWaves; ++w) tot += s_cnt[w][threadIdx.x];
+      for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][threadIdx.x];
     }
     uint32_t incl = tot;
 #pragma unroll
@@ -309,7 +346,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
       run += tot;
       uint32_t r = loc;
 #pragma unroll
-      for (int w = 0; w < kRadixWaves; ++w) {
+      for (int w = 0; w < kWaves; ++w) {
         const uint32_t c = s_cnt[w][d];
         s_cnt[w][d] = r;
         r += c;
@@ -325,17 +362,56 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(
       }
     }
     __syncthreads();
+    if (write_keys) {
 #pragma unroll
-    for (int it = 0; it < kRadixItems; ++it) {
-      const int i = it * kRadixThreads + static_cast<int>(threadIdx.x);
-      if (i < nvalid) {
-        const uint32_t k = s_key[i];
-        const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
-        if (write_keys) kout[pos] = k & out_mask;
-        if (VALS) vout[pos] = s_val[i];
+      for (int it = 0; it < kRadixItems; ++it) {
+        const int i = it * TH + static_cast<int>(threadIdx.x);
+        if (FULL || i < nvalid) {
+          const uint32_t k = s_key[i];
+          const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
+          kout[pos] = k & out_mask;
+          if (VALS) vout[pos] = s_val[i];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kRadixItems; ++it) {
+        const int i = it * TH + static_cast<int>(threadIdx.x);
+        if (FULL || i < nvalid) {
+          const uint32_t pos = s_delta[(s_key[i] >> shift) & mask] + static_cast<uint32_t>(i);
+          vout[pos] = s_val[i];
+        }
       }
     }
+    // Orders this tile's reads of s_key/s_delta/s_wsum before the next
+    // tile's writes, and clears the digit counters for it.
+    __syncthreads();
+    for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
+      s_cnt[e / kBins][e % kBins] = 0;
+    __syncthreads();
+  };
+
+  for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
+    s_cnt[e / kBins][e % kBins] = 0;
+  __syncthreads();
+  // The keys (and values) of the next tile are loaded while this one is
+  // ranked and written: each tile's load latency hides behind the previous
+  // tile's work instead of adding to it.
+  const int64_t woff = static_cast<int64_t>(wave) * (kRadixItems * 64);
+  uint32_t key[kRadixItems], val[kRadixItems], nkey[kRadixItems], nval[kRadixItems];
+  int64_t bbase = pstart;
+  if (bbase < pend) load_tile<VALS>(kin, vin, bbase + woff, pend, lane, nkey, nval);
+  for (; bbase + kTile <= pend; bbase += kTile) {
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      key[it] = nkey[it];
+      val[it] = nval[it];
+    }
+    if (bbase + kTile < pend)
+      load_tile<VALS>(kin, vin, bbase + kTile + woff, pend, lane, nkey, nval);
+    tile(std::true_type{}, bbase, key, val);
   }
+  if (bbase < pend) tile(std::false_type{}, bbase, nkey, nval);
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
@@ -882,17 +958,21 @@ size_t radix_scratch_elems(int64_t n) {
 
 namespace {
 
-// Partitioning of n keys: `sub` tiles of kRadixTile per partition, `np`
-// partitions.  sub stays 1 below 2*kRadixTargetParts tiles (every tile its
-// own block) and grows beyond, capped at kRadixMaxSub; np <= tiles, so the
-// spine fits the scratch that radix_scratch_elems sizes for one row per tile.
+// Partitioning of n keys: `sub` tiles of `threads` * kRadixItems keys per
+// partition, `np` partitions.  sub stays 1 below 2*kRadixTargetParts tiles
+// (every tile its own block) and grows beyond, capped at kRadixMaxSub;
+// np <= tiles <= the count of kRadixTile tiles, so the spine fits the
+// scratch that radix_scratch_elems sizes for one row per kRadixTile tile.
 struct RadixParts {
   int np;
   int sub;
+  int threads;  // block size of the passes: kRadixThreads or kRadixThreadsLarge
 };
 
 int radix_parts(int64_t n, RadixParts* p) {
-  const int64_t tiles = (n + kRadixTile - 1) / kRadixTile;
+  p->threads = n >= kRadixLargeMinKeys ? kRadixThreadsLarge : kRadixThreads;
+  const int64_t tile = static_cast<int64_t>(p->threads) * kRadixItems;
+  const int64_t tiles = (n + tile - 1) / tile;
   int64_t sub = tiles / kRadixTargetParts;
   if (sub < 1) sub = 1;
   if (sub > kRadixMaxSub) sub = kRadixMaxSub;
@@ -917,17 +997,29 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
   const int64_t hist_n = static_cast<int64_t>(np) << RB;
   uint32_t* hist = scratch;
   uint32_t* totals = scratch + hist_n;
+  const bool large = rp.threads == kRadixThreadsLarge;
   if (!fp) {
-    hipLaunchKernelGGL(k_radix_hist<RB>, dim3(rp.np), dim3(kRadixThreads), 0, s, src_k, n, shift,
-                       mask, hist, rp.np, rp.sub, run_flag);
+    if (large)
+      hipLaunchKernelGGL((k_radix_hist<RB, kRadixThreadsLarge>), dim3(rp.np),
+                         dim3(kRadixThreadsLarge), 0, s, src_k, n, shift, mask, hist, rp.np,
+                         rp.sub, run_flag);
+    else
+      hipLaunchKernelGGL((k_radix_hist<RB, kRadixThreads>), dim3(rp.np), dim3(kRadixThreads), 0,
+                         s, src_k, n, shift, mask, hist, rp.np, rp.sub, run_flag);
     HRF_LAUNCH_CHECK();
   }
   hipLaunchKernelGGL(k_radix_rowscan, dim3(1 << RB), dim3(kRowScanThreads), 0, s, hist, np,
                      totals, run_flag);
   HRF_LAUNCH_CHECK();
-  hipLaunchKernelGGL((k_radix_scatter<RB, VALS>), dim3(np), dim3(kRadixThreads), 0, s, src_k,
-                     src_v, dst_k, dst_v, n, shift, mask, hist, totals, np, rp.sub, run_flag,
-                     out_mask, fp ? fp->bounds : nullptr);
+  const int64_t* bounds = fp ? fp->bounds : nullptr;
+  if (large)
+    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(np),
+                       dim3(kRadixThreadsLarge), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask,
+                       hist, totals, np, rp.sub, run_flag, out_mask, bounds);
+  else
+    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreads>), dim3(np), dim3(kRadixThreads),
+                       0, s, src_k, src_v, dst_k, dst_v, n, shift, mask, hist, totals, np, rp.sub,
+                       run_flag, out_mask, bounds);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1083,7 +1175,7 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 
 namespace {
 // Minimum average pairs per emission block for the emission to take the
-// first sort pass's histogram: 16 sort tiles.
+// first sort pass's histogram: 16 of the smaller sort tiles.
 constexpr int64_t kFirstPassMinPairs = 16 * static_cast<int64_t>(kRadixTile);
 int digit_template_bits(int bits) { return bits <= 4 ? 4 : bits; }
 // Offset of the partition bounds in the sort scratch: after the spine and

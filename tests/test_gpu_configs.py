@@ -15,7 +15,8 @@ cfg4 (3M Gaussians at 1920x1080, ~8.7e8 pairs) also exercises the key/value
 sort path (tile and gaussian bits do not fit one 32-bit word); the headline
 geometry with larger Gaussians (2.4e7 pairs) runs the packed sort with several
 key tiles per scatter block; a 160 x 125-tile grid with 150k Gaussians runs the
-key/value sort with ranges formed from the sorted tiles."""
+key/value sort with ranges formed from the sorted tiles; 8.3e7 pairs run the
+packed sort over the larger (8192-key) tiles."""
 import numpy as np
 import pytest
 
@@ -240,5 +241,35 @@ def test_packed_sort_first_pass_from_emission(hrf, oracle_mod):
     fT, nc, pl, ranges, vis = fr.fwd_state
     gx, gy = (spec.width + 15) // 16, (spec.height + 15) // 16
     _check_binning(t, pl, ranges, tiles_ref, rect_ref, gx, gx * gy)
+    del fr
+    torch.cuda.empty_cache()
+
+
+def test_packed_sort_large_tiles(hrf, oracle_mod):
+    """250k large Gaussians at 800x800 (8.3e7 pairs, above the 2^26 keys from
+    which the sort passes run 1024-thread blocks over 8192-key tiles): the
+    first pass over the emission's partitions and the second with its own
+    histogram both run the larger tiles; binning checked exactly."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from complex_valued_holographic_radiance_fields_amd.frame import Frame
+
+    spec = scenes.SceneSpec("large_tiles", 13, 250_000, 800, 800, 1, [515e-9], [-2e-3],
+                            "object", log_scale_mean=-2.0)
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    pr = oracle_mod.project(g, cam)
+    _, tiles_ref, rect_ref = oracle_mod.preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
+    K = int(tiles_ref.astype(np.int64).sum())
+    print(f"large_tiles: N={g.n} K={K}", flush=True)
+    assert K >= (1 << 26)
+    t = scenes.to_torch(sc)
+    fr = Frame(t, spec, sc.fx, sc.fy, sc.px, sc.py)
+    fr.forward()
+    torch.cuda.synchronize()
+    fT, nc, pl, ranges, vis = fr.fwd_state
+    gx, gy = (spec.width + 15) // 16, (spec.height + 15) // 16
+    _check_binning(t, pl, ranges, tiles_ref, rect_ref, gx, gx * gy)
+    assert bool(((fT > 0) & (fT <= 1)).all())
     del fr
     torch.cuda.empty_cache()
