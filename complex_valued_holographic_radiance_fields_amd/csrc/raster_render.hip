@@ -256,19 +256,30 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
 
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
   if (threadIdx.x == 0) s_kcull = 0;
+  // Each batch's list entries and their plane masks are loaded during the
+  // previous batch: they depend only on the list, and two dependent loads
+  // per batch (entry, then mask) would otherwise precede the record loads.
+  int g_next = 0;
+  uint32_t m_next = 0;
+  if (static_cast<int>(threadIdx.x) < n) {
+    g_next = p.plist[r0 + static_cast<int>(threadIdx.x)];
+    if (static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
+      m_next = p.pmask[g_next];
+  }
   for (int base = 0; base < n; base += kBlock) {
     if (__syncthreads_and(T < kTermT)) break;
     const int k = base + static_cast<int>(threadIdx.x);
-    bool mem = false;
-    int g = 0;
+    const int g = g_next;
+    bool mem = k < n && static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+               ((m_next >> plane) & 1u);
     // geometry quads; the amplitude quads load at the LDS write
     float4 rq[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
     float w = 0.0f;
     const float4* src = nullptr;
-    if (k < n) {
-      g = p.plist[r0 + k];
-      mem = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
-            ((p.pmask[g] >> plane) & 1u);
+    {
+      const int kn = k + kBlock;
+      g_next = kn < n ? p.plist[r0 + kn] : 0;
+      m_next = 0;
     }
     if (mem) {
       src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
@@ -282,6 +293,9 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
         atomicMax(&s_kcull, k + 1);
       }
     }
+    if (base + kBlock + static_cast<int>(threadIdx.x) < n &&
+        static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
+      m_next = p.pmask[g_next];
     int cnt;
     const int pos = block_compact(mem, s_wt, &cnt);
     // Any staged conic that is not safe: this batch runs the exact loop.
