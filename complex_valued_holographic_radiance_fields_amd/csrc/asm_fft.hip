@@ -153,6 +153,55 @@ __device__ __forceinline__ void dft8_half(float2 (&x)[8]) {
   x[7] = csub(e[3], o3);
 }
 
+// DFT-16 as two DFT-8 (even and odd inputs) combined with the twiddles
+// w16^k, k < 8.  HALF: the inputs are zero at t < 4 and t >= 12 (the
+// first stage of a transform whose nonzero input lies in [N/4, 3N/4)): the
+// even and odd halves are then both DFT-8s of inputs zero at 0, 1, 6, 7.
+template <bool INV, bool HALF>
+__device__ __forceinline__ void dft16(float2 (&x)[16]) {
+  float2 e[8], o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (!HALF || (j >= 2 && j <= 5)) {
+      e[j] = x[2 * j];
+      o[j] = x[2 * j + 1];
+    }
+  }
+  if constexpr (HALF) {
+    dft8_half<INV>(e);
+    dft8_half<INV>(o);
+  } else {
+    Dft<8, INV>::run(e);
+    Dft<8, INV>::run(o);
+  }
+  // o[k] * w16^k: k = 2, 6 are the DFT-8's 1/sqrt(2) products, k = 4 is
+  // -/+ i, k odd a full complex product with cos/sin(pi k/8).
+  constexpr float c1 = 0.92387953251128676f;  // cos(pi/8)
+  constexpr float s1 = 0.38268343236508977f;  // sin(pi/8)
+  constexpr float h = 0.70710678118654752f;
+  const float sg = INV ? 1.0f : -1.0f;
+  float2 t[8];
+  t[0] = o[0];
+  t[1] = cmulf(o[1], make_float2(c1, sg * s1));
+  t[2] = INV ? make_float2((o[2].x - o[2].y) * h, (o[2].x + o[2].y) * h)
+             : make_float2((o[2].x + o[2].y) * h, (o[2].y - o[2].x) * h);
+  t[3] = cmulf(o[3], make_float2(s1, sg * c1));
+  t[4] = mul_mi<INV>(o[4]);
+  t[5] = cmulf(o[5], make_float2(-s1, sg * c1));
+  t[6] = INV ? make_float2(-(o[6].x + o[6].y) * h, (o[6].x - o[6].y) * h)
+             : make_float2((o[6].y - o[6].x) * h, -(o[6].x + o[6].y) * h);
+  t[7] = cmulf(o[7], make_float2(-c1, sg * s1));
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    x[k] = cadd(e[k], t[k]);
+    x[k + 8] = csub(e[k], t[k]);
+  }
+}
+template <bool INV>
+struct Dft<16, INV> {
+  __device__ __forceinline__ static void run(float2 (&x)[16]) { dft16<INV, false>(x); }
+};
+
 // Odd radix by symmetric pairing: X_m = x0 + sum_j cos(2 pi jm/R)(x_j+x_{R-j})
 //   -/+ i sum_j sin(2 pi jm/R)(x_j-x_{R-j}),  X_{R-m} with the opposite sign.
 template <int R>
@@ -230,6 +279,29 @@ template <bool INV>
 struct Dft<5, INV> : DftOdd<5, INV> {};
 template <bool INV>
 struct Dft<7, INV> : DftOdd<7, INV> {};
+// DFT-10 by the prime-factor mapping 10 = 2 x 5 (no inner twiddles): input
+// n = (5 n1 + 2 n2) mod 10 and output k = (5 k1 + 6 k2) mod 10, i.e. a
+// DFT-2 over (x[2j], x[2j+5 mod 10]) for each j, then a DFT-5 over each of
+// the two results.
+template <bool INV>
+struct Dft<10, INV> {
+  __device__ __forceinline__ static void run(float2 (&x)[10]) {
+    float2 a[5], b[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const float2 u = x[2 * j], v = x[(2 * j + 5) % 10];
+      a[j] = cadd(u, v);
+      b[j] = csub(u, v);
+    }
+    Dft<5, INV>::run(a);
+    Dft<5, INV>::run(b);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      x[(6 * k) % 10] = a[k];
+      x[(5 + 6 * k) % 10] = b[k];
+    }
+  }
+};
 
 // LDS layout.  A batch of B = 4 transforms of length N is interleaved:
 // element i of transform b is at 4*i + b, so rows and columns share one
@@ -254,11 +326,11 @@ constexpr int kCopyIters = (B * N + T - 1) / T;
 // k < NS, 1 <= t < R (OFF = sum of NS (R - 1) over the earlier stages; N - 1
 // entries in all).  A butterfly then reads its R - 1 twiddles at one base
 // address plus constant offsets.
-// HALF (first stage only, R = 8): the inputs at t = 0, 1, 6, 7 are zero and
-// are neither read nor stored by the caller.
+// HALF (first stage only, R = 8 or 16): the inputs at t < R/4 and t >= 3R/4
+// are zero and are neither read nor stored by the caller.
 template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF, int B>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
-  static_assert(!HALF || (R == 8 && NS == 1), "pruned first stage is radix 8");
+  static_assert(!HALF || ((R == 8 || R == 16) && NS == 1), "pruned first stage is radix 8 or 16");
   static_assert(B > 0 && (B & (B - 1)) == 0, "the batch is a power of two");
   constexpr int NR = N / R;
   constexpr int NB = B * NR;
@@ -268,6 +340,10 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   constexpr bool lin_load = LS % 32 == 0;
   constexpr bool lin_store = SS % 32 == 0 || (NS == 1 && (B * R) % 32 == 0);
   constexpr int LSP = LS / 32 * 36;
+  // First stage (NS = 1, B R a multiple of 32): butterfly j's outputs are
+  // the B R words from B R j + b on (b < B) at stride B, so the padded
+  // address of output t is pad(a0) + pad(t B) (a run of 64 crosses one
+  // padding gap, at t B = 32).
   constexpr int SSP = SS % 32 == 0 ? SS / 32 * 36 : SS;
   // The thread index and a zero twiddle offset pass through empty asm
   // statements, so a caller that runs the transform inside a loop (the plane
@@ -291,11 +367,11 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
         const int base = pad(q);
 #pragma unroll
         for (int t = 0; t < R; ++t)
-          if (!HALF || (t >= 2 && t <= 5)) x[t] = lds[base + t * LSP];
+          if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[base + t * LSP];
       } else {
 #pragma unroll
         for (int t = 0; t < R; ++t)
-          if (!HALF || (t >= 2 && t <= 5)) x[t] = lds[pad(q + t * LS)];
+          if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[pad(q + t * LS)];
       }
       if (NS > 1) {
         const float2* wk = tw + (twoff + OFF + k * (R - 1) - 1);
@@ -306,8 +382,10 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
           x[t] = cmulf(x[t], w);
         }
       }
-      if constexpr (HALF)
+      if constexpr (HALF && R == 8)
         dft8_half<INV>(x);
+      else if constexpr (HALF)
+        dft16<INV, true>(x);
       else
         Dft<R, INV>::run(x);
 #pragma unroll
@@ -323,7 +401,8 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
     if (ob[u] >= 0) {
       if (lin_store) {
 #pragma unroll
-        for (int t = 0; t < R; ++t) lds[ob[u] + t * SSP] = y[u][t];
+        for (int t = 0; t < R; ++t)
+          lds[ob[u] + (SS % 32 == 0 ? t * SSP : pad(t * SS))] = y[u][t];
       } else {
 #pragma unroll
         for (int t = 0; t < R; ++t) lds[pad(ob[u] + t * SS)] = y[u][t];
@@ -348,7 +427,7 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   X(192, 8, 8, 3)        \
   X(512, 8, 8, 8)        \
   X(1024, 8, 8, 4, 4)    \
-  X(1600, 8, 8, 5, 5)    \
+  X(1600, 16, 10, 10)    \
   X(2016, 8, 4, 7, 3, 3) \
   X(2048, 8, 8, 8, 4)    \
   X(3840, 8, 8, 4, 5, 3) \
@@ -367,10 +446,34 @@ struct Plan;
 HRF_FFT_PLANS(HRF_FFT_PLAN)
 #undef HRF_FFT_PLAN
 
-// Host: the radix sequence of a plan (empty for lengths without one).
-std::vector<int> plan_radices(int N) {
+// Plans of the forward column pass where it differs from the length's
+// plan: its per-plane transforms run with the transfer state (kz and the
+// plane sum, 39 registers per thread at 1600 points) live, and 16 10 10
+// spills there (66 registers at the 128 budget of two blocks per CU), so
+// that pass keeps 8 8 5 5.  The other passes at 1600 points take 16 10 10
+// (one stage fewer: adjoint column pass 87.9 -> 81.2 us per frame).
+#define HRF_FFT_COLFWD_PLANS(X) X(1600, 8, 8, 5, 5)
+template <int N>
+struct PlanColFwd : Plan<N> {};
+#define HRF_FFT_PLAN(NN, ...)                                                       \
+  template <>                                                                       \
+  struct PlanColFwd<NN> {                                                           \
+    template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
+    __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
+      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
+    }                                                                               \
+  };
+HRF_FFT_COLFWD_PLANS(HRF_FFT_PLAN)
+#undef HRF_FFT_PLAN
+
+// Host: the radix sequence of a plan (empty for lengths without one);
+// col_fwd: the forward column pass's.
+std::vector<int> plan_radices(int N, bool col_fwd) {
 #define HRF_FFT_RADICES(NN, ...) \
   if (N == NN) return std::vector<int>{__VA_ARGS__};
+  if (col_fwd) {
+    HRF_FFT_COLFWD_PLANS(HRF_FFT_RADICES)
+  }
   HRF_FFT_PLANS(HRF_FFT_RADICES)
 #undef HRF_FFT_RADICES
   return {};
@@ -626,7 +729,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
       }
     }
     __syncthreads();
-    Plan<N>::template run<false, T, HALF, B>(lds, twp);
+    PlanColFwd<N>::template run<false, T, HALF, B>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -659,7 +762,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<true, T, false, B>(lds, twp);
+  PlanColFwd<N>::template run<true, T, false, B>(lds, twp);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
   if (accumulate) {
     for (int e = threadIdx.x; e < B * S; e += T) {
@@ -773,11 +876,13 @@ std::map<std::pair<int, int>, float2*>& tw_tables() {
   return m;
 }
 
-int twiddles(int N, const float2** out) {
+// The twiddle table of the length-N plan (col_fwd: the forward column
+// pass's plan), built once per device.
+int twiddles(int N, const float2** out, bool col_fwd = false) {
   int dev = 0;
   HRF_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  auto key = std::make_pair(dev, N);
+  auto key = std::make_pair(dev, 2 * N + (col_fwd ? 1 : 0));
   auto it = tw_tables().find(key);
   if (it != tw_tables().end()) {
     *out = it->second;
@@ -788,7 +893,7 @@ int twiddles(int N, const float2** out) {
   std::vector<float2> h;
   h.reserve(N);
   int ns = 1;
-  for (int r : plan_radices(N)) {
+  for (int r : plan_radices(N, col_fwd)) {
     for (int k = 0; k < ns; ++k)
       for (int t = 1; t < r; ++t) {
         const long long m = static_cast<long long>(t) * k * (N / (ns * r));
@@ -863,8 +968,9 @@ int pass_rows_out(const float2* Z, float2* dst, int nimg, int h, int w, const fl
 // B with P transfer functions summed: X (P*C, h_in, N) -> Z (C, h_out, N).
 template <int N>
 int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
-                 float ap, const AsmFftConsts& mc, const float2* tw, bool accumulate,
-                 hipStream_t s) {
+                 float ap, const AsmFftConsts& mc, bool accumulate, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw, true));
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
@@ -922,7 +1028,7 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   }
   {
     HRF_STAGE("asm_col_fwd", s);
-    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, tw, false, s));
+    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, false, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
@@ -1002,7 +1108,7 @@ int run_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double
     }
     {
       HRF_STAGE("asm_col_fwd", s);
-      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, tw, d0 > 0, s));
+      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, d0 > 0, s));
     }
   }
   {
