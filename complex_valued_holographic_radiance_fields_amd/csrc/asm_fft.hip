@@ -446,34 +446,10 @@ struct Plan;
 HRF_FFT_PLANS(HRF_FFT_PLAN)
 #undef HRF_FFT_PLAN
 
-// Plans of the forward column pass where it differs from the length's
-// plan: its per-plane transforms run with the transfer state (kz and the
-// plane sum, 39 registers per thread at 1600 points) live, and 16 10 10
-// spills there (66 registers at the 128 budget of two blocks per CU), so
-// that pass keeps 8 8 5 5.  The other passes at 1600 points take 16 10 10
-// (one stage fewer: adjoint column pass 87.9 -> 81.2 us per frame).
-#define HRF_FFT_COLFWD_PLANS(X) X(1600, 8, 8, 5, 5)
-template <int N>
-struct PlanColFwd : Plan<N> {};
-#define HRF_FFT_PLAN(NN, ...)                                                       \
-  template <>                                                                       \
-  struct PlanColFwd<NN> {                                                           \
-    template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
-    __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
-    }                                                                               \
-  };
-HRF_FFT_COLFWD_PLANS(HRF_FFT_PLAN)
-#undef HRF_FFT_PLAN
-
-// Host: the radix sequence of a plan (empty for lengths without one);
-// col_fwd: the forward column pass's.
-std::vector<int> plan_radices(int N, bool col_fwd) {
+// Host: the radix sequence of a plan (empty for lengths without one).
+std::vector<int> plan_radices(int N) {
 #define HRF_FFT_RADICES(NN, ...) \
   if (N == NN) return std::vector<int>{__VA_ARGS__};
-  if (col_fwd) {
-    HRF_FFT_COLFWD_PLANS(HRF_FFT_RADICES)
-  }
   HRF_FFT_PLANS(HRF_FFT_RADICES)
 #undef HRF_FFT_RADICES
   return {};
@@ -729,13 +705,20 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
       }
     }
     __syncthreads();
-    PlanColFwd<N>::template run<false, T, HALF, B>(lds, twp);
+    Plan<N>::template run<false, T, HALF, B>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
+    // At 1600 points the thread index is opaque per plane: the band-limit
+    // coordinates below are then recomputed here rather than hoisted out of
+    // the plane loop and held through the transforms, which spilled 66
+    // registers with the 16 10 10 plan.  (At the other lengths holding them
+    // measured faster.)
+    int tid = static_cast<int>(threadIdx.x);
+    if constexpr (N == 1600) asm volatile("" : "+v"(tid));
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-      const int q = threadIdx.x + u * T;
+      const int q = tid + u * T;
       if (q < B * N && kz[u] >= 0.0f) {
         bool within = band_all;
         if (!within) {
@@ -762,7 +745,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  PlanColFwd<N>::template run<true, T, false, B>(lds, twp);
+  Plan<N>::template run<true, T, false, B>(lds, twp);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
   if (accumulate) {
     for (int e = threadIdx.x; e < B * S; e += T) {
@@ -876,13 +859,11 @@ std::map<std::pair<int, int>, float2*>& tw_tables() {
   return m;
 }
 
-// The twiddle table of the length-N plan (col_fwd: the forward column
-// pass's plan), built once per device.
-int twiddles(int N, const float2** out, bool col_fwd = false) {
+int twiddles(int N, const float2** out) {
   int dev = 0;
   HRF_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  auto key = std::make_pair(dev, 2 * N + (col_fwd ? 1 : 0));
+  auto key = std::make_pair(dev, N);
   auto it = tw_tables().find(key);
   if (it != tw_tables().end()) {
     *out = it->second;
@@ -893,7 +874,7 @@ int twiddles(int N, const float2** out, bool col_fwd = false) {
   std::vector<float2> h;
   h.reserve(N);
   int ns = 1;
-  for (int r : plan_radices(N, col_fwd)) {
+  for (int r : plan_radices(N)) {
     for (int k = 0; k < ns; ++k)
       for (int t = 1; t < r; ++t) {
         const long long m = static_cast<long long>(t) * k * (N / (ns * r));
@@ -968,9 +949,8 @@ int pass_rows_out(const float2* Z, float2* dst, int nimg, int h, int w, const fl
 // B with P transfer functions summed: X (P*C, h_in, N) -> Z (C, h_out, N).
 template <int N>
 int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
-                 float ap, const AsmFftConsts& mc, bool accumulate, hipStream_t s) {
-  const float2* tw = nullptr;
-  HRF_TRY(twiddles(N, &tw, true));
+                 float ap, const AsmFftConsts& mc, const float2* tw, bool accumulate,
+                 hipStream_t s) {
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
@@ -1028,7 +1008,7 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   }
   {
     HRF_STAGE("asm_col_fwd", s);
-    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, false, s));
+    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, tw, false, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
@@ -1108,7 +1088,7 @@ int run_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double
     }
     {
       HRF_STAGE("asm_col_fwd", s);
-      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, d0 > 0, s));
+      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, tw, d0 > 0, s));
     }
   }
   {
