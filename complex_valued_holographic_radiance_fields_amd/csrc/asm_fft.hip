@@ -240,6 +240,30 @@ struct OddConsts<7> {
   }
 };
 
+template <>
+struct OddConsts<9> {
+  // cos/sin(2 pi k / 9), k = 0..8 (9 is not prime: j m = 9 at j = m = 3
+  // gives k = 0): c(9 - k) = c(k), s(9 - k) = -s(k)
+  __device__ static constexpr float c(int k) {
+    return k == 0 ? 1.0f
+           : (k == 1 || k == 8) ? 0.76604444311897804f
+                              : ((k == 2 || k == 7) ? 0.17364817766693035f
+                                                    : ((k == 3 || k == 6) ? -0.5f
+                                                                          : -0.93969262078590838f));
+  }
+  __device__ static constexpr float s(int k) {
+    return k == 0   ? 0.0f
+           : k == 1 ? 0.64278760968653933f
+           : k == 2 ? 0.98480775301220806f
+           : k == 3 ? 0.86602540378443865f
+           : k == 4 ? 0.34202014332566873f
+           : k == 5 ? -0.34202014332566873f
+           : k == 6 ? -0.86602540378443865f
+           : k == 7 ? -0.98480775301220806f
+                    : -0.64278760968653933f;
+  }
+};
+
 template <int R, bool INV>
 struct DftOdd {
   __device__ __forceinline__ static void run(float2 (&x)[R]) {
@@ -279,6 +303,8 @@ template <bool INV>
 struct Dft<5, INV> : DftOdd<5, INV> {};
 template <bool INV>
 struct Dft<7, INV> : DftOdd<7, INV> {};
+template <bool INV>
+struct Dft<9, INV> : DftOdd<9, INV> {};
 // DFT-10 by the prime-factor mapping 10 = 2 x 5 (no inner twiddles): input
 // n = (5 n1 + 2 n2) mod 10 and output k = (5 k1 + 6 k2) mod 10, i.e. a
 // DFT-2 over (x[2j], x[2j+5 mod 10]) for each j, then a DFT-5 over each of
@@ -428,9 +454,9 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   X(512, 8, 8, 8)        \
   X(1024, 8, 8, 4, 4)    \
   X(1600, 16, 10, 10)    \
-  X(2016, 8, 4, 7, 3, 3) \
+  X(2016, 8, 4, 7, 9)     \
   X(2048, 8, 8, 8, 4)    \
-  X(3840, 8, 8, 4, 5, 3) \
+  X(3840, 16, 16, 5, 3)  \
   X(4096, 8, 8, 8, 8)
 
 template <int N>
