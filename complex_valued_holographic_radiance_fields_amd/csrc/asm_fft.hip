@@ -457,7 +457,7 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   X(2016, 8, 4, 7, 9)     \
   X(2048, 8, 8, 8, 4)    \
   X(3840, 16, 16, 5, 3)  \
-  X(4096, 8, 8, 8, 8)
+  X(4096, 16, 16, 16)
 
 template <int N>
 struct Plan;
@@ -472,10 +472,32 @@ struct Plan;
 HRF_FFT_PLANS(HRF_FFT_PLAN)
 #undef HRF_FFT_PLAN
 
-// Host: the radix sequence of a plan (empty for lengths without one).
-std::vector<int> plan_radices(int N) {
+// Plans of the column passes where they differ from the length's: at 4096
+// points the column blocks (1024 threads, two transforms) would leave half
+// their waves idle in every radix-16 stage (512 butterflies), so they keep
+// 8 8 8 8, while the row passes (512 threads) take 16 16 16.
+#define HRF_FFT_COL_PLANS(X) X(4096, 8, 8, 8, 8)
+template <int N>
+struct PlanCol : Plan<N> {};
+#define HRF_FFT_PLAN(NN, ...)                                                       \
+  template <>                                                                       \
+  struct PlanCol<NN> {                                                              \
+    template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
+    __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
+      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
+    }                                                                               \
+  };
+HRF_FFT_COL_PLANS(HRF_FFT_PLAN)
+#undef HRF_FFT_PLAN
+
+// Host: the radix sequence of a plan (empty for lengths without one); col:
+// the column passes' plan.
+std::vector<int> plan_radices(int N, bool col) {
 #define HRF_FFT_RADICES(NN, ...) \
   if (N == NN) return std::vector<int>{__VA_ARGS__};
+  if (col) {
+    HRF_FFT_COL_PLANS(HRF_FFT_RADICES)
+  }
   HRF_FFT_PLANS(HRF_FFT_RADICES)
 #undef HRF_FFT_RADICES
   return {};
@@ -731,7 +753,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
       }
     }
     __syncthreads();
-    Plan<N>::template run<false, T, HALF, B>(lds, twp);
+    PlanCol<N>::template run<false, T, HALF, B>(lds, twp);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -771,7 +793,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     if (q < B * N) lds[pad(q)] = acc[u];
   }
   __syncthreads();
-  Plan<N>::template run<true, T, false, B>(lds, twp);
+  PlanCol<N>::template run<true, T, false, B>(lds, twp);
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
   if (accumulate) {
     for (int e = threadIdx.x; e < B * S; e += T) {
@@ -825,7 +847,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
     }
   }
   __syncthreads();
-  Plan<N>::template run<false, T, HALF, B>(lds, twp);
+  PlanCol<N>::template run<false, T, HALF, B>(lds, twp);
   float kz[EPT];
   float2 gs[EPT];
 #pragma unroll
@@ -872,7 +894,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
       }
     }
     __syncthreads();
-    Plan<N>::template run<true, T, false, B>(lds, twp);
+    PlanCol<N>::template run<true, T, false, B>(lds, twp);
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
     for (int e = threadIdx.x; e < B * H; e += T) dst[(e / B) * TB + e % B] = lds[pad(e + r_crop * B)];
   }
@@ -885,11 +907,13 @@ std::map<std::pair<int, int>, float2*>& tw_tables() {
   return m;
 }
 
-int twiddles(int N, const float2** out) {
+// The twiddle table of the length-N plan (col: the column passes' plan),
+// built once per device.
+int twiddles(int N, const float2** out, bool col = false) {
   int dev = 0;
   HRF_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(g_tw_mu);
-  auto key = std::make_pair(dev, N);
+  auto key = std::make_pair(dev, 2 * N + (col ? 1 : 0));
   auto it = tw_tables().find(key);
   if (it != tw_tables().end()) {
     *out = it->second;
@@ -900,7 +924,7 @@ int twiddles(int N, const float2** out) {
   std::vector<float2> h;
   h.reserve(N);
   int ns = 1;
-  for (int r : plan_radices(N)) {
+  for (int r : plan_radices(N, col)) {
     for (int k = 0; k < ns; ++k)
       for (int t = 1; t < r; ++t) {
         const long long m = static_cast<long long>(t) * k * (N / (ns * r));
@@ -975,8 +999,9 @@ int pass_rows_out(const float2* Z, float2* dst, int nimg, int h, int w, const fl
 // B with P transfer functions summed: X (P*C, h_in, N) -> Z (C, h_out, N).
 template <int N>
 int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
-                 float ap, const AsmFftConsts& mc, const float2* tw, bool accumulate,
-                 hipStream_t s) {
+                 float ap, const AsmFftConsts& mc, bool accumulate, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw, true));
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
@@ -994,7 +1019,9 @@ int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, 
 // Z (P*C, h_out, N).
 template <int N>
 int pass_col_adj(const float2* X, float2* Z, int P, int C, int h_in, int h_out, float sfreq,
-                 float ap, const AsmFftConsts& mc, const float2* tw, hipStream_t s) {
+                 float ap, const AsmFftConsts& mc, hipStream_t s) {
+  const float2* tw = nullptr;
+  HRF_TRY(twiddles(N, &tw, true));
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
   if (2 * h_in <= N)
     hipLaunchKernelGGL((k_col_adj<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
@@ -1034,7 +1061,7 @@ int run_forward(const float2* fields, int P, int C, int H, int W, int S, double 
   }
   {
     HRF_STAGE("asm_col_fwd", s);
-    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, tw, false, s));
+    HRF_TRY(pass_col_fwd<N>(X, Z, P, C, H, S, freq_step_of(N, pitch), ap, mc, false, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
@@ -1056,7 +1083,7 @@ int run_adjoint(const float2* gholo, int P, int C, int H, int W, int S, double p
   }
   {
     HRF_STAGE("asm_col_adj", s);
-    HRF_TRY(pass_col_adj<N>(X, Z, P, C, S, H, freq_step_of(N, pitch), ap, mc, tw, s));
+    HRF_TRY(pass_col_adj<N>(X, Z, P, C, S, H, freq_step_of(N, pitch), ap, mc, s));
   }
   {
     HRF_STAGE("asm_rows_out", s);
@@ -1085,7 +1112,7 @@ int run_md_forward(const float2* field, int D, int C, int H, int W, int S, doubl
     const AsmFftConsts mc = fft_consts_reversed(g, C, N, pitch, wl, dist + d0);
     {
       HRF_STAGE("asm_col_adj", s);
-      HRF_TRY(pass_col_adj<N>(X, Z, g, C, H, S, freq_step_of(N, pitch), ap, mc, tw, s));
+      HRF_TRY(pass_col_adj<N>(X, Z, g, C, H, S, freq_step_of(N, pitch), ap, mc, s));
     }
     {
       HRF_STAGE("asm_rows_out", s);
@@ -1114,7 +1141,7 @@ int run_md_adjoint(const float2* gout, int D, int C, int H, int W, int S, double
     }
     {
       HRF_STAGE("asm_col_fwd", s);
-      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, tw, d0 > 0, s));
+      HRF_TRY(pass_col_fwd<N>(X, Z, g, C, S, H, freq_step_of(N, pitch), ap, mc, d0 > 0, s));
     }
   }
   {
