@@ -454,7 +454,7 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   X(512, 8, 8, 8)        \
   X(1024, 8, 8, 4, 4)    \
   X(1600, 16, 10, 10)    \
-  X(2016, 8, 4, 7, 9)     \
+  X(2016, 8, 4, 7, 9)    \
   X(2048, 8, 8, 8, 4)    \
   X(3840, 16, 16, 5, 3)  \
   X(4096, 16, 16, 16)
