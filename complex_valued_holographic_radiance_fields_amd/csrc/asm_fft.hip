@@ -329,18 +329,26 @@ struct Dft<10, INV> {
   }
 };
 
-// LDS layout.  A batch of B = 4 transforms of length N is interleaved:
-// element i of transform b is at 4*i + b, so rows and columns share one
-// layout and one thread's butterfly inputs (and outputs) sit at a base
-// address plus a stride.  Four padding slots follow every 32 elements: the
-// first stage's stride-32 stores then land on distinct bank pairs, and for
-// every stride that is a multiple of 32 (all strides of these plans but the
-// first stage's loads at N = 160, 2016) the padded addresses stay a base
-// plus a compile-time offset.
-__device__ __forceinline__ constexpr int pad(int a) { return a + ((a >> 5) << 2); }
-template <int N, int B = kFftBatch>
+// LDS layout.  A batch of B transforms of length N is interleaved: element
+// i of transform b is at B*i + b, so rows and columns share one layout and
+// one thread's butterfly inputs (and outputs) sit at a base address plus a
+// stride.  K padding slots follow every 32 elements (K per plan and batch,
+// below): the first stage's strided stores then spread over the banks, and
+// for every stride that is a multiple of 32 the padded addresses stay a
+// base plus a compile-time offset.
+template <int K = 4>
+__device__ __forceinline__ constexpr int pad(int a) { return a + (a >> 5) * K; }
+// Padding slots per 32 elements for a batch of B transforms whose plan
+// starts with radix R1: 2 for radix 16 over two transforms, whose first
+// stage's 32-word output runs would otherwise put a half-wave's stores on 16
+// of the 32 banks (4-way conflicts; config 4's passes 1-2% faster with 2),
+// else 4 (at 1600 points, four transforms, 4 measured faster than 2 though
+// a half-wave's radix-16 stores then meet 2-way conflicts).
+template <int R1, int B>
+constexpr int kPadSlots = (R1 == 16 && B == 2) ? 2 : 4;
+template <int N, int B = kFftBatch, int K = 4>
 constexpr int lds_elems() {
-  return pad(B * N - 1) + 1;
+  return pad<K>(B * N - 1) + 1;
 }
 // Elements per thread when a block copies its B x N batch.
 template <int N, int T = kFftThreads, int B = kFftBatch>
@@ -354,7 +362,7 @@ constexpr int kCopyIters = (B * N + T - 1) / T;
 // address plus constant offsets.
 // HALF (first stage only, R = 8 or 16): the inputs at t < R/4 and t >= 3R/4
 // are zero and are neither read nor stored by the caller.
-template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF, int B>
+template <int N, int R, int NS, bool INV, int OFF, int T, bool HALF, int B, int K>
 __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict__ tw) {
   static_assert(!HALF || ((R == 8 || R == 16) && NS == 1), "pruned first stage is radix 8 or 16");
   static_assert(B > 0 && (B & (B - 1)) == 0, "the batch is a power of two");
@@ -365,12 +373,12 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   constexpr int SS = B * NS;  // store stride between butterfly outputs
   constexpr bool lin_load = LS % 32 == 0;
   constexpr bool lin_store = SS % 32 == 0 || (NS == 1 && (B * R) % 32 == 0);
-  constexpr int LSP = LS / 32 * 36;
+  constexpr int LSP = LS / 32 * (32 + K);
   // First stage (NS = 1, B R a multiple of 32): butterfly j's outputs are
   // the B R words from B R j + b on (b < B) at stride B, so the padded
-  // address of output t is pad(a0) + pad(t B) (a run of 64 crosses one
+  // address of output t is pad<K>(a0) + pad<K>(t B) (a run of 64 crosses one
   // padding gap, at t B = 32).
-  constexpr int SSP = SS % 32 == 0 ? SS / 32 * 36 : SS;
+  constexpr int SSP = SS % 32 == 0 ? SS / 32 * (32 + K) : SS;
   // The thread index and a zero twiddle offset pass through empty asm
   // statements, so a caller that runs the transform inside a loop (the plane
   // loop of the column passes) cannot hoist this stage's addresses and
@@ -390,14 +398,14 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
       const int k = j % NS;
       float2 x[R];
       if (lin_load) {
-        const int base = pad(q);
+        const int base = pad<K>(q);
 #pragma unroll
         for (int t = 0; t < R; ++t)
           if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[base + t * LSP];
       } else {
 #pragma unroll
         for (int t = 0; t < R; ++t)
-          if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[pad(q + t * LS)];
+          if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[pad<K>(q + t * LS)];
       }
       if (NS > 1) {
         const float2* wk = tw + (twoff + OFF + k * (R - 1) - 1);
@@ -418,7 +426,7 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
       for (int t = 0; t < R; ++t) y[u][t] = x[t];
       // Stockham output position (j/NS)*NS*R + k + t*NS, interleaved.
       const int a0 = q + B * (j / NS) * NS * (R - 1);
-      ob[u] = lin_store ? pad(a0) : a0;
+      ob[u] = lin_store ? pad<K>(a0) : a0;
     }
   }
   __syncthreads();
@@ -428,21 +436,25 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
       if (lin_store) {
 #pragma unroll
         for (int t = 0; t < R; ++t)
-          lds[ob[u] + (SS % 32 == 0 ? t * SSP : pad(t * SS))] = y[u][t];
+          lds[ob[u] + (SS % 32 == 0 ? t * SSP : pad<K>(t * SS))] = y[u][t];
       } else {
 #pragma unroll
-        for (int t = 0; t < R; ++t) lds[pad(ob[u] + t * SS)] = y[u][t];
+        for (int t = 0; t < R; ++t) lds[pad<K>(ob[u] + t * SS)] = y[u][t];
       }
     }
   }
   __syncthreads();
 }
 
-template <int T, int B, int N, bool INV, bool HALF, int NS, int OFF, int R, int... Rest>
+template <int T, int B, int K, int N, bool INV, bool HALF, int NS, int OFF, int R, int... Rest>
 __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict__ tw) {
-  fft_stage<N, R, NS, INV, OFF, T, HALF && NS == 1, B>(lds, tw);
+  fft_stage<N, R, NS, INV, OFF, T, HALF && NS == 1, B, K>(lds, tw);
   if constexpr (sizeof...(Rest) > 0)
-    run_stages<T, B, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
+    run_stages<T, B, K, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
+}
+template <typename... A>
+constexpr int first_radix(int r, A...) {
+  return r;
 }
 
 // The plans (radix sequence per length), shared by the device transforms
@@ -464,9 +476,11 @@ struct Plan;
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct Plan<NN> {                                                                 \
+    template <int B>                                                                \
+    static constexpr int kPad = kPadSlots<first_radix(__VA_ARGS__), B>;             \
     template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
+      run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
     }                                                                               \
   };
 HRF_FFT_PLANS(HRF_FFT_PLAN)
@@ -482,9 +496,11 @@ struct PlanCol : Plan<N> {};
 #define HRF_FFT_PLAN(NN, ...)                                                       \
   template <>                                                                       \
   struct PlanCol<NN> {                                                              \
+    template <int B>                                                                \
+    static constexpr int kPad = kPadSlots<first_radix(__VA_ARGS__), B>;             \
     template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
-      run_stages<T, B, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);                  \
+      run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
     }                                                                               \
   };
 HRF_FFT_COL_PLANS(HRF_FFT_PLAN)
@@ -588,7 +604,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __rest
   constexpr int T = kRowThreads<N>;
   constexpr int TB = kFftBatch;     // columns of an intermediate tile
   constexpr int ncb = N / TB;
-  __shared__ float2 lds[lds_elems<N, RB>()];
+  __shared__ float2 lds[lds_elems<N, RB, Plan<N>::template kPad<RB>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   const int blocks_per_img = (h + RB - 1) / RB;
@@ -613,7 +629,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __rest
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      if (e < E0 + EN) lds[pad(e)] = v[it];
+      if (e < E0 + EN) lds[pad<Plan<N>::template kPad<RB>>(e)] = v[it];
     }
   }
   __syncthreads();
@@ -622,7 +638,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __rest
   for (int e = threadIdx.x; e < RB * N; e += T) {
     const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
     const int r = r0 + rr;
-    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, TB)] = lds[pad(RB * (TB * cb + bc) + rr)];
+    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, TB)] = lds[pad<Plan<N>::template kPad<RB>>(RB * (TB * cb + bc) + rr)];
   }
 }
 
@@ -640,7 +656,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
   constexpr int TB = kFftBatch;
   constexpr int ncb = N / TB;
   constexpr int IT = kCopyIters<N, T, RB>;
-  __shared__ float2 lds[lds_elems<N, RB>()];
+  __shared__ float2 lds[lds_elems<N, RB, Plan<N>::template kPad<RB>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   const int blocks_per_img = (h + RB - 1) / RB;
@@ -660,7 +676,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
     for (int it = 0; it < IT; ++it) {
       const int e = static_cast<int>(threadIdx.x) + it * T;
       const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
-      if (e < RB * N) lds[pad(RB * (TB * cb + bc) + rr)] = v[it];
+      if (e < RB * N) lds[pad<Plan<N>::template kPad<RB>>(RB * (TB * cb + bc) + rr)] = v[it];
     }
   }
   __syncthreads();
@@ -669,7 +685,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
     const int rr = e % RB, i = e / RB;
     const int r = r0 + rr;
     if (r < h) {
-      const float2 v = lds[pad(RB * (c_out + i) + rr)];
+      const float2 v = lds[pad<Plan<N>::template kPad<RB>>(RB * (c_out + i) + rr)];
       dst[(static_cast<int64_t>(img) * h + r) * w_out + i] = cscale(v, scale);
     }
   }
@@ -702,7 +718,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   constexpr int T = kColThreads<N>;
   constexpr int ncb = N / TB;
   constexpr int EPT = (B * N + T - 1) / T;
-  __shared__ float2 lds[lds_elems<N, B>()];
+  __shared__ float2 lds[lds_elems<N, B, PlanCol<N>::template kPad<B>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   int c, hb;
@@ -749,7 +765,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
 #pragma unroll
       for (int u = 0; u < kPlaneLoads; ++u) {
         const int e = e0 + u * T;
-        if (e < E1) lds[pad(e)] = v[u];
+        if (e < E1) lds[pad<PlanCol<N>::template kPad<B>>(e)] = v[u];
       }
     }
     __syncthreads();
@@ -779,7 +795,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
         if (within) {
           float sn, cs;
           sincos_big(d * kz[u], &sn, &cs);
-          const float2 x = lds[pad(q)];
+          const float2 x = lds[pad<PlanCol<N>::template kPad<B>>(q)];
           acc[u].x += x.x * cs - x.y * sn;
           acc[u].y += x.x * sn + x.y * cs;
         }
@@ -790,7 +806,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
 #pragma unroll
   for (int u = 0; u < EPT; ++u) {
     const int q = threadIdx.x + u * T;
-    if (q < B * N) lds[pad(q)] = acc[u];
+    if (q < B * N) lds[pad<PlanCol<N>::template kPad<B>>(q)] = acc[u];
   }
   __syncthreads();
   PlanCol<N>::template run<true, T, false, B>(lds, twp);
@@ -798,10 +814,10 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   if (accumulate) {
     for (int e = threadIdx.x; e < B * S; e += T) {
       const int o = (e / B) * TB + e % B;
-      dst[o] = cadd(dst[o], lds[pad(e + s_crop * B)]);
+      dst[o] = cadd(dst[o], lds[pad<PlanCol<N>::template kPad<B>>(e + s_crop * B)]);
     }
   } else {
-    for (int e = threadIdx.x; e < B * S; e += T) dst[(e / B) * TB + e % B] = lds[pad(e + s_crop * B)];
+    for (int e = threadIdx.x; e < B * S; e += T) dst[(e / B) * TB + e % B] = lds[pad<PlanCol<N>::template kPad<B>>(e + s_crop * B)];
   }
 }
 
@@ -819,7 +835,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
   constexpr int T = kColThreads<N>;
   constexpr int ncb = N / TB;
   constexpr int EPT = (B * N + T - 1) / T;
-  __shared__ float2 lds[lds_elems<N, B>()];
+  __shared__ float2 lds[lds_elems<N, B, PlanCol<N>::template kPad<B>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   int c, hb;
@@ -843,7 +859,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      if (e < E0 + EN) lds[pad(e)] = v[it];
+      if (e < E0 + EN) lds[pad<PlanCol<N>::template kPad<B>>(e)] = v[it];
     }
   }
   __syncthreads();
@@ -862,7 +878,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
       coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &inap);
       const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
       if (inap && prop) kz[u] = kk;
-      gs[u] = lds[pad(q)];
+      gs[u] = lds[pad<PlanCol<N>::template kPad<B>>(q)];
     }
   }
   for (int p = 0; p < P; ++p) {
@@ -890,13 +906,13 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
             r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
           }
         }
-        lds[pad(q)] = r;
+        lds[pad<PlanCol<N>::template kPad<B>>(q)] = r;
       }
     }
     __syncthreads();
     PlanCol<N>::template run<true, T, false, B>(lds, twp);
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
-    for (int e = threadIdx.x; e < B * H; e += T) dst[(e / B) * TB + e % B] = lds[pad(e + r_crop * B)];
+    for (int e = threadIdx.x; e < B * H; e += T) dst[(e / B) * TB + e % B] = lds[pad<PlanCol<N>::template kPad<B>>(e + r_crop * B)];
   }
 }
 
