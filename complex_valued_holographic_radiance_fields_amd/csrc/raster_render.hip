@@ -64,24 +64,10 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
 // Gaussian's exponent comes out in base 2 with the -1/2 folded in.
 constexpr float kBwdConicScale = -0.72134752044448170368f;
 
-// Ballot compaction of one flag per thread across the block.  Returns the
-// compacted position of this thread's entry and the block-wide count.
-__device__ __forceinline__ int block_compact(bool flag, int* s_wt, int* count) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t bal = __ballot(flag);
-  if (lane == 0) s_wt[wave] = __popcll(bal);
-  __syncthreads();
-  int off = 0, cnt = 0;
-#pragma unroll
-  for (int w = 0; w < kBlock / 64; ++w) {
-    const int t = s_wt[w];
-    off += (w < wave) ? t : 0;
-    cnt += t;
-  }
-  *count = cnt;
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  return off + __popcll(bal & lt);
-}
+// The forward's per-wave batch word: member count and two flags.
+constexpr int kWtCount = 0xFF;
+constexpr int kWtUnsafe = 0x100;
+constexpr int kWtDone = 0x200;
 
 // Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
 // only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
@@ -266,8 +252,8 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     if (static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
       m_next = p.pmask[g_next];
   }
+  __syncthreads();  // s_kcull's initialisation before the batches' culls
   for (int base = 0; base < n; base += kBlock) {
-    if (__syncthreads_and(T < kTermT)) break;
     const int k = base + static_cast<int>(threadIdx.x);
     const int g = g_next;
     bool mem = k < n && static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
@@ -296,10 +282,36 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     if (base + kBlock + static_cast<int>(threadIdx.x) < n &&
         static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
       m_next = p.pmask[g_next];
-    int cnt;
-    const int pos = block_compact(mem, s_wt, &cnt);
-    // Any staged conic that is not safe: this batch runs the exact loop.
-    const bool exact = __syncthreads_or(mem && !conic_safe(rq[0].z, rq[0].w, rq[1].x, rq[1].y));
+    // One barrier publishes each wave's member count (the compaction), whether
+    // it stages a conic that is not safe (then the batch runs the exact
+    // loop) and whether all its pixels are done (then the block is).  The
+    // previous batch's LDS reads all precede it: its member loop ends before
+    // the lanes reach this point.
+    int pos, cnt = 0;
+    bool exact = false;
+    {
+      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+      const uint64_t bal = __ballot(mem);
+      const bool w_unsafe = __ballot(mem && !conic_safe(rq[0].z, rq[0].w, rq[1].x, rq[1].y)) != 0ull;
+      const bool w_done = __ballot(!(T < kTermT)) == 0ull;
+      if (lane == 0)
+        s_wt[wave] = __popcll(bal) | (w_unsafe ? kWtUnsafe : 0) | (w_done ? kWtDone : 0);
+      __syncthreads();
+      int off = 0;
+      bool all_done = true;
+#pragma unroll
+      for (int wv = 0; wv < kBlock / 64; ++wv) {
+        const int t = s_wt[wv];
+        const int c = t & kWtCount;
+        off += (wv < wave) ? c : 0;
+        cnt += c;
+        exact = exact || (t & kWtUnsafe) != 0;
+        all_done = all_done && (t & kWtDone) != 0;
+      }
+      if (all_done) break;
+      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      pos = off + __popcll(bal & lt);
+    }
     if (mem) {
       if (sub_out) sub_out[listed + pos] = make_int2(g, k);
       const float4 am = src[2];  // (re0, im0, re1, im1)
