@@ -491,7 +491,10 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   }
   for (int end = lim; end > 0; end -= kBlock) {
     const int start = end > kBlock ? end - kBlock : 0;
-    __syncthreads();
+    // No barrier here: until the count barrier below, a batch writes only
+    // s_cnt, which the previous batch last read before its member loop; the
+    // staging writes that the previous flush's reads must precede come after
+    // that barrier.
     const int idx = start + static_cast<int>(threadIdx.x);
     int k = idx;
     int g = 0;
