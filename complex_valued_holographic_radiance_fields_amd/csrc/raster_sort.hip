@@ -362,6 +362,10 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
       }
     }
     __syncthreads();
+    // The digit counters are read no more in this tile: clear them for the
+    // next one (the barrier after the write-out orders it).
+    for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
+      s_cnt[e / kBins][e % kBins] = 0;
     if (write_keys) {
 #pragma unroll
       for (int it = 0; it < kRadixItems; ++it) {
@@ -383,11 +387,8 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
         }
       }
     }
-    // Orders this tile's reads of s_key/s_delta/s_wsum before the next
-    // tile's writes, and clears the digit counters for it.
-    __syncthreads();
-    for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
-      s_cnt[e / kBins][e % kBins] = 0;
+    // Orders this tile's reads of s_key/s_val/s_delta and the counter
+    // clear before the next tile's writes.
     __syncthreads();
   };
 
