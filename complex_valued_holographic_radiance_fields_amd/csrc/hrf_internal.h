@@ -152,8 +152,8 @@ __host__ __device__ constexpr int rec_quads(int channels) {
 __host__ __device__ constexpr int rec_stride(int channels) {
   return 4 * rec_quads(channels);
 }
-// Per-Gaussian backward accumulator: [dmx, dmy, dconic_x, dconic_y,
-// dconic_z, A_0..A_{C-1}, B_0..B_{C-1}, Q_0..Q_{P-1}].
+// Per-Gaussian backward accumulator: [dmx, dmy, dcov_xx, dcov_xy,
+// dcov_yy, A_0..A_{C-1}, B_0..B_{C-1}, Q_0..Q_{P-1}].
 __host__ __device__ constexpr int acc_stride(int channels, int planes) {
   return 5 + 2 * channels + planes;
 }

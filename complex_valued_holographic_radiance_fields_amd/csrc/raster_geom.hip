@@ -127,13 +127,14 @@ __device__ __forceinline__ bool project_one(const ProjectParams& p, int64_t g) {
   p.pmask[g] = mask;
 
   // Render record: conic as the render kernels evaluate it
-  // (forward_splat.cu:217-223), opacity, complex amplitude colour*e^{i phase}.
+  // (forward_splat.cu:217-223), opacity, 1/det (for the backward's
+  // conic-to-covariance gradient map), complex amplitude colour*e^{i phase}.
   const int RS = rec_stride(C);
   float* r = p.rec + g * RS;
   const float det = c_x * c_w - c_y * c_z;
   const float det_inv = 1.0f / det;
   float4 q0 = make_float4(mx, my, c_w * det_inv, -c_y * det_inv);
-  float4 q1 = make_float4(-c_z * det_inv, c_x * det_inv, p.opac[g], 0.0f);
+  float4 q1 = make_float4(-c_z * det_inv, c_x * det_inv, p.opac[g], det_inv);
   reinterpret_cast<float4*>(r)[0] = q0;
   reinterpret_cast<float4*>(r)[1] = q1;
   float amp[8];
@@ -253,23 +254,10 @@ __global__ __launch_bounds__(kGeomBwdThreads) void k_geom_backward(GeomBwdParams
   // grad means2D (accumulated by the render backward, already scaled by
   // (0.5W, 0.5H) as backward_splat.cu:160-161,275-276).
   const float gmx = a[0], gmy = a[1];
-  // Conic gradients -> cov2D gradients with the reference's own map
-  // (backward_splat.cu:285-296), applied to the per-Gaussian sums (the map
-  // is linear in the conic gradients).
-  const float dcx = a[2], dcy = a[3], dcz = a[4];
-  float gxx = 0.f, gxy = 0.f, gyy = 0.f;
-  if (dcx != 0.f || dcy != 0.f || dcz != 0.f) {
-    const float cx = cv[0][0], cy = cv[0][1], cz = cv[1][0], cw = cv[1][1];
-    const float det = cx * cw - cy * cz;
-    const float di = __builtin_amdgcn_rcpf(det);
-    const float a1 = cw * di * di;
-    const float a2 = -cy * di * di;
-    const float a3 = cx * di * di;
-    gxx = dcx * a1 * cw + dcz * a2 * (-cy);
-    gxy = dcx * a1 * (-cy) + dcy * (-di) + dcz * a2 * cx;
-    gyy = dcx * a2 * (-cy) + dcz * a3 * cx;
-  }
-  const float G2[2][2] = {{gxx, gxy}, {gxy, gyy}};
+  // cov2D gradients: the render backward already applied the reference's
+  // conic-to-covariance map (backward_splat.cu:285-296), per pixel or per
+  // block, before the sums reached these records.
+  const float G2[2][2] = {{a[2], a[3]}, {a[3], a[4]}};
 
   float gm[3], dSig[3][3], dJ[2][3], gj[3];
   means2d_bwd<true>(tx, ty, tz, p.fx, p.fy, p.near_plane, p.far_plane, gmx, gmy, gm);

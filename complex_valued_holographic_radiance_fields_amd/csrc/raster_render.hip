@@ -23,6 +23,8 @@
 // with one ds_add per lane, and flushes one global atomic per (block,
 // Gaussian, value) into a per-Gaussian accumulator.  The reference issues
 // 8+2C global atomics per contributing (pixel, Gaussian).
+#include <type_traits>
+
 #include "hrf_internal.h"
 #include "wave_reduce.h"
 
@@ -49,6 +51,12 @@ __device__ __forceinline__ void map_block(int b, int nb, int P, int* tile, int* 
   *plane = logical - (*tile) * P;
 }
 
+// Number of set bits of a wave mask below the calling lane (v_mbcnt).
+__device__ __forceinline__ int bits_below_lane(uint64_t m) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+      static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
 // Tile range [r0, r0+n), clamped to the pair list so malformed caller input
 // (the backward takes ranges from the caller) cannot index out of bounds.
 __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int* r0, int* n) {
@@ -63,6 +71,19 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
 // -log2(e)/2: the render kernels stage the conic pre-scaled by it, so the
 // Gaussian's exponent comes out in base 2 with the -1/2 folded in.
 constexpr float kBwdConicScale = -0.72134752044448170368f;
+constexpr float kLog2E = 1.44269504088896340736f;
+
+// a / b for b in [0.01, 1] and a normal: the hardware reciprocal, then one
+// residual correction (the residual a - q b is exact in a fused
+// multiply-add), which rounds like the reference's IEEE division
+// (backward_splat.cu:222) except in rare near-tie cases.  The backward
+// recovers T by up to 1e5 such divisions in a row, so the reciprocal's own
+// error (up to 1 ulp, not zero-mean) would drift T by more than 1e-4.
+__device__ __forceinline__ float div_rn(float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q = a * r;
+  return fmaf(fmaf(-q, b, a), r, q);
+}
 
 // The forward's per-wave batch word: member count and two flags.
 constexpr int kWtCount = 0xFF;
@@ -139,7 +160,8 @@ __device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape&
 // Forward members without effect.  A Gaussian whose alpha stays below 2^-26
 // at every pixel of the tile (q > 2 ln(o w 2^26) over the tile's pixel
 // centres, widened as above) cannot change T there: alpha T is below half
-// an ulp of T, so T - alpha T rounds back to T, and the termination test and
+// an ulp of T, so T (1 - alpha) rounds back to T (1 - alpha rounds to 1), and
+// the termination test and
 // final_T are exactly as if it had been composited.  Its field contribution
 // is below 2^-25 T |amplitude|.  Such members are not staged; the tile's
 // largest such list position still counts as the last contributor for
@@ -150,13 +172,19 @@ __device__ __forceinline__ float invisible_threshold(float ow) {
   return fmaxf(thr, 0.0f) * 1.001f + 0.01f;
 }
 
-// A staged conic whose exponent cannot round to a positive value at any
-// pixel: positive definite with |correlation| below 0.99995.  The exponent
-// dx (A dx + B dy) + C dy^2 is then a sum whose rounding error (a few ulps
-// of its terms) stays below its true, non-positive value, so the reference's
-// "power > 0: skip" test can never fire and the member loop omits it.
+// A conic the fast member loops may evaluate in their own form: positive
+// definite with |correlation| below 0.99 (b b2 < 0.98 a c).  The exponent
+// dx (A dx + B dy) + C dy^2 is a sum of terms at most (1 + r) / (1 - r) = 199
+// times its value, so any evaluation order rounds it alike to within a few
+// 1e-5 relative even in a Gaussian's far tail, and it cannot round to a
+// positive value (the reference's "power > 0: skip" test never fires).  A
+// batch that stages any other conic runs the exact loop, which evaluates the
+// exponent in the reference's order: for nearly singular conics (the
+// highly anisotropic Gaussians of a stress scene) the terms cancel by four
+// or more orders of magnitude and only the same rounding sequence
+// reproduces the reference's alpha.
 __device__ __forceinline__ bool conic_safe(float a, float b, float b2, float c) {
-  return a > 0.0f && c > 0.0f && a * c - b * b2 > 1e-4f * (a * c);
+  return a > 0.0f && c > 0.0f && a * c - b * b2 > 0.02f * (a * c);
 }
 
 // Forward staged record: full quads only (a 12-byte LDS read occupies the
@@ -165,8 +193,13 @@ __device__ __forceinline__ bool conic_safe(float a, float b, float b2, float c) 
 //   quad 0: (mx, my, kc*i00, kc*(i01 + i10))
 //   quad 1: (kc*i11, log2(o w), re0, im0)
 //   quad 2: (re1, im1, re2, im2)            (C >= 2)
-// with kc = -log2(e)/2.
+// with kc = -log2(e)/2.  Exact batches stage the conic unscaled, in the
+// reference's layout, followed by the amplitude quads of the global record:
+//   quad 0: (mx, my, i00, i10)
+//   quad 1: (i01, log2(o w), i11, 0)
+//   quads 2..: (re0, im0, re1, im1), (re2, im2, 0, 0)
 __host__ __device__ constexpr int fwd_quads(int C) { return C == 1 ? 2 : 3; }
+__host__ __device__ constexpr int fwd_quads_exact(int C) { return rec_quads(C); }
 
 // Forward member evaluation.  Exponent in base 2 with log2(o w) folded in:
 // pw = dx (A dx + B dy) + (C dy) dy + log2(o w), so alpha = min(0.99,
@@ -201,19 +234,53 @@ __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const
     acc[2 * k] = fmaf(sT, amp[2 * k], acc[2 * k]);
     acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
   }
-  T = T - sT;  // T (1 - alpha), reusing alpha T
+  // The reference's rounding: 1 - alpha rounded first (forward_splat.cu:237).
+  // Over lists of 1e5 members the rounded factor's bias (small alphas are
+  // quantised to multiples of 2^-24) moves T by more than 1e-4, so the
+  // exactly rounded T - alpha T would not reproduce it.
+  T = T * (1.0f - alpha);
   if (kExact)
     lastj = (ok && real) ? j : lastj;
   else
     lastj += ok ? 1 : 0;
 }
 
+// Exact-batch member evaluation: the exponent in the reference's order
+// (forward_splat.cu:222-225), power = -0.5 s with
+// s = dx (i00 dx + i10 dy) + dy (i01 dx + i11 dy), each product and sum
+// rounded on its own (the library is built without contraction), the
+// "power > 0: skip" test as s < 0, then alpha from exp2(kc s + log2(o w))
+// (kc = -log2(e)/2, one rounding in the fused multiply-add).  The rest is
+// fwd_member's exact variant.
+template <int C>
+__device__ __forceinline__ void fwd_member_ref(const float4 a, const float4 b, const float4 c,
+                                               const float4 d, float pxf, float pyf, float& T,
+                                               float (&acc)[2 * C], int& lastj, int j,
+                                               bool real) {
+  const float dx = a.x - pxf, dy = a.y - pyf;
+  const float s = dx * (a.z * dx + a.w * dy) + dy * (b.x * dx + b.z * dy);
+  const bool live = !(T < kTermT);
+  const bool ok = live && !(s < 0.0f);
+  const float pw = fmaf(kBwdConicScale, s, b.y);
+  const float alpha = ok ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
+  const float sT = alpha * T;
+  const float amp[6] = {c.x, c.y, c.z, c.w, d.x, d.y};
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    acc[2 * k] = fmaf(sT, amp[2 * k], acc[2 * k]);
+    acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
+  }
+  T = T * (1.0f - alpha);
+  lastj = (ok && real) ? j : lastj;
+}
+
 template <int C>
 __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderParams p) {
   constexpr int NQ = fwd_quads(C);
+  constexpr int NQX = fwd_quads_exact(C);
   constexpr int RS = rec_stride(C);
   constexpr int kUnroll = 8;
-  __shared__ float4 s_rec[kBlock * NQ];
+  __shared__ float4 s_rec[kBlock * NQX];
   __shared__ int s_pos[kBlock];  // list position + 1 of each staged member
   __shared__ int s_wt[kBlock / 64];
   __shared__ int s_kcull;  // 1 + the largest list position culled as invisible
@@ -309,32 +376,42 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
         all_done = all_done && (t & kWtDone) != 0;
       }
       if (all_done) break;
-      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      pos = off + __popcll(bal & lt);
+      pos = off + bits_below_lane(bal);
     }
     if (mem) {
       if (sub_out) sub_out[listed + pos] = make_int2(g, k);
       const float4 am = src[2];  // (re0, im0, re1, im1)
-      s_rec[pos * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
-                                    kBwdConicScale * (rq[0].w + rq[1].x));
-      s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].y,
-                                        __builtin_amdgcn_logf(rq[1].z * w), am.x, am.y);
-      if (NQ > 2) {
-        const float4 am2 = rec_quads(C) > 3 ? src[3] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        s_rec[pos * NQ + (NQ > 2 ? 2 : 0)] = make_float4(am.z, am.w, am2.x, am2.y);
+      const float lw = __builtin_amdgcn_logf(rq[1].z * w);
+      if (!exact) {
+        s_rec[pos * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
+                                      kBwdConicScale * (rq[0].w + rq[1].x));
+        s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, lw, am.x, am.y);
+        if (NQ > 2) {
+          const float4 am2 = rec_quads(C) > 3 ? src[3] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          s_rec[pos * NQ + (NQ > 2 ? 2 : 0)] = make_float4(am.z, am.w, am2.x, am2.y);
+        }
+      } else {
+        s_rec[pos * NQX] = make_float4(rq[0].x, rq[0].y, rq[0].z, rq[1].x);
+        s_rec[pos * NQX + 1] = make_float4(rq[0].w, lw, rq[1].y, 0.0f);
+        s_rec[pos * NQX + 2] = am;
+        if (NQX > 3) s_rec[pos * NQX + (NQX > 3 ? 3 : 2)] = src[3];
       }
       s_pos[pos] = k + 1;
     }
     // Pad the staged batch to a multiple of kUnroll with members no pixel
-    // can use: log2(o w) = -inf (alpha 0, T unchanged).
+    // can use: log2(o w) = -inf (alpha 0, T unchanged), in the same slot of
+    // both layouts (the exact layout's zero conic gives s = 0, which passes
+    // the power test).
     listed += cnt;
     const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
     if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
-      const int q0 = static_cast<int>(threadIdx.x) * NQ;
+      const int nq = exact ? NQX : NQ;
+      const int q0 = static_cast<int>(threadIdx.x) * nq;
       s_rec[q0] = make_float4(1e6f, 1e6f, 0.0f, 0.0f);
       s_rec[q0 + 1] = make_float4(0.0f, -__builtin_inff(), 0.0f, 0.0f);
 #pragma unroll
-      for (int q = 2; q < NQ; ++q) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int q = 2; q < NQX; ++q)
+        if (q < nq) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     __syncthreads();
     // Branch-free per member; a wave leaves the batch once all its lanes
@@ -361,11 +438,13 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     } else {
       for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
         if (__all(T < kTermT)) break;
-#pragma unroll
+        // four at a time: the unscaled layout's fourth quad would not fit
+        // the 64 registers of 8 waves per SIMD at eight
+#pragma unroll 2
         for (int jj = 0; jj < kUnroll; ++jj) {
           const int j = j0 + jj;
-          fwd_member<C, true>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf,
-                              pyf, T, acc, lastj, j, j < cnt);
+          fwd_member_ref<C>(s_rec[j * NQX], s_rec[j * NQX + 1], s_rec[j * NQX + 2],
+                            s_rec[j * NQX + (NQX - 1)], pxf, pyf, T, acc, lastj, j, j < cnt);
         }
       }
     }
@@ -397,25 +476,27 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
 template <int C, bool kSub>
 __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   constexpr int NQ = rec_quads(C);
+  // Exact batches' staged layout: quad 0 (mx, my, cxx, cxy), quad 1 (czz,
+  // log2(o w), k, o w), quad 2 (cxx^2, cxy^2, cxx cxy, cxy czz), quad 3
+  // (czz^2, -det_inv, re0, im0), quad 4 (re1, im1, re2, im2) for C >= 2
+  // (the conic unscaled, in the reference's backward form; quads 2-3 hold
+  // the coefficients of its conic-to-covariance gradient map).
+  constexpr int NQE = C >= 2 ? 5 : 4;
+  constexpr int NQM = NQE > NQ ? NQE : NQ;
   constexpr int RS = rec_stride(C);
   constexpr int NV = 6 + 2 * C;
   constexpr int G = 64 / NV;
-  // Slot kBlock of s_rec is a dummy member that no pixel can use (mean far
-  // away, list position beyond every n_contrib): the per-wave lists are
-  // padded with it to a multiple of G, so the member loop needs no bounds.
+  // Slot kBlock of s_rec is a dummy member that no pixel can use (list
+  // position beyond every n_contrib): the per-wave lists are padded with it
+  // to a multiple of G, so the member loop needs no bounds.  It is written
+  // per batch in that batch's layout.
   constexpr int kDummy = kBlock;
-  __shared__ float4 s_rec[(kBlock + 1) * NQ];
+  __shared__ float4 s_rec[(kBlock + 1) * NQM];
   __shared__ int s_g[kBlock];
   __shared__ float s_acc[kBlock * NV];
   __shared__ unsigned short s_wl[4][kBlock + G];
   __shared__ int s_cnt[4][5];
   __shared__ int s_wmax[4];
-  if (threadIdx.x < NQ) {
-    s_rec[kDummy * NQ + threadIdx.x] =
-        threadIdx.x == 0   ? make_float4(1e6f, 1e6f, kBwdConicScale, 0.0f)
-        : threadIdx.x == 1 ? make_float4(kBwdConicScale, 0.0f, __int_as_float(0x7FFFFFFF), 1.0f)
-                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  }
 
   int tile, plane;
   if (kSub) {
@@ -442,7 +523,6 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   const int64_t HW = static_cast<int64_t>(p.W) * p.H;
   const int64_t pix = static_cast<int64_t>(pyi) * p.W + pxi;
   const int AS = acc_stride(C, p.P);
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
   float T = 0.0f;
   int last = 0;
@@ -499,6 +579,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     int k = idx;
     int g = 0;
     unsigned qm = 0;
+    bool ill = false;  // conic outside the fast loop's domain (conic_safe)
     float4 rq[2];  // quads 0-1 (geometry); the amplitude quads load once culled
     float wpl = 0.0f;
     const float4* src = nullptr;
@@ -521,6 +602,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
         const float thr = alpha_threshold(rq[1].z * wpl);
         if (thr >= 0.0f) {
+          ill = !conic_safe(rq[0].z, rq[0].w, rq[0].w, rq[1].y);
           const CullShape cs = cull_shape(rq[0].z, rq[0].w, rq[1].y);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
@@ -535,25 +617,37 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     bal[0] = __ballot(qm != 0u);
 #pragma unroll
     for (int w = 0; w < 4; ++w) bal[1 + w] = __ballot((qm >> w) & 1u);
+    // A batch staging any conic outside the fast loop's domain runs the
+    // reference-order loop (the flag rides in the wave's staged count).
+    const bool w_ill = __ballot(qm != 0u && ill) != 0ull;
     if (lane == 0) {
 #pragma unroll
-      for (int f = 0; f < 5; ++f) s_cnt[wave][f] = __popcll(bal[f]);
+      for (int f = 0; f < 5; ++f) s_cnt[wave][f] = __popcll(bal[f]) | (f == 0 && w_ill ? 0x100 : 0);
     }
     __syncthreads();
     int off[5], tot[5];
+    bool exact = false;
 #pragma unroll
     for (int f = 0; f < 5; ++f) {
       off[f] = 0;
       tot[f] = 0;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const int c = __builtin_amdgcn_readfirstlane(s_cnt[w][f]);  // same in every lane
+        const int sc = __builtin_amdgcn_readfirstlane(s_cnt[w][f]);  // same in every lane
+        const int c = sc & 0xFF;
+        if (f == 0) exact = exact || (sc & 0x100) != 0;
         off[f] += (w < wave) ? c : 0;
         tot[f] += c;
       }
-      off[f] += __popcll(bal[f] & lt);
+      off[f] += bits_below_lane(bal[f]);
     }
     const int cnt = tot[0];
+    const int nqb = exact ? NQE : NQ;  // this batch's staged quads per member
+    if (static_cast<int>(threadIdx.x) < nqb)
+      s_rec[kDummy * nqb + threadIdx.x] =
+          threadIdx.x == 0   ? make_float4(1e6f, 1e6f, 0.0f, 0.0f)
+          : threadIdx.x == 1 ? make_float4(0.0f, 0.0f, __int_as_float(0x7FFFFFFF), 1.0f)
+                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (qm != 0u) {
       const int slot = off[0];
       // quad 0: (mx, my, kc*cxx, 2 kc*cxy); quad 1: (kc*czz, log2(o*w), k,
@@ -562,15 +656,30 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       // exp2(pw) = o w G (the reference's backward exponent: one
       // off-diagonal, doubled, backward_splat.cu:208-210).  Quad 1 also
       // carries the list position (int bits) for the n_contrib test.
+      // Exact batches stage the NQE-quad layout above.  Amplitude quads
+      // only for members that survived the cull (same 64-byte record as
+      // quads 0-1, so the loads hit the cache).
       const float ow = rq[1].z * wpl;
-      s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
-                                     2.0f * kBwdConicScale * rq[0].w);
-      s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, __builtin_amdgcn_logf(ow),
-                                         __int_as_float(k), ow);
-      // Amplitude quads only for members that survived the cull (same
-      // 64-byte record as quads 0-1, so the loads hit the cache).
+      if (!exact) {
+        s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
+                                       2.0f * kBwdConicScale * rq[0].w);
+        s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, __builtin_amdgcn_logf(ow),
+                                           __int_as_float(k), ow);
 #pragma unroll
-      for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = src[q];
+        for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = src[q];
+      } else {
+        const float cxx = rq[0].z, cxy = rq[0].w, czz = rq[1].y, di = rq[1].w;
+        const float4 am = src[2];
+        s_rec[slot * NQE] = rq[0];
+        s_rec[slot * NQE + 1] =
+            make_float4(czz, __builtin_amdgcn_logf(ow), __int_as_float(k), ow);
+        s_rec[slot * NQE + 2] = make_float4(cxx * cxx, cxy * cxy, cxx * cxy, cxy * czz);
+        s_rec[slot * NQE + 3] = make_float4(czz * czz, -di, am.x, am.y);
+        if (NQE > 4) {
+          const float4 am2 = NQ > 3 ? src[NQ > 3 ? 3 : 2] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          s_rec[slot * NQE + (NQE > 4 ? 4 : 3)] = make_float4(am.z, am.w, am2.x, am2.y);
+        }
+      }
       s_g[slot] = g;
       // Each wave's list is stored after its padding, so it ends at a
       // multiple of G.
@@ -591,6 +700,11 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     int nl = 0;  // this wave's padded list length (a multiple of G)
 #pragma unroll
     for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] + (G - tot[1 + w] % G) % G : nl;
+    // The member walk, instantiated for the fast exponent and for the
+    // reference-order one (exact batches).
+    auto walk = [&](auto ref_tag) {
+    constexpr bool kRef = decltype(ref_tag)::value;
+    constexpr int nq = kRef ? NQE : NQ;
     for (int hi = nl - 1; hi >= 0; hi -= G) {
       // Branch-free: every lane evaluates every member of the group and a
       // single predicate `ok` (list position < n_contrib, power <= 0,
@@ -600,29 +714,50 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
       for (int m = 0; m < G; ++m) {
         const int slot = s_wl[wave][hi - m];
-        const float4 a = s_rec[slot * NQ];
-        const float4 b = s_rec[slot * NQ + 1];
+        const float4 a = s_rec[slot * nq];
+        const float4 b = s_rec[slot * nq + 1];
         const int kk = __float_as_int(b.z);
         const float dx = a.x - pxf, dy = a.y - pyf;
-        const float t = fmaf(a.z, dx, a.w * dy);
-        const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));  // log2(e) power + log2(o w)
-        const float Ga = __builtin_amdgcn_exp2f(pw);             // o w G
+        float pw;  // log2(e) power + log2(o w)
+        bool skip;
+        if (kRef) {
+          // backward_splat.cu:211 in its order, each step rounded on its own
+          const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+          pw = fmaf(kLog2E, power, b.y);
+          skip = power > 0.0f;
+        } else {
+          const float t = fmaf(a.z, dx, a.w * dy);
+          pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
+          skip = pw > b.y;
+        }
+        const float Ga = __builtin_amdgcn_exp2f(pw);  // o w G
         const float alpha = fminf(kMaxAlpha, Ga);
-        const bool ok = kk < last && !(pw > b.y) && alpha >= kMinAlphaBwd;
+        const bool ok = kk < last && !skip && alpha >= kMinAlphaBwd;
         any = any || ok;
         // A member that does not contribute at this pixel takes alpha = 0:
         // T * rcp(1) and 0 * x leave T and the partials exactly unchanged.
         const float ae = ok ? alpha : 0.0f;
-        T = T * __builtin_amdgcn_rcpf(1.0f - ae);
+        T = div_rn(T, 1.0f - ae);
         const float dcol = ae * T;
         // Re(colour * conj(g)) summed over channels; the reference's complex
         // recurrence acc = la*last + (1-la)*acc is linear, so only its
         // projection R = sum_c Re(acc_c conj(g_c)) is carried.
         float S;
+        float4 mc, c0, c1;  // exact: map coefficients (quads 2-3)
         {
-          const float4 c0 = s_rec[slot * NQ + 2];
-          const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
-          const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+          float amp[8];
+          if (kRef) {
+            mc = s_rec[slot * NQE + 2];
+            c0 = s_rec[slot * NQE + 3];
+            c1 = s_rec[slot * NQE + (NQE > 4 ? 4 : 3)];
+            amp[0] = c0.z, amp[1] = c0.w, amp[2] = c1.x, amp[3] = c1.y;
+            amp[4] = c1.z, amp[5] = c1.w, amp[6] = 0.0f, amp[7] = 0.0f;
+          } else {
+            c0 = s_rec[slot * NQ + 2];
+            c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
+            amp[0] = c0.x, amp[1] = c0.y, amp[2] = c0.z, amp[3] = c0.w;
+            amp[4] = c1.x, amp[5] = c1.y, amp[6] = c1.z, amp[7] = c1.w;
+          }
           S = amp[0] * gre[0];
           S = fmaf(amp[1], gim[0], S);
 #pragma unroll
@@ -639,13 +774,28 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         pend = ok ? alpha * dS : pend;
         const float Q = (ok ? Ga : 0.0f) * (dS * T);  // o w times dL/dG
         const float Qdx = Q * dx, Qdy = Q * dy;
-        // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v: the
-        // flush forms them from these two sums and the member's conic
-        buf[m * NV + 0] = Qdx;
-        buf[m * NV + 1] = Qdy;
-        buf[m * NV + 2] = Qdx * dx;
-        buf[m * NV + 3] = Qdx * dy;
-        buf[m * NV + 4] = Qdy * dy;
+        if (kRef) {
+          // Per pixel, as the reference (backward_splat.cu:270-291): the
+          // mean terms Q (cxx dx + cxy dy), Q (cxy dx + czz dy) and the
+          // covariance terms through the conic-to-covariance map (times
+          // -2), so no sum is mapped afterwards: for a nearly singular
+          // conic the map would amplify the sums' rounding by ~1/(1 - r^2).
+          const float u = Qdx * dx, v = Qdx * dy, w = Qdy * dy;
+          buf[m * NV + 0] = Q * fmaf(a.z, dx, a.w * dy);
+          buf[m * NV + 1] = Q * fmaf(a.w, dx, b.x * dy);
+          buf[m * NV + 2] = fmaf(mc.x, u, mc.y * w);
+          buf[m * NV + 3] = fmaf(mc.z, u, fmaf(c0.y, v, mc.w * w));
+          buf[m * NV + 4] = fmaf(mc.y, u, c0.x * w);
+        } else {
+          // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v:
+          // the flush forms them from these two sums and the member's
+          // conic, and maps the three second moments
+          buf[m * NV + 0] = Qdx;
+          buf[m * NV + 1] = Qdy;
+          buf[m * NV + 2] = Qdx * dx;
+          buf[m * NV + 3] = Qdx * dy;
+          buf[m * NV + 4] = Qdy * dy;
+        }
         buf[m * NV + 5] = Q;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -664,11 +814,17 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         }
       }
     }
+    };
+    if (exact)
+      walk(std::true_type{});
+    else
+      walk(std::false_type{});
     __syncthreads();
     for (int e = threadIdx.x; e < cnt * NV; e += kBlock) {
       const int j = e / NV, i = e - j * NV;
       float val = s_acc[e];
-      if (i < 2) {
+      const int gg = s_g[j];
+      if (!exact && i < 2) {
         // sum Q u = kc cxx sum Q dx + kc cxy sum Q dy; sum Q v = kc cxy
         // sum Q dx + kc czz sum Q dy (the staged conic is scaled by kc, the
         // off-diagonal doubled)
@@ -676,21 +832,33 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         const float sx = s_acc[j * NV], sy = s_acc[j * NV + 1];
         const float kxy = 0.5f * a.w;
         val = i == 0 ? fmaf(a.z, sx, kxy * sy) : fmaf(kxy, sx, s_rec[j * NQ + 1].x * sy);
+      } else if (!exact && i < 5) {
+        // The reference's conic-to-covariance map (backward_splat.cu:285-
+        // 291) on the block's second moments U, V, W of the member (a conic
+        // in the fast loop's domain, so the map is well conditioned), with
+        // the record's unscaled conic and 1/det: xx = cxx^2 U + cxy^2 W,
+        // xy = cxx cxy U - V / det + cxy czz W, yy = cxy^2 U + czz^2 W.
+        const float4* r = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(gg) * RS);
+        const float4 r0 = r[0], r1 = r[1];
+        const float cxx = r0.z, cxy = r0.w, czz = r1.y;
+        const float U = s_acc[j * NV + 2], V = s_acc[j * NV + 3], Wm = s_acc[j * NV + 4];
+        val = i == 2   ? fmaf(cxx * cxx, U, (cxy * cxy) * Wm)
+              : i == 3 ? fmaf(cxx * cxy, U, fmaf(-r1.w, V, (cxy * czz) * Wm))
+                       : fmaf(cxy * cxy, U, (czz * czz) * Wm);
       }
       if (val == 0.0f) continue;
-      const int gg = s_g[j];
       // The partials carry o w (Q = o w dL/dG): the mean and conic terms
       // need exactly that factor, the o w term (sum G dL/dalpha) its
       // removal.
-      const float ow = s_rec[j * NQ + 1].w;
+      const float ow = s_rec[j * nqb + 1].w;
       int slot;
       float scale;
       if (i == 0) {  // sum Q u, u = kc*(cxx dx + cxy dy)
         slot = 0;
-        scale = -half_w / kBwdConicScale;
+        scale = exact ? -half_w : -half_w / kBwdConicScale;
       } else if (i == 1) {
         slot = 1;
-        scale = -half_h / kBwdConicScale;
+        scale = exact ? -half_h : -half_h / kBwdConicScale;
       } else if (i < 5) {
         slot = i;
         scale = -0.5f;

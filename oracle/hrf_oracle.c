@@ -391,31 +391,32 @@ void oracle_render_forward(int W, int H, int P, int C, const int32_t* ranges,
  * complex interleaved.  Outputs (double accumulators, zeroed here):
  * g_means2d (N,2), g_cov2d (N,4), g_col (N,C), g_phase (N,C), g_opac (N),
  * g_plane (N,P).  tile_mask as in oracle_render_forward: only the pixels of
- * the selected tiles contribute. */
-void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t* ranges,
-                            const int32_t* point_list, const float* means2d,
-                            const float* cov2d, const float* colours, const float* phase,
-                            const float* opac, const float* pprobs, const float* final_T,
-                            const int32_t* n_contrib, const float* grad_field,
-                            double* g_means2d, double* g_cov2d, double* g_col, double* g_phase,
-                            double* g_opac, double* g_plane, const uint8_t* tile_mask) {
+ * the selected tiles contribute.
+ *
+ * The (tile, plane) pairs run in parallel, each summing its pixels' terms
+ * into doubles indexed by tile-list position (pixels in row-major order
+ * within the tile); those partial sums are then added into the
+ * per-Gaussian accumulators in (tile, plane, position) order, so the result
+ * does not depend on the thread count.  The per-pixel float arithmetic is
+ * the reference's, in its order. */
+enum { BW_MX, BW_MY, BW_CXX, BW_CXY, BW_CYY, BW_OPAC, BW_PLANE, BW_COL };
+
+static void render_backward_tile_plane(int W, int H, int P, int C, int tile, int p, int r0,
+                                       int r1, const int32_t* point_list,
+                                       const float* means2d, const float* cov2d,
+                                       const float* colours, const float* phase,
+                                       const float* opac, const float* pprobs,
+                                       const float* final_T, const int32_t* n_contrib,
+                                       const float* grad_field, double* acc, int nv) {
   const int gx = (W + TILE - 1) / TILE;
   const int64_t HW = (int64_t)W * H;
-  memset(g_means2d, 0, sizeof(double) * 2 * n);
-  memset(g_cov2d, 0, sizeof(double) * 4 * n);
-  memset(g_col, 0, sizeof(double) * C * n);
-  memset(g_phase, 0, sizeof(double) * C * n);
-  memset(g_opac, 0, sizeof(double) * n);
-  memset(g_plane, 0, sizeof(double) * P * n);
   const float ddelx_dx = 0.5f * (float)W;
   const float ddely_dy = 0.5f * (float)H;
-  for (int64_t pix = 0; pix < HW; ++pix) {
-    const int py = (int)(pix / W), px = (int)(pix % W);
-    const int tile = (py / TILE) * gx + (px / TILE);
-    if (tile_mask && !tile_mask[tile]) continue;
-    const int r0 = ranges[2 * tile], r1 = ranges[2 * tile + 1];
-    const float pxf = (float)px, pyf = (float)py;
-    for (int p = 0; p < P; ++p) {
+  const int tx = tile % gx, ty = tile / gx;
+  for (int py = ty * TILE; py < ty * TILE + TILE && py < H; ++py)
+    for (int px = tx * TILE; px < tx * TILE + TILE && px < W; ++px) {
+      const int64_t pix = (int64_t)py * W + px;
+      const float pxf = (float)px, pyf = (float)py;
       float gre[3], gim[3];
       for (int c = 0; c < C; ++c) {
         const int64_t idx = ((int64_t)p * C + c) * HW + pix;
@@ -430,6 +431,7 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
         const int contributor = k - r0; /* 0-based position in the tile list */
         if (contributor >= last) continue;
         const int g = point_list[k];
+        double* a = acc + (int64_t)contributor * nv;
         const float w = pprobs[(int64_t)g * P + p];
         if (w < PLANE_CUTOFF) continue;
         const float dx = means2d[g * 2 + 0] - pxf, dy = means2d[g * 2 + 1] - pyf;
@@ -464,9 +466,9 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
           dL_dalpha += (color_real - accr[c]) * gre[c];
           dL_dalpha += (color_imag - acci[c]) * gim[c];
           const float dL_dcolor = dchannel_dcolor * (cs * gre[c] + sn * gim[c]);
-          g_col[(int64_t)g * C + c] += dL_dcolor;
+          a[BW_COL + c] += dL_dcolor;
           const float dL_dphase = dchannel_dcolor * color * (-sn * gre[c] + cs * gim[c]);
-          g_phase[(int64_t)g * C + c] += dL_dphase;
+          a[BW_COL + C + c] += dL_dphase;
         }
         dL_dalpha *= T;
         last_alpha = alpha;
@@ -475,8 +477,8 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
         const float gdy = G * dy;
         const float dG_ddelx = -gdx * conic_x - gdy * conic_y;
         const float dG_ddely = -gdy * conic_z - gdx * conic_y;
-        g_means2d[g * 2 + 0] += dL_dG * dG_ddelx * ddelx_dx;
-        g_means2d[g * 2 + 1] += dL_dG * dG_ddely * ddely_dy;
+        a[BW_MX] += dL_dG * dG_ddelx * ddelx_dx;
+        a[BW_MY] += dL_dG * dG_ddely * ddely_dy;
         const float dL_dconic_x = -0.5f * gdx * dx * dL_dG;
         const float dL_dconic_y = -0.5f * gdx * dy * dL_dG;
         const float dL_dconic_z = -0.5f * gdy * dy * dL_dG;
@@ -487,15 +489,69 @@ void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t
                                  dL_dconic_z * (-cy * det_inv * det_inv) * cx;
         const float dL_dcov_yy = dL_dconic_x * (-cy * det_inv * det_inv) * (-cy) +
                                  dL_dconic_z * (cx * det_inv * det_inv) * cx;
-        g_cov2d[g * 4 + 0] += dL_dcov_xx;
-        g_cov2d[g * 4 + 1] += dL_dcov_xy;
-        g_cov2d[g * 4 + 2] += dL_dcov_xy;
-        g_cov2d[g * 4 + 3] += dL_dcov_yy;
-        g_opac[g] += G * w * dL_dalpha;
-        g_plane[(int64_t)g * P + p] += o * G * dL_dalpha;
+        a[BW_CXX] += dL_dcov_xx;
+        a[BW_CXY] += dL_dcov_xy; /* the reference adds it to both off-diagonals */
+        a[BW_CYY] += dL_dcov_yy;
+        a[BW_OPAC] += G * w * dL_dalpha;
+        a[BW_PLANE] += o * G * dL_dalpha;
       }
     }
+}
+
+void oracle_render_backward(int64_t n, int W, int H, int P, int C, const int32_t* ranges,
+                            const int32_t* point_list, const float* means2d,
+                            const float* cov2d, const float* colours, const float* phase,
+                            const float* opac, const float* pprobs, const float* final_T,
+                            const int32_t* n_contrib, const float* grad_field,
+                            double* g_means2d, double* g_cov2d, double* g_col, double* g_phase,
+                            double* g_opac, double* g_plane, const uint8_t* tile_mask) {
+  const int gx = (W + TILE - 1) / TILE, gy = (H + TILE - 1) / TILE;
+  const int64_t njobs = (int64_t)gx * gy * P;
+  const int nv = BW_COL + 2 * C;
+  memset(g_means2d, 0, sizeof(double) * 2 * n);
+  memset(g_cov2d, 0, sizeof(double) * 4 * n);
+  memset(g_col, 0, sizeof(double) * C * n);
+  memset(g_phase, 0, sizeof(double) * C * n);
+  memset(g_opac, 0, sizeof(double) * n);
+  memset(g_plane, 0, sizeof(double) * P * n);
+  double** part = (double**)calloc((size_t)(njobs > 0 ? njobs : 1), sizeof(double*));
+  if (!part) abort();
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t job = 0; job < njobs; ++job) {
+    const int tile = (int)(job / P), p = (int)(job % P);
+    if (tile_mask && !tile_mask[tile]) continue;
+    const int r0 = ranges[2 * tile], r1 = ranges[2 * tile + 1];
+    if (r1 <= r0) continue;
+    double* acc = (double*)calloc((size_t)(r1 - r0) * nv, sizeof(double));
+    if (!acc) abort();
+    render_backward_tile_plane(W, H, P, C, tile, p, r0, r1, point_list, means2d, cov2d, colours,
+                               phase, opac, pprobs, final_T, n_contrib, grad_field, acc, nv);
+    part[job] = acc;
   }
+  for (int64_t job = 0; job < njobs; ++job) {
+    double* acc = part[job];
+    if (!acc) continue;
+    const int tile = (int)(job / P), p = (int)(job % P);
+    const int r0 = ranges[2 * tile], r1 = ranges[2 * tile + 1];
+    for (int k = r0; k < r1; ++k) {
+      const double* a = acc + (int64_t)(k - r0) * nv;
+      const int64_t g = point_list[k];
+      g_means2d[g * 2 + 0] += a[BW_MX];
+      g_means2d[g * 2 + 1] += a[BW_MY];
+      g_cov2d[g * 4 + 0] += a[BW_CXX];
+      g_cov2d[g * 4 + 1] += a[BW_CXY];
+      g_cov2d[g * 4 + 2] += a[BW_CXY];
+      g_cov2d[g * 4 + 3] += a[BW_CYY];
+      for (int c = 0; c < C; ++c) {
+        g_col[g * C + c] += a[BW_COL + c];
+        g_phase[g * C + c] += a[BW_COL + C + c];
+      }
+      g_opac[g] += a[BW_OPAC];
+      g_plane[g * P + p] += a[BW_PLANE];
+    }
+    free(acc);
+  }
+  free(part);
 }
 
 /* ----------------------------------------------------- geometry backward */

@@ -16,6 +16,11 @@ row), plus random non-empty tiles:
   member lists reused) against the oracle's tile-masked render backward and
   its geometry backward over all Gaussians.
 
+Config 4 (3M Gaussians at 1920x1080, ~8.7e8 pairs, ~1e5-entry lists in its
+densest tiles) takes the same checks; only the selected tiles' slices of
+point_list are copied to the host (the whole list is 3.5 GB), and the oracle
+renders from those slices with the ranges rebased onto them.
+
 Config 0 (10k Gaussians at 256x256, P = C = 1) is small enough for the
 oracle's full render: whole-image forward and backward parity, and the
 frame's hologram through the multi-plane ASM.
@@ -74,7 +79,24 @@ def _pixel_mask(sel, gx, gy, W, H):
     return tm, pm
 
 
-@pytest.mark.parametrize("name", ["headline", "cfg1", "cfg2"])
+def _selected_lists(pl, ranges_h, sel):
+    """The selected tiles' slices of the device point list, concatenated, and
+    ranges rebased onto that host array ((0, 0) for every other tile)."""
+    import torch
+
+    parts, rr = [], np.zeros_like(ranges_h)
+    at = 0
+    for t in sel:
+        a, b = int(ranges_h[t, 0]), int(ranges_h[t, 1])
+        if b > a:
+            parts.append(pl[a:b])
+            rr[t] = (at, at + b - a)
+            at += b - a
+    pl_h = torch.cat(parts).cpu().numpy() if parts else np.zeros(0, np.int32)
+    return pl_h, rr
+
+
+@pytest.mark.parametrize("name", ["headline", "cfg1", "cfg2", "cfg4"])
 def test_config_tiles_forward_backward_parity(hrf, oracle_mod, name):
     import torch
     from complex_valued_holographic_radiance_fields_amd import rasterizer, scenes
@@ -96,24 +118,27 @@ def test_config_tiles_forward_backward_parity(hrf, oracle_mod, name):
     K = int(pl.numel())
     print(f"{name}: N={g.n} K={K} tiles={sel}", flush=True)
     assert 16 <= len(sel)
-    if name == "cfg2":
+    if name in ("cfg2", "cfg4"):
         assert H % 16 != 0 and any(tt // gx == gy - 1 for tt in sel)  # partial bottom row
+    lens = ranges_h[:, 1].astype(np.int64) - ranges_h[:, 0]
+    print(f"{name}: selected list lengths {sorted(int(lens[tt]) for tt in sel)}", flush=True)
 
     pr = oracle_mod.project(g, cam)
     _, tiles_ref, rect_ref = oracle_mod.preprocess(pr["means2d"], pr["cov2d"], g.z, cam)
     assert K == int(tiles_ref.astype(np.int64).sum())
-    pl_h = pl.cpu().numpy()
-    _check_tile_lists(sel, lambda tt: pl_h[ranges_h[tt, 0]:ranges_h[tt, 1]], ranges_h,
+    pl_h, rr_h = _selected_lists(pl, ranges_h, sel)
+    _check_tile_lists(sel, lambda tt: pl_h[rr_h[tt, 0]:rr_h[tt, 1]], ranges_h,
                       rect_ref.astype(np.int64), _depth_key(g.z), gx)
 
     tm, pm = _pixel_mask(sel, gx, gy, W, H)
-    rf, rT, rn = oracle_mod.render_forward(g, cam, pr["means2d"], pr["cov2d"], pl_h, ranges_h,
+    rf, rT, rn = oracle_mod.render_forward(g, cam, pr["means2d"], pr["cov2d"], pl_h, rr_h,
                                            tile_mask=tm)
     f_h = field.cpu().numpy()
-    assert rel_l2(f_h[:, :, pm], rf[:, :, pm]) < TOL
-    assert rel_l2(fT.cpu().numpy()[:, pm], rT[:, pm]) < TOL
-    mism = np.mean(nc.cpu().numpy()[:, pm] != rn[:, pm])
-    assert mism < 1e-3, mism
+    e_f = rel_l2(f_h[:, :, pm], rf[:, :, pm])
+    e_t = rel_l2(fT.cpu().numpy()[:, pm], rT[:, pm])
+    mism = float(np.mean(nc.cpu().numpy()[:, pm] != rn[:, pm]))
+    print(f"{name}: field rel_l2={e_f:.2e} final_T rel_l2={e_t:.2e} "
+          f"n_contrib mismatch={mism:.2e}", flush=True)
 
     rng = np.random.default_rng(17)
     gf = ((rng.normal(size=(P, C, H, W)) + 1j * rng.normal(size=(P, C, H, W))) *
@@ -124,7 +149,7 @@ def test_config_tiles_forward_backward_parity(hrf, oracle_mod, name):
                                 sc.fx, sc.fy, sc.px, sc.py, t["view"], (W, H), (16, 16), fT, nc,
                                 pl, ranges, 1.0, 1000.0, geometry=geom)
     torch.cuda.synchronize()
-    rb = oracle_mod.render_backward(g, cam, pr["means2d"], pr["cov2d"], pl_h, ranges_h, rT, rn,
+    rb = oracle_mod.render_backward(g, cam, pr["means2d"], pr["cov2d"], pl_h, rr_h, rT, rn,
                                     gf, tile_mask=tm)
     gc, gq, gs = oracle_mod.geom_backward(g, cam, rb["means2d"].astype(np.float32),
                                           rb["cov2d"].astype(np.float32))
@@ -133,12 +158,18 @@ def test_config_tiles_forward_backward_parity(hrf, oracle_mod, name):
     touched = int(np.count_nonzero(np.any(rb["colours"] != 0, axis=1)))
     print(f"{name}: {touched} Gaussians with nonzero colour gradients", flush=True)
     assert touched > 100
+    errs = {}
     for nm, gg in zip(NAMES, grads):
         got = gg.cpu().numpy()
         if nm == "z":
             assert not got.any()
             continue
-        e = rel_l2(got, ref[nm])
+        errs[nm] = rel_l2(got, ref[nm])
+    print(f"{name}: gradient rel_l2 " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()),
+          flush=True)
+    assert e_f < TOL and e_t < TOL, (e_f, e_t)
+    assert mism < 1e-3, mism
+    for nm, e in errs.items():
         assert e < TOL, (nm, e)
     del field, info, geom, grads
     torch.cuda.empty_cache()
