@@ -661,6 +661,11 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.n = n;
   rp.num_pairs = num_pairs;
   if (plane_lists) {
+    if (n >= (int64_t{1} << 28)) {
+      set_error("plane member lists need fewer than 2^28 Gaussians (got %lld)",
+                static_cast<long long>(n));
+      return HRF_ERR_INVALID;
+    }
     HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
                      hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
                      "plane lists"));
@@ -723,6 +728,11 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
   // lists' order words).
   SubWs sw{};
   const bool use_sub = plane_lists && num_pairs > 0;
+  if (use_sub && n >= (int64_t{1} << 28)) {
+    set_error("plane member lists need fewer than 2^28 Gaussians (got %lld)",
+              static_cast<long long>(n));
+    return HRF_ERR_INVALID;
+  }
   if (use_sub) {
     HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
                      hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),

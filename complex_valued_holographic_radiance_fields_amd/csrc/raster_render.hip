@@ -85,10 +85,20 @@ __device__ __forceinline__ float div_rn(float a, float b) {
   return fmaf(fmaf(-q, b, a), r, q);
 }
 
-// The forward's per-wave batch word: member count and two flags.
+// The forward's per-wave batch word: member count, two flags, and the count
+// of members written to the plane member lists (bits 16-23).
 constexpr int kWtCount = 0xFF;
 constexpr int kWtUnsafe = 0x100;
 constexpr int kWtDone = 0x200;
+constexpr int kWtSubShift = 16;
+
+// Plane member list entries: (gaussian, list position | quadrant mask << 28).
+// The mask has bit w set when the member's alpha >= 1/255 region meets the
+// 8x8 quadrant w of the tile (the backward's box test, made once in the
+// forward); members meeting no quadrant are not listed.  List positions are
+// below the Gaussian count, which the library keeps under 2^28 for lists.
+constexpr int kSubPosBits = 28;
+constexpr uint32_t kSubPosMask = (1u << kSubPosBits) - 1u;
 
 // Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
 // only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
@@ -328,6 +338,7 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     // geometry quads; the amplitude quads load at the LDS write
     float4 rq[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
     float w = 0.0f;
+    unsigned qm4 = 0;  // quadrants the member reaches at alpha >= 1/255
     const float4* src = nullptr;
     {
       const int kn = k + kBlock;
@@ -344,6 +355,18 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       if (!box_reaches(rq[0].x, rq[0].y, cs, thr, tx0, ty0, static_cast<float>(kTile - 1))) {
         mem = false;
         atomicMax(&s_kcull, k + 1);
+      } else if (sub_out) {
+        // The backward's per-quadrant alpha >= 1/255 test, with the same
+        // threshold and shape (k_render_bwd's cull), for the list entry.
+        const float thb = alpha_threshold(rq[1].z * w);
+        if (thb >= 0.0f) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            qm4 |= box_reaches(rq[0].x, rq[0].y, cs, thb, tx0 + (q & 1) * 8, ty0 + (q >> 1) * 8,
+                               7.0f)
+                       ? (1u << q)
+                       : 0u;
+        }
       }
     }
     if (base + kBlock + static_cast<int>(threadIdx.x) < n &&
@@ -354,32 +377,40 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     // loop) and whether all its pixels are done (then the block is).  The
     // previous batch's LDS reads all precede it: its member loop ends before
     // the lanes reach this point.
-    int pos, cnt = 0;
+    int pos, cnt = 0, spos = 0, scnt = 0;
     bool exact = false;
     {
       const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
       const uint64_t bal = __ballot(mem);
+      const uint64_t bsub = __ballot(qm4 != 0u);
       const bool w_unsafe = __ballot(mem && !conic_safe(rq[0].z, rq[0].w, rq[1].x, rq[1].y)) != 0ull;
       const bool w_done = __ballot(!(T < kTermT)) == 0ull;
       if (lane == 0)
-        s_wt[wave] = __popcll(bal) | (w_unsafe ? kWtUnsafe : 0) | (w_done ? kWtDone : 0);
+        s_wt[wave] = __popcll(bal) | (w_unsafe ? kWtUnsafe : 0) | (w_done ? kWtDone : 0) |
+                     (__popcll(bsub) << kWtSubShift);
       __syncthreads();
-      int off = 0;
+      int off = 0, soff = 0;
       bool all_done = true;
 #pragma unroll
       for (int wv = 0; wv < kBlock / 64; ++wv) {
         const int t = s_wt[wv];
         const int c = t & kWtCount;
+        const int sc = (t >> kWtSubShift) & kWtCount;
         off += (wv < wave) ? c : 0;
         cnt += c;
+        soff += (wv < wave) ? sc : 0;
+        scnt += sc;
         exact = exact || (t & kWtUnsafe) != 0;
         all_done = all_done && (t & kWtDone) != 0;
       }
       if (all_done) break;
       pos = off + bits_below_lane(bal);
+      spos = soff + bits_below_lane(bsub);
     }
     if (mem) {
-      if (sub_out) sub_out[listed + pos] = make_int2(g, k);
+      if (qm4 != 0u)
+        sub_out[listed + spos] = make_int2(g, static_cast<int>(static_cast<uint32_t>(k) |
+                                                                (qm4 << kSubPosBits)));
       const float4 am = src[2];  // (re0, im0, re1, im1)
       const float lw = __builtin_amdgcn_logf(rq[1].z * w);
       if (!exact) {
@@ -402,13 +433,17 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     // can use: log2(o w) = -inf (alpha 0, T unchanged), in the same slot of
     // both layouts (the exact layout's zero conic gives s = 0, which passes
     // the power test).
-    listed += cnt;
+    listed += scnt;
     const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
     if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
       const int nq = exact ? NQX : NQ;
       const int q0 = static_cast<int>(threadIdx.x) * nq;
-      s_rec[q0] = make_float4(1e6f, 1e6f, 0.0f, 0.0f);
-      s_rec[q0 + 1] = make_float4(0.0f, -__builtin_inff(), 0.0f, 0.0f);
+      // Materialised here: hoisted out of the batch loop, these constants
+      // would not fit the 64 registers of 8 waves per SIMD.
+      float far = 1e6f, ninf = -__builtin_inff();
+      asm volatile("" : "+v"(far), "+v"(ninf));
+      s_rec[q0] = make_float4(far, far, 0.0f, 0.0f);
+      s_rec[q0 + 1] = make_float4(0.0f, ninf, 0.0f, 0.0f);
 #pragma unroll
       for (int q = 2; q < NQX; ++q)
         if (q < nq) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -466,6 +501,17 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
   }
 }
 
+// Backward staged record: the global record's quad count, one more at C = 2
+// for 1/det (see k_render_bwd).
+__host__ __device__ constexpr int bwd_quads(int C) { return C == 2 ? 4 : rec_quads(C); }
+
+// 1/det of the staged member's cov2D from its amplitude quads (c0 = quad 2,
+// c1 = the last quad).
+template <int C>
+__device__ __forceinline__ float bwd_det_inv(const float4 c0, const float4 c1) {
+  return C == 1 ? c0.z : (C == 2 ? c1.x : c1.z);
+}
+
 // Backward.  Waves own 8x8 quadrants of the tile.  Per batch, every staged
 // Gaussian gets a 4-bit quadrant mask (its alpha >= 1/255 region meets the
 // quadrant and its list position is below that quadrant's max n_contrib);
@@ -474,15 +520,14 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
 // transpose_reduce64.  Skipping a member for a whole wave is exact: every
 // lane of that wave would skip it (alpha < 1/255 or position >= n_contrib).
 template <int C, bool kSub>
-__global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
-  constexpr int NQ = rec_quads(C);
-  // Exact batches' staged layout: quad 0 (mx, my, cxx, cxy), quad 1 (czz,
-  // log2(o w), k, o w), quad 2 (cxx^2, cxy^2, cxx cxy, cxy czz), quad 3
-  // (czz^2, -det_inv, re0, im0), quad 4 (re1, im1, re2, im2) for C >= 2
-  // (the conic unscaled, in the reference's backward form; quads 2-3 hold
-  // the coefficients of its conic-to-covariance gradient map).
-  constexpr int NQE = C >= 2 ? 5 : 4;
-  constexpr int NQM = NQE > NQ ? NQE : NQ;
+__global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderParams p) {
+  // Staged record: quads 0-1 as below, then the amplitude quads of the
+  // global record, with 1/det of the member's cov2D in the first free slot
+  // after the amplitudes (an extra quad at C = 2).  Fast batches: quad 0
+  // (mx, my, kc cxx, 2 kc cxy), quad 1 (kc czz, log2(o w), k, o w).  Exact
+  // batches stage the conic unscaled, in the reference's backward form:
+  // quad 0 (mx, my, cxx, cxy), quad 1 (czz, log2(o w), k, o w).
+  constexpr int NQ = bwd_quads(C);
   constexpr int RS = rec_stride(C);
   constexpr int NV = 6 + 2 * C;
   constexpr int G = 64 / NV;
@@ -491,7 +536,7 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
   // to a multiple of G, so the member loop needs no bounds.  It is written
   // per batch in that batch's layout.
   constexpr int kDummy = kBlock;
-  __shared__ float4 s_rec[(kBlock + 1) * NQM];
+  __shared__ float4 s_rec[(kBlock + 1) * NQ];
   __shared__ int s_g[kBlock];
   __shared__ float s_acc[kBlock * NV];
   __shared__ unsigned short s_wl[4][kBlock + G];
@@ -583,18 +628,28 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     float4 rq[2];  // quads 0-1 (geometry); the amplitude quads load once culled
     float wpl = 0.0f;
     const float4* src = nullptr;
-    if (idx < end) {
-      bool member;
-      if (kSub) {
-        const int2 e = sub[idx];
-        g = e.x;
-        k = e.y;
-        member = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n);
-      } else {
-        g = p.plist[r0 + idx];
-        member = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
-                 ((p.pmask[g] >> plane) & 1u);
+    if (idx < end && kSub) {
+      // The forward's quadrant mask (alpha >= 1/255 box test); only the
+      // n_contrib bounds remain, and only survivors gather their records.
+      const int2 e = sub[idx];
+      g = e.x;
+      k = static_cast<int>(static_cast<uint32_t>(e.y) & kSubPosMask);
+      const uint32_t m4 = static_cast<uint32_t>(e.y) >> kSubPosBits;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) qm |= (((m4 >> w) & 1u) && k < wmax[w]) ? (1u << w) : 0u;
+      if (static_cast<uint64_t>(static_cast<uint32_t>(g)) >= static_cast<uint64_t>(p.n)) qm = 0;
+      if (qm != 0u) {
+        src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
+        rq[0] = src[0];
+        rq[1] = src[1];
+        wpl = p.pprobs[static_cast<int64_t>(g) * p.P + plane];
+        ill = !conic_safe(rq[0].z, rq[0].w, rq[0].w, rq[1].y);
       }
+    } else if (idx < end) {
+      g = p.plist[r0 + idx];
+      const bool member =
+          static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+          ((p.pmask[g] >> plane) & 1u);
       if (member) {
         src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
         rq[0] = src[0];
@@ -642,9 +697,8 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       off[f] += bits_below_lane(bal[f]);
     }
     const int cnt = tot[0];
-    const int nqb = exact ? NQE : NQ;  // this batch's staged quads per member
-    if (static_cast<int>(threadIdx.x) < nqb)
-      s_rec[kDummy * nqb + threadIdx.x] =
+    if (static_cast<int>(threadIdx.x) < NQ)
+      s_rec[kDummy * NQ + threadIdx.x] =
           threadIdx.x == 0   ? make_float4(1e6f, 1e6f, 0.0f, 0.0f)
           : threadIdx.x == 1 ? make_float4(0.0f, 0.0f, __int_as_float(0x7FFFFFFF), 1.0f)
                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -656,29 +710,28 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       // exp2(pw) = o w G (the reference's backward exponent: one
       // off-diagonal, doubled, backward_splat.cu:208-210).  Quad 1 also
       // carries the list position (int bits) for the n_contrib test.
-      // Exact batches stage the NQE-quad layout above.  Amplitude quads
-      // only for members that survived the cull (same 64-byte record as
-      // quads 0-1, so the loads hit the cache).
+      // Amplitude quads only for members that survived the cull (same
+      // 64-byte record as quads 0-1, so the loads hit the cache).
       const float ow = rq[1].z * wpl;
+      const float lw = __builtin_amdgcn_logf(ow);
       if (!exact) {
         s_rec[slot * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
                                        2.0f * kBwdConicScale * rq[0].w);
-        s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, __builtin_amdgcn_logf(ow),
-                                           __int_as_float(k), ow);
-#pragma unroll
-        for (int q = 2; q < NQ; ++q) s_rec[slot * NQ + q] = src[q];
+        s_rec[slot * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, lw, __int_as_float(k), ow);
       } else {
-        const float cxx = rq[0].z, cxy = rq[0].w, czz = rq[1].y, di = rq[1].w;
-        const float4 am = src[2];
-        s_rec[slot * NQE] = rq[0];
-        s_rec[slot * NQE + 1] =
-            make_float4(czz, __builtin_amdgcn_logf(ow), __int_as_float(k), ow);
-        s_rec[slot * NQE + 2] = make_float4(cxx * cxx, cxy * cxy, cxx * cxy, cxy * czz);
-        s_rec[slot * NQE + 3] = make_float4(czz * czz, -di, am.x, am.y);
-        if (NQE > 4) {
-          const float4 am2 = NQ > 3 ? src[NQ > 3 ? 3 : 2] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          s_rec[slot * NQE + (NQE > 4 ? 4 : 3)] = make_float4(am.z, am.w, am2.x, am2.y);
-        }
+        s_rec[slot * NQ] = rq[0];
+        s_rec[slot * NQ + 1] = make_float4(rq[1].y, lw, __int_as_float(k), ow);
+      }
+      const float4 am0 = src[2];
+      const float4 am1 = rec_quads(C) > 3 ? src[rec_quads(C) > 3 ? 3 : 2] : am0;
+      if (C == 1) {
+        s_rec[slot * NQ + 2] = make_float4(am0.x, am0.y, rq[1].w, 0.0f);
+      } else if (C == 2) {
+        s_rec[slot * NQ + 2] = am0;
+        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(rq[1].w, 0.0f, 0.0f, 0.0f);
+      } else {
+        s_rec[slot * NQ + 2] = am0;
+        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(am1.x, am1.y, rq[1].w, 0.0f);
       }
       s_g[slot] = g;
       // Each wave's list is stored after its padding, so it ends at a
@@ -704,7 +757,6 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
     // reference-order one (exact batches).
     auto walk = [&](auto ref_tag) {
     constexpr bool kRef = decltype(ref_tag)::value;
-    constexpr int nq = kRef ? NQE : NQ;
     for (int hi = nl - 1; hi >= 0; hi -= G) {
       // Branch-free: every lane evaluates every member of the group and a
       // single predicate `ok` (list position < n_contrib, power <= 0,
@@ -714,50 +766,39 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
 #pragma unroll
       for (int m = 0; m < G; ++m) {
         const int slot = s_wl[wave][hi - m];
-        const float4 a = s_rec[slot * nq];
-        const float4 b = s_rec[slot * nq + 1];
+        const float4 a = s_rec[slot * NQ];
+        const float4 b = s_rec[slot * NQ + 1];
         const int kk = __float_as_int(b.z);
         const float dx = a.x - pxf, dy = a.y - pyf;
-        float pw;  // log2(e) power + log2(o w)
-        bool skip;
+        bool ok;
+        float Ga;  // o w G
         if (kRef) {
           // backward_splat.cu:211 in its order, each step rounded on its own
           const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-          pw = fmaf(kLog2E, power, b.y);
-          skip = power > 0.0f;
+          Ga = __builtin_amdgcn_exp2f(fmaf(kLog2E, power, b.y));
+          ok = kk < last && !(power > 0.0f) && fminf(kMaxAlpha, Ga) >= kMinAlphaBwd;
         } else {
+          // A conic in this loop's domain cannot round to a positive
+          // exponent, and its alpha is finite: the alpha test reads o w G.
           const float t = fmaf(a.z, dx, a.w * dy);
-          pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
-          skip = pw > b.y;
+          Ga = __builtin_amdgcn_exp2f(fmaf(dx, t, fmaf(b.x * dy, dy, b.y)));
+          ok = kk < last && Ga >= kMinAlphaBwd;
         }
-        const float Ga = __builtin_amdgcn_exp2f(pw);  // o w G
-        const float alpha = fminf(kMaxAlpha, Ga);
-        const bool ok = kk < last && !skip && alpha >= kMinAlphaBwd;
         any = any || ok;
-        // A member that does not contribute at this pixel takes alpha = 0:
-        // T * rcp(1) and 0 * x leave T and the partials exactly unchanged.
-        const float ae = ok ? alpha : 0.0f;
+        // A member that does not contribute at this pixel takes G = alpha =
+        // 0: T / 1 and 0 * x leave T and the partials exactly unchanged.
+        const float Gz = ok ? Ga : 0.0f;
+        const float ae = fminf(kMaxAlpha, Gz);
         T = div_rn(T, 1.0f - ae);
         const float dcol = ae * T;
         // Re(colour * conj(g)) summed over channels; the reference's complex
         // recurrence acc = la*last + (1-la)*acc is linear, so only its
         // projection R = sum_c Re(acc_c conj(g_c)) is carried.
         float S;
-        float4 mc, c0, c1;  // exact: map coefficients (quads 2-3)
+        const float4 c0 = s_rec[slot * NQ + 2];
+        const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
         {
-          float amp[8];
-          if (kRef) {
-            mc = s_rec[slot * NQE + 2];
-            c0 = s_rec[slot * NQE + 3];
-            c1 = s_rec[slot * NQE + (NQE > 4 ? 4 : 3)];
-            amp[0] = c0.z, amp[1] = c0.w, amp[2] = c1.x, amp[3] = c1.y;
-            amp[4] = c1.z, amp[5] = c1.w, amp[6] = 0.0f, amp[7] = 0.0f;
-          } else {
-            c0 = s_rec[slot * NQ + 2];
-            c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
-            amp[0] = c0.x, amp[1] = c0.y, amp[2] = c0.z, amp[3] = c0.w;
-            amp[4] = c1.x, amp[5] = c1.y, amp[6] = c1.z, amp[7] = c1.w;
-          }
+          const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
           S = amp[0] * gre[0];
           S = fmaf(amp[1], gim[0], S);
 #pragma unroll
@@ -768,11 +809,13 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
         }
         // The reference's recurrence acc = a_l S_l + (1 - a_l) acc over the
         // contributing members: R advances by the pending a_l (S_l - R) of
-        // the previous contributor, and this member's becomes pending.
-        R += ok ? pend : 0.0f;
+        // the previous contributor, and this member's becomes pending.  A
+        // non-contributor (alpha 0) takes the pending increment early and
+        // leaves none, so the updates need no selects.
+        R += pend;
         const float dS = S - R;
-        pend = ok ? alpha * dS : pend;
-        const float Q = (ok ? Ga : 0.0f) * (dS * T);  // o w times dL/dG
+        pend = ae * dS;
+        const float Q = Gz * (dS * T);  // o w times dL/dG
         const float Qdx = Q * dx, Qdy = Q * dy;
         if (kRef) {
           // Per pixel, as the reference (backward_splat.cu:270-291): the
@@ -781,11 +824,13 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
           // -2), so no sum is mapped afterwards: for a nearly singular
           // conic the map would amplify the sums' rounding by ~1/(1 - r^2).
           const float u = Qdx * dx, v = Qdx * dy, w = Qdy * dy;
-          buf[m * NV + 0] = Q * fmaf(a.z, dx, a.w * dy);
-          buf[m * NV + 1] = Q * fmaf(a.w, dx, b.x * dy);
-          buf[m * NV + 2] = fmaf(mc.x, u, mc.y * w);
-          buf[m * NV + 3] = fmaf(mc.z, u, fmaf(c0.y, v, mc.w * w));
-          buf[m * NV + 4] = fmaf(mc.y, u, c0.x * w);
+          const float cxx = a.z, cxy = a.w, czz = b.x;
+          const float ndi = -bwd_det_inv<C>(c0, c1);
+          buf[m * NV + 0] = Q * fmaf(cxx, dx, cxy * dy);
+          buf[m * NV + 1] = Q * fmaf(cxy, dx, czz * dy);
+          buf[m * NV + 2] = fmaf(cxx * cxx, u, (cxy * cxy) * w);
+          buf[m * NV + 3] = fmaf(cxx * cxy, u, fmaf(ndi, v, (cxy * czz) * w));
+          buf[m * NV + 4] = fmaf(cxy * cxy, u, (czz * czz) * w);
         } else {
           // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v:
           // the flush forms them from these two sums and the member's
@@ -835,22 +880,26 @@ __global__ __launch_bounds__(kBlock) void k_render_bwd(RenderParams p) {
       } else if (!exact && i < 5) {
         // The reference's conic-to-covariance map (backward_splat.cu:285-
         // 291) on the block's second moments U, V, W of the member (a conic
-        // in the fast loop's domain, so the map is well conditioned), with
-        // the record's unscaled conic and 1/det: xx = cxx^2 U + cxy^2 W,
+        // in the fast loop's domain, so the map is well conditioned; the
+        // staged conic is unscaled by 1/kc): xx = cxx^2 U + cxy^2 W,
         // xy = cxx cxy U - V / det + cxy czz W, yy = cxy^2 U + czz^2 W.
-        const float4* r = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(gg) * RS);
-        const float4 r0 = r[0], r1 = r[1];
-        const float cxx = r0.z, cxy = r0.w, czz = r1.y;
+        const float4 a = s_rec[j * NQ];
+        const float cxx = a.z * (1.0f / kBwdConicScale);
+        const float cxy = a.w * (0.5f / kBwdConicScale);
+        const float czz = s_rec[j * NQ + 1].x * (1.0f / kBwdConicScale);
         const float U = s_acc[j * NV + 2], V = s_acc[j * NV + 3], Wm = s_acc[j * NV + 4];
         val = i == 2   ? fmaf(cxx * cxx, U, (cxy * cxy) * Wm)
-              : i == 3 ? fmaf(cxx * cxy, U, fmaf(-r1.w, V, (cxy * czz) * Wm))
+              : i == 3 ? fmaf(cxx * cxy, U,
+                              fmaf(-bwd_det_inv<C>(s_rec[j * NQ + 2],
+                                                   s_rec[j * NQ + (NQ > 3 ? 3 : 2)]),
+                                   V, (cxy * czz) * Wm))
                        : fmaf(cxy * cxy, U, (czz * czz) * Wm);
       }
       if (val == 0.0f) continue;
       // The partials carry o w (Q = o w dL/dG): the mean and conic terms
       // need exactly that factor, the o w term (sum G dL/dalpha) its
       // removal.
-      const float ow = s_rec[j * nqb + 1].w;
+      const float ow = s_rec[j * NQ + 1].w;
       int slot;
       float scale;
       if (i == 0) {  // sum Q u, u = kc*(cxx dx + cxy dy)

@@ -112,7 +112,9 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam,
  * ids t*P + q ordered by count, largest first (the backward's block order).
  * hrf_raster_forward_render fills the lists and counts (plane_lists
  * non-NULL) with each (tile, plane)'s members, in list order, over the
- * entries its compositing visited; hrf_raster_backward given the same
+ * entries its compositing visited, that can reach alpha >= 1/255 in some
+ * 8x8 quadrant of the tile (the quadrant mask rides in bits 28-31 of the
+ * list position, so lists need N < 2^28); hrf_raster_backward given the same
  * buffer writes the block order from the counts and walks those lists
  * instead of filtering every tile list once per plane.  No
  * counterpart in the reference (its backward re-reads the whole tile list

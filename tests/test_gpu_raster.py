@@ -406,6 +406,9 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     buf = geom.plane_lists.cpu().numpy()
     ntiles = ranges.shape[0]
     ent = buf[:P * K * 8].view(np.int32).reshape(P, K, 2)
+    # entry: (gaussian, list position | quadrant mask << 28)
+    epos = (ent[..., 1].view(np.uint32) & 0x0FFFFFFF).astype(np.int64)
+    emask = ent[..., 1].view(np.uint32) >> 28
     c0 = (P * K * 8 + 255) // 256 * 256
     cnt = buf[c0:c0 + ntiles * P * 4].view(np.int32).reshape(ntiles, P)
     o0 = (c0 + ntiles * P * 4 + 255) // 256 * 256
@@ -417,7 +420,18 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
     det = cov[:, 0] * cov[:, 3] - cov[:, 1] * cov[:, 2]
     cxx, cxy, czz = cov[:, 3] / det, -cov[:, 1] / det, cov[:, 0] / det
     gx = (W + 15) // 16
-    truncated = invisible = 0
+    # quadrant w of the tile: pixels (w & 1) * 8 .. +8 across, (w >> 1) * 8 .. +8 down
+    quad_of = ((np.repeat(np.arange(16), 16) >= 8) * 2 + (np.tile(np.arange(16), 16) >= 8))
+
+    def alpha_tile(gg, p, px, py):
+        dx = m2[gg, 0][:, None] - px[None, :]
+        dy = m2[gg, 1][:, None] - py[None, :]
+        q = cxx[gg][:, None] * dx * dx + 2 * cxy[gg][:, None] * dx * dy \
+            + czz[gg][:, None] * dy * dy
+        ow = g.opac[gg].astype(np.float64) * g.pprobs[gg, p]
+        return ow[:, None] * np.exp(-0.5 * q)
+
+    truncated = invisible = faint = listed = 0
     for tile in range(ntiles):
         r0, r1 = r_np[tile]
         ty, tx = divmod(tile, gx)
@@ -428,29 +442,41 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
             ks = np.nonzero(member[pl_np[r0:r1], p])[0]
             c = int(cnt[tile, p])
             assert 0 <= c <= len(ks)
-            got = ent[p, r0:r0 + c]
+            got, gpos, gmask = ent[p, r0:r0 + c], epos[p, r0:r0 + c], emask[p, r0:r0 + c]
             # the list: plane members in list order ...
-            assert np.all(np.diff(got[:, 1]) > 0) and np.all(np.isin(got[:, 1], ks))
-            np.testing.assert_array_equal(got[:, 0], pl_np[r0 + got[:, 1]])
+            assert np.all(np.diff(gpos) > 0) and np.all(np.isin(gpos, ks))
+            np.testing.assert_array_equal(got[:, 0], pl_np[r0 + gpos])
+            # ... each with the quadrants where it reaches alpha >= 1/255
+            # (the kernel's test has a margin of ~1% in alpha on the inside)
+            if c:
+                gg = pl_np[r0 + gpos]
+                aq = alpha_tile(gg, p, px, py)
+                amax = np.stack([aq[:, quad_of == w].max(1) for w in range(4)], 1)
+                # over the box spanned by the quadrant's pixel centres
+                abox = np.stack([_alpha_box_max(m2[gg], cxx[gg], cxy[gg], czz[gg],
+                                                g.opac[gg].astype(np.float64) * g.pprobs[gg, p],
+                                                tx * 16 + (w & 1) * 8, ty * 16 + (w >> 1) * 8, 7.0)
+                                 for w in range(4)], 1)
+                bits = (gmask[:, None] >> np.arange(4)) & 1
+                assert np.all(gmask != 0)
+                assert np.all(abox[bits == 1] >= 0.98 / 255), (tile, p)
+                assert np.all(amax[bits == 0] < (1 + 1e-5) / 255), (tile, p)
+                listed += c
             # ... and every member it leaves out lies beyond every pixel's
-            # n_contrib or has alpha < 2^-25 at every pixel of the tile
-            # (culled by the forward as without effect)
-            missing = np.setdiff1d(ks, got[:, 1])
+            # n_contrib, has alpha < 2^-25 at every pixel of the tile (culled
+            # by the forward as without effect) or alpha < 1/255 at every
+            # pixel (nothing for the backward)
+            missing = np.setdiff1d(ks, gpos)
             inner = missing[missing < tile_nc.max()]
             if len(inner):
-                gg = pl_np[r0 + inner]
-                dx = m2[gg, 0][:, None] - px[None, :]
-                dy = m2[gg, 1][:, None] - py[None, :]
-                q = cxx[gg][:, None] * dx * dx + 2 * cxy[gg][:, None] * dx * dy \
-                    + czz[gg][:, None] * dy * dy
-                ow = g.opac[gg].astype(np.float64) * g.pprobs[gg, p]
-                alpha = ow[:, None] * np.exp(-0.5 * q)
-                assert np.all(alpha < 2.0 ** -25), (tile, p, alpha.max())
-                invisible += len(inner)
+                alpha = alpha_tile(pl_np[r0 + inner], p, px, py).max(1)
+                assert np.all(alpha < (1 + 1e-5) / 255), (tile, p, alpha.max())
+                invisible += int(np.sum(alpha < 2.0 ** -25))
+                faint += int(np.sum(alpha >= 2.0 ** -25))
             if np.any(missing >= tile_nc.max()):
                 truncated += 1
-    print(f"plane lists: {truncated} cut short, {invisible} invisible members left out",
-          flush=True)
+    print(f"plane lists: {listed} listed, {truncated} cut short, {invisible} invisible and "
+          f"{faint} faint members left out", flush=True)
     if case == "dense":
         assert truncated > 0
 
@@ -483,6 +509,28 @@ def test_backward_with_plane_lists(hrf, oracle_mod, case):
         err = rel_l2(a, rb[name])
         print(f"{case} grad_{name}: rel_l2={err:.3e}", flush=True)
         assert err < TOL, (name, err)
+
+
+def _alpha_box_max(m2, cxx, cxy, czz, ow, x0, y0, ext):
+    """float64 max of o w exp(-q/2) over the box [x0, x0+ext] x [y0, y0+ext]
+    (q = d^T A d, d = mean - point; A positive definite): the minimum of q
+    is 0 with the mean inside, else on the boundary, where each edge is a
+    1-D convex quadratic minimised by clamping its vertex."""
+    mx, my = m2[:, 0], m2[:, 1]
+    inside = (mx >= x0) & (mx <= x0 + ext) & (my >= y0) & (my <= y0 + ext)
+    best = np.full(len(mx), np.inf)
+    for fixed_x in (True, False):
+        for edge in (0.0, ext):
+            if fixed_x:
+                dx = mx - (x0 + edge)
+                # q(dy) = czz dy^2 + 2 cxy dx dy + cxx dx^2, dy = my - y, y in [y0, y0+ext]
+                dy = np.clip(-cxy * dx / czz, my - (y0 + ext), my - y0)
+            else:
+                dy = my - (y0 + edge)
+                dx = np.clip(-cxy * dy / cxx, mx - (x0 + ext), mx - x0)
+            best = np.minimum(best, cxx * dx * dx + 2 * cxy * dx * dy + czz * dy * dy)
+    q = np.where(inside, 0.0, best)
+    return ow * np.exp(-0.5 * q)
 
 
 @pytest.mark.parametrize("W,H", [(16, 16), (8, 12)])
