@@ -81,10 +81,15 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
 // carrying each digit's running output offset.
 
 // Digit histogram of each partition: digit = (key >> shift) & mask with at
-// most 2^RB values; one LDS histogram per wave (fewer same-address atomic
-// collisions between the waves), summed at the end.  hist is digit-major
-// ([digit][partition]): a scan along each digit's row plus the totals of
-// the lower digits give every (digit, partition) output offset.
+// most 2^RB values.  The keys come in long runs of equal digits (a
+// Gaussian's consecutive tiles), so one histogram per wave made most lanes
+// of an atomic add hit one address.  Here the block keeps 16 copies, lane l
+// adding into copy l % 16, each copy one padded row (2^RB + 1 words): the
+// lanes of a run of equal digits hit 16 different banks, and at most the 4
+// lanes l, l+16, l+32, l+48 share an address.  The copies are summed at the
+// end.  hist is digit-major ([digit][partition]): a scan along each digit's
+// row plus the totals of the lower digits give every (digit, partition)
+// output offset.
 template <int RB, int TH>
 __global__ __launch_bounds__(TH) void k_radix_hist(const uint32_t* __restrict__ keys,
                                                               int64_t n, int shift,
@@ -93,13 +98,12 @@ __global__ __launch_bounds__(TH) void k_radix_hist(const uint32_t* __restrict__ 
                                                               int nparts, int sub,
                                                               const uint32_t* __restrict__ run_flag) {
   constexpr int kBins = 1 << RB;
-  constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
+  constexpr int kCopies = 16, kRow = kBins + 1, kTile = TH * kRadixItems;
   if (run_flag && *run_flag == 0u) return;
-  __shared__ uint32_t s_hist[kWaves][kBins];
-  for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
-    s_hist[e / kBins][e % kBins] = 0;
+  __shared__ uint32_t s_hist[kCopies * kRow];
+  for (int e = threadIdx.x; e < kCopies * kRow; e += TH) s_hist[e] = 0;
   __syncthreads();
-  const int wave = threadIdx.x >> 6;
+  uint32_t* const my_hist = s_hist + (threadIdx.x & (kCopies - 1)) * kRow;
   const int64_t pbase = static_cast<int64_t>(blockIdx.x) * sub * kTile;
   for (int t = 0; t < sub; ++t) {
     const int64_t base = pbase + static_cast<int64_t>(t) * kTile;
@@ -113,14 +117,14 @@ __global__ __launch_bounds__(TH) void k_radix_hist(const uint32_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < kRadixItems; ++i) {
       const int64_t idx = base + i * TH + threadIdx.x;
-      if (idx < n) atomicAdd(&s_hist[wave][(k[i] >> shift) & mask], 1u);
+      if (idx < n) atomicAdd(&my_hist[(k[i] >> shift) & mask], 1u);
     }
   }
   __syncthreads();
   for (int d = threadIdx.x; d < kBins; d += TH) {
     uint32_t c = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) c += s_hist[w][d];
+    for (int w = 0; w < kCopies; ++w) c += s_hist[w * kRow + d];
     hist[static_cast<int64_t>(d) * nparts + blockIdx.x] = c;
   }
 }
