@@ -383,6 +383,69 @@ def cpu_baseline_leg(spec, sc, budget_s):
                 "sample": f"failed: {e!r}"}
 
 
+def cpu_whole_frame(name):
+    """One whole frame of a BASELINE configuration on the reference's CPU
+    PyTorch path (oracle/cpu_baseline.py) on all of this host's cores, under
+    the protocol's 600 s did-not-finish cap; never sampled or extrapolated.
+    Configurations with a backward run it tile by tile (run_frame_tiled: the
+    whole graph would not fit in host memory); config 3 runs its 24
+    propagations (3 wavelengths x 8 distances, 2048^2 fields on the 4096 grid)
+    forward + backward one after another."""
+    import torch
+
+    from complex_valued_holographic_radiance_fields_amd import scenes
+    from oracle import cpu_baseline
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t0 = time.perf_counter()
+    if name in ("cfg3", "3"):
+        field, wl, dist = scenes.cfg3_fields()
+        C, S = field.shape[0], field.shape[1]
+        fwd = bwd = 0.0
+        done = 0
+        finished = True
+        for d in dist:
+            for c in range(C):
+                f, b = cpu_baseline.time_propagations(
+                    [(torch.from_numpy(field[c]), wl[c], d)], S, float(S), pitch=scenes.PITCH,
+                    seed=done)
+                fwd += f
+                bwd += b
+                done += 1
+                print(f"[cpu cfg3] propagation {done}/{len(dist) * C}: {f + b:.0f} ms",
+                      file=sys.stderr, flush=True)
+                if time.perf_counter() - t0 > CPU_CAP_S:
+                    finished = False
+                    break
+            if not finished:
+                break
+        res = dict(finished=finished, fwd_ms=fwd if finished else None,
+                   bwd_ms=bwd if finished else None, propagations_done=done,
+                   propagations=len(dist) * C)
+        run = ("config 3 whole: 24 pure-torch propagations (python_function.py:35-78) of "
+               "(2048, 2048) fields on the 4096 grid, forward + autograd backward each")
+    else:
+        spec = scenes.config(name)
+        sc = scenes.generate(spec)
+        res = cpu_baseline.run_frame_tiled(
+            sc, cap_s=CPU_CAP_S,
+            progress=lambda d, n: print(f"[cpu {name}] {d}/{n} tiles, "
+                                        f"{time.perf_counter() - t0:.0f} s", file=sys.stderr,
+                                        flush=True))
+        res.pop("grads", None)
+        res.pop("hologram", None)
+        run = (f"{spec.name} whole: every 64x64 tile of the Python splat forward + backward "
+               "(backward tile by tile, its upstream field gradient the propagation adjoint of "
+               "the scene's hologram gradient) and every (plane, wavelength) propagation")
+    total = (res["fwd_ms"] + res["bwd_ms"]) if res["finished"] else None
+    return {"cpu_frame": name, "value": round(total, 1) if total else None, "unit": "ms/frame",
+            "did_not_finish": not res["finished"], "cap_s": CPU_CAP_S, "cores": cores,
+            "kind": "port", "run": run,
+            "detail": {k: (round(v, 1) if isinstance(v, float) else v) for k, v in res.items()},
+            "wall_s": round(time.perf_counter() - t0, 1)}
+
+
 def bench_cfg3(args, dev):
     """Config 3, the propagation-only microbench: a (3, 2048, 2048) field to
     8 distances on the 4096 grid, forward (D*C outputs) + adjoint (sum over
@@ -469,6 +532,11 @@ def main():
     ap.add_argument("--config", default="headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-frame", default=None, metavar="CONFIG",
+                    help="run only the CPU baseline, one whole frame of CONFIG (cfg1, headline: "
+                         "forward + backward, the backward tile by tile; cfg3: the 24 "
+                         "propagations forward + backward), under the 600 s did-not-finish cap, "
+                         "and print one JSON line (no GPU is used)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run 3 elementwise copies of 256 MiB (x*2 -> y), a kernel of "
                          "known HBM traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -478,6 +546,10 @@ def main():
         print("bench.py: this build measures one MI355X; --gpus/WORLD_SIZE above 1 is not "
               "supported (the hot path has no multi-GPU leg in this build).", file=sys.stderr)
         sys.exit(2)
+
+    if args.cpu_frame:
+        print(json.dumps(cpu_whole_frame(args.cpu_frame)), flush=True)
+        return
 
     import numpy as np
     import torch

@@ -147,6 +147,37 @@ def asm_torch(field, wavelength, pitch, distance, S, aperture):
     return out[s0:s0 + S, s0:s0 + S]
 
 
+def asm_torch_adjoint(grad, wavelength, pitch, distance, S, aperture, H, W):
+    """The exact adjoint of ``asm_torch`` (a linear map of the field): the
+    pure-torch ASM's autograd backward written out (python_function.py:35-78
+    differentiated): pad the (S, S) gradient into the M x M grid, forward
+    FFT, shift, multiply by the conjugate transfer function and aperture,
+    unshift, inverse FFT, crop to (H, W).  Same FFT and elementwise work as
+    a forward propagation."""
+    M = 2 * S
+    pad = torch.zeros((M, M), dtype=torch.complex64)
+    s0 = M // 2 - S // 2
+    pad = pad.index_put((torch.arange(s0, s0 + S)[:, None], torch.arange(s0, s0 + S)[None, :]),
+                        grad)
+    yy, xx = torch.meshgrid(torch.arange(M), torch.arange(M), indexing="ij")
+    ap = (((xx - M / 2) ** 2 + (yy - M / 2) ** 2) < aperture ** 2).float()
+    gf = torch.fft.fftshift(torch.fft.fft2(pad))
+    fx = torch.fft.fftshift(torch.fft.fftfreq(M, d=pitch))
+    FX, FY = torch.meshgrid(fx, fx, indexing="ij")
+    L = torch.tensor(pitch * M)
+    d = torch.tensor(distance)
+    lam = torch.tensor(wavelength)
+    fxmax = 1 / torch.sqrt((2 * d * (1 / L)) ** 2 + 1) / lam
+    mask = (torch.abs(FX) < fxmax) & (torch.abs(FY) < fxmax)
+    k = 2 * torch.pi / lam
+    kz = torch.sqrt(k ** 2 - (2 * torch.pi * FX) ** 2 - (2 * torch.pi * FY) ** 2)
+    kz = torch.where(torch.isnan(kz), torch.zeros_like(kz), kz)
+    Hc = torch.exp(-1j * d * kz) * mask
+    out = torch.fft.ifft2(torch.fft.ifftshift(gf * Hc * ap))
+    r0, c0 = M // 2 - H // 2, M // 2 - W // 2
+    return out[r0:r0 + H, c0:c0 + W]
+
+
 def _cpu_params(sc, grad: bool):
     t = lambda a: torch.from_numpy(a.copy()).requires_grad_(grad)  # noqa: E731
     return [t(sc.cam_means), t(sc.quats), t(sc.scales), t(sc.colours), t(sc.phase), t(sc.opac),
@@ -209,8 +240,96 @@ def run_frame(sc, backward: bool = True, cap_s: float = 600.0):
         g = torch.from_numpy(sc.grad_holo.copy())
         (holo.real * g.real + holo.imag * g.imag).sum().backward()
         res["bwd_ms"] = (time.perf_counter() - t1) * 1e3
+        res["grads"] = [q.grad for q in params]
     res["elapsed_s"] = time.perf_counter() - t0
     res["finished"] = res["elapsed_s"] <= cap_s
+    res["hologram"] = holo.detach()
+    return res
+
+
+def run_frame_tiled(sc, cap_s: float = 600.0, progress=None):
+    """The whole CPU frame of scene ``sc``, forward and backward, with the
+    backward run tile by tile so that it fits in host memory (the whole
+    graph of every 64x64 tile's per-(Gaussian, pixel) tensors would hold
+    ~1e2 GB at 3e5 Gaussians).  The frame's loss Re<hologram, g> is linear
+    in the plane fields, so their gradient is the propagation's adjoint of g
+    whatever the fields are: it is formed first (asm_torch_adjoint per
+    (plane, wavelength), summed into the plane field gradients), then each
+    tile runs its forward with autograd and its backward with its slice of
+    that gradient, and frees its graph; the propagation forward of the
+    assembled fields gives the hologram.  The same operations as run_frame's
+    forward + backward, in a different order.  Forward time: the tiles'
+    forwards + the propagations; backward time: the adjoints + the tiles'
+    backwards.  Stops at ``cap_s`` seconds of wall time (did not finish).
+    ``progress`` (optional) is called with (tiles done, tiles) after each
+    row of tiles.  Returns dict(finished, fwd_ms, bwd_ms, elapsed_s,
+    tiles_done, tiles, grads (the 7 parameter gradients), hologram)."""
+    spec = sc.spec
+    W, H, P, C, S = spec.width, spec.height, spec.planes, len(spec.wavelengths), spec.size
+    params = _cpu_params(sc, True)
+    R = torch.from_numpy(sc.view.copy())
+    fx, fy, px, py = sc.fx, sc.fy, sc.px, sc.py
+    tile = 64
+    xt, yt = math.ceil(W / tile), math.ceil(H / tile)
+    res = dict(finished=False, fwd_ms=None, bwd_ms=None, tiles=xt * yt, tiles_done=0)
+    t_start = time.perf_counter()
+    fwd = bwd = 0.0
+    g = torch.from_numpy(sc.grad_holo.copy())
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        gfield = torch.zeros((P, C, H, W), dtype=torch.complex64)
+        for p in range(P):
+            for c in range(C):
+                gfield[p, c] = asm_torch_adjoint(g[c], spec.wavelengths[c], 3.74e-6,
+                                                 -spec.distances[p], S, float(S), H, W)
+    bwd += time.perf_counter() - t0
+    with torch.no_grad():
+        m = means_2d(params[0], fx, fy, px, py)
+        c2 = cov_2d(params[0], params[1], params[2], fx, fy, R, W, H)
+        bounds = gaussian_bounds(m, c2, W, H)
+    field = torch.zeros((P, C, H, W), dtype=torch.complex64)
+    for yi in range(yt):
+        for xi in range(xt):
+            x, y = xi * tile, yi * tile
+            tw, th = min(tile, W - x), min(tile, H - y)
+            t0 = time.perf_counter()
+            sel = ((bounds[:, 0] <= x + tw - 1) & (bounds[:, 2] >= x) &
+                   (bounds[:, 1] <= y + th - 1) & (bounds[:, 3] >= y))
+            out = splat_tile(params, torch.where(sel)[0], x, y, tw, th, fx, fy, px, py, R, W, H,
+                             P, C)
+            t1 = time.perf_counter()
+            if out.requires_grad:
+                gt = gfield[:, :, y:y + th, x:x + tw]
+                (out.real * gt.real + out.imag * gt.imag).sum().backward()
+            t2 = time.perf_counter()
+            fwd += t1 - t0
+            bwd += t2 - t1
+            field[:, :, y:y + th, x:x + tw] = out.detach()
+            del out
+            res["tiles_done"] += 1
+            if time.perf_counter() - t_start > cap_s:
+                res["elapsed_s"] = time.perf_counter() - t_start
+                return res
+        if progress:
+            progress(res["tiles_done"], res["tiles"])
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        holo = []
+        for c in range(C):
+            acc = None
+            for p in range(P):
+                o = asm_torch(field[p, c], spec.wavelengths[c], 3.74e-6, -spec.distances[p], S,
+                              float(S))
+                acc = o if acc is None else acc + o
+            holo.append(acc)
+        holo = torch.stack(holo, 0)
+    fwd += time.perf_counter() - t0
+    res["fwd_ms"] = fwd * 1e3
+    res["bwd_ms"] = bwd * 1e3
+    res["elapsed_s"] = time.perf_counter() - t_start
+    res["finished"] = res["elapsed_s"] <= cap_s
+    res["grads"] = [q.grad for q in params]
+    res["hologram"] = holo
     return res
 
 

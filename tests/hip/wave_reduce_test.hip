@@ -54,11 +54,37 @@ __global__ __launch_bounds__(256) void k_calib_exp(float* out, int iters, float 
   for (int i = 0; i < 8; ++i) s += x[i];
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
+// The render kernels' instruction mix: per iteration one v_exp_f32 and one
+// v_mul_f32 on chain 0 and one v_fma_f32 on each of chains 1-7, all
+// independent of each other within the iteration (9 VALU instructions, one
+// of them transcendental).  Against k_calib_fma's 8 per iteration, its time
+// shows whether a transcendental among independent VALU work holds its SIMD
+// for two issue slots or overlaps with the instructions around it.
+__global__ __launch_bounds__(256) void k_calib_mix(float* out, int iters, float a) {
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(threadIdx.x) * 1e-3f + 0.1f * i;
+  for (int it = 0; it < iters; ++it) {
+    x[0] = __builtin_amdgcn_exp2f(x[0]) * a;
+#pragma unroll
+    for (int i = 1; i < 8; ++i) x[i] = fmaf(x[i], a, 0.5f);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
 }  // namespace
 
 // out: blocks * 256 floats.
 extern "C" int calib_valu_fma(float* out, int blocks, int iters, float a, void* stream) {
   hipLaunchKernelGGL(k_calib_fma, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     out, iters, a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int calib_valu_mix(float* out, int blocks, int iters, float a, void* stream) {
+  hipLaunchKernelGGL(k_calib_mix, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      out, iters, a);
   return static_cast<int>(hipGetLastError());
 }

@@ -20,6 +20,46 @@ BLOCKS = 2048  # x 4 waves = 8192 waves: 8 per SIMD on 256 CUs
 ITERS = 4096
 
 
+def _time_kernel(lib, kind, iters):
+    import torch
+
+    f = getattr(lib, f"calib_valu_{kind}")
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    out = torch.empty(BLOCKS * 256, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    assert f(out.data_ptr(), BLOCKS, 16, 0.5, stream) == 0  # warm-up
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ms = []
+    for _ in range(3):
+        e0.record()
+        assert f(out.data_ptr(), BLOCKS, iters, 0.5, stream) == 0
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    assert bool(torch.isfinite(out).all())
+    return min(ms)
+
+
+def test_transcendental_issue_cost_in_a_mix(hrf):
+    """k_calib_mix issues 9 VALU instructions per iteration, one of them a
+    v_exp_f32 independent of the 8 others; k_calib_fma issues 8 v_fma_f32.
+    With every instruction taking one issue slot of its SIMD and the
+    transcendental two, the mix takes 10/8 of the FMA kernel's time; if the
+    transcendental overlaps the independent instructions, 9/8 (one slot).
+    The printed cost per transcendental (in issue slots) is the figure the
+    render kernels' VALU model uses (profiles/valu_*.txt)."""
+    lib = ctypes.CDLL(LIB)
+    t_fma = _time_kernel(lib, "fma", ITERS)
+    t_mix = _time_kernel(lib, "mix", ITERS)
+    slot = t_fma / 8.0  # one issue slot per iteration per wave, in ms
+    trans_slots = t_mix / slot - 8.0  # the mix's 9 instructions: 8 one-slot + 1 exp
+    print(f"calib mix: fma {t_fma:.4f} ms (8 slots/iter), mix {t_mix:.4f} ms "
+          f"-> a transcendental among independent VALU costs {trans_slots:.2f} issue slots",
+          flush=True)
+    assert 0.5 < trans_slots < 3.5
+
+
 @pytest.mark.parametrize("kind", ["fma", "exp"])
 def test_calibration_kernel_rates(hrf, kind):
     import torch
