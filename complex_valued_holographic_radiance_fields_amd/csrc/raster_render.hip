@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "hrf_internal.h"
+#include "render_member.h"
 #include "wave_reduce.h"
 
 namespace hrf {
@@ -211,57 +212,15 @@ __device__ __forceinline__ bool conic_safe(float a, float b, float b2, float c) 
 __host__ __device__ constexpr int fwd_quads(int C) { return C == 1 ? 2 : 3; }
 __host__ __device__ constexpr int fwd_quads_exact(int C) { return rec_quads(C); }
 
-// Forward member evaluation.  Exponent in base 2 with log2(o w) folded in:
-// pw = dx (A dx + B dy) + (C dy) dy + log2(o w), so alpha = min(0.99,
-// exp2(pw)) needs no multiply by the opacity; at the mean (dx = dy = 0) pw
-// is log2(o w) exactly.  A lane is done exactly when T < 1e-4 (T changes
-// only on composited members, and a lane stops at the member that takes T
-// below 1e-4; lanes outside the image start at T = 0), so no separate flag
-// is carried.  Branch-free: lanes that are done (or, in the exact variant,
-// where the reference's power > 0 test skips the member) take alpha = 0,
-// which leaves T and the field exactly unchanged.  Exact variant: `lastj`
-// becomes the member's batch index j (a scalar) where the lane composites
-// it; `real` (scalar) is false for padding members.  Fast variant: `lastj`
-// counts the members evaluated while the lane was live (one add of the
-// live mask, no index select): a lane composites every member until the
-// one that ends it, so the count minus one is that member's index.
-template <int C, bool kExact>
-__device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
-                                           float pxf, float pyf, float& T,
-                                           float (&acc)[2 * C], int& lastj, int j, bool real) {
-  const float dx = a.x - pxf, dy = a.y - pyf;
-  const float t = fmaf(a.z, dx, a.w * dy);
-  const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
-  const bool live = !(T < kTermT);
-  // NaN passes the power test (alpha 0.99), as in the reference; only
-  // batches holding a conic that is not safe evaluate the test.
-  const bool ok = kExact ? (live && !(pw > b.y)) : live;
-  const float alpha = ok ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
-  const float sT = alpha * T;
-  const float amp[6] = {b.z, b.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-  for (int k = 0; k < C; ++k) {
-    acc[2 * k] = fmaf(sT, amp[2 * k], acc[2 * k]);
-    acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
-  }
-  // The reference's rounding: 1 - alpha rounded first (forward_splat.cu:237).
-  // Over lists of 1e5 members the rounded factor's bias (small alphas are
-  // quantised to multiples of 2^-24) moves T by more than 1e-4, so the
-  // exactly rounded T - alpha T would not reproduce it.
-  T = T * (1.0f - alpha);
-  if (kExact)
-    lastj = (ok && real) ? j : lastj;
-  else
-    lastj += ok ? 1 : 0;
-}
-
 // Exact-batch member evaluation: the exponent in the reference's order
 // (forward_splat.cu:222-225), power = -0.5 s with
 // s = dx (i00 dx + i10 dy) + dy (i01 dx + i11 dy), each product and sum
 // rounded on its own (the library is built without contraction), the
 // "power > 0: skip" test as s < 0, then alpha from exp2(kc s + log2(o w))
 // (kc = -log2(e)/2, one rounding in the fused multiply-add).  The rest is
-// fwd_member's exact variant.
+// fwd_member with the power test and the list index of the last
+// contributor (`lastj` becomes j where the lane composites it; `real`
+// (scalar) is false for padding members).
 template <int C>
 __device__ __forceinline__ void fwd_member_ref(const float4 a, const float4 b, const float4 c,
                                                const float4 d, float pxf, float pyf, float& T,
@@ -460,8 +419,8 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
 #pragma unroll
         for (int jj = 0; jj < kUnroll; ++jj) {
           const int j = j0 + jj;
-          fwd_member<C, false>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf,
-                               pyf, T, acc, evaluated, j, j < cnt);
+          fwd_member<C>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf, pyf, T,
+                        acc, evaluated);
         }
       }
       // A lane still running composited every member of the batch (no

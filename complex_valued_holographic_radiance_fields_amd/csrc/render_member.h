@@ -1,0 +1,48 @@
+// render_member.h — the forward render's per-member compositing step for
+// its fast loop (k_render_fwd), shared with the VALU calibration kernel of
+// the tests (which runs the same loop body over staged members of known
+// count to measure the issue rate this instruction mix reaches).
+#pragma once
+
+#include "hrf_internal.h"
+
+namespace hrf {
+
+// Forward member evaluation (fast loop: staged conics that cannot round to
+// a positive exponent, so the reference's "power > 0: skip" test is not
+// evaluated).  Exponent in base 2 with log2(o w) folded in:
+// pw = dx (A dx + B dy) + (C dy) dy + log2(o w), so alpha = min(0.99,
+// exp2(pw)) needs no multiply by the opacity; at the mean (dx = dy = 0) pw
+// is log2(o w) exactly.  A lane is done exactly when T < 1e-4 (T changes
+// only on composited members, and a lane stops at the member that takes T
+// below 1e-4; lanes outside the image start at T = 0), so no separate flag
+// is carried.  Branch-free: lanes that are done take alpha = 0, which leaves
+// T and the field exactly unchanged.  `evaluated` counts the members
+// evaluated while the lane was live (one add of the live mask, no index
+// select): a lane composites every member until the one that ends it, so
+// the count minus one is that member's index.  Staged record quads:
+// a = (mx, my, kc*i00, kc*(i01 + i10)), b = (kc*i11, log2(o w), re0, im0),
+// c = (re1, im1, re2, im2) (C >= 2), kc = -log2(e)/2.
+template <int C>
+__device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
+                                           float pxf, float pyf, float& T,
+                                           float (&acc)[2 * C], int& evaluated) {
+  const float dx = a.x - pxf, dy = a.y - pyf;
+  const float t = fmaf(a.z, dx, a.w * dy);
+  const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
+  const bool live = !(T < kTermT);
+  const float alpha = live ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
+  const float sT = alpha * T;
+  const float amp[6] = {b.z, b.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    acc[2 * k] = fmaf(sT, amp[2 * k], acc[2 * k]);
+    acc[2 * k + 1] = fmaf(sT, amp[2 * k + 1], acc[2 * k + 1]);
+  }
+  // The reference's rounding: 1 - alpha rounded first (forward_splat.cu:237);
+  // the exactly rounded T - alpha T differs from it in the last bit.
+  T = T * (1.0f - alpha);
+  evaluated += live ? 1 : 0;
+}
+
+}  // namespace hrf

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "fast_trig.h"
+#include "render_member.h"
 #include "wave_reduce.h"
 
 namespace {
@@ -54,6 +55,25 @@ __global__ __launch_bounds__(256) void k_calib_exp(float* out, int iters, float 
   for (int i = 0; i < 8; ++i) s += x[i];
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
+// As k_calib_fma, with the two factors in VGPRs: x = fma(u, v, x) compiles
+// to the 4-byte VOP2 v_fmac_f32 (k_calib_fma's fma(x, a, 0.5) with a scalar
+// operand and a constant is the 8-byte VOP3 v_fma_f32).
+__global__ __launch_bounds__(256) void k_calib_fmac(float* out, int iters, float a) {
+  float x[8];
+  const float u = a * 1e-3f * static_cast<float>(threadIdx.x & 7);
+  const float v = 1e-3f * static_cast<float>(threadIdx.x >> 3);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(threadIdx.x) * 1e-3f + i;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = fmaf(u, v, x[i]);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += x[i];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 // The render kernels' instruction mix: per iteration one v_exp_f32 and one
 // v_mul_f32 on chain 0 and one v_fma_f32 on each of chains 1-7, all
 // independent of each other within the iteration (9 VALU instructions, one
@@ -74,6 +94,42 @@ __global__ __launch_bounds__(256) void k_calib_mix(float* out, int iters, float 
   for (int i = 0; i < 8; ++i) s += x[i];
   out[blockIdx.x * 256 + threadIdx.x] = s;
 }
+// The forward render's fast member loop (hrf::fwd_member, C = 3), as
+// k_render_fwd runs it: 256 staged members per batch in LDS (3 quads each),
+// walked 8 at a time with the per-group all-done vote, one pixel per lane.
+// The members are synthetic and faint (alpha ~ 2^-20), so no lane ever
+// terminates and every iteration runs the whole batch: the counted VALU
+// instructions over the kernel's time give the issue rate this instruction
+// mix reaches on its own (no staging, barriers or memory).
+__global__ __launch_bounds__(256, 8) void k_calib_fwdloop(float* out, int iters) {
+  __shared__ float4 s_rec[256 * 3];
+  const int tid = threadIdx.x;
+  {
+    const float fi = static_cast<float>(tid);
+    s_rec[tid * 3] = make_float4(4.0f + 0.03f * fi, 6.0f - 0.02f * fi, -0.02f, 0.001f);
+    s_rec[tid * 3 + 1] = make_float4(-0.03f, -20.0f, 0.5f, 0.25f);
+    s_rec[tid * 3 + 2] = make_float4(0.125f, -0.5f, 0.75f, 0.3f);
+  }
+  __syncthreads();
+  const float pxf = static_cast<float>(tid & 15), pyf = static_cast<float>(tid >> 4);
+  float T = 1.0f, acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int evaluated = 0;
+  for (int it = 0; it < iters; ++it) {
+    for (int j0 = 0; j0 < 256; j0 += 8) {
+      if (__all(T < hrf::kTermT)) break;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = j0 + jj;
+        hrf::fwd_member<3>(s_rec[j * 3], s_rec[j * 3 + 1], s_rec[j * 3 + 2], pxf, pyf, T, acc,
+                           evaluated);
+      }
+    }
+  }
+  float sum = T + static_cast<float>(evaluated);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) sum += acc[i];
+  out[blockIdx.x * 256 + tid] = sum;
+}
 }  // namespace
 
 // out: blocks * 256 floats.
@@ -85,6 +141,19 @@ extern "C" int calib_valu_fma(float* out, int blocks, int iters, float a, void* 
 
 extern "C" int calib_valu_mix(float* out, int blocks, int iters, float a, void* stream) {
   hipLaunchKernelGGL(k_calib_mix, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     out, iters, a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int calib_valu_fwdloop(float* out, int blocks, int iters, float a, void* stream) {
+  (void)a;
+  hipLaunchKernelGGL(k_calib_fwdloop, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), out, iters);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int calib_valu_fmac(float* out, int blocks, int iters, float a, void* stream) {
+  hipLaunchKernelGGL(k_calib_fmac, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      out, iters, a);
   return static_cast<int>(hipGetLastError());
 }

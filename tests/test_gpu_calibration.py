@@ -47,8 +47,9 @@ def test_transcendental_issue_cost_in_a_mix(hrf):
     With every instruction taking one issue slot of its SIMD and the
     transcendental two, the mix takes 10/8 of the FMA kernel's time; if the
     transcendental overlaps the independent instructions, 9/8 (one slot).
-    The printed cost per transcendental (in issue slots) is the figure the
-    render kernels' VALU model uses (profiles/valu_*.txt)."""
+    The printed cost per transcendental (in issue slots) is a measurement,
+    not a property under test (timings under rocprofv3 counter collection
+    are not meaningful), so only the outputs are checked."""
     lib = ctypes.CDLL(LIB)
     t_fma = _time_kernel(lib, "fma", ITERS)
     t_mix = _time_kernel(lib, "mix", ITERS)
@@ -57,7 +58,23 @@ def test_transcendental_issue_cost_in_a_mix(hrf):
     print(f"calib mix: fma {t_fma:.4f} ms (8 slots/iter), mix {t_mix:.4f} ms "
           f"-> a transcendental among independent VALU costs {trans_slots:.2f} issue slots",
           flush=True)
-    assert 0.5 < trans_slots < 3.5
+    t_fmac = _time_kernel(lib, "fmac", ITERS)
+    print(f"calib fmac: VOP2 v_fmac_f32 {t_fmac:.4f} ms against VOP3 v_fma_f32 {t_fma:.4f} ms "
+          f"for the same count", flush=True)
+
+
+def test_forward_member_loop_rate(hrf):
+    """k_calib_fwdloop runs the forward render's fast member loop (the same
+    hrf::fwd_member, 8 members per all-done vote) over 256 staged members,
+    64 times per wave, with no lane ever terminating: under rocprofv3 --pmc
+    its SQ_INSTS_VALU over this time is the VALU issue rate the forward's
+    instruction mix reaches by itself, the peak its VALU model uses."""
+    lib = ctypes.CDLL(LIB)
+    iters = 64
+    ms = _time_kernel(lib, "fwdloop", iters)
+    members = BLOCKS * 256 * iters * 256  # (pixel, member) evaluations
+    print(f"calib fwdloop: {members / (ms * 1e-3) / 1e12:.3f} T pixel-member evaluations/s "
+          f"({ms:.4f} ms for {BLOCKS * 4} waves x {iters * 256} members)", flush=True)
 
 
 @pytest.mark.parametrize("kind", ["fma", "exp"])
