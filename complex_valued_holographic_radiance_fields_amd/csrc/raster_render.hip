@@ -74,6 +74,9 @@ __device__ __forceinline__ void tile_range(const RenderParams& p, int tile, int*
 constexpr float kBwdConicScale = -0.72134752044448170368f;
 constexpr float kLog2E = 1.44269504088896340736f;
 
+// Members per chunk of the backward's two-phase member walk.
+constexpr int kBwdChunk = 4;
+
 // a / b for b in [0.01, 1] and a normal: the hardware reciprocal, then one
 // residual correction (the residual a - q b is exact in a fused
 // multiply-add), which rounds like the reference's IEEE division
@@ -488,19 +491,24 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
   // quad 0 (mx, my, cxx, cxy), quad 1 (czz, log2(o w), k, o w).
   constexpr int NQ = bwd_quads(C);
   constexpr int RS = rec_stride(C);
-  constexpr int NV = 6 + 2 * C;
-  constexpr int G = 64 / NV;
+  constexpr int NV = 6 + 2 * C;  // partial sums per member
+  static_assert(NV <= 16, "one 16-lane row holds a member's sums");
+  constexpr int G = kBwdChunk;
   // Slot kBlock of s_rec is a dummy member that no pixel can use (list
   // position beyond every n_contrib): the per-wave lists are padded with it
   // to a multiple of G, so the member loop needs no bounds.  It is written
-  // per batch in that batch's layout.
+  // per batch.
   constexpr int kDummy = kBlock;
   __shared__ float4 s_rec[(kBlock + 1) * NQ];
   __shared__ int s_g[kBlock];
-  __shared__ float s_acc[kBlock * NV];
   __shared__ unsigned short s_wl[4][kBlock + G];
   __shared__ int s_cnt[4][5];
   __shared__ int s_wmax[4];
+  // Per wave: the chunk's (Q, dcol) per (member, pixel), written by the
+  // pixel lanes and read by the member lanes; the quadrant's upstream
+  // gradient per pixel (re, im per channel).
+  __shared__ float2 s_qd[4][G][64];
+  __shared__ float2 s_gp[4][64][C];
 
   int tile, plane;
   if (kSub) {
@@ -543,6 +551,8 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
       gim[c] = gv.y;
     }
   }
+#pragma unroll
+  for (int c = 0; c < C; ++c) s_gp[wave][lane][c] = make_float2(gre[c], gim[c]);
   {
     int m = inside ? last : 0;
 #pragma unroll
@@ -562,6 +572,8 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
   const float half_w = 0.5f * static_cast<float>(p.W);
   const float half_h = 0.5f * static_cast<float>(p.H);
   const float tx0 = static_cast<float>(tx * kTile), ty0 = static_cast<float>(ty * kTile);
+  const float qx0 = tx0 + static_cast<float>((wave & 1) * 8);  // this wave's quadrant
+  const float qy0 = ty0 + static_cast<float>((wave >> 1) * 8);
 
   // Entries walked: list positions [0, maxlast) of the tile list, or the
   // whole member list of this plane (entries at positions >= maxlast are
@@ -706,179 +718,184 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
       const int tw = w == 0 ? tot[1] : (w == 1 ? tot[2] : (w == 2 ? tot[3] : tot[4]));
       if (j < (G - tw % G) % G) s_wl[w][j] = static_cast<unsigned short>(kDummy);
     }
-    for (int e = threadIdx.x; e < cnt * NV; e += kBlock) s_acc[e] = 0.0f;
     __syncthreads();
 
     int nl = 0;  // this wave's padded list length (a multiple of G)
 #pragma unroll
     for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] + (G - tot[1 + w] % G) % G : nl;
-    // The member walk, instantiated for the fast exponent and for the
-    // reference-order one (exact batches).
+    // The member walk in chunks of G members, back to front, instantiated
+    // for the fast exponent and for the reference-order one (exact batches).
     auto walk = [&](auto ref_tag) {
-    constexpr bool kRef = decltype(ref_tag)::value;
-    for (int hi = nl - 1; hi >= 0; hi -= G) {
-      // Branch-free: every lane evaluates every member of the group and a
-      // single predicate `ok` (list position < n_contrib, power <= 0,
-      // alpha >= 1/255) selects the state updates and zeroes the partials.
-      float buf[64];
-      bool any = false;
+      constexpr bool kRef = decltype(ref_tag)::value;
+      for (int hi = nl - 1; hi >= 0; hi -= G) {
+        // Phase 1, one pixel per lane: the back-to-front recurrence over the
+        // chunk's members, branch-free (a member that does not contribute at
+        // the pixel takes G = alpha = 0: T / 1 and 0 * x leave T and the
+        // sums exactly unchanged), leaving per (member, pixel) Q = o w G
+        // dL/dG and dcol = alpha T in LDS.
+        bool any = false;
 #pragma unroll
-      for (int m = 0; m < G; ++m) {
-        const int slot = s_wl[wave][hi - m];
-        const float4 a = s_rec[slot * NQ];
-        const float4 b = s_rec[slot * NQ + 1];
-        const int kk = __float_as_int(b.z);
-        const float dx = a.x - pxf, dy = a.y - pyf;
-        bool ok;
-        float Ga;  // o w G
-        if (kRef) {
-          // backward_splat.cu:211 in its order, each step rounded on its own
-          const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
-          Ga = __builtin_amdgcn_exp2f(fmaf(kLog2E, power, b.y));
-          ok = kk < last && !(power > 0.0f) && fminf(kMaxAlpha, Ga) >= kMinAlphaBwd;
-        } else {
-          // A conic in this loop's domain cannot round to a positive
-          // exponent, and its alpha is finite: the alpha test reads o w G.
-          const float t = fmaf(a.z, dx, a.w * dy);
-          Ga = __builtin_amdgcn_exp2f(fmaf(dx, t, fmaf(b.x * dy, dy, b.y)));
-          ok = kk < last && Ga >= kMinAlphaBwd;
-        }
-        any = any || ok;
-        // A member that does not contribute at this pixel takes G = alpha =
-        // 0: T / 1 and 0 * x leave T and the partials exactly unchanged.
-        const float Gz = ok ? Ga : 0.0f;
-        const float ae = fminf(kMaxAlpha, Gz);
-        T = div_rn(T, 1.0f - ae);
-        const float dcol = ae * T;
-        // Re(colour * conj(g)) summed over channels; the reference's complex
-        // recurrence acc = la*last + (1-la)*acc is linear, so only its
-        // projection R = sum_c Re(acc_c conj(g_c)) is carried.
-        float S;
-        const float4 c0 = s_rec[slot * NQ + 2];
-        const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
-        {
+        for (int m = 0; m < G; ++m) {
+          const int slot = s_wl[wave][hi - m];
+          const float4 a = s_rec[slot * NQ];
+          const float4 b = s_rec[slot * NQ + 1];
+          const int kk = __float_as_int(b.z);
+          const float dx = a.x - pxf, dy = a.y - pyf;
+          bool ok;
+          float Ga;  // o w G
+          if (kRef) {
+            // backward_splat.cu:211 in its order, each step rounded on its own
+            const float power = -0.5f * (a.z * dx * dx + b.x * dy * dy) - a.w * dx * dy;
+            Ga = __builtin_amdgcn_exp2f(fmaf(kLog2E, power, b.y));
+            ok = kk < last && !(power > 0.0f) && fminf(kMaxAlpha, Ga) >= kMinAlphaBwd;
+          } else {
+            // A conic in this loop's domain cannot round to a positive
+            // exponent, and its alpha is finite: the alpha test reads o w G.
+            const float t = fmaf(a.z, dx, a.w * dy);
+            Ga = __builtin_amdgcn_exp2f(fmaf(dx, t, fmaf(b.x * dy, dy, b.y)));
+            ok = kk < last && Ga >= kMinAlphaBwd;
+          }
+          any = any || ok;
+          const float Gz = ok ? Ga : 0.0f;
+          const float ae = fminf(kMaxAlpha, Gz);
+          T = div_rn(T, 1.0f - ae);
+          const float dcol = ae * T;
+          // Re(colour * conj(g)) summed over channels; the reference's
+          // complex recurrence acc = la*last + (1-la)*acc is linear, so only
+          // its projection R = sum_c Re(acc_c conj(g_c)) is carried.
+          const float4 c0 = s_rec[slot * NQ + 2];
+          const float4 c1 = s_rec[slot * NQ + (NQ > 3 ? 3 : 2)];
           const float amp[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-          S = amp[0] * gre[0];
+          float S = amp[0] * gre[0];
           S = fmaf(amp[1], gim[0], S);
 #pragma unroll
           for (int c = 1; c < C; ++c) {
             S = fmaf(amp[2 * c], gre[c], S);
             S = fmaf(amp[2 * c + 1], gim[c], S);
           }
+          // acc = a_l S_l + (1 - a_l) acc over the contributing members: R
+          // advances by the pending a_l (S_l - R) of the previous
+          // contributor, and this member's becomes pending.  A
+          // non-contributor (alpha 0) takes the pending increment early and
+          // leaves none, so the updates need no selects.
+          R += pend;
+          const float dS = S - R;
+          pend = ae * dS;
+          s_qd[wave][m][lane] = make_float2(Gz * (dS * T), dcol);
         }
-        // The reference's recurrence acc = a_l S_l + (1 - a_l) acc over the
-        // contributing members: R advances by the pending a_l (S_l - R) of
-        // the previous contributor, and this member's becomes pending.  A
-        // non-contributor (alpha 0) takes the pending increment early and
-        // leaves none, so the updates need no selects.
-        R += pend;
-        const float dS = S - R;
-        pend = ae * dS;
-        const float Q = Gz * (dS * T);  // o w times dL/dG
-        const float Qdx = Q * dx, Qdy = Q * dy;
-        if (kRef) {
-          // Per pixel, as the reference (backward_splat.cu:270-291): the
-          // mean terms Q (cxx dx + cxy dy), Q (cxy dx + czz dy) and the
-          // covariance terms through the conic-to-covariance map (times
-          // -2), so no sum is mapped afterwards: for a nearly singular
-          // conic the map would amplify the sums' rounding by ~1/(1 - r^2).
-          const float u = Qdx * dx, v = Qdx * dy, w = Qdy * dy;
-          const float cxx = a.z, cxy = a.w, czz = b.x;
-          const float ndi = -bwd_det_inv<C>(c0, c1);
-          buf[m * NV + 0] = Q * fmaf(cxx, dx, cxy * dy);
-          buf[m * NV + 1] = Q * fmaf(cxy, dx, czz * dy);
-          buf[m * NV + 2] = fmaf(cxx * cxx, u, (cxy * cxy) * w);
-          buf[m * NV + 3] = fmaf(cxx * cxy, u, fmaf(ndi, v, (cxy * czz) * w));
-          buf[m * NV + 4] = fmaf(cxy * cxy, u, (czz * czz) * w);
-        } else {
-          // sum Q u = kc (cxx sum Q dx + cxy sum Q dy) and likewise for v:
-          // the flush forms them from these two sums and the member's
-          // conic, and maps the three second moments
-          buf[m * NV + 0] = Qdx;
-          buf[m * NV + 1] = Qdy;
-          buf[m * NV + 2] = Qdx * dx;
-          buf[m * NV + 3] = Qdx * dy;
-          buf[m * NV + 4] = Qdy * dy;
-        }
-        buf[m * NV + 5] = Q;
+        if (__ballot(any) == 0ull) continue;
+        // The pixel lanes' writes before the member lanes' reads (one wave:
+        // the LDS keeps its order; this keeps the compiler's).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // Phase 2, lane (member mm = lane / 16, part sp = lane % 16): the
+        // member's NV partial sums over 4 pixels of the quadrant (column
+        // sp % 8, rows sp / 8 + 2j), in registers; then the 16 lanes of the
+        // member's row reduce them with one transpose (lane sp ends with sum
+        // sp) and each lane with a sum adds it to the member's accumulator.
+        const int mm = lane >> 4, sp = lane & 15;
+        const int slot2 = s_wl[wave][hi - mm];
+        const float4 a2 = s_rec[slot2 * NQ];
+        const float4 b2 = s_rec[slot2 * NQ + 1];
+        const float4 c02 = s_rec[slot2 * NQ + 2];
+        const float4 c12 = s_rec[slot2 * NQ + (NQ > 3 ? 3 : 2)];
+        const float di2 = bwd_det_inv<C>(c02, c12);
+        const int col = sp & 7;
+        const float dx = a2.x - (qx0 + static_cast<float>(col));
+        // exact batches: the reference's conic-to-covariance map per pixel
+        // (backward_splat.cu:285-291) with the unscaled conic: xx = cxx^2 U
+        // + cxy^2 W, xy = cxx cxy U - V / det + cxy czz W, yy = cxy^2 U +
+        // czz^2 W for the pixel's second moments (U, V, W) = Q (dx^2, dx dy,
+        // dy^2), all terms of one sign, so no sum is mapped afterwards (for
+        // a nearly singular conic the map would amplify the sums' rounding
+        // by ~1/(1 - r^2)).
+        const float m_xx = a2.z * a2.z, m_yy = a2.w * a2.w, m_xy = a2.z * a2.w;
+        const float m_yz = a2.w * b2.x, m_zz = b2.x * b2.x;
+        float v[16];
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-          buf[m * NV + 6 + c] = dcol * gre[c];
-          buf[m * NV + 6 + C + c] = dcol * gim[c];
-        }
-      }
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
 #pragma unroll
-      for (int i = G * NV; i < 64; ++i) buf[i] = 0.0f;
-      if (__ballot(any) != 0ull) {
-        const float tot_v = transpose_reduce64(buf);
-        if (lane < G * NV) {
-          const int m = lane / NV, v = lane - m * NV;
-          const int sl = s_wl[wave][hi - m];
-          if (sl != kDummy && tot_v != 0.0f) atomicAdd(&s_acc[sl * NV + v], tot_v);
+        for (int j = 0; j < 4; ++j) {
+          const int row = (sp >> 3) + 2 * j;
+          const int pp = row * 8 + col;
+          const float dy = a2.y - (qy0 + static_cast<float>(row));
+          const float2 qd = s_qd[wave][mm][pp];
+          const float Q = qd.x, dcol = qd.y;
+          const float Qdx = Q * dx, Qdy = Q * dy;
+          if (kRef) {
+            const float u = Qdx * dx, vv = Qdx * dy, w = Qdy * dy;
+            v[0] = fmaf(Q, fmaf(a2.z, dx, a2.w * dy), v[0]);
+            v[1] = fmaf(Q, fmaf(a2.w, dx, b2.x * dy), v[1]);
+            v[2] = fmaf(m_xx, u, fmaf(m_yy, w, v[2]));
+            v[3] = fmaf(m_xy, u, fmaf(-di2, vv, fmaf(m_yz, w, v[3])));
+            v[4] = fmaf(m_yy, u, fmaf(m_zz, w, v[4]));
+          } else {
+            v[0] += Qdx;
+            v[1] += Qdy;
+            v[2] = fmaf(Qdx, dx, v[2]);
+            v[3] = fmaf(Qdx, dy, v[3]);
+            v[4] = fmaf(Qdy, dy, v[4]);
+          }
+          v[5] += Q;
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            const float2 gv = s_gp[wave][pp][c];
+            v[6 + c] = fmaf(dcol, gv.x, v[6 + c]);
+            v[6 + C + c] = fmaf(dcol, gv.y, v[6 + C + c]);
+          }
         }
+        if (!kRef) {
+          // The mean and covariance maps on the lane's sums (linear in them;
+          // the conic is in the fast loop's domain, so the maps are well
+          // conditioned).  Staged conic: kc cxx, 2 kc cxy, kc czz.
+          const float sx = v[0], sy = v[1];
+          const float kxy = 0.5f * a2.w;
+          v[0] = fmaf(a2.z, sx, kxy * sy);  // kc (cxx sum Q dx + cxy sum Q dy)
+          v[1] = fmaf(kxy, sx, b2.x * sy);  // kc (cxy sum Q dx + czz sum Q dy)
+          const float cxx = a2.z * (1.0f / kBwdConicScale);
+          const float cxy = a2.w * (0.5f / kBwdConicScale);
+          const float czz = b2.x * (1.0f / kBwdConicScale);
+          const float U = v[2], V = v[3], Wm = v[4];
+          v[2] = fmaf(cxx * cxx, U, (cxy * cxy) * Wm);
+          v[3] = fmaf(cxx * cxy, U, fmaf(-di2, V, (cxy * czz) * Wm));
+          v[4] = fmaf(cxy * cxy, U, (czz * czz) * Wm);
+        }
+        const float tv = transpose_reduce16(v);
+        if (sp < NV && slot2 != kDummy && tv != 0.0f) {
+          // Accumulator slots: 0-1 the mean gradient (times W/2, H/2), 2-4
+          // the cov2D gradient, 5+c / 5+C+c the colour sums, 5+2C+plane the
+          // plane term.  The sums carry o w (Q = o w dL/dG): the mean and
+          // covariance terms need exactly that factor, the o w term (sum G
+          // dL/dalpha) its removal.
+          int aslot;
+          float scale;
+          if (sp == 0) {
+            aslot = 0;
+            scale = kRef ? -half_w : -half_w / kBwdConicScale;
+          } else if (sp == 1) {
+            aslot = 1;
+            scale = kRef ? -half_h : -half_h / kBwdConicScale;
+          } else if (sp < 5) {
+            aslot = sp;
+            scale = -0.5f;
+          } else if (sp == 5) {
+            aslot = 5 + 2 * C + plane;
+            scale = __builtin_amdgcn_rcpf(b2.w);
+          } else {
+            aslot = sp - 1;  // A_c at 5+c (sp = 6+c), B_c at 5+C+c (sp = 6+C+c)
+            scale = 1.0f;
+          }
+          unsafeAtomicAdd(p.acc + static_cast<int64_t>(s_g[slot2]) * AS + aslot, tv * scale);
+        }
+        // The next chunk's phase-1 writes after this chunk's reads.
+        __builtin_amdgcn_wave_barrier();
       }
-    }
     };
     if (exact)
       walk(std::true_type{});
     else
       walk(std::false_type{});
-    __syncthreads();
-    for (int e = threadIdx.x; e < cnt * NV; e += kBlock) {
-      const int j = e / NV, i = e - j * NV;
-      float val = s_acc[e];
-      const int gg = s_g[j];
-      if (!exact && i < 2) {
-        // sum Q u = kc cxx sum Q dx + kc cxy sum Q dy; sum Q v = kc cxy
-        // sum Q dx + kc czz sum Q dy (the staged conic is scaled by kc, the
-        // off-diagonal doubled)
-        const float4 a = s_rec[j * NQ];
-        const float sx = s_acc[j * NV], sy = s_acc[j * NV + 1];
-        const float kxy = 0.5f * a.w;
-        val = i == 0 ? fmaf(a.z, sx, kxy * sy) : fmaf(kxy, sx, s_rec[j * NQ + 1].x * sy);
-      } else if (!exact && i < 5) {
-        // The reference's conic-to-covariance map (backward_splat.cu:285-
-        // 291) on the block's second moments U, V, W of the member (a conic
-        // in the fast loop's domain, so the map is well conditioned; the
-        // staged conic is unscaled by 1/kc): xx = cxx^2 U + cxy^2 W,
-        // xy = cxx cxy U - V / det + cxy czz W, yy = cxy^2 U + czz^2 W.
-        const float4 a = s_rec[j * NQ];
-        const float cxx = a.z * (1.0f / kBwdConicScale);
-        const float cxy = a.w * (0.5f / kBwdConicScale);
-        const float czz = s_rec[j * NQ + 1].x * (1.0f / kBwdConicScale);
-        const float U = s_acc[j * NV + 2], V = s_acc[j * NV + 3], Wm = s_acc[j * NV + 4];
-        val = i == 2   ? fmaf(cxx * cxx, U, (cxy * cxy) * Wm)
-              : i == 3 ? fmaf(cxx * cxy, U,
-                              fmaf(-bwd_det_inv<C>(s_rec[j * NQ + 2],
-                                                   s_rec[j * NQ + (NQ > 3 ? 3 : 2)]),
-                                   V, (cxy * czz) * Wm))
-                       : fmaf(cxy * cxy, U, (czz * czz) * Wm);
-      }
-      if (val == 0.0f) continue;
-      // The partials carry o w (Q = o w dL/dG): the mean and conic terms
-      // need exactly that factor, the o w term (sum G dL/dalpha) its
-      // removal.
-      const float ow = s_rec[j * NQ + 1].w;
-      int slot;
-      float scale;
-      if (i == 0) {  // sum Q u, u = kc*(cxx dx + cxy dy)
-        slot = 0;
-        scale = exact ? -half_w : -half_w / kBwdConicScale;
-      } else if (i == 1) {
-        slot = 1;
-        scale = exact ? -half_h : -half_h / kBwdConicScale;
-      } else if (i < 5) {
-        slot = i;
-        scale = -0.5f;
-      } else if (i == 5) {
-        slot = 5 + 2 * C + plane;
-        scale = 1.0f / ow;
-      } else {
-        slot = i - 1;  // A_c at 5+c (i = 6+c), B_c at 5+C+c (i = 6+C+c)
-        scale = 1.0f;
-      }
-      unsafeAtomicAdd(p.acc + static_cast<int64_t>(gg) * AS + slot, val * scale);
-    }
   }
 }
 

@@ -33,8 +33,8 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   return v;
 }
 
-template <int CTRL, int HALF>
-__device__ __forceinline__ void butterfly_dpp(float (&v)[64], bool sel) {
+template <int CTRL, int HALF, int N>
+__device__ __forceinline__ void butterfly_dpp(float (&v)[N], bool sel) {
 #pragma unroll
   for (int i = 0; i < HALF; ++i) {
     const float lo = v[i], hi = v[i + HALF];
@@ -60,6 +60,19 @@ __device__ __forceinline__ float transpose_reduce64(float (&v)[64]) {
                                               false, false);
     v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
+  butterfly_dpp<0x140, 8>(v, (lane >> 3) & 1);  // row_mirror: lane xor 15
+  butterfly_dpp<0x141, 4>(v, (lane >> 2) & 1);  // row_half_mirror: lane xor 7
+  butterfly_dpp<0x4E, 2>(v, (lane >> 1) & 1);   // quad_perm [2,3,0,1]: lane xor 2
+  butterfly_dpp<0xB1, 1>(v, lane & 1);          // quad_perm [1,0,3,2]: lane xor 1
+  return v[0];
+}
+
+// transpose_reduce16: within each row of 16 lanes, every lane holds 16
+// values v[0..15]; afterwards lane L holds the sum over the 16 lanes of its
+// row of v[L & 15].  The in-row steps of transpose_reduce64 (lane xor 15, 7,
+// 2, 1 by DPP row_mirror, row_half_mirror and quad_perm).
+__device__ __forceinline__ float transpose_reduce16(float (&v)[16]) {
+  const int lane = __lane_id();
   butterfly_dpp<0x140, 8>(v, (lane >> 3) & 1);  // row_mirror: lane xor 15
   butterfly_dpp<0x141, 4>(v, (lane >> 2) & 1);  // row_half_mirror: lane xor 7
   butterfly_dpp<0x4E, 2>(v, (lane >> 1) & 1);   // quad_perm [2,3,0,1]: lane xor 2
