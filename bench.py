@@ -58,29 +58,30 @@ def profiled_traffic(config, stage, C, M):
 
 
 def profiled_valu(config, stage, C, M):
-    """(VALU wave-instructions, transcendental wave-instructions, issue peak
-    in wave-instructions/s) per dispatch of `stage`'s kernel from the
-    committed rocprofv3 summary of this workload, or None.  The peak is one
-    wave64 instruction per SIMD every 4 cycles at the shader clock the
-    summary measured on its calibration kernels (1024 SIMDs); a
-    transcendental holds its SIMD for two of those slots."""
+    """VALU issue model of `stage`'s kernel from the committed rocprofv3
+    summary of this workload, or None: a dict with the wave-instruction and
+    transcendental counts per dispatch, the issue peak (the published FP32
+    vector peak in wave64 instructions/s), the extra issue slots a
+    transcendental takes, and the measured rate of the forward's own member
+    loop (a calibration kernel with no memory traffic or barriers)."""
     path = os.path.join(REPO, "profiles", f"valu_{config}.txt")
     name = STAGE_KERNEL.get(stage, "").format(C=C, M=M)
     if not name or not os.path.exists(path):
         return None
-    row, clock = None, None
+    row, keys = None, {}
     with open(path) as f:
         for line in f:
-            if line.startswith("clock_ghz "):
-                clock = float(line.split()[1])
+            parts = line.split()
+            if len(parts) == 2 and parts[0] in ("valu_peak", "trans_extra_slots", "fwdloop_rate"):
+                keys[parts[0]] = float(parts[1])
             elif not line.startswith("#") and line.startswith(name + " "):
                 # columns after the name: n, waves, valu, trans, salu, lds, ...
                 rest = line[len(name):].split()
                 if len(rest) >= 4:
                     row = (int(float(rest[2])), int(float(rest[3])))
-    if row is None or clock is None:
+    if row is None or len(keys) < 3:
         return None
-    return row[0], row[1], 1024 * clock * 1e9 / 4
+    return {"valu": row[0], "trans": row[1], **keys}
 
 
 def algorithmic_bytes(N, K, P, C, W, H, S, T):
@@ -678,11 +679,19 @@ def main():
         prof = profiled_valu(spec.name, st, C, 2 * S)
         t_ms = dom_live if (st == dom and dom_live) else stages.get(st, {}).get("avg_launch_ms")
         if prof and t_ms:
-            instr, trans, peak = prof
-            issue_ms = (instr + trans) / peak * 1e3
-            valu[st] = {"wave_instructions": instr, "transcendental": trans,
-                        "issue_ms_at_peak": round(issue_ms, 4), "peak_wave_instr_per_s": peak,
+            slots = prof["valu"] + prof["trans_extra_slots"] * prof["trans"]
+            issue_ms = slots / prof["valu_peak"] * 1e3
+            valu[st] = {"wave_instructions": prof["valu"], "transcendental": prof["trans"],
+                        "issue_ms_at_peak": round(issue_ms, 4),
+                        "peak_wave_instr_per_s": prof["valu_peak"],
                         "measured_ms": round(t_ms, 4), "frac": round(issue_ms / t_ms, 3)}
+            if st == "render_fwd":
+                # the same instructions at the rate the forward's member
+                # loop reaches on its own (calibration kernel)
+                loop_ms = prof["valu"] / prof["fwdloop_rate"] * 1e3
+                valu[st].update({"member_loop_rate": prof["fwdloop_rate"],
+                                 "ms_at_member_loop_rate": round(loop_ms, 4),
+                                 "frac_of_member_loop_rate": round(loop_ms / t_ms, 3)})
     if valu:
         valu["source"] = f"profiles/valu_{spec.name}.txt"
 

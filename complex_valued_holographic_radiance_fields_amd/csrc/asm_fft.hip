@@ -383,7 +383,10 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   // statements, so a caller that runs the transform inside a loop (the plane
   // loop of the column passes) cannot hoist this stage's addresses and
   // twiddle loads out of the loop and hold them in registers throughout.
-  int tid = static_cast<int>(threadIdx.x);
+  // Indices are unsigned: the empty asm hides that the thread index is
+  // non-negative, and signed division and remainder by the batch and the
+  // stage span would cost three or four extra instructions each.
+  unsigned tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   int twoff = 0;
   asm volatile("" : "+s"(twoff));
@@ -391,21 +394,22 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
   int ob[BPT];
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
-    const int q = tid + u * T;
+    const unsigned q = tid + u * T;
     ob[u] = -1;
-    if (BPT * T == NB || q < NB) {
-      const int j = q / B;  // butterfly index within its transform
-      const int k = j % NS;
+    if (BPT * T == NB || q < static_cast<unsigned>(NB)) {
+      const unsigned j = q / B;  // butterfly index within its transform
+      const int k = static_cast<int>(j % NS);
       float2 x[R];
       if (lin_load) {
-        const int base = pad<K>(q);
+        const int base = pad<K>(static_cast<int>(q));
 #pragma unroll
         for (int t = 0; t < R; ++t)
           if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[base + t * LSP];
       } else {
 #pragma unroll
         for (int t = 0; t < R; ++t)
-          if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = lds[pad<K>(q + t * LS)];
+          if (!HALF || (t >= R / 4 && t < 3 * R / 4))
+            x[t] = lds[pad<K>(static_cast<int>(q + t * LS))];
       }
       if (NS > 1) {
         const float2* wk = tw + (twoff + OFF + k * (R - 1) - 1);
@@ -425,7 +429,7 @@ __device__ __forceinline__ void fft_stage(float2* lds, const float2* __restrict_
 #pragma unroll
       for (int t = 0; t < R; ++t) y[u][t] = x[t];
       // Stockham output position (j/NS)*NS*R + k + t*NS, interleaved.
-      const int a0 = q + B * (j / NS) * NS * (R - 1);
+      const int a0 = static_cast<int>(q + B * (j / NS) * NS * (R - 1));
       ob[u] = lin_store ? pad<K>(a0) : a0;
     }
   }
