@@ -273,9 +273,12 @@ int64_t total_chunks(const int64_t* numels, int nt) {
   return c;
 }
 
+// traced: open the "grad_norm" stage timer (hipEvents, taken from a pool
+// that grows on demand, when stage tracing is on).  The allocation-free
+// entry point passes false.
 int launch_grad_norm(const float* const* grads, const int64_t* numels, int num_tensors,
                      float max_norm, float* total_norm, float* clip_coef, float* partial,
-                     hipStream_t s);
+                     hipStream_t s, bool traced = true);
 
 int check_grad_list(const float* const* grads, const int64_t* numels, int nt) {
   if (nt < 0 || (nt > 0 && (!grads || !numels))) {
@@ -405,7 +408,7 @@ int hrf_grad_norm_static(const float* const* grads, const int64_t* numels, int32
   float* partial = nullptr;
   HRF_TRY(static_norm_scratch(&partial));
   return launch_grad_norm(grads, numels, num_tensors, max_norm, total_norm, clip_coef, partial,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream), /*traced=*/false);
 }
 
 }  // extern "C"
@@ -415,8 +418,12 @@ namespace {
 
 int launch_grad_norm(const float* const* grads, const int64_t* numels, int num_tensors,
                      float max_norm, float* total_norm, float* clip_coef, float* partial,
-                     hipStream_t s) {
-  HRF_STAGE("grad_norm", s);
+                     hipStream_t s, bool traced) {
+  if (traced) {
+    HRF_STAGE("grad_norm", s);
+    return launch_grad_norm(grads, numels, num_tensors, max_norm, total_norm, clip_coef, partial,
+                            s, false);
+  }
   HRF_TRY(for_tensor_groups<GradTable>(
       num_tensors, numels, [&](GradTable& t, int slot, int i) { t.g[slot] = grads[i]; },
       [&](const GradTable& t, int blocks, int64_t off) -> int {

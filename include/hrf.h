@@ -445,7 +445,11 @@ int hrf_grad_norm(const float* const* grads, const int64_t* numels, int32_t num_
  * 134217728 gradient elements in total (HRF_ERR_WORKSPACE beyond).  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams or host threads) race and must be ordered by the caller.
- * Same results as hrf_grad_norm (same kernels, same summation order). */
+ * Same results as hrf_grad_norm (same kernels, same summation order).  The
+ * first call on a device looks up the array's device address
+ * (hipGetSymbolAddress, which allocates nothing); a caller that captures the
+ * call into a HIP graph makes one call on that device before capturing.
+ * Stage tracing (hrf_trace_enable) does not time this entry point. */
 int hrf_grad_norm_static(const float* const* grads, const int64_t* numels, int32_t num_tensors,
                          float max_norm, float* total_norm, float* clip_coef, void* stream);
 

@@ -60,3 +60,62 @@ def test_grad_norm_static_matches_workspace_entry(hrf):
     # a third call with the first input again gives the first result
     o3 = _norm_both(L, lib, big, 1.0)
     assert o3[2] == o1[0] and o3[3] == o1[1]
+
+
+def test_grad_norm_static_allocates_nothing_and_replays_in_a_graph(hrf):
+    """The reasons the entry point exists: free device memory (hipMemGetInfo,
+    through torch.cuda.mem_get_info) is the same before and after calls once
+    the device's array address is known, and the call captured into a HIP
+    graph (after one call on the device) replays correctly: each replay, with
+    new gradient values written eagerly between replays, equals the
+    workspace entry point run eagerly on the same values, bit for bit."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import _lib as L
+
+    lib = L.load()
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    grads = [torch.empty(s, device="cuda") for s in ((300_000, 3), (300_000,), (4097,))]
+    for g in grads:
+        g.copy_(torch.randn(g.shape, generator=gen, device="cuda"))
+    n = len(grads)
+    ptrs = (ctypes.c_void_p * n)(*[g.data_ptr() for g in grads])
+    numels = (ctypes.c_int64 * n)(*[g.numel() for g in grads])
+    out = torch.zeros(2, device="cuda")
+
+    def static_call():
+        L.check(lib.hrf_grad_norm_static(ptrs, numels, n, 1.5, out[0:].data_ptr(),
+                                         out[1:].data_ptr(), L.stream_ptr(out.device)))
+
+    static_call()  # the device's array address is looked up here
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        static_call()
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    print(f"free device memory before/after three calls: {free0} / {free1}", flush=True)
+    assert free1 == free0
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        static_call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        static_call()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for g in grads:
+            g.copy_(torch.randn(g.shape, generator=gen, device="cuda") * (rep + 1))
+        torch.cuda.synchronize()
+        out.fill_(-1.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().copy()
+        ref = _norm_both(L, lib, grads, 1.5)
+        print(f"replay {rep}: norm {got[0]:.6f} (eager {ref[0]:.6f}), coef {got[1]:.6g} "
+              f"(eager {ref[1]:.6g})", flush=True)
+        assert got[0] == ref[0] and got[1] == ref[1]
+        assert got[0] == ref[2] and got[1] == ref[3]
