@@ -234,12 +234,14 @@ size_t radix_scratch_elems(int64_t n);
 // ones last).  With index_values, the values are taken to be 0..n-1 (va is
 // only used as a buffer).  keys_needed == false: the last pass writes only
 // the values (the sorted keys are then left nowhere).
-// A first sort pass whose histogram the pair emission took: np partitions
-// (the emission blocks), partition b being pairs [bounds[b], bounds[b + 1]),
-// the counts already in the sort scratch (digit-major, np columns).
+// A first sort pass whose histogram the pair emission took: np emission
+// blocks, block b's pairs being [bounds[b], bounds[b + 1]), their counts
+// already in the sort scratch (digit-major, np columns).  The pass's
+// scatter partitions are `group` consecutive emission blocks each.
 struct SortFirstPass {
   int np;
   const int64_t* bounds;
+  int group;
 };
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
@@ -257,11 +259,12 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
                     uint32_t* final_out = nullptr, uint32_t final_mask = 0xFFFFFFFFu,
                     const SortFirstPass* first = nullptr);
 // Whether the pair emission of n Gaussians and k pairs takes the first
-// tile-sort pass's histogram (of `bits` digit bits): only when its blocks
-// average many sort tiles of pairs (with ~1-2 tiles per block the partial
-// tiles of such partitions would cost the scatter what the histogram
-// saves) and the spine and partition bounds fit `scratch` (radix scratch
-// for k keys).  Fills *first (its bounds inside the scratch) when so.
+// tile-sort pass's histogram (of `bits` digit bits): only when groups of
+// consecutive emission blocks hold several sort tiles of pairs each while
+// enough groups remain to fill the GPU (with ~1-2 tiles per partition the
+// partial tiles would cost the scatter what the histogram saves), and the
+// spine and partition bounds fit `scratch` (radix scratch for k keys).
+// Fills *first (its bounds inside the scratch, the group size) when so.
 bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirstPass* first);
 // Digit bits of the first pass of a sort over nbits bits (the narrowest).
 int radix_first_bits(int nbits);

@@ -292,17 +292,21 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
       const int d = threadIdx.x;
       uint32_t gbase = gincl - gtot;
       for (int w = 0; w < wave; ++w) gbase += s_wsum[w];
-      run = gbase + hist_scan[static_cast<int64_t>(d) * nparts + blockIdx.x];
+      // the partition's first spine column (its first emission block)
+      const int col = bounds ? static_cast<int>(blockIdx.x) * sub : static_cast<int>(blockIdx.x);
+      run = gbase + hist_scan[static_cast<int64_t>(d) * nparts + col];
     }
   }
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
   // This block's partition [pstart, pend): sub tiles from blockIdx.x * sub,
-  // or the range `bounds` gives (the emission block's pairs).
+  // or (bounds) the pairs of emission blocks [blockIdx.x * sub, + sub).
   int64_t pstart, pend;
   if (bounds) {
-    pstart = bounds[blockIdx.x] < n ? bounds[blockIdx.x] : n;
-    pend = bounds[blockIdx.x + 1] < n ? bounds[blockIdx.x + 1] : n;
+    const int b0 = static_cast<int>(blockIdx.x) * sub;
+    const int b1 = b0 + sub < nparts ? b0 + sub : nparts;
+    pstart = bounds[b0] < n ? bounds[b0] : n;
+    pend = bounds[b1] < n ? bounds[b1] : n;
   } else {
     pstart = static_cast<int64_t>(blockIdx.x) * sub * kTile;
     pend = pstart + static_cast<int64_t>(sub) * kTile < n
@@ -1017,14 +1021,18 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
                      totals, run_flag);
   HRF_LAUNCH_CHECK();
   const int64_t* bounds = fp ? fp->bounds : nullptr;
+  // With the emission's histogram a scatter block takes fp->group emission
+  // blocks (the spine still has one column per emission block).
+  const int sub = fp ? fp->group : rp.sub;
+  const int nblk = fp ? (np + fp->group - 1) / fp->group : np;
   if (large)
-    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(np),
+    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(nblk),
                        dim3(kRadixThreadsLarge), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask,
-                       hist, totals, np, rp.sub, run_flag, out_mask, bounds);
+                       hist, totals, np, sub, run_flag, out_mask, bounds);
   else
-    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreads>), dim3(np), dim3(kRadixThreads),
-                       0, s, src_k, src_v, dst_k, dst_v, n, shift, mask, hist, totals, np, rp.sub,
-                       run_flag, out_mask, bounds);
+    hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreads>), dim3(nblk),
+                       dim3(kRadixThreads), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask, hist,
+                       totals, np, sub, run_flag, out_mask, bounds);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1179,9 +1187,12 @@ int launch_offsets(const uint32_t* order, const uint32_t* tiles, const uint32_t*
 }
 
 namespace {
-// Minimum average pairs per emission block for the emission to take the
-// first sort pass's histogram: 16 of the smaller sort tiles.
-constexpr int64_t kFirstPassMinPairs = 16 * static_cast<int64_t>(kRadixTile);
+// Emission blocks grouped into the first pass's scatter partitions: groups
+// of at least kFirstPassTargetPairs pairs where that leaves at least
+// kFirstPassMinParts partitions; no fused histogram when the groups would
+// hold fewer than half that many pairs.
+constexpr int64_t kFirstPassTargetPairs = 4 * static_cast<int64_t>(kRadixTile);
+constexpr int64_t kFirstPassMinParts = 1024;
 int digit_template_bits(int bits) { return bits <= 4 ? 4 : bits; }
 // Offset of the partition bounds in the sort scratch: after the spine and
 // the digit totals (at most kRadixBins), 8-byte aligned.
@@ -1200,11 +1211,17 @@ int radix_first_bits(int nbits) { return nbits > 0 ? nbits / radix_passes(nbits)
 bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirstPass* first) {
   if (n <= 0 || k <= 1 || bits < 1 || bits > 8 || !scratch) return false;
   const int64_t np = blocks_for(n, kEmitThreads);
-  if (k / np < kFirstPassMinPairs || np > 0x7FFFFFFF) return false;
+  if (np > 0x7FFFFFFF) return false;
+  const int64_t avg = k / np > 0 ? k / np : 1;  // pairs per emission block
+  int64_t group = (kFirstPassTargetPairs + avg - 1) / avg;
+  if (np / group < kFirstPassMinParts) group = np / kFirstPassMinParts;
+  if (group < 1) group = 1;
+  if (avg * group < kFirstPassTargetPairs / 2) return false;
   const int64_t need = first_bounds_off(np, bits) + 2 * (np + 1);
   if (need > static_cast<int64_t>(radix_scratch_elems(k))) return false;
   first->np = static_cast<int>(np);
   first->bounds = reinterpret_cast<const int64_t*>(scratch + first_bounds_off(np, bits));
+  first->group = static_cast<int>(group);
   return true;
 }
 
