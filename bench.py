@@ -372,16 +372,37 @@ def cpu_baseline_leg(spec, sc, budget_s):
             return {"value": cfg0["fwd_ms"], "unit": "ms/frame", "cores": cores, "kind": "port",
                     "sample": "the whole frame (not sampled): " + cfg0["run"], "config0": cfg0}
         est_ms, desc = cpu_baseline.time_frame(sc, budget_s=budget_s)
-        return {"value": None, "unit": "ms/frame", "cores": cores, "kind": "port",
-                "sample": f"the {spec.name} frame on the reference's CPU PyTorch path "
-                          "(oracle/cpu_baseline.py) is not run whole by the bench (about "
-                          f"{est_ms / 60e3:.0f} min of host time by the estimate below, "
-                          "against a bench budget of minutes); config 0 is run whole",
-                "estimate_ms_per_frame": round(est_ms, 1), "estimate_from": desc,
-                "config0": cfg0}
+        out = {"value": None, "unit": "ms/frame", "cores": cores, "kind": "port",
+               "sample": f"the {spec.name} frame on the reference's CPU PyTorch path "
+                         "(oracle/cpu_baseline.py) is not run whole by the bench (about "
+                         f"{est_ms / 60e3:.0f} min of host time by the estimate below, "
+                         "against a bench budget of minutes); config 0 is run whole",
+               "estimate_ms_per_frame": round(est_ms, 1), "estimate_from": desc,
+               "config0": cfg0}
+        whole = committed_cpu_frame(spec.name)
+        if whole:
+            out["whole_frame"] = whole
+        return out
     except Exception as e:  # reported, never fatal to the GPU measurement
         return {"value": None, "unit": "ms/frame", "cores": None, "kind": "port",
                 "sample": f"failed: {e!r}"}
+
+
+def committed_cpu_frame(name):
+    """The whole-frame CPU measurement of this workload committed under
+    profiles/ (`bench.py --cpu-frame NAME` on a GPU box's host), or None."""
+    path = os.path.join(REPO, "profiles", f"cpu_baseline_{name}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rows = [l for l in f if l.startswith("{")]
+    if not rows:
+        return None
+    d = json.loads(rows[-1])
+    return {"value": d.get("value"), "unit": d.get("unit"), "cores": d.get("cores"),
+            "did_not_finish": d.get("did_not_finish"), "kind": d.get("kind"),
+            "source": os.path.relpath(path, REPO),
+            "command": f"python bench.py --cpu-frame {name}"}
 
 
 def cpu_whole_frame(name):

@@ -594,6 +594,12 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   const int first_bits = radix_first_bits(end_bit);  // 0 without tile bits (one tile)
   const bool first_fused =
       first_bits > 0 && emit_first_pass(n, num_pairs, first_bits, b.radix, &first);
+  // Large sorts of two or more passes: the emission only counts, and the
+  // first pass regenerates the pairs (one write of them instead of a
+  // write, a read and a write).
+  const EmitGen gen{w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect,
+                    n, num_pairs, f.gx, vbits};
+  if (first_fused && first.regenerate && radix_passes(end_bit) >= 2) first.gen = &gen;
   if (end_bit + vbits <= 32) {
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {

@@ -238,10 +238,30 @@ size_t radix_scratch_elems(int64_t n);
 // blocks, block b's pairs being [bounds[b], bounds[b + 1]), their counts
 // already in the sort scratch (digit-major, np columns).  The pass's
 // scatter partitions are `group` consecutive emission blocks each.
+// What the fused emission-scatter needs to regenerate the emission's pairs
+// (the emission launch's own inputs).
+struct EmitGen {
+  const uint64_t* part_t;
+  const uint64_t* part_r;
+  const uint32_t* tiles;
+  const uint32_t* order;
+  const uint32_t* sorted_flag;
+  const uint2* rect;
+  int64_t n;
+  int64_t k;
+  int gx;
+  int vbits;
+};
+// regenerate (set by emit_first_pass): the sort is large enough (8192-key
+// tiles, one emission block per partition) for the emission to store no
+// pair and the first pass to regenerate them from `gen`, which the caller
+// sets (nullptr: the emission stores the pairs and the pass reads them).
 struct SortFirstPass {
   int np;
   const int64_t* bounds;
   int group;
+  bool regenerate;
+  const EmitGen* gen;
 };
 int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      int64_t n, int end_bit, uint32_t* scratch, bool* result_in_b,
@@ -314,6 +334,8 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
                       int64_t vmax = 0, uint32_t* scratch = nullptr,
                       const SortFirstPass* first = nullptr, int first_shift = 0,
                       int first_bits = 0);
+// (first->gen set: the emission only counts the first pass's digits and
+// stores no pair; the sort's first pass regenerates them.)
 int launch_tile_ranges(const uint32_t* keys, int64_t k, int32_t* ranges,
                        int ntiles, hipStream_t s);
 // Packed binning (tile bits + gaussian bits <= 32): word = tile << vbits | g.

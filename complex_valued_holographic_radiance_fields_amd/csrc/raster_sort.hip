@@ -8,6 +8,7 @@
 // stable-sorted once by depth' (4 passes over N), pairs are emitted in that
 // rank order, and a stable sort by tile id alone (ceil(log2 T / 8) passes,
 // 2 for T <= 65536) finishes the job: same order, far fewer bytes moved.
+#include <cstdlib>
 #include <type_traits>
 
 #include "hrf_internal.h"
@@ -243,17 +244,134 @@ __device__ __forceinline__ void rank_tile(const uint32_t (&key)[kRadixItems], in
   }
 }
 
-// Stable scatter of one partition, tile by tile.  In a tile, wave w owns
-// the contiguous sub-range [base + w*512, base + (w+1)*512) processed as 8
-// iterations of 64 keys; the rank of a key among equal digits before it is
-// found with a ballot match (RB ballots) plus per-wave LDS digit counters.
-// The tile's keys are then reordered by digit in LDS (stable: digit, wave,
-// rank), and written out from there in order: consecutive threads store
-// consecutive elements of each digit's output run, so the global stores
-// coalesce instead of spreading every wave-wide store over up to 2^RB runs.
-// Thread d < 2^RB holds digit d's next output position in the partition
-// (`run`), advanced by the digit's count after each tile.  kout == nullptr
-// with VALS: only the values are written (the caller needs no sorted keys).
+// Digit d's first output position in the pass for partition column `col`
+// of the scanned spine (thread d < 2^RB; 0 in the other threads): the
+// global totals of the lower digits plus the column's offset along digit
+// d's row.  Holds a barrier.
+template <int RB>
+__device__ __forceinline__ uint32_t digit_run_start(const uint32_t* __restrict__ digit_totals,
+                                                    const uint32_t* __restrict__ hist_scan,
+                                                    int nparts, int col, int wave, int lane,
+                                                    uint32_t* s_wsum) {
+  constexpr int kBins = 1 << RB;
+  const uint32_t gtot = threadIdx.x < kBins ? digit_totals[threadIdx.x] : 0u;
+  uint32_t gincl = gtot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t gy = __shfl_up(gincl, o, 64);
+    if (lane >= o) gincl += gy;
+  }
+  if (lane == 63) s_wsum[wave] = gincl;
+  __syncthreads();
+  uint32_t run = 0;
+  if (threadIdx.x < kBins) {
+    const int d = threadIdx.x;
+    uint32_t gbase = gincl - gtot;
+    for (int w = 0; w < wave; ++w) gbase += s_wsum[w];
+    run = gbase + hist_scan[static_cast<int64_t>(d) * nparts + col];
+  }
+  return run;
+}
+
+// One tile of a stable scatter pass: this lane's kRadixItems keys (and
+// values) of the tile at bbase in the wave-contiguous layout (wave w owns
+// [bbase + w * 512, + 512), item it at w * 512 + it * 64 + lane), the valid
+// ones those below pend (FULL: all kTile).  The keys are ranked by digit
+// (ballot match plus per-wave LDS digit counters), reordered by digit in
+// LDS (stable: digit, wave, rank) and written from there in order, so
+// consecutive threads store consecutive elements of each digit's output
+// run.  Thread d < 2^RB holds digit d's next output position (`run`),
+// advanced by the digit's count.  The caller has cleared s_cnt before the
+// first tile; this clears it again for the next.
+template <int RB, bool VALS, int TH, bool FULL>
+__device__ __forceinline__ void scatter_tile(
+    const uint32_t (&key)[kRadixItems], const uint32_t (&val)[kRadixItems], int64_t bbase,
+    int64_t pend, int wave, int lane, uint64_t lt_mask, int shift, uint32_t mask,
+    uint32_t (*s_cnt)[1 << RB], uint32_t* s_delta, uint32_t* s_wsum, uint32_t* s_key,
+    uint32_t* s_val, uint32_t& run, bool write_keys, uint32_t* __restrict__ kout,
+    uint32_t* __restrict__ vout, uint32_t out_mask) {
+  constexpr int kBins = 1 << RB;
+  constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
+  const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
+  const int nvalid =
+      FULL ? kTile : static_cast<int>(pend - bbase < kTile ? pend - bbase : kTile);
+  uint32_t rank[kRadixItems];
+  int dig[kRadixItems];
+  rank_tile<RB, FULL>(key, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave], rank, dig);
+  __syncthreads();
+  // Per digit: the counts of the lower waves (s_cnt becomes each wave's
+  // local start), the tile total, and the exclusive scan over the digits
+  // of the tile totals (the digit's local start in the reordered tile).
+  uint32_t tot = 0;
+  if (threadIdx.x < kBins) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][threadIdx.x];
+  }
+  uint32_t incl = tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  if (threadIdx.x < kBins) {
+    const int d = threadIdx.x;
+    uint32_t loc = incl - tot;
+    for (int w = 0; w < wave; ++w) loc += s_wsum[w];
+    s_delta[d] = run - loc;
+    run += tot;
+    uint32_t r = loc;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const uint32_t c = s_cnt[w][d];
+      s_cnt[w][d] = r;
+      r += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kRadixItems; ++it) {
+    if (dig[it] >= 0) {
+      const uint32_t lp = s_cnt[wave][dig[it]] + rank[it];
+      s_key[lp] = key[it];
+      if (VALS) s_val[lp] = val[it];
+    }
+  }
+  __syncthreads();
+  // The digit counters are read no more in this tile: clear them for the
+  // next one (the barrier after the write-out orders it).
+  for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
+    s_cnt[e / kBins][e % kBins] = 0;
+  if (write_keys) {
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int i = it * TH + static_cast<int>(threadIdx.x);
+      if (FULL || i < nvalid) {
+        const uint32_t k = s_key[i];
+        const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
+        kout[pos] = k & out_mask;
+        if (VALS) vout[pos] = s_val[i];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int i = it * TH + static_cast<int>(threadIdx.x);
+      if (FULL || i < nvalid) {
+        const uint32_t pos = s_delta[(s_key[i] >> shift) & mask] + static_cast<uint32_t>(i);
+        vout[pos] = s_val[i];
+      }
+    }
+  }
+  // Orders this tile's reads of s_key/s_val/s_delta and the counter
+  // clear before the next tile's writes.
+  __syncthreads();
+}
+
+// Stable scatter of one partition, tile by tile (scatter_tile), each
+// tile's keys loaded during the previous tile.  kout == nullptr with VALS:
+// only the values are written (the caller needs no sorted keys).
 template <int RB, bool VALS, int TH>
 __global__ __launch_bounds__(TH) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
@@ -275,28 +393,10 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const bool write_keys = !VALS || kout != nullptr;
 
-  // Digit d's first output position in this partition: the global totals
-  // of the lower digits plus the partition's offset along digit d's row.
-  uint32_t run = 0;
-  {
-    const uint32_t gtot = threadIdx.x < kBins ? digit_totals[threadIdx.x] : 0u;
-    uint32_t gincl = gtot;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t gy = __shfl_up(gincl, o, 64);
-      if (lane >= o) gincl += gy;
-    }
-    if (lane == 63) s_wsum[wave] = gincl;
-    __syncthreads();
-    if (threadIdx.x < kBins) {
-      const int d = threadIdx.x;
-      uint32_t gbase = gincl - gtot;
-      for (int w = 0; w < wave; ++w) gbase += s_wsum[w];
-      // the partition's first spine column (its first emission block)
-      const int col = bounds ? static_cast<int>(blockIdx.x) * sub : static_cast<int>(blockIdx.x);
-      run = gbase + hist_scan[static_cast<int64_t>(d) * nparts + col];
-    }
-  }
+  // The partition's first spine column is its first emission block when
+  // `bounds` gives the partitions.
+  const int col = bounds ? static_cast<int>(blockIdx.x) * sub : static_cast<int>(blockIdx.x);
+  uint32_t run = digit_run_start<RB>(digit_totals, hist_scan, nparts, col, wave, lane, s_wsum);
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
   // This block's partition [pstart, pend): sub tiles from blockIdx.x * sub,
@@ -318,88 +418,6 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
   pstart = uniform_i64(pstart);
   pend = uniform_i64(pend);
 
-  // One tile at bbase whose keys and values are loaded; FULL: all
-  // kTile of them are in the partition.
-  auto tile = [&](auto full, int64_t bbase, const uint32_t(&key)[kRadixItems],
-                  const uint32_t(&val)[kRadixItems]) {
-    constexpr bool FULL = decltype(full)::value;
-    const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
-    const int nvalid =
-        FULL ? kTile : static_cast<int>(pend - bbase < kTile ? pend - bbase : kTile);
-    uint32_t rank[kRadixItems];
-    int dig[kRadixItems];
-    rank_tile<RB, FULL>(key, wbase, pend, lane, lt_mask, shift, mask, s_cnt[wave], rank, dig);
-    __syncthreads();
-    // Per digit: the counts of the lower waves (s_cnt becomes each wave's
-    // local start), the tile total, and the exclusive scan over the digits
-    // of the tile totals (the digit's local start in the reordered tile).
-    uint32_t tot = 0;
-    if (threadIdx.x < kBins) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][threadIdx.x];
-    }
-    uint32_t incl = tot;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += y;
-    }
-    if (lane == 63) s_wsum[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x < kBins) {
-      const int d = threadIdx.x;
-      uint32_t loc = incl - tot;
-      for (int w = 0; w < wave; ++w) loc += s_wsum[w];
-      s_delta[d] = run - loc;
-      run += tot;
-      uint32_t r = loc;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const uint32_t c = s_cnt[w][d];
-        s_cnt[w][d] = r;
-        r += c;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < kRadixItems; ++it) {
-      if (dig[it] >= 0) {
-        const uint32_t lp = s_cnt[wave][dig[it]] + rank[it];
-        s_key[lp] = key[it];
-        if (VALS) s_val[lp] = val[it];
-      }
-    }
-    __syncthreads();
-    // The digit counters are read no more in this tile: clear them for the
-    // next one (the barrier after the write-out orders it).
-    for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
-      s_cnt[e / kBins][e % kBins] = 0;
-    if (write_keys) {
-#pragma unroll
-      for (int it = 0; it < kRadixItems; ++it) {
-        const int i = it * TH + static_cast<int>(threadIdx.x);
-        if (FULL || i < nvalid) {
-          const uint32_t k = s_key[i];
-          const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
-          kout[pos] = k & out_mask;
-          if (VALS) vout[pos] = s_val[i];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int it = 0; it < kRadixItems; ++it) {
-        const int i = it * TH + static_cast<int>(threadIdx.x);
-        if (FULL || i < nvalid) {
-          const uint32_t pos = s_delta[(s_key[i] >> shift) & mask] + static_cast<uint32_t>(i);
-          vout[pos] = s_val[i];
-        }
-      }
-    }
-    // Orders this tile's reads of s_key/s_val/s_delta and the counter
-    // clear before the next tile's writes.
-    __syncthreads();
-  };
-
   for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
     s_cnt[e / kBins][e % kBins] = 0;
   __syncthreads();
@@ -418,9 +436,14 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
     }
     if (bbase + kTile < pend)
       load_tile<VALS>(kin, vin, bbase + kTile + woff, pend, lane, nkey, nval);
-    tile(std::true_type{}, bbase, key, val);
+    scatter_tile<RB, VALS, TH, true>(key, val, bbase, pend, wave, lane, lt_mask, shift, mask,
+                                     s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
+                                     kout, vout, out_mask);
   }
-  if (bbase < pend) tile(std::false_type{}, bbase, nkey, nval);
+  if (bbase < pend)
+    scatter_tile<RB, VALS, TH, false>(nkey, nval, bbase, pend, wave, lane, lt_mask, shift, mask,
+                                      s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
+                                      kout, vout, out_mask);
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
@@ -660,6 +683,54 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
   }
 }
 
+// Pairs [a, a + cnt) of an emission block, whose pair offsets are
+// s_off[0..nr] and whose Gaussians and packed rectangles are s_g and s_rect
+// (rank order), handed to store(j, tile id, gaussian) for j = 0..cnt-1: one
+// binary search finds the first pair's Gaussian and tile (one division by
+// the rectangle width), then a walk goes on (next tile of the rectangle, y
+// outer and x inner as rasterizer_splat.cu:162-173 emits them; next
+// Gaussian with pairs).
+template <typename Store>
+__device__ __forceinline__ void walk_pairs(uint64_t a, int cnt, const uint64_t* s_off, int nr,
+                                           const uint2* s_rect, const uint32_t* s_g, uint32_t ugx,
+                                           Store store) {
+  int lo = 0, hi = nr;  // the largest lo with s_off[lo] <= a: a < s_off[lo + 1]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_off[mid] <= a)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  uint64_t next = s_off[lo + 1];
+  uint2 rc = s_rect[lo];
+  uint32_t minx = rc.x & 0xFFFF, maxx = rc.y & 0xFFFF;
+  const uint32_t w0 = maxx - minx;
+  const uint32_t i0 = static_cast<uint32_t>(a - s_off[lo]);
+  uint32_t ty = (rc.x >> 16) + i0 / w0, tx = minx + i0 % w0;
+  uint32_t gb = s_g[lo];
+  for (int j = 0; j < cnt; ++j) {
+    const uint64_t e = a + j;
+    if (e == next) {  // this Gaussian is done: the next one with pairs
+      do {
+        ++lo;
+        next = s_off[lo + 1];
+      } while (next == e);
+      rc = s_rect[lo];
+      minx = rc.x & 0xFFFF;
+      maxx = rc.y & 0xFFFF;
+      tx = minx;
+      ty = rc.x >> 16;
+      gb = s_g[lo];
+    }
+    store(j, ty * ugx + tx, gb);
+    if (++tx == maxx) {
+      tx = minx;
+      ++ty;
+    }
+  }
+}
+
 // Pair emission.  A block owns kEmitThreads consecutive ranks; it forms
 // their exclusive pair offsets in LDS (a block scan of their tile counts
 // plus the block's scanned base) and writes the block's output range
@@ -697,7 +768,9 @@ __device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int6
 // hit distinct banks); the chunk then leaves in coalesced stores.
 // kWide == false: one word (tile << vbits) | gaussian per pair into
 // `words`.  kWide: the tile id into `words` and the gaussian into `vals`
-// (tile and gaussian bits do not fit one word).
+// (tile and gaussian bits do not fit one word).  kStore == false (with
+// kHist): the pairs are only counted for the first sort pass's histogram;
+// k_emit_scatter regenerates and scatters them.
 constexpr int kEmitPer = 16;
 constexpr int kEmitChunk = kEmitThreads * kEmitPer;
 __device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
@@ -715,7 +788,7 @@ struct EmitHist {
   int rows;  // digit rows of the pass's histogram (2^RB >= mask + 1; the rest are zero)
 };
 
-template <bool kWide, bool kHist>
+template <bool kWide, bool kHist, bool kStore = true>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
     const uint64_t* __restrict__ part_t, const uint64_t* __restrict__ part_r,
     const uint32_t* __restrict__ tiles, const uint32_t* __restrict__ order,
@@ -723,11 +796,12 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
     int64_t k, int gx, int vbits, uint32_t* __restrict__ words, uint32_t* __restrict__ vals,
     VisibleOut vo, EmitHist eh) {
   compact_visible_block(vo, n);
-  __shared__ uint32_t s_dh[kHist ? kEmitThreads / 64 : 1][kHist ? kRadixBins : 1];
+  // (one more slot per wave: the counting path's difference arrays)
+  __shared__ uint32_t s_dh[kHist ? kEmitThreads / 64 : 1][kHist ? kRadixBins + 1 : 1];
   const int wave = threadIdx.x >> 6;
   if (kHist) {
-    for (int e = threadIdx.x; e < (kEmitThreads / 64) * kRadixBins; e += kEmitThreads)
-      s_dh[e / kRadixBins][e % kRadixBins] = 0u;
+    for (int e = threadIdx.x; e < (kEmitThreads / 64) * (kRadixBins + 1); e += kEmitThreads)
+      s_dh[e / (kRadixBins + 1)][e % (kRadixBins + 1)] = 0u;
   }
   __shared__ uint64_t s_off[kEmitThreads + 1];
   __shared__ uint32_t s_g[kEmitThreads];
@@ -749,58 +823,78 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
   const uint64_t uk = static_cast<uint64_t>(k);
   const uint64_t e0 = s_off[0], e1 = s_off[nr] < uk ? s_off[nr] : uk;
   const uint32_t ugx = static_cast<uint32_t>(gx);
+  if (!kStore && s_off[nr] <= uk) {
+    // Counting only, every pair of the block below k: a Gaussian's pairs
+    // are the rows of its tile rectangle, each row a run of consecutive
+    // tile ids, and the first digit is the tile id's low bits (eh.shift
+    // selects them in both key layouts), so a row adds whole cycles of the
+    // 2^bits digits plus one cyclic digit range: a difference array per
+    // wave (two to four LDS atomics per row, none per pair), then a scan
+    // over the digits.
+    __shared__ uint32_t s_wv1[kEmitThreads / 64], s_wv2[kEmitThreads / 64];
+    const uint32_t M = eh.mask + 1u;
+    uint32_t full = 0;
+    if (static_cast<int>(threadIdx.x) < nr && s_off[threadIdx.x + 1] > s_off[threadIdx.x]) {
+      const uint2 rc = s_rect[threadIdx.x];
+      const uint32_t minx = rc.x & 0xFFFF, maxx = rc.y & 0xFFFF;
+      const uint32_t miny = rc.x >> 16, maxy = rc.y >> 16;
+      const uint32_t L = maxx - minx, rem = L & eh.mask;
+      full = (L / M) * (maxy - miny);
+      if (rem) {
+        for (uint32_t ty = miny; ty < maxy; ++ty) {
+          const uint32_t a = (ty * ugx + minx) & eh.mask, b = a + rem;
+          atomicAdd(&s_dh[wave][a], 1u);
+          if (b <= M) {
+            atomicAdd(&s_dh[wave][b], 0xFFFFFFFFu);
+          } else {
+            atomicAdd(&s_dh[wave][M], 0xFFFFFFFFu);
+            atomicAdd(&s_dh[wave][0], 1u);
+            atomicAdd(&s_dh[wave][b - M], 0xFFFFFFFFu);
+          }
+        }
+      }
+    }
+    uint32_t ftot;
+    block_exclusive_scan<uint32_t>(full, &ftot, s_wv1);  // the block's whole cycles
+    __syncthreads();
+    const int d = static_cast<int>(threadIdx.x);
+    uint32_t v = 0;
+    if (d <= static_cast<int>(eh.mask)) {
+#pragma unroll
+      for (int w = 0; w < kEmitThreads / 64; ++w) v += s_dh[w][d];
+    }
+    uint32_t vtot;
+    const uint32_t incl = block_exclusive_scan<uint32_t>(v, &vtot, s_wv2) + v;
+    for (int r = d; r < eh.rows; r += kEmitThreads)
+      eh.hist[static_cast<int64_t>(r) * gridDim.x + blockIdx.x] =
+          r <= static_cast<int>(eh.mask) ? incl + ftot : 0u;
+    if (threadIdx.x == 0) {
+      eh.bounds[blockIdx.x] = static_cast<int64_t>(e0);
+      if (blockIdx.x == gridDim.x - 1) eh.bounds[gridDim.x] = k;
+    }
+    return;
+  }
   for (uint64_t c0 = e0; c0 < e1; c0 += kEmitChunk) {
     const int clen = static_cast<int>(e1 - c0 < kEmitChunk ? e1 - c0 : kEmitChunk);
     const int j0 = static_cast<int>(threadIdx.x) * kEmitPer;
     if (j0 < clen) {
-      const uint64_t a = c0 + j0;
-      int lo = 0, hi = nr;  // the largest lo with s_off[lo] <= a: a < s_off[lo + 1]
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (s_off[mid] <= a)
-          lo = mid;
-        else
-          hi = mid;
-      }
-      uint64_t next = s_off[lo + 1];
-      uint2 rc = s_rect[lo];
-      uint32_t minx = rc.x & 0xFFFF, maxx = rc.y & 0xFFFF;
-      const uint32_t w0 = maxx - minx;
-      const uint32_t i0 = static_cast<uint32_t>(a - s_off[lo]);
-      uint32_t ty = (rc.x >> 16) + i0 / w0, tx = minx + i0 % w0;
-      uint32_t gb = s_g[lo];
       const int cnt = clen - j0 < kEmitPer ? clen - j0 : kEmitPer;
-      for (int j = 0; j < cnt; ++j) {
-        const uint64_t e = a + j;
-        if (e == next) {  // this Gaussian is done: the next one with pairs
-          do {
-            ++lo;
-            next = s_off[lo + 1];
-          } while (next == e);
-          rc = s_rect[lo];
-          minx = rc.x & 0xFFFF;
-          maxx = rc.y & 0xFFFF;
-          tx = minx;
-          ty = rc.x >> 16;
-          gb = s_g[lo];
-        }
+      walk_pairs(c0 + j0, cnt, s_off, nr, s_rect, s_g, ugx, [&](int j, uint32_t tile, uint32_t gb) {
         if (kWide) {
-          s_words[emit_pad(j0 + j)] = ty * ugx + tx;
+          s_words[emit_pad(j0 + j)] = tile;
           s_vals[emit_pad(j0 + j)] = gb;
         } else {
-          s_words[emit_pad(j0 + j)] = ((ty * ugx + tx) << vbits) | gb;
+          s_words[emit_pad(j0 + j)] = (tile << vbits) | gb;
         }
-        if (++tx == maxx) {
-          tx = minx;
-          ++ty;
-        }
-      }
+      });
     }
     __syncthreads();
     for (int i = threadIdx.x; i < clen; i += kEmitThreads) {
       const uint32_t w = s_words[emit_pad(i)];
-      words[c0 + i] = w;
-      if (kWide) vals[c0 + i] = s_vals[emit_pad(i)];
+      if (kStore) {
+        words[c0 + i] = w;
+        if (kWide) vals[c0 + i] = s_vals[emit_pad(i)];
+      }
       if (kHist) atomicAdd(&s_dh[wave][(w >> eh.shift) & eh.mask], 1u);
     }
     __syncthreads();
@@ -818,6 +912,98 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
       eh.bounds[blockIdx.x] = static_cast<int64_t>(e0);
       if (blockIdx.x == gridDim.x - 1) eh.bounds[gridDim.x] = k;
     }
+  }
+}
+
+// The pair emission fused with the first tile-sort pass (large sorts): the
+// counting launch (k_emit_packed<kWide, true, false>) has taken the pass's
+// digit histogram and partition bounds over the emission blocks and stored
+// no pair.  Block b regenerates emission block b's pairs tile by tile (each
+// thread walks kRadixItems consecutive pairs of the tile into LDS) and
+// scatters each tile by the first digit as k_radix_scatter does a loaded
+// one: one write of the pairs instead of a write, a read and a write.
+// The partition is [s_off[0], min(s_off[nr], k)), as the counting launch
+// recorded it; its spine column is b.  The generated tile is stored at
+// index i ^ ((i >> 6) & 7): a thread's 8 consecutive pairs then hit
+// distinct banks across the wave (lane t writes 8t + (j ^ (t >> 3))), and
+// the scatter's reads (64 consecutive items per wave) stay one contiguous
+// run, so the tile needs no padding.
+template <bool kWide, int RB, int TH>
+__global__ __launch_bounds__(TH) void k_emit_scatter(
+    const uint64_t* __restrict__ part_t, const uint64_t* __restrict__ part_r,
+    const uint32_t* __restrict__ tiles, const uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ sorted_flag, const uint2* __restrict__ rect, int64_t n,
+    int64_t k, int gx, int vbits, uint32_t* __restrict__ kout, uint32_t* __restrict__ vout,
+    int shift, uint32_t mask, const uint32_t* __restrict__ hist_scan,
+    const uint32_t* __restrict__ digit_totals, int nparts) {
+  constexpr bool VALS = kWide;
+  constexpr int kBins = 1 << RB;
+  constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
+  static_assert(kBins <= TH && kEmitThreads <= TH, "one thread per digit and per rank");
+  static_assert(kRadixItems == 8, "the swizzle assumes 8 items per thread");
+  __shared__ uint32_t s_cnt[kWaves][kBins];
+  __shared__ uint32_t s_delta[kBins];
+  __shared__ uint32_t s_wsum[kWaves];
+  __shared__ uint32_t s_key[kTile];
+  __shared__ uint32_t s_val[VALS ? kTile : 1];
+  __shared__ uint64_t s_off[kEmitThreads + 1];
+  __shared__ uint32_t s_g[kEmitThreads];
+  __shared__ uint2 s_rect[kEmitThreads];
+  __shared__ uint64_t s_wave[kWaves];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  uint32_t run = digit_run_start<RB>(digit_totals, hist_scan, nparts,
+                                     static_cast<int>(blockIdx.x), wave, lane, s_wsum);
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
+  const int nr = static_cast<int>(n - rb < kEmitThreads ? n - rb : kEmitThreads);
+  block_offsets(part_t, part_r, tiles, order, sorted_flag, rb, nr, s_off, s_wave);
+  if (static_cast<int>(threadIdx.x) < nr) {
+    const uint32_t g = ordered(order, sorted_flag, rb + threadIdx.x);
+    s_g[threadIdx.x] = g;
+    s_rect[threadIdx.x] = rect[g];
+  }
+  for (int e = threadIdx.x; e < kWaves * kBins; e += TH) s_cnt[e / kBins][e % kBins] = 0;
+  __syncthreads();
+  const int64_t e0 = uniform_i64(static_cast<int64_t>(s_off[0]));
+  const int64_t e1 = uniform_i64(static_cast<int64_t>(
+      s_off[nr] < static_cast<uint64_t>(k) ? s_off[nr] : static_cast<uint64_t>(k)));
+  const uint32_t ugx = static_cast<uint32_t>(gx);
+  const int j0 = static_cast<int>(threadIdx.x) * kRadixItems;
+  for (int64_t c0 = e0; c0 < e1; c0 += kTile) {
+    const int clen = static_cast<int>(e1 - c0 < kTile ? e1 - c0 : kTile);
+    if (j0 < clen) {
+      const int cnt = clen - j0 < kRadixItems ? clen - j0 : kRadixItems;
+      walk_pairs(static_cast<uint64_t>(c0 + j0), cnt, s_off, nr, s_rect, s_g, ugx,
+                 [&](int j, uint32_t tile, uint32_t gb) {
+                   const int i = j0 + j;
+                   const int sw = i ^ ((i >> 6) & 7);
+                   s_key[sw] = kWide ? tile : ((tile << vbits) | gb);
+                   if (VALS) s_val[sw] = gb;
+                 });
+    }
+    __syncthreads();
+    // This lane's items in the scatter's wave-contiguous layout (entries
+    // past clen are read but never ranked or written).
+    uint32_t key[kRadixItems], val[kRadixItems];
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int i = wave * (kRadixItems * 64) + it * 64 + lane;
+      const int sw = i ^ ((i >> 6) & 7);
+      key[it] = s_key[sw];
+      val[it] = VALS ? s_val[sw] : 0u;
+    }
+    // scatter_tile's first barrier orders these reads before its reorder
+    // writes; its last one orders its reads before the next generation.
+    if (clen == kTile)
+      scatter_tile<RB, VALS, TH, true>(key, val, c0, e1, wave, lane, lt_mask, shift, mask, s_cnt,
+                                       s_delta, s_wsum, s_key, s_val, run, true, kout, vout,
+                                       0xFFFFFFFFu);
+    else
+      scatter_tile<RB, VALS, TH, false>(key, val, c0, e1, wave, lane, lt_mask, shift, mask, s_cnt,
+                                        s_delta, s_wsum, s_key, s_val, run, true, kout, vout,
+                                        0xFFFFFFFFu);
   }
 }
 
@@ -1025,6 +1211,27 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
   // blocks (the spine still has one column per emission block).
   const int sub = fp ? fp->group : rp.sub;
   const int nblk = fp ? (np + fp->group - 1) / fp->group : np;
+  if (fp && fp->gen) {
+    // The emission stored no pair: regenerate and scatter them (one block
+    // per emission block).
+    const EmitGen& g = *fp->gen;
+    if (fp->group != 1 || g.k != n) {
+      set_error("internal: fused emission-scatter needs one emission block per partition");
+      return HRF_ERR_INVALID;
+    }
+    if (large)
+      hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreadsLarge>), dim3(np),
+                         dim3(kRadixThreadsLarge), 0, s, g.part_t, g.part_r, g.tiles, g.order,
+                         g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
+                         mask, hist, totals, np);
+    else
+      hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreads>), dim3(np),
+                         dim3(kRadixThreads), 0, s, g.part_t, g.part_r, g.tiles, g.order,
+                         g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
+                         mask, hist, totals, np);
+    HRF_LAUNCH_CHECK();
+    return HRF_OK;
+  }
   if (large)
     hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(nblk),
                        dim3(kRadixThreadsLarge), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask,
@@ -1212,16 +1419,22 @@ bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirs
   if (n <= 0 || k <= 1 || bits < 1 || bits > 8 || !scratch) return false;
   const int64_t np = blocks_for(n, kEmitThreads);
   if (np > 0x7FFFFFFF) return false;
+  // HRF_SORT_REGENERATE=1 (for tests) takes the fused emission-scatter at
+  // any size: one emission block per partition.
+  const char* force = std::getenv("HRF_SORT_REGENERATE");
+  const bool forced = force && force[0] == '1';
   const int64_t avg = k / np > 0 ? k / np : 1;  // pairs per emission block
   int64_t group = (kFirstPassTargetPairs + avg - 1) / avg;
   if (np / group < kFirstPassMinParts) group = np / kFirstPassMinParts;
-  if (group < 1) group = 1;
-  if (avg * group < kFirstPassTargetPairs / 2) return false;
+  if (group < 1 || forced) group = 1;
+  if (!forced && avg * group < kFirstPassTargetPairs / 2) return false;
   const int64_t need = first_bounds_off(np, bits) + 2 * (np + 1);
   if (need > static_cast<int64_t>(radix_scratch_elems(k))) return false;
   first->np = static_cast<int>(np);
   first->bounds = reinterpret_cast<const int64_t*>(scratch + first_bounds_off(np, bits));
   first->group = static_cast<int>(group);
+  first->regenerate = group == 1 && (k >= kRadixLargeMinKeys || forced);
+  first->gen = nullptr;
   return true;
 }
 
@@ -1234,7 +1447,11 @@ int launch_emit_pairs(const uint64_t* part_t, const uint64_t* part_r, const uint
   if (k <= 0 || n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
   const EmitHist eh = emit_hist_of(scratch, first, first_shift, first_bits);
-  if (eh.hist)
+  if (eh.hist && first->gen)
+    hipLaunchKernelGGL((k_emit_packed<true, true, false>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, 0, keys, vals, vo, eh);
+  else if (eh.hist)
     hipLaunchKernelGGL((k_emit_packed<true, true>), dim3(blocks_for(n, kEmitThreads)),
                        dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
                        n, k, gx, 0, keys, vals, vo, eh);
@@ -1255,7 +1472,11 @@ int launch_emit_packed(const uint64_t* part_t, const uint64_t* part_r, const uin
   if (n <= 0) return HRF_OK;
   const VisibleOut vo{vis, part_v, visible, vmax};
   const EmitHist eh = emit_hist_of(scratch, first, first_shift, first_bits);
-  if (eh.hist)
+  if (eh.hist && first->gen)
+    hipLaunchKernelGGL((k_emit_packed<false, true, false>), dim3(blocks_for(n, kEmitThreads)),
+                       dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
+                       n, k, gx, vbits, words, nullptr, vo, eh);
+  else if (eh.hist)
     hipLaunchKernelGGL((k_emit_packed<false, true>), dim3(blocks_for(n, kEmitThreads)),
                        dim3(kEmitThreads), 0, s, part_t, part_r, tiles, order, sorted_flag, rect,
                        n, k, gx, vbits, words, nullptr, vo, eh);

@@ -345,6 +345,44 @@ def test_forward_parity_large_grid_packed(hrf, oracle_mod):
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
+REGEN_SCENES = {
+    # 17689 tiles (15 bits, packed words), few pairs per emission block
+    "grid": dict(name="grid", seed=7, n=6000, W=2112, H=2112, P=1, wl=[515e-9], d=[-2e-3],
+                 layout="uniform", log_scale_mean=-5.0, log_scale_std=0.3),
+    # 1024 tiles (10 bits, packed), several sort tiles of pairs per block
+    "mid": dict(name="mid", seed=9, n=60_000, W=512, H=512, P=3, wl=[639e-9, 532e-9, 473e-9],
+                d=[-1e-3, 0.0, 1e-3], layout="object", log_scale_mean=-4.0, log_scale_std=0.5),
+    # tile and index past 32 bits: separate keys and values
+    "wide": dict(name="wide", seed=6, n=270_000, W=2048, H=2048, P=1, wl=[515e-9], d=[-2e-3],
+                 layout="uniform", log_scale_mean=-6.0, log_scale_std=0.3),
+}
+
+
+@pytest.mark.parametrize("case", list(REGEN_SCENES))
+def test_forward_parity_regenerated_first_pass(hrf, oracle_mod, monkeypatch, case):
+    """The fused emission-scatter (the emission only counts the first sort
+    pass's digits; that pass regenerates each emission block's pairs and
+    scatters them) runs by itself only for sorts of 2^26 pairs or more
+    (config 4); HRF_SORT_REGENERATE=1 takes it at these sizes.  The binning
+    must equal the oracle's bit for bit, packed and wide keys alike."""
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    a = REGEN_SCENES[case]
+    spec = scenes.SceneSpec(a["name"], a["seed"], a["n"], a["W"], a["H"], a["P"], a["wl"],
+                            a["d"], a["layout"], log_scale_mean=a["log_scale_mean"],
+                            log_scale_std=a["log_scale_std"])
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    print(f"regenerated first pass, {case}: N={g.n} K={ref['K']}", flush=True)
+    monkeypatch.setenv("HRF_SORT_REGENERATE", "1")
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 def _plane_list_scene(case):
     import dataclasses
 
