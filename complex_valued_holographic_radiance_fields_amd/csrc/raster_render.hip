@@ -267,7 +267,10 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
   tile_range(p, tile, &r0, &n);
   if (p.ranges_out && plane == 0 && threadIdx.x < 2)
     p.ranges_out[2 * tile + threadIdx.x] = p.ranges[2 * tile + threadIdx.x];
-  const float pxf = static_cast<float>(pxi), pyf = static_cast<float>(pyi);
+  // The pixel's offset from the tile centre (exact: small half-integers).
+  const float xc = static_cast<float>(tx * kTile) + 0.5f * (kTile - 1);
+  const float yc = static_cast<float>(ty * kTile) + 0.5f * (kTile - 1);
+  const float u = static_cast<float>(pxi) - xc, v = static_cast<float>(pyi) - yc;
 
   // Lanes outside the image start done (T = 0 < 1e-4) and write nothing.
   float T = inside ? 1.0f : 0.0f;
@@ -376,9 +379,19 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       const float4 am = src[2];  // (re0, im0, re1, im1)
       const float lw = __builtin_amdgcn_logf(rq[1].z * w);
       if (!exact) {
-        s_rec[pos * NQ] = make_float4(rq[0].x, rq[0].y, kBwdConicScale * rq[0].z,
-                                      kBwdConicScale * (rq[0].w + rq[1].x));
-        s_rec[pos * NQ + 1] = make_float4(kBwdConicScale * rq[1].y, lw, am.x, am.y);
+        // The exponent as a quadratic in the offset from the tile centre
+        // (fwd_member): with M = mean - centre and the scaled conic
+        // (A, B, C) = kc (i00, i01 + i10, i11), c0 = M.x (A M.x + B M.y) +
+        // C M.y^2 + log2(o w) (the exponent at the centre), c1 = -(2 A M.x
+        // + B M.y), c2 = -(B M.x + 2 C M.y), c3..c5 = A, B, C.
+        const float qa = kBwdConicScale * rq[0].z, qb = kBwdConicScale * (rq[0].w + rq[1].x);
+        const float qc = kBwdConicScale * rq[1].y;
+        const float mx = rq[0].x - xc, my = rq[0].y - yc;
+        const float c0 = fmaf(mx, fmaf(qa, mx, qb * my), fmaf(qc * my, my, lw));
+        const float c1 = -fmaf(2.0f * qa, mx, qb * my);
+        const float c2 = -fmaf(qb, mx, (2.0f * qc) * my);
+        s_rec[pos * NQ] = make_float4(c0, c1, c2, qa);
+        s_rec[pos * NQ + 1] = make_float4(qb, qc, am.x, am.y);
         if (NQ > 2) {
           const float4 am2 = rec_quads(C) > 3 ? src[3] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
           s_rec[pos * NQ + (NQ > 2 ? 2 : 0)] = make_float4(am.z, am.w, am2.x, am2.y);
@@ -392,9 +405,9 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       s_pos[pos] = k + 1;
     }
     // Pad the staged batch to a multiple of kUnroll with members no pixel
-    // can use: log2(o w) = -inf (alpha 0, T unchanged), in the same slot of
-    // both layouts (the exact layout's zero conic gives s = 0, which passes
-    // the power test).
+    // can use: an exponent of -inf (alpha 0, T unchanged); in the exact
+    // layout log2(o w) = -inf with a zero conic (s = 0, which passes the
+    // power test).
     listed += scnt;
     const int cnt_pad = (cnt + kUnroll - 1) / kUnroll * kUnroll;
     if (static_cast<int>(threadIdx.x) >= cnt && static_cast<int>(threadIdx.x) < cnt_pad) {
@@ -402,13 +415,19 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       const int q0 = static_cast<int>(threadIdx.x) * nq;
       // Materialised here: hoisted out of the batch loop, these constants
       // would not fit the 64 registers of 8 waves per SIMD.
-      float far = 1e6f, ninf = -__builtin_inff();
-      asm volatile("" : "+v"(far), "+v"(ninf));
-      s_rec[q0] = make_float4(far, far, 0.0f, 0.0f);
-      s_rec[q0 + 1] = make_float4(0.0f, ninf, 0.0f, 0.0f);
+      float far = 1e6f, ninf = -__builtin_inff(), zero = 0.0f;
+      asm volatile("" : "+v"(far), "+v"(ninf), "+v"(zero));
+      if (!exact) {
+        // c0 = -inf, the other coefficients 0: pw = -inf at every pixel
+        s_rec[q0] = make_float4(ninf, zero, zero, zero);
+        s_rec[q0 + 1] = make_float4(zero, zero, zero, zero);
+      } else {
+        s_rec[q0] = make_float4(far, far, zero, zero);
+        s_rec[q0 + 1] = make_float4(zero, ninf, zero, zero);
+      }
 #pragma unroll
       for (int q = 2; q < NQX; ++q)
-        if (q < nq) s_rec[q0 + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (q < nq) s_rec[q0 + q] = make_float4(zero, zero, zero, zero);
     }
     __syncthreads();
     // Branch-free per member; a wave leaves the batch once all its lanes
@@ -422,8 +441,8 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
 #pragma unroll
         for (int jj = 0; jj < kUnroll; ++jj) {
           const int j = j0 + jj;
-          fwd_member<C>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], pxf, pyf, T,
-                        acc, evaluated);
+          fwd_member<C>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], u, v, T, acc,
+                        evaluated);
         }
       }
       // A lane still running composited every member of the batch (no
@@ -441,7 +460,8 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
         for (int jj = 0; jj < kUnroll; ++jj) {
           const int j = j0 + jj;
           fwd_member_ref<C>(s_rec[j * NQX], s_rec[j * NQX + 1], s_rec[j * NQX + 2],
-                            s_rec[j * NQX + (NQX - 1)], pxf, pyf, T, acc, lastj, j, j < cnt);
+                            s_rec[j * NQX + (NQX - 1)], u + xc, v + yc, T, acc, lastj, j,
+                            j < cnt);
         }
       }
     }

@@ -10,26 +10,28 @@ namespace hrf {
 
 // Forward member evaluation (fast loop: staged conics that cannot round to
 // a positive exponent, so the reference's "power > 0: skip" test is not
-// evaluated).  Exponent in base 2 with log2(o w) folded in:
-// pw = dx (A dx + B dy) + (C dy) dy + log2(o w), so alpha = min(0.99,
-// exp2(pw)) needs no multiply by the opacity; at the mean (dx = dy = 0) pw
-// is log2(o w) exactly.  A lane is done exactly when T < 1e-4 (T changes
-// only on composited members, and a lane stops at the member that takes T
-// below 1e-4; lanes outside the image start at T = 0), so no separate flag
-// is carried.  Branch-free: lanes that are done take alpha = 0, which leaves
-// T and the field exactly unchanged.  `evaluated` counts the members
-// evaluated while the lane was live (one add of the live mask, no index
-// select): a lane composites every member until the one that ends it, so
-// the count minus one is that member's index.  Staged record quads:
-// a = (mx, my, kc*i00, kc*(i01 + i10)), b = (kc*i11, log2(o w), re0, im0),
-// c = (re1, im1, re2, im2) (C >= 2), kc = -log2(e)/2.
+// evaluated).  The exponent is in base 2 with log2(o w) folded in, as a
+// quadratic in the pixel's offset (u, v) from the tile centre:
+// pw = c0 + u (c1 + c3 u + c4 v) + v (c2 + c5 v), five fused multiply-adds
+// (the staging forms c0..c5 from the mean, the conic scaled by
+// kc = -log2(e)/2 and log2(o w); |u|, |v| <= 7.5, so the terms stay within
+// a few times the exponent's own size), and alpha = min(0.99, exp2(pw)).
+// A lane is done exactly when T < 1e-4 (T changes only on composited
+// members, and a lane stops at the member that takes T below 1e-4; lanes
+// outside the image start at T = 0), so no separate flag is carried.
+// Branch-free: lanes that are done take alpha = 0, which leaves T and the
+// field exactly unchanged.  `evaluated` counts the members evaluated while
+// the lane was live (one add of the live mask, no index select): a lane
+// composites every member until the one that ends it, so the count minus
+// one is that member's index.  Staged record quads: a = (c0, c1, c2, c3),
+// b = (c4, c5, re0, im0), c = (re1, im1, re2, im2) (C >= 2).
 template <int C>
 __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
-                                           float pxf, float pyf, float& T,
+                                           float u, float v, float& T,
                                            float (&acc)[2 * C], int& evaluated) {
-  const float dx = a.x - pxf, dy = a.y - pyf;
-  const float t = fmaf(a.z, dx, a.w * dy);
-  const float pw = fmaf(dx, t, fmaf(b.x * dy, dy, b.y));
+  const float t1 = fmaf(b.x, v, fmaf(a.w, u, a.y));
+  const float t2 = fmaf(b.y, v, a.z);
+  const float pw = fmaf(v, t2, fmaf(u, t1, a.x));
   const bool live = !(T < kTermT);
   const float alpha = live ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
   const float sT = alpha * T;

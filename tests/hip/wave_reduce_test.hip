@@ -106,12 +106,14 @@ __global__ __launch_bounds__(256, 8) void k_calib_fwdloop(float* out, int iters)
   const int tid = threadIdx.x;
   {
     const float fi = static_cast<float>(tid);
-    s_rec[tid * 3] = make_float4(4.0f + 0.03f * fi, 6.0f - 0.02f * fi, -0.02f, 0.001f);
-    s_rec[tid * 3 + 1] = make_float4(-0.03f, -20.0f, 0.5f, 0.25f);
+    // (c0, c1, c2, c3), (c4, c5, re0, im0), (re1, im1, re2, im2): an
+    // exponent near -20 over the tile
+    s_rec[tid * 3] = make_float4(-20.0f + 0.001f * fi, 0.01f, -0.01f, -0.002f);
+    s_rec[tid * 3 + 1] = make_float4(0.001f, -0.003f, 0.5f, 0.25f);
     s_rec[tid * 3 + 2] = make_float4(0.125f, -0.5f, 0.75f, 0.3f);
   }
   __syncthreads();
-  const float pxf = static_cast<float>(tid & 15), pyf = static_cast<float>(tid >> 4);
+  const float pxf = static_cast<float>(tid & 15) - 7.5f, pyf = static_cast<float>(tid >> 4) - 7.5f;
   float T = 1.0f, acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int evaluated = 0;
   for (int it = 0; it < iters; ++it) {
