@@ -798,7 +798,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
         }
         if (within) {
           float sn, cs;
-          sincos_big(d * kz[u], &sn, &cs);
+          sincos_big_ff(d * kz[u], &sn, &cs);
           const float2 x = lds[pad<PlanCol<N>::template kPad<B>>(q)];
           acc[u].x += x.x * cs - x.y * sn;
           acc[u].y += x.x * sn + x.y * cs;
@@ -906,7 +906,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
           }
           if (within) {
             float sn, cs;
-            sincos_big(nd * kz[u], &sn, &cs);
+            sincos_big_ff(nd * kz[u], &sn, &cs);
             r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
           }
         }
