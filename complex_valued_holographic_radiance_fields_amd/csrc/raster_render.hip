@@ -380,16 +380,12 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
       const float lw = __builtin_amdgcn_logf(rq[1].z * w);
       if (!exact) {
         // The exponent as a quadratic in the offset from the tile centre
-        // (fwd_member): with M = mean - centre and the scaled conic
-        // (A, B, C) = kc (i00, i01 + i10, i11), c0 = M.x (A M.x + B M.y) +
-        // C M.y^2 + log2(o w) (the exponent at the centre), c1 = -(2 A M.x
-        // + B M.y), c2 = -(B M.x + 2 C M.y), c3..c5 = A, B, C.
+        // (fwd_member, quad_coeffs) for the scaled conic
+        // (A, B, C) = kc (i00, i01 + i10, i11); c3..c5 = A, B, C.
         const float qa = kBwdConicScale * rq[0].z, qb = kBwdConicScale * (rq[0].w + rq[1].x);
         const float qc = kBwdConicScale * rq[1].y;
-        const float mx = rq[0].x - xc, my = rq[0].y - yc;
-        const float c0 = fmaf(mx, fmaf(qa, mx, qb * my), fmaf(qc * my, my, lw));
-        const float c1 = -fmaf(2.0f * qa, mx, qb * my);
-        const float c2 = -fmaf(qb, mx, (2.0f * qc) * my);
+        float c0, c1, c2;
+        quad_coeffs(rq[0].x, rq[0].y, qa, qb, qc, lw, xc, yc, &c0, &c1, &c2);
         s_rec[pos * NQ] = make_float4(c0, c1, c2, qa);
         s_rec[pos * NQ + 1] = make_float4(qb, qc, am.x, am.y);
         if (NQ > 2) {

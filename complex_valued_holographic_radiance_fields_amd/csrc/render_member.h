@@ -25,13 +25,33 @@ namespace hrf {
 // composites every member until the one that ends it, so the count minus
 // one is that member's index.  Staged record quads: a = (c0, c1, c2, c3),
 // b = (c4, c5, re0, im0), c = (re1, im1, re2, im2) (C >= 2).
+// The quadratic's coefficients for a member with mean (mx, my), scaled
+// conic (qa, qb, qc) (exponent qa dx^2 + qb dx dy + qc dy^2 + lw in the
+// offsets dx, dy from the mean) about the tile centre (xc, yc): with
+// M = mean - centre, c0 = M.x (qa M.x + qb M.y) + qc M.y^2 + lw (the
+// exponent at the centre), c1 = -(2 qa M.x + qb M.y), c2 = -(qb M.x + 2 qc
+// M.y); the exponent at offset (u, v) from the centre is then
+// c0 + u (c1 + qa u + qb v) + v (c2 + qc v) (quad_exponent).
+__device__ __forceinline__ void quad_coeffs(float mx, float my, float qa, float qb, float qc,
+                                            float lw, float xc, float yc, float* c0, float* c1,
+                                            float* c2) {
+  const float ax = mx - xc, ay = my - yc;
+  *c0 = fmaf(ax, fmaf(qa, ax, qb * ay), fmaf(qc * ay, ay, lw));
+  *c1 = -fmaf(2.0f * qa, ax, qb * ay);
+  *c2 = -fmaf(qb, ax, (2.0f * qc) * ay);
+}
+__device__ __forceinline__ float quad_exponent(float c0, float c1, float c2, float qa, float qb,
+                                               float qc, float u, float v) {
+  const float t1 = fmaf(qb, v, fmaf(qa, u, c1));
+  const float t2 = fmaf(qc, v, c2);
+  return fmaf(v, t2, fmaf(u, t1, c0));
+}
+
 template <int C>
 __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
                                            float u, float v, float& T,
                                            float (&acc)[2 * C], int& evaluated) {
-  const float t1 = fmaf(b.x, v, fmaf(a.w, u, a.y));
-  const float t2 = fmaf(b.y, v, a.z);
-  const float pw = fmaf(v, t2, fmaf(u, t1, a.x));
+  const float pw = quad_exponent(a.x, a.y, a.z, a.w, b.x, b.y, u, v);
   const bool live = !(T < kTermT);
   const float alpha = live ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
   const float sT = alpha * T;
