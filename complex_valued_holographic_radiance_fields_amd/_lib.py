@@ -86,6 +86,8 @@ SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "hrf_raster_plane_lists_size": (_sz, [_i64, _i32, _i32, _i32]),
     "hrf_raster_backward_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "hrf_raster_backward_prepare": (ctypes.c_int, [
+        _P(HrfGaussians), _P(HrfCamera), _i64, _vp, _sz, _vp, _sz, _vp]),
     "hrf_raster_backward": (ctypes.c_int, [
         _P(HrfGaussians), _P(HrfCamera), _vp, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp, _sz,
         _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

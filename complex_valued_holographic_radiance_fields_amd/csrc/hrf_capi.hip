@@ -156,6 +156,23 @@ int prepared_check(const void* ws, int64_t n, int64_t k, int64_t v) {
 
 namespace {
 
+// Backward workspaces whose prologue (accumulator clear + block order)
+// hrf_raster_backward_prepare has queued: the workspace, what it was
+// prepared for, and an event recorded after the prologue on the preparing
+// stream.  hrf_raster_backward on a matching record waits for the event
+// instead of running the prologue, and consumes the record.
+struct BwdPrepared {
+  const void* ws;
+  int64_t n, num_pairs;
+  int C, P;
+  const void* plane_lists;
+  hipEvent_t done;
+  bool armed;
+};
+constexpr size_t kMaxBwdPrepared = 64;
+std::mutex g_bprep_mu;
+std::vector<BwdPrepared> g_bprep;
+
 // ------------------------------------------------------------ validation --
 int check_raster_args(const hrf_gaussians* g, const hrf_camera* cam) {
   if (!g || !cam) {
@@ -687,6 +704,63 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   return HRF_OK;
 }
 
+int hrf_raster_backward_prepare(const hrf_gaussians* g, const hrf_camera* cam,
+                                int64_t num_pairs, void* ws, size_t ws_bytes, void* plane_lists,
+                                size_t plane_lists_bytes, void* stream) {
+  HRF_TRY(check_raster_args(g, cam));
+  const int64_t n = g->n;
+  if (n == 0) return HRF_OK;
+  HRF_TRY(check_pair_count(num_pairs));
+  HRF_TRY(check_ws(ws, ws_bytes, hrf_raster_backward_workspace_size(n, g->channels, g->planes),
+                   "backward"));
+  const bool use_sub = plane_lists && num_pairs > 0;
+  if (use_sub && n >= (int64_t{1} << 28)) {
+    set_error("plane member lists need fewer than 2^28 Gaussians (got %lld)",
+              static_cast<long long>(n));
+    return HRF_ERR_INVALID;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Frame f = frame_of(cam);
+  Carver cv(ws);
+  BwdWs w = carve_bwd(cv, n, g->channels, g->planes);
+  SubWs sw{};
+  if (use_sub) {
+    HRF_TRY(check_ws(plane_lists, plane_lists_bytes,
+                     hrf_raster_plane_lists_size(num_pairs, cam->width, cam->height, g->planes),
+                     "plane lists"));
+    Carver cs(plane_lists);
+    sw = carve_sub(cs, num_pairs, f.ntiles, g->planes);
+  }
+  std::lock_guard<std::mutex> lk(g_bprep_mu);
+  BwdPrepared* rec = nullptr;
+  for (auto& e : g_bprep)
+    if (e.ws == ws) rec = &e;
+  if (!rec) {
+    if (g_bprep.size() >= kMaxBwdPrepared) {
+      set_error("backward prepare: more than %d workspaces prepared at once",
+                static_cast<int>(kMaxBwdPrepared));
+      return HRF_ERR_INVALID;
+    }
+    hipEvent_t ev = nullptr;
+    HRF_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    g_bprep.push_back(BwdPrepared{ws, 0, 0, 0, 0, nullptr, ev, false});
+    rec = &g_bprep.back();
+  }
+  {
+    HRF_STAGE("bwd_prologue", s);
+    HRF_TRY(launch_bwd_prologue(w.acc, n * acc_stride(g->channels, g->planes), sw.counts,
+                                use_sub ? f.ntiles * g->planes : 0, sw.order, s));
+  }
+  HRF_HIP(hipEventRecord(rec->done, s));
+  rec->n = n;
+  rec->num_pairs = num_pairs;
+  rec->C = g->channels;
+  rec->P = g->planes;
+  rec->plane_lists = use_sub ? plane_lists : nullptr;
+  rec->armed = true;
+  return HRF_OK;
+}
+
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const void* grad_field,
                         const float* final_T, const int32_t* n_contrib,
                         const int32_t* point_list, const int32_t* ranges, int64_t num_pairs,
@@ -758,8 +832,25 @@ int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam, const voi
       pp.vis = w.vis;
       HRF_TRY(launch_project(pp, s));
     }
-    HRF_TRY(launch_bwd_prologue(w.acc, n * acc_stride(g->channels, g->planes), sw.counts,
-                                use_sub ? f.ntiles * g->planes : 0, sw.order, s));
+    // A prologue that hrf_raster_backward_prepare queued for this same
+    // workspace and configuration: wait for it instead.
+    bool prepared = false;
+    {
+      std::lock_guard<std::mutex> lk(g_bprep_mu);
+      for (auto& e : g_bprep) {
+        if (e.ws != ws || !e.armed) continue;
+        e.armed = false;  // consumed (or stale): this call decides
+        if (e.n == n && e.num_pairs == num_pairs && e.C == g->channels && e.P == g->planes &&
+            e.plane_lists == (use_sub ? plane_lists : nullptr)) {
+          HRF_HIP(hipStreamWaitEvent(s, e.done, 0));
+          prepared = true;
+        }
+        break;
+      }
+    }
+    if (!prepared)
+      HRF_TRY(launch_bwd_prologue(w.acc, n * acc_stride(g->channels, g->planes), sw.counts,
+                                  use_sub ? f.ntiles * g->planes : 0, sw.order, s));
   }
 
   if (num_pairs > 0) {

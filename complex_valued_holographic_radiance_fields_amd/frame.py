@@ -27,6 +27,7 @@ class Frame:
         self.fwd_state = None
         self.fields = None
         self.geometry = None
+        self._side = None  # stream of the backward prologue
 
     def forward(self):
         t = self.t
@@ -43,10 +44,21 @@ class Frame:
 
     def backward(self, grad_holo):
         t = self.t
+        final_T, n_contrib, point_list, ranges, _vis = self.fwd_state
+        # The rasterizer backward's prologue (accumulator clear, block order)
+        # depends only on the forward: it runs on a second stream beside the
+        # propagation adjoint, and the backward waits for it.
+        main = torch.cuda.current_stream(grad_holo.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=grad_holo.device)
+        self._side.wait_stream(main)
+        rasterizer.backward_prepare(t["cam_means"], t["z"], t["quats"], t["scales"],
+                                    t["colours"], t["phase"], t["opac"], t["pprobs"], self.fx,
+                                    self.fy, self.px, self.py, t["view"], self.img, point_list,
+                                    NEAR, FAR, geometry=self.geometry, stream=self._side)
         gf = propagation.multiplane_adjoint(grad_holo, (self.spec.height, self.spec.width),
                                             self.spec.wavelengths, PITCH, self.prop_dist,
                                             (self.S, self.S), float(self.S))
-        final_T, n_contrib, point_list, ranges, _vis = self.fwd_state
         return rasterizer.backward(gf, t["cam_means"], t["z"], t["quats"], t["scales"],
                                    t["colours"], t["phase"], t["opac"], t["pprobs"], self.fx,
                                    self.fy, self.px, self.py, t["view"], self.img, (16, 16),

@@ -165,6 +165,35 @@ def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plan
     return field, (final_T, n_contrib, point_list, ranges, visible)
 
 
+def backward_prepare(cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
+                     plane_probs, fx, fy, px, py, view_matrix, img_size, point_list,
+                     near_plane=1.0, far_plane=1000.0,
+                     geometry: ForwardGeometry | None = None, stream=None):
+    """Queues the backward's prologue (accumulator clear and block order) on
+    `stream` (a torch stream; default the current one) for the next
+    backward(...) of these inputs on the current stream, which then waits
+    for it instead of running it: the prologue can run beside the
+    propagation adjoint.  The caller orders `stream` after the forward (and
+    after the previous backward on this device and thread)."""
+    inp = _Inputs(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plane_probs,
+                  fx, fy, px, py, view_matrix, img_size, near_plane, far_plane)
+    plane_lists = geometry.plane_lists if isinstance(geometry, ForwardGeometry) else None
+    lib = _lib.load()
+    dev = inp.device
+    n, C, P = inp.n, inp.C, inp.P
+    if n == 0:
+        return
+    with torch.cuda.device(dev):
+        # the workspace the backward on the current stream will use
+        wbytes = lib.hrf_raster_backward_workspace_size(n, C, P)
+        ws = _lib.workspace("raster_bwd", dev, _lib.stream_ptr(dev), wbytes)
+        s = stream.cuda_stream if stream is not None else _lib.stream_ptr(dev)
+        _lib.check(lib.hrf_raster_backward_prepare(
+            ctypes.byref(inp.g), ctypes.byref(inp.c), int(point_list.numel()), ws.data_ptr(),
+            wbytes, _lib.ptr(plane_lists),
+            int(plane_lists.numel()) if plane_lists is not None else 0, s))
+
+
 def backward(grad_output, cam_means_3D, z_vals, quats, scales, colours, phase, opacities,
              plane_probs, fx, fy, px, py, view_matrix, img_size, tile_size, final_Ts,
              n_contrib, point_list, ranges, near_plane=1.0, far_plane=1000.0,

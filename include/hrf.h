@@ -140,6 +140,19 @@ size_t hrf_raster_backward_workspace_size(int64_t n, int32_t channels, int32_t p
  * read).
  * Replaces Rasterizer::backward (rasterizer_splat.cu:551-684),
  * backward_splat.cu:78-417 and backward.cu. */
+/* Queues the backward's prologue (clearing the per-Gaussian accumulators in
+ * ws and forming the block order from the plane lists' counts) on `stream`
+ * ahead of the backward, so that it can run beside other work (the
+ * propagation adjoint) on another stream.  The next hrf_raster_backward on
+ * the same ws, N, channels, planes, num_pairs and plane_lists waits for it
+ * (an event recorded after it) instead of running it; with anything else
+ * that call runs its own prologue.  The caller orders `stream` after the
+ * forward that wrote plane_lists and after any earlier use of ws.  No
+ * counterpart in the reference (its backward clears inside
+ * Rasterizer::backward, rasterizer_splat.cu:551-684). */
+int hrf_raster_backward_prepare(const hrf_gaussians* g, const hrf_camera* cam,
+                                int64_t num_pairs, void* ws, size_t ws_bytes,
+                                void* plane_lists, size_t plane_lists_bytes, void* stream);
 int hrf_raster_backward(const hrf_gaussians* g, const hrf_camera* cam,
                         const void* grad_field, const float* final_T,
                         const int32_t* n_contrib, const int32_t* point_list,
