@@ -508,7 +508,8 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
   constexpr int NQ = bwd_quads(C);
   constexpr int RS = rec_stride(C);
   constexpr int NV = 6 + 2 * C;  // partial sums per member
-  static_assert(NV <= 16, "one 16-lane row holds a member's sums");
+  constexpr int NVP = (NV + 3) / 4 * 4;  // padded for row_sum16
+  static_assert(NVP <= 16, "one 16-lane row holds a member's sums");
   constexpr int G = kBwdChunk;
   // Slot kBlock of s_rec is a dummy member that no pixel can use (list
   // position beyond every n_contrib): the per-wave lists are padded with it
@@ -808,8 +809,9 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
         // Phase 2, lane (member mm = lane / 16, part sp = lane % 16): the
         // member's NV partial sums over 4 pixels of the quadrant (column
         // sp % 8, rows sp / 8 + 2j), in registers; then the 16 lanes of the
-        // member's row reduce them with one transpose (lane sp ends with sum
-        // sp) and each lane with a sum adds it to the member's accumulator.
+        // member's row reduce them (row_sum16: each lane ends with NVP/4 of
+        // the sums) and each lane with a sum to add adds it to the member's
+        // accumulator.
         const int mm = lane >> 4, sp = lane & 15;
         const int slot2 = s_wl[wave][hi - mm];
         const float4 a2 = s_rec[slot2 * NQ];
@@ -819,41 +821,35 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
         const float di2 = bwd_det_inv<C>(c02, c12);
         const int col = sp & 7;
         const float dx = a2.x - (qx0 + static_cast<float>(col));
-        // exact batches: the reference's conic-to-covariance map per pixel
-        // (backward_splat.cu:285-291) with the unscaled conic: xx = cxx^2 U
-        // + cxy^2 W, xy = cxx cxy U - V / det + cxy czz W, yy = cxy^2 U +
-        // czz^2 W for the pixel's second moments (U, V, W) = Q (dx^2, dx dy,
-        // dy^2), all terms of one sign, so no sum is mapped afterwards (for
-        // a nearly singular conic the map would amplify the sums' rounding
-        // by ~1/(1 - r^2)).
-        const float m_xx = a2.z * a2.z, m_yy = a2.w * a2.w, m_xy = a2.z * a2.w;
-        const float m_yz = a2.w * b2.x, m_zz = b2.x * b2.x;
-        float v[16];
+        float v[NVP];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+        for (int i = 0; i < NVP; ++i) v[i] = 0.0f;
+        float Qj[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int row = (sp >> 3) + 2 * j;
           const int pp = row * 8 + col;
-          const float dy = a2.y - (qy0 + static_cast<float>(row));
           const float2 qd = s_qd[wave][mm][pp];
           const float Q = qd.x, dcol = qd.y;
-          const float Qdx = Q * dx, Qdy = Q * dy;
+          Qj[j] = Q;
           if (kRef) {
+            // exact batches: the reference's conic-to-covariance map per
+            // pixel (backward_splat.cu:285-291) with the unscaled conic: xx =
+            // cxx^2 U + cxy^2 W, xy = cxx cxy U - V / det + cxy czz W, yy =
+            // cxy^2 U + czz^2 W for the pixel's second moments (U, V, W) =
+            // Q (dx^2, dx dy, dy^2), all terms of one sign, so no sum is
+            // mapped afterwards (for a nearly singular conic the map would
+            // amplify the sums' rounding by ~1/(1 - r^2)).
+            const float dy = a2.y - (qy0 + static_cast<float>(row));
+            const float Qdx = Q * dx, Qdy = Q * dy;
             const float u = Qdx * dx, vv = Qdx * dy, w = Qdy * dy;
             v[0] = fmaf(Q, fmaf(a2.z, dx, a2.w * dy), v[0]);
             v[1] = fmaf(Q, fmaf(a2.w, dx, b2.x * dy), v[1]);
-            v[2] = fmaf(m_xx, u, fmaf(m_yy, w, v[2]));
-            v[3] = fmaf(m_xy, u, fmaf(-di2, vv, fmaf(m_yz, w, v[3])));
-            v[4] = fmaf(m_yy, u, fmaf(m_zz, w, v[4]));
-          } else {
-            v[0] += Qdx;
-            v[1] += Qdy;
-            v[2] = fmaf(Qdx, dx, v[2]);
-            v[3] = fmaf(Qdx, dy, v[3]);
-            v[4] = fmaf(Qdy, dy, v[4]);
+            v[2] = fmaf(a2.z * a2.z, u, fmaf(a2.w * a2.w, w, v[2]));
+            v[3] = fmaf(a2.z * a2.w, u, fmaf(-di2, vv, fmaf(a2.w * b2.x, w, v[3])));
+            v[4] = fmaf(a2.w * a2.w, u, fmaf(b2.x * b2.x, w, v[4]));
+            v[5] += Q;
           }
-          v[5] += Q;
 #pragma unroll
           for (int c = 0; c < C; ++c) {
             const float2 gv = s_gp[wave][pp][c];
@@ -862,48 +858,58 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
           }
         }
         if (!kRef) {
+          // The geometric sums from three moments of Q over the lane's rows:
+          // with dyc = dy at the rows' centre, row j has dy = dyc - e_j, e_j
+          // = 2j - 3 (exact small integers), so sum Q dy = dyc B0 - B1 and
+          // sum Q dy^2 = dyc (dyc B0 - 2 B1) + B2 for B_k = sum e_j^k Q_j;
+          // dx is the lane's own.
+          const float dyc = a2.y - (qy0 + static_cast<float>((sp >> 3) + 3));
+          const float s03 = Qj[0] + Qj[3], s12 = Qj[1] + Qj[2];
+          const float d03 = Qj[3] - Qj[0], d12 = Qj[2] - Qj[1];
+          const float B0 = s03 + s12;
+          const float B1 = fmaf(3.0f, d03, d12);
+          const float B2 = fmaf(9.0f, s03, s12);
+          const float m = dyc * B0;
+          const float sy = m - B1;                                // sum Q dy
+          const float syy = fmaf(dyc, fmaf(-2.0f, B1, m), B2);  // sum Q dy^2
+          const float sx = dx * B0;                               // sum Q dx
           // The mean and covariance maps on the lane's sums (linear in them;
           // the conic is in the fast loop's domain, so the maps are well
           // conditioned).  Staged conic: kc cxx, 2 kc cxy, kc czz.
-          const float sx = v[0], sy = v[1];
           const float kxy = 0.5f * a2.w;
           v[0] = fmaf(a2.z, sx, kxy * sy);  // kc (cxx sum Q dx + cxy sum Q dy)
           v[1] = fmaf(kxy, sx, b2.x * sy);  // kc (cxy sum Q dx + czz sum Q dy)
           const float cxx = a2.z * (1.0f / kBwdConicScale);
           const float cxy = a2.w * (0.5f / kBwdConicScale);
           const float czz = b2.x * (1.0f / kBwdConicScale);
-          const float U = v[2], V = v[3], Wm = v[4];
+          const float U = dx * sx, V = dx * sy, Wm = syy;
           v[2] = fmaf(cxx * cxx, U, (cxy * cxy) * Wm);
           v[3] = fmaf(cxx * cxy, U, fmaf(-di2, V, (cxy * czz) * Wm));
           v[4] = fmaf(cxy * cxy, U, (czz * czz) * Wm);
+          v[5] = B0;
         }
-        const float tv = transpose_reduce16(v);
-        if (sp < NV && slot2 != kDummy && tv != 0.0f) {
-          // Accumulator slots: 0-1 the mean gradient (times W/2, H/2), 2-4
-          // the cov2D gradient, 5+c / 5+C+c the colour sums, 5+2C+plane the
-          // plane term.  The sums carry o w (Q = o w dL/dG): the mean and
-          // covariance terms need exactly that factor, the o w term (sum G
-          // dL/dalpha) its removal.
-          int aslot;
-          float scale;
-          if (sp == 0) {
-            aslot = 0;
-            scale = kRef ? -half_w : -half_w / kBwdConicScale;
-          } else if (sp == 1) {
-            aslot = 1;
-            scale = kRef ? -half_h : -half_h / kBwdConicScale;
-          } else if (sp < 5) {
-            aslot = sp;
-            scale = -0.5f;
-          } else if (sp == 5) {
-            aslot = 5 + 2 * C + plane;
-            scale = __builtin_amdgcn_rcpf(b2.w);
-          } else {
-            aslot = sp - 1;  // A_c at 5+c (sp = 6+c), B_c at 5+C+c (sp = 6+C+c)
-            scale = 1.0f;
-          }
+        float xs[NVP / 4];
+        row_sum16<NVP>(v, xs);
+        // This lane's sum: value vi of the member (row_sum16's layout).
+        const int q = sp & 3;
+        const int vi = (NVP / 2) * ((sp >> 3) & 1) + (NVP / 4) * ((sp >> 2) & 1) + q;
+        float tv = xs[0];
+#pragma unroll
+        for (int i = 1; i < NVP / 4; ++i) tv = (q == i) ? xs[i] : tv;
+        // Accumulator slots: 0-1 the mean gradient (times W/2, H/2), 2-4 the
+        // cov2D gradient, 5+c / 5+C+c the colour sums, 5+2C+plane the plane
+        // term.  The sums carry o w (Q = o w dL/dG): the mean and covariance
+        // terms need exactly that factor, the o w term (sum G dL/dalpha) its
+        // removal.  Slot and scale are fixed per lane except that removal
+        // (selects, so that they stay out of the loop).
+        const int aslot = vi == 5 ? 5 + 2 * C + plane : (vi < 5 ? vi : vi - 1);
+        const float scale_mean = vi == 0 ? half_w : half_h;
+        const float scale_l =
+            vi < 2 ? (kRef ? -scale_mean : scale_mean * (-1.0f / kBwdConicScale))
+                   : (vi < 5 ? -0.5f : 1.0f);
+        const float scale = vi == 5 ? __builtin_amdgcn_rcpf(b2.w) : scale_l;
+        if (q < NVP / 4 && vi < NV && slot2 != kDummy && tv != 0.0f)
           unsafeAtomicAdd(p.acc + static_cast<int64_t>(s_g[slot2]) * AS + aslot, tv * scale);
-        }
         // The next chunk's phase-1 writes after this chunk's reads.
         __builtin_amdgcn_wave_barrier();
       }

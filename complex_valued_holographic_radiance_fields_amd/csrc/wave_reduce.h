@@ -67,17 +67,38 @@ __device__ __forceinline__ float transpose_reduce64(float (&v)[64]) {
   return v[0];
 }
 
-// transpose_reduce16: within each row of 16 lanes, every lane holds 16
-// values v[0..15]; afterwards lane L holds the sum over the 16 lanes of its
-// row of v[L & 15].  The in-row steps of transpose_reduce64 (lane xor 15, 7,
-// 2, 1 by DPP row_mirror, row_half_mirror and quad_perm).
-__device__ __forceinline__ float transpose_reduce16(float (&v)[16]) {
+// row_sum16: within each row of 16 lanes, every lane holds NVP values
+// v[0..NVP) (NVP a multiple of 4, at most 16); afterwards each lane L holds
+// in x[0..NVP/4) the sums over the 16 lanes of its row of values
+// (NVP/2) b3 + (NVP/4) b2 + i, with b3, b2 bits 3 and 2 of L: two butterfly
+// steps that halve the values (lane xor 15 by DPP row_mirror, lane xor 7 by
+// row_half_mirror), then plain DPP adds over the remaining partners (lane
+// xor 2, xor 1).  The four lanes of a quad end with the same sums.  Cost
+// 3 NVP/2 + 3 NVP/4 + NVP/2 instructions (33 at NVP = 12), against 45 for a
+// full 16-value transpose.
+template <int NVP>
+__device__ __forceinline__ void row_sum16(const float (&v)[NVP], float (&x)[NVP / 4]) {
+  static_assert(NVP % 4 == 0 && NVP <= 16, "row_sum16 takes 4, 8, 12 or 16 values");
+  constexpr int H = NVP / 2, Q = NVP / 4;
   const int lane = __lane_id();
-  butterfly_dpp<0x140, 8>(v, (lane >> 3) & 1);  // row_mirror: lane xor 15
-  butterfly_dpp<0x141, 4>(v, (lane >> 2) & 1);  // row_half_mirror: lane xor 7
-  butterfly_dpp<0x4E, 2>(v, (lane >> 1) & 1);   // quad_perm [2,3,0,1]: lane xor 2
-  butterfly_dpp<0xB1, 1>(v, lane & 1);          // quad_perm [1,0,3,2]: lane xor 1
-  return v[0];
+  const bool b3 = (lane >> 3) & 1, b2 = (lane >> 2) & 1;
+  float w[H];
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float send = b3 ? v[i] : v[i + H];
+    const float keep = b3 ? v[i + H] : v[i];
+    w[i] = keep + dpp_f<0x140>(send);  // row_mirror: lane xor 15
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) {
+    const float send = b2 ? w[i] : w[i + Q];
+    const float keep = b2 ? w[i + Q] : w[i];
+    x[i] = keep + dpp_f<0x141>(send);  // row_half_mirror: lane xor 7
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i) x[i] += dpp_f<0x4E>(x[i]);  // quad_perm [2,3,0,1]
+#pragma unroll
+  for (int i = 0; i < Q; ++i) x[i] += dpp_f<0xB1>(x[i]);  // quad_perm [1,0,3,2]
 }
 
 }  // namespace hrf

@@ -1,5 +1,5 @@
 // Test-only kernels exercising csrc/wave_reduce.h on one wave64 (in bounds:
-// exactly 64 threads, 64x64 inputs) and csrc/fast_trig.h (n elements, bounds
+// exactly 64 threads, 64x64 or 64x12 inputs) and csrc/fast_trig.h (n elements, bounds
 // checked), and calibration kernels of known VALU work for the hardware
 // counters.  Built into tests/hip/libwave_test.so.
 #include <hip/hip_runtime.h>
@@ -14,6 +14,17 @@ __global__ __launch_bounds__(64) void k_transpose(const float* in, float* out) {
 #pragma unroll
   for (int i = 0; i < 64; ++i) v[i] = in[threadIdx.x * 64 + i];
   out[threadIdx.x] = hrf::transpose_reduce64(v);
+}
+// row_sum16 over 12 values per lane: lane L writes its 3 sums to
+// out[L * 3 .. L * 3 + 3).
+__global__ __launch_bounds__(64) void k_row_sum16(const float* in, float* out) {
+  float v[12];
+#pragma unroll
+  for (int i = 0; i < 12; ++i) v[i] = in[threadIdx.x * 12 + i];
+  float x[3];
+  hrf::row_sum16<12>(v, x);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) out[threadIdx.x * 3 + i] = x[i];
 }
 __global__ __launch_bounds__(64) void k_sum(const float* in, float* out) {
   out[threadIdx.x] = hrf::wave_sum_to_lane63(in[threadIdx.x]);
@@ -173,6 +184,11 @@ extern "C" int trig_test_sincos(const float* x, float* s, float* c, int n) {
 
 extern "C" int wave_test_transpose(const float* in, float* out) {
   hipLaunchKernelGGL(k_transpose, dim3(1), dim3(64), 0, nullptr, in, out);
+  return static_cast<int>(hipDeviceSynchronize());
+}
+
+extern "C" int wave_test_row_sum16(const float* in, float* out) {
+  hipLaunchKernelGGL(k_row_sum16, dim3(1), dim3(64), 0, nullptr, in, out);
   return static_cast<int>(hipDeviceSynchronize());
 }
 

@@ -15,7 +15,7 @@ LIB = os.path.join(REPO, "tests", "hip", "libwave_test.so")
 @pytest.fixture(scope="module")
 def wlib(hrf):
     lib = ctypes.CDLL(LIB)
-    for f in (lib.wave_test_transpose, lib.wave_test_sum):
+    for f in (lib.wave_test_transpose, lib.wave_test_sum, lib.wave_test_row_sum16):
         f.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         f.restype = ctypes.c_int
     return lib
@@ -30,6 +30,23 @@ def test_transpose_reduce64(wlib):
     out = torch.zeros(64, dtype=torch.float32, device="cuda")
     assert wlib.wave_test_transpose(xin.data_ptr(), out.data_ptr()) == 0
     np.testing.assert_array_equal(out.cpu().numpy(), x.sum(axis=0))
+
+
+def test_row_sum16(wlib):
+    """Each lane L ends with the 16-lane row sums of values 6 b3 + 3 b2 + i
+    (b3, b2 = bits 3 and 2 of L), i = 0..2."""
+    import torch
+
+    rng = np.random.default_rng(1)
+    x = rng.integers(-1000, 1000, size=(64, 12)).astype(np.float32)  # exact sums
+    xin = torch.from_numpy(x).cuda()
+    out = torch.zeros(64 * 3, dtype=torch.float32, device="cuda")
+    assert wlib.wave_test_row_sum16(xin.data_ptr(), out.data_ptr()) == 0
+    got = out.cpu().numpy().reshape(64, 3)
+    rows = x.reshape(4, 16, 12).sum(axis=1)  # (row, value)
+    lane = np.arange(64)
+    idx = 6 * ((lane >> 3) & 1)[:, None] + 3 * ((lane >> 2) & 1)[:, None] + np.arange(3)[None, :]
+    np.testing.assert_array_equal(got, rows[lane[:, None] // 16, idx])
 
 
 def test_wave_sum_lane63(wlib):
