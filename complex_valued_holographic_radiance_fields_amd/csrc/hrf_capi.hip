@@ -643,6 +643,24 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
       HRF_TRY(launch_unpack_ranges(in_b ? b.keys_b : b.keys_a, num_pairs, vbits, point_list,
                                    ranges, f.ntiles, s));
     }
+  } else if (diff_ranges && num_pairs > 1 && narrowed_sort_fits(end_bit, vbits)) {
+    // Tile and gaussian need two words, but after the first sort pass the
+    // remaining tile bits and the gaussian fit one: that pass writes packed
+    // words and the later ones sort them as the packed path does (4 bytes
+    // per pair read and written after the first pass instead of 8).
+    {
+      HRF_STAGE("emit", s);
+      HRF_TRY(launch_emit_pairs(w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect, n,
+                                num_pairs, f.gx, b.keys_a, b.vals_s, s, w.vis, w.part_v,
+                                num_visible > 0 ? visible : nullptr, num_visible, b.radix,
+                                first_fused ? &first : nullptr, 0, first_bits));
+    }
+    {
+      HRF_STAGE("tile_sort", s);
+      HRF_TRY(radix_sort_pairs_narrowed(b.keys_a, b.vals_s, b.keys_b, num_pairs, end_bit, vbits,
+                                        b.radix, s, reinterpret_cast<uint32_t*>(point_list),
+                                        first_fused ? &first : nullptr));
+    }
   } else {
     const bool odd = (radix_passes(end_bit) % 2) == 1;
     uint32_t* vals_a = odd ? b.vals_s : reinterpret_cast<uint32_t*>(point_list);

@@ -269,6 +269,25 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb,
                      bool index_values = false, bool keys_needed = true,
                      const SortFirstPass* first = nullptr);
 int radix_passes(int end_bit);
+// Stable sort of (key, value) pairs on key bits [0, end_bit) (two or more
+// passes) that keeps one word per pair after the first pass: that pass
+// writes (key >> d0) << vbits | value into kb (d0 its digit bits; needs
+// end_bit - d0 + vbits <= 32 and values below 2^vbits), and the later
+// passes sort those words on bits [vbits, vbits + end_bit - d0) as
+// radix_sort_keys, the last writing the values into final_out.  Four bytes
+// move per pair in the later passes instead of eight.  ka and kb are
+// overwritten; first: as for radix_sort_pairs.
+int radix_sort_pairs_narrowed(uint32_t* ka, const uint32_t* va, uint32_t* kb, int64_t n,
+                              int end_bit, int vbits, uint32_t* scratch, hipStream_t s,
+                              uint32_t* final_out, const SortFirstPass* first = nullptr);
+// Whether radix_sort_pairs_narrowed applies to end_bit key bits and vbits
+// value bits.
+inline bool narrowed_sort_fits(int end_bit, int vbits) {
+  const int passes = radix_passes(end_bit);
+  if (passes < 2 || end_bit > 32) return false;
+  const int d0 = end_bit / passes;  // the first pass's digit (the narrowest)
+  return end_bit - d0 + vbits <= 32;
+}
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
 // (the other bits ride along unsorted), in ceil(nbits/8) passes with the
 // digit widths of radix_sort_pairs; same scratch and ping-pong convention.

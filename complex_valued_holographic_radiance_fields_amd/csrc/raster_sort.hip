@@ -282,14 +282,16 @@ __device__ __forceinline__ uint32_t digit_run_start(const uint32_t* __restrict__
 // consecutive threads store consecutive elements of each digit's output
 // run.  Thread d < 2^RB holds digit d's next output position (`run`),
 // advanced by the digit's count.  The caller has cleared s_cnt before the
-// first tile; this clears it again for the next.
+// first tile; this clears it again for the next.  narrow >= 0 (with
+// values): one word per element into kout, (key >> nshift) << narrow | value
+// — the key bits the later passes sort on, above the value's narrow bits.
 template <int RB, bool VALS, int TH, bool FULL>
 __device__ __forceinline__ void scatter_tile(
     const uint32_t (&key)[kRadixItems], const uint32_t (&val)[kRadixItems], int64_t bbase,
     int64_t pend, int wave, int lane, uint64_t lt_mask, int shift, uint32_t mask,
     uint32_t (*s_cnt)[1 << RB], uint32_t* s_delta, uint32_t* s_wsum, uint32_t* s_key,
     uint32_t* s_val, uint32_t& run, bool write_keys, uint32_t* __restrict__ kout,
-    uint32_t* __restrict__ vout, uint32_t out_mask) {
+    uint32_t* __restrict__ vout, uint32_t out_mask, int narrow = -1, int nshift = 0) {
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
   const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
@@ -343,7 +345,17 @@ __device__ __forceinline__ void scatter_tile(
   // next one (the barrier after the write-out orders it).
   for (int e = threadIdx.x; e < kWaves * kBins; e += TH)
     s_cnt[e / kBins][e % kBins] = 0;
-  if (write_keys) {
+  if (VALS && narrow >= 0) {
+#pragma unroll
+    for (int it = 0; it < kRadixItems; ++it) {
+      const int i = it * TH + static_cast<int>(threadIdx.x);
+      if (FULL || i < nvalid) {
+        const uint32_t k = s_key[i];
+        const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
+        kout[pos] = ((k >> nshift) << narrow) | s_val[i];
+      }
+    }
+  } else if (write_keys) {
 #pragma unroll
     for (int it = 0; it < kRadixItems; ++it) {
       const int i = it * TH + static_cast<int>(threadIdx.x);
@@ -371,7 +383,8 @@ __device__ __forceinline__ void scatter_tile(
 
 // Stable scatter of one partition, tile by tile (scatter_tile), each
 // tile's keys loaded during the previous tile.  kout == nullptr with VALS:
-// only the values are written (the caller needs no sorted keys).
+// only the values are written (the caller needs no sorted keys); narrow >=
+// 0: one narrowed word per element into kout (scatter_tile).
 template <int RB, bool VALS, int TH>
 __global__ __launch_bounds__(TH) void k_radix_scatter(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
@@ -379,7 +392,7 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
     uint32_t mask, const uint32_t* __restrict__ hist_scan,
     const uint32_t* __restrict__ digit_totals, int nparts, int sub,
     const uint32_t* __restrict__ run_flag, uint32_t out_mask,
-    const int64_t* __restrict__ bounds) {
+    const int64_t* __restrict__ bounds, int narrow, int nshift) {
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
   static_assert(kBins <= TH, "one thread per digit");
@@ -438,12 +451,12 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
       load_tile<VALS>(kin, vin, bbase + kTile + woff, pend, lane, nkey, nval);
     scatter_tile<RB, VALS, TH, true>(key, val, bbase, pend, wave, lane, lt_mask, shift, mask,
                                      s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
-                                     kout, vout, out_mask);
+                                     kout, vout, out_mask, narrow, nshift);
   }
   if (bbase < pend)
     scatter_tile<RB, VALS, TH, false>(nkey, nval, bbase, pend, wave, lane, lt_mask, shift, mask,
                                       s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
-                                      kout, vout, out_mask);
+                                      kout, vout, out_mask, narrow, nshift);
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
@@ -935,7 +948,7 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     const uint32_t* __restrict__ sorted_flag, const uint2* __restrict__ rect, int64_t n,
     int64_t k, int gx, int vbits, uint32_t* __restrict__ kout, uint32_t* __restrict__ vout,
     int shift, uint32_t mask, const uint32_t* __restrict__ hist_scan,
-    const uint32_t* __restrict__ digit_totals, int nparts) {
+    const uint32_t* __restrict__ digit_totals, int nparts, int narrow, int nshift) {
   constexpr bool VALS = kWide;
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
@@ -999,11 +1012,11 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     if (clen == kTile)
       scatter_tile<RB, VALS, TH, true>(key, val, c0, e1, wave, lane, lt_mask, shift, mask, s_cnt,
                                        s_delta, s_wsum, s_key, s_val, run, true, kout, vout,
-                                       0xFFFFFFFFu);
+                                       0xFFFFFFFFu, narrow, nshift);
     else
       scatter_tile<RB, VALS, TH, false>(key, val, c0, e1, wave, lane, lt_mask, shift, mask, s_cnt,
                                         s_delta, s_wsum, s_key, s_val, run, true, kout, vout,
-                                        0xFFFFFFFFu);
+                                        0xFFFFFFFFu, narrow, nshift);
   }
 }
 
@@ -1185,9 +1198,12 @@ template <int RB, bool VALS>
 int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
                int64_t n, const RadixParts& rp, int shift, uint32_t mask, uint32_t* scratch,
                const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu,
-               const SortFirstPass* fp = nullptr) {
+               const SortFirstPass* fp = nullptr, int narrow = -1) {
   // fp: the histogram is in the scratch already (taken by the pair
-  // emission over its blocks, which are this pass's partitions).
+  // emission over its blocks, which are this pass's partitions).  narrow
+  // >= 0: the pass writes one word per pair into dst_k, the key bits above
+  // this digit shifted over the value's `narrow` bits (VALS only).
+  const int nshift = shift + __builtin_popcount(mask);
   const int np = fp ? fp->np : rp.np;
   const int64_t hist_n = static_cast<int64_t>(np) << RB;
   uint32_t* hist = scratch;
@@ -1211,6 +1227,10 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
   // blocks (the spine still has one column per emission block).
   const int sub = fp ? fp->group : rp.sub;
   const int nblk = fp ? (np + fp->group - 1) / fp->group : np;
+  if (narrow >= 0 && (!VALS || !dst_k)) {
+    set_error("internal: a narrowing radix pass needs values and a word output");
+    return HRF_ERR_INVALID;
+  }
   if (fp && fp->gen) {
     // The emission stored no pair: regenerate and scatter them (one block
     // per emission block).
@@ -1223,23 +1243,23 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
       hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreadsLarge>), dim3(np),
                          dim3(kRadixThreadsLarge), 0, s, g.part_t, g.part_r, g.tiles, g.order,
                          g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
-                         mask, hist, totals, np);
+                         mask, hist, totals, np, narrow, nshift);
     else
       hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreads>), dim3(np),
                          dim3(kRadixThreads), 0, s, g.part_t, g.part_r, g.tiles, g.order,
                          g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
-                         mask, hist, totals, np);
+                         mask, hist, totals, np, narrow, nshift);
     HRF_LAUNCH_CHECK();
     return HRF_OK;
   }
   if (large)
     hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(nblk),
                        dim3(kRadixThreadsLarge), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask,
-                       hist, totals, np, sub, run_flag, out_mask, bounds);
+                       hist, totals, np, sub, run_flag, out_mask, bounds, narrow, nshift);
   else
     hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreads>), dim3(nblk),
                        dim3(kRadixThreads), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask, hist,
-                       totals, np, sub, run_flag, out_mask, bounds);
+                       totals, np, sub, run_flag, out_mask, bounds, narrow, nshift);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1259,24 +1279,25 @@ template <bool VALS>
 int radix_pass_bits(int bits, const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k,
                     uint32_t* dst_v, int64_t n, const RadixParts& rp, int shift,
                     uint32_t* scratch, const uint32_t* run_flag, hipStream_t s,
-                    uint32_t out_mask = 0xFFFFFFFFu, const SortFirstPass* fp = nullptr) {
+                    uint32_t out_mask = 0xFFFFFFFFu, const SortFirstPass* fp = nullptr,
+                    int narrow = -1) {
   const uint32_t mask = (1u << bits) - 1u;
   switch (bits) {
     case 1: case 2: case 3: case 4:
       return radix_pass<4, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp);
+                                 run_flag, s, out_mask, fp, narrow);
     case 5:
       return radix_pass<5, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp);
+                                 run_flag, s, out_mask, fp, narrow);
     case 6:
       return radix_pass<6, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp);
+                                 run_flag, s, out_mask, fp, narrow);
     case 7:
       return radix_pass<7, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp);
+                                 run_flag, s, out_mask, fp, narrow);
     case 8:
       return radix_pass<8, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp);
+                                 run_flag, s, out_mask, fp, narrow);
     default:
       set_error("internal: radix digit of %d bits", bits);
       return HRF_ERR_INVALID;
@@ -1316,6 +1337,28 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
   }
   *result_in_b = (passes % 2) == 1;
   return HRF_OK;
+}
+
+int radix_sort_pairs_narrowed(uint32_t* ka, const uint32_t* va, uint32_t* kb, int64_t n,
+                              int end_bit, int vbits, uint32_t* scratch, hipStream_t s,
+                              uint32_t* final_out, const SortFirstPass* first) {
+  const int passes = radix_passes(end_bit);
+  const int bits0 = passes >= 2 ? digit_bits(end_bit, passes, 0) : 0;
+  if (n <= 1 || passes < 2 || end_bit > 32 || vbits < 1 || end_bit - bits0 + vbits > 32 ||
+      !final_out) {
+    set_error("internal: narrowed pair sort of %d key bits over %d value bits", end_bit, vbits);
+    return HRF_ERR_INVALID;
+  }
+  RadixParts rp{};
+  HRF_TRY(radix_parts(n, &rp));
+  // Pass 0 on the low digit, writing (key >> bits0) << vbits | value into kb.
+  HRF_TRY(radix_pass_bits<true>(bits0, ka, va, kb, nullptr, n, rp, 0, scratch, nullptr, s,
+                                0xFFFFFFFFu, first, vbits));
+  // The remaining key bits sit at [vbits, vbits + end_bit - bits0) of the
+  // words: a key sort whose last pass writes the values into final_out.
+  bool in_b = false;
+  return radix_sort_keys(kb, ka, n, vbits, end_bit - bits0, scratch, &in_b, s, final_out,
+                         (1u << vbits) - 1u, nullptr);
 }
 
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
