@@ -94,6 +94,15 @@ __device__ __forceinline__ float div_rn(float a, float b) {
 constexpr int kWtCount = 0xFF;
 constexpr int kWtUnsafe = 0x100;
 constexpr int kWtDone = 0x200;
+constexpr int kWtClamp = 0x400;
+
+// A batch whose staged members all have o w <= kNoClampOw runs the fast
+// loops without the reference's alpha = min(0.99, .) clamp: there the fast
+// exponent is log2(o w) plus a quadratic form that is negative and rounds
+// by far less than log2(0.99 / 0.98) (the 2-D covariance carries the +0.3
+// dilation, so the conic is bounded), so exp2 of it stays below 0.99 and
+// the clamp would return its argument unchanged.
+constexpr float kNoClampOw = 0.98f;
 constexpr int kWtSubShift = 16;
 
 // Plane member list entries: (gaussian, list position | quadrant mask << 28).
@@ -343,15 +352,17 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     // previous batch's LDS reads all precede it: its member loop ends before
     // the lanes reach this point.
     int pos, cnt = 0, spos = 0, scnt = 0;
-    bool exact = false;
+    bool exact = false, clamp = false;
     {
       const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
       const uint64_t bal = __ballot(mem);
       const uint64_t bsub = __ballot(qm4 != 0u);
       const bool w_unsafe = __ballot(mem && !conic_safe(rq[0].z, rq[0].w, rq[1].x, rq[1].y)) != 0ull;
+      const bool w_clamp = __ballot(mem && !(rq[1].z * w <= kNoClampOw)) != 0ull;
       const bool w_done = __ballot(!(T < kTermT)) == 0ull;
       if (lane == 0)
         s_wt[wave] = __popcll(bal) | (w_unsafe ? kWtUnsafe : 0) | (w_done ? kWtDone : 0) |
+                     (w_clamp ? kWtClamp : 0) |
                      (__popcll(bsub) << kWtSubShift);
       __syncthreads();
       int off = 0, soff = 0;
@@ -366,6 +377,7 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
         soff += (wv < wave) ? sc : 0;
         scnt += sc;
         exact = exact || (t & kWtUnsafe) != 0;
+        clamp = clamp || (t & kWtClamp) != 0;
         all_done = all_done && (t & kWtDone) != 0;
       }
       if (all_done) break;
@@ -431,22 +443,30 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     const bool live0 = !(T < kTermT);
     int lastj = -1;
     if (!exact) {
-      int evaluated = 0;
-      for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
-        if (__all(T < kTermT)) break;
+      // Instantiated with and without the alpha clamp (kNoClampOw).
+      auto fast = [&](auto clamp_tag) {
+        constexpr bool kClamp = decltype(clamp_tag)::value;
+        int evaluated = 0;
+        for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
+          if (__all(T < kTermT)) break;
 #pragma unroll
-        for (int jj = 0; jj < kUnroll; ++jj) {
-          const int j = j0 + jj;
-          fwd_member<C>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], u, v, T, acc,
-                        evaluated);
+          for (int jj = 0; jj < kUnroll; ++jj) {
+            const int j = j0 + jj;
+            fwd_member<C, kClamp>(s_rec[j * NQ], s_rec[j * NQ + 1], s_rec[j * NQ + (NQ - 1)], u,
+                                  v, T, acc, evaluated);
+          }
         }
-      }
-      // A lane still running composited every member of the batch (no
-      // power test could fail): the batch's last member is its last
-      // contributor.  One that terminated here composited members
-      // 0..evaluated-1 (padding follows every real member, so it ended on
-      // a real one).
-      lastj = !(T < kTermT) ? cnt - 1 : evaluated - 1;
+        // A lane still running composited every member of the batch (no
+        // power test could fail): the batch's last member is its last
+        // contributor.  One that terminated here composited members
+        // 0..evaluated-1 (padding follows every real member, so it ended on
+        // a real one).
+        lastj = !(T < kTermT) ? cnt - 1 : evaluated - 1;
+      };
+      if (clamp)
+        fast(std::true_type{});
+      else
+        fast(std::false_type{});
     } else {
       for (int j0 = 0; j0 < cnt_pad; j0 += kUnroll) {
         if (__all(T < kTermT)) break;
@@ -663,13 +683,18 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
     // A batch staging any conic outside the fast loop's domain runs the
     // reference-order loop (the flag rides in the wave's staged count).
     const bool w_ill = __ballot(qm != 0u && ill) != 0ull;
+    // ... and one staging a member with o w above kNoClampOw keeps the alpha
+    // clamp.
+    const bool w_clamp = __ballot(qm != 0u && !(rq[1].z * wpl <= kNoClampOw)) != 0ull;
     if (lane == 0) {
 #pragma unroll
-      for (int f = 0; f < 5; ++f) s_cnt[wave][f] = __popcll(bal[f]) | (f == 0 && w_ill ? 0x100 : 0);
+      for (int f = 0; f < 5; ++f)
+        s_cnt[wave][f] = __popcll(bal[f]) | (f == 0 && w_ill ? 0x100 : 0) |
+                         (f == 0 && w_clamp ? 0x200 : 0);
     }
     __syncthreads();
     int off[5], tot[5];
-    bool exact = false;
+    bool exact = false, clamp = false;
 #pragma unroll
     for (int f = 0; f < 5; ++f) {
       off[f] = 0;
@@ -679,6 +704,7 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
         const int sc = __builtin_amdgcn_readfirstlane(s_cnt[w][f]);  // same in every lane
         const int c = sc & 0xFF;
         if (f == 0) exact = exact || (sc & 0x100) != 0;
+        if (f == 0) clamp = clamp || (sc & 0x200) != 0;
         off[f] += (w < wave) ? c : 0;
         tot[f] += c;
       }
@@ -742,8 +768,9 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
     for (int w = 0; w < 4; ++w) nl = (w == wave) ? tot[1 + w] + (G - tot[1 + w] % G) % G : nl;
     // The member walk in chunks of G members, back to front, instantiated
     // for the fast exponent and for the reference-order one (exact batches).
-    auto walk = [&](auto ref_tag) {
+    auto walk = [&](auto ref_tag, auto clamp_tag) {
       constexpr bool kRef = decltype(ref_tag)::value;
+      constexpr bool kClamp = decltype(clamp_tag)::value;
       for (int hi = nl - 1; hi >= 0; hi -= G) {
         // Phase 1, one pixel per lane: the back-to-front recurrence over the
         // chunk's members, branch-free (a member that does not contribute at
@@ -774,7 +801,7 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
           }
           any = any || ok;
           const float Gz = ok ? Ga : 0.0f;
-          const float ae = fminf(kMaxAlpha, Gz);
+          const float ae = kClamp ? fminf(kMaxAlpha, Gz) : Gz;
           T = div_rn(T, 1.0f - ae);
           const float dcol = ae * T;
           // Re(colour * conj(g)) summed over channels; the reference's
@@ -915,9 +942,11 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
       }
     };
     if (exact)
-      walk(std::true_type{});
+      walk(std::true_type{}, std::true_type{});
+    else if (clamp)
+      walk(std::false_type{}, std::true_type{});
     else
-      walk(std::false_type{});
+      walk(std::false_type{}, std::false_type{});
   }
 }
 

@@ -47,13 +47,16 @@ __device__ __forceinline__ float quad_exponent(float c0, float c1, float c2, flo
   return fmaf(v, t2, fmaf(u, t1, c0));
 }
 
-template <int C>
+// kClamp false: the batch's members have o w small enough that exp2(pw)
+// stays below kMaxAlpha, and the clamp is left out (same result).
+template <int C, bool kClamp = true>
 __device__ __forceinline__ void fwd_member(const float4 a, const float4 b, const float4 c,
                                            float u, float v, float& T,
                                            float (&acc)[2 * C], int& evaluated) {
   const float pw = quad_exponent(a.x, a.y, a.z, a.w, b.x, b.y, u, v);
   const bool live = !(T < kTermT);
-  const float alpha = live ? fminf(kMaxAlpha, __builtin_amdgcn_exp2f(pw)) : 0.0f;
+  const float e = __builtin_amdgcn_exp2f(pw);
+  const float alpha = live ? (kClamp ? fminf(kMaxAlpha, e) : e) : 0.0f;
   const float sT = alpha * T;
   const float amp[6] = {b.z, b.w, c.x, c.y, c.z, c.w};
 #pragma unroll
