@@ -229,9 +229,13 @@ __device__ __forceinline__ void rank_tile(const uint32_t (&key)[kRadixItems], in
     uint32_t lo = static_cast<uint32_t>(vb), hi = static_cast<uint32_t>(vb >> 32);
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-      const uint32_t bit = (d >> b) & 1u;
-      const uint64_t bb = __ballot(bit);
-      const uint32_t m = 0u - bit;
+      // m: all ones where bit b of the digit is set (a sign-extending bit
+      // field extract), and the wave's mask of those lanes from one compare
+      // (a ballot of an int predicate would be materialised and compared
+      // again).
+      uint32_t m = static_cast<uint32_t>(static_cast<int32_t>(d << (31 - b)) >> 31);
+      asm("" : "+v"(m));  // compare m itself, not the shifted digit again
+      const uint64_t bb = __builtin_amdgcn_ballot_w64(m != 0u);
       lo = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(bb), lo, m, 0x84);
       hi = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(bb >> 32), hi, m, 0x84);
     }
