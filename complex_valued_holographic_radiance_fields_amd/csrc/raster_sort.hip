@@ -240,7 +240,9 @@ __device__ __forceinline__ void rank_tile(const uint32_t (&key)[kRadixItems], in
       hi = __builtin_amdgcn_bitop3_b32(static_cast<uint32_t>(bb >> 32), hi, m, 0x84);
     }
     const uint64_t peers = (static_cast<uint64_t>(hi) << 32) | lo;
-    const uint32_t before = static_cast<uint32_t>(__popcll(peers & lt_mask));
+    // peers in the lanes below this one (mbcnt: the mask's bits below the
+    // lane; lt_mask holds the same lanes)
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u));
     uint32_t prev = 0;
     if (valid) prev = cnt[d];
     rank[it] = prev + before;

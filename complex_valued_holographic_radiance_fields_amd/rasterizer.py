@@ -87,6 +87,12 @@ class _Inputs:
 # its backward; beyond it the backward filters the tile lists itself.
 PLANE_LISTS_MAX_BYTES = 32 << 30
 
+# The pair count of the last forward per (device, image size, Gaussian
+# count): the next forward allocates its pair-sized buffers for that count
+# plus an eighth before it waits for its own count, so that little host work
+# lies between the count read-back and the launches that follow it.
+_LAST_PAIRS: dict = {}
+
 
 class ForwardGeometry(NamedTuple):
     """What forward(..., keep_geometry=True) hands to backward(geometry=):
@@ -129,25 +135,44 @@ def forward(cam_means_3D, z_vals, quats, scales, colours, phase, opacities, plan
         final_T = torch.empty((P, H, W), dtype=torch.float32, device=dev)
         n_contrib = torch.empty((P, H, W), dtype=torch.int32, device=dev)
         ranges = torch.empty((inp.ntiles, 2), dtype=torch.int32, device=dev)
+        key = (str(dev), W, H, P, inp.n)
+        last = _LAST_PAIRS.get(key, 0)
+        cap = last + last // 8 + 4096 if last > 0 else 0
+        if cap > 0:
+            pl_buf = torch.empty(cap, dtype=torch.int32, device=dev)
+            vis_buf = torch.empty(max(inp.n, 1), dtype=torch.int64, device=dev)
+            cap_bbytes = lib.hrf_raster_binning_workspace_size(cap, W, H)
+            cap_bin_ws = _lib.workspace("raster_bin", dev, stream, cap_bbytes)
+            cap_sbytes = lib.hrf_raster_plane_lists_size(cap, W, H, P) if keep_geometry else 0
+            cap_planes = (torch.empty(cap_sbytes, dtype=torch.uint8, device=dev)
+                          if 0 < cap_sbytes <= PLANE_LISTS_MAX_BYTES else None)
         K = ctypes.c_int64(0)
         V = ctypes.c_int64(0)
         _lib.check(lib.hrf_raster_forward_prepare(ctypes.byref(inp.g), ctypes.byref(inp.c),
                                                   geom_ws.data_ptr(), gbytes, stream,
                                                   ctypes.byref(K), ctypes.byref(V)))
         K, V = int(K.value), int(V.value)
+        _LAST_PAIRS[key] = K
+        plane_lists = None
+        sbytes = 0
         if K == 0:
             point_list = torch.zeros(1, dtype=torch.int32, device=dev)
             visible = torch.zeros(0, dtype=torch.int64, device=dev)
             bbytes = 0
             bin_ws = None
+        elif K <= cap:
+            # The buffers allocated for the last call's count hold this one.
+            point_list = pl_buf[:K]
+            visible = vis_buf[:V]
+            bbytes, bin_ws = cap_bbytes, cap_bin_ws
+            if keep_geometry and cap_planes is not None:
+                plane_lists, sbytes = cap_planes, cap_sbytes
         else:
             point_list = torch.empty(K, dtype=torch.int32, device=dev)
             visible = torch.empty(V, dtype=torch.int64, device=dev)
             bbytes = lib.hrf_raster_binning_workspace_size(K, W, H)
             bin_ws = _lib.workspace("raster_bin", dev, stream, bbytes)
-        plane_lists = None
-        sbytes = 0
-        if keep_geometry and K > 0:
+        if keep_geometry and K > 0 and plane_lists is None:
             sbytes = lib.hrf_raster_plane_lists_size(K, W, H, P)
             if sbytes <= PLANE_LISTS_MAX_BYTES:
                 plane_lists = torch.empty(sbytes, dtype=torch.uint8, device=dev)

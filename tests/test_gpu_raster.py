@@ -197,6 +197,41 @@ def test_parity_alpha_clamp_batches(hrf, oracle_mod, opacity):
         assert err < TOL, (name, err)
 
 
+def test_pair_buffers_sized_from_the_last_call(hrf, oracle_mod):
+    """The forward allocates its pair-sized outputs (point_list, visible,
+    plane member lists) for the last call's pair count plus an eighth
+    before it reads its own count back: a call with fewer pairs than that
+    returns views of those buffers, one with more allocates them for its
+    count.  Lists and fields match the oracle either way."""
+    import dataclasses
+
+    from complex_valued_holographic_radiance_fields_amd import rasterizer, scenes
+
+    base = scenes.small("capacity", 3000, 128, 96, 2, 3, "object", seed=23)
+    big = scenes.generate(dataclasses.replace(base, log_scale_mean=-2.5))
+    small = scenes.generate(base)
+    rasterizer._LAST_PAIRS.clear()
+
+    def check(sc, label):
+        g, cam = oracle_inputs(sc)
+        ref = oracle_mod.rasterize_forward(g, cam)
+        t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+        print(f"{label}: K={ref['K']} storage={pl.untyped_storage().nbytes() // 4}", flush=True)
+        assert pl.numel() == ref["K"] and vis.numel() == ref["visible"].size
+        np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+        np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+        np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+        assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+        return ref["K"], pl
+
+    k_big, _ = check(big, "first call")
+    k_small, pl = check(small, "fewer pairs")  # views of buffers sized for k_big
+    assert k_big > k_small + k_small // 8 + 4096  # the capacity the small call left
+    assert pl.untyped_storage().nbytes() // 4 > k_small
+    _, pl = check(big, "more pairs")  # beyond k_small's capacity: exact buffers
+    assert pl.untyped_storage().nbytes() // 4 == k_big
+
+
 def test_empty_scene(hrf):
     """All Gaussians behind the near plane: the reference's total_pairs == 0
     path (rasterizer_splat.cu:434-449)."""
