@@ -600,7 +600,14 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
 
   // Pair emission in depth-rank order, then a stable sort on the tile id.
   const int end_bit = bits_for(f.ntiles);
-  const int vbits = bits_for(static_cast<int>(n < 0x7FFFFFFF ? n : 0x7FFFFFFF));
+  int vbits = bits_for(static_cast<int>(n < 0x7FFFFFFF ? n : 0x7FFFFFFF));
+  // HRF_SORT_VBITS=b (for tests): at least b gaussian bits, which takes the
+  // two-word key path (and with HRF_SORT_REGENERATE=1 its pair tags) at
+  // sizes where one word would hold tile and gaussian.
+  if (const char* e = std::getenv("HRF_SORT_VBITS")) {
+    const int want = std::atoi(e);
+    if (want > vbits && want <= 31) vbits = want;
+  }
   // Usual case: the prepare call formed the tile ranges from the Gaussians'
   // rectangles in the geometry workspace (no pass over the sorted pairs);
   // the forward render copies them into `ranges`.
@@ -614,9 +621,21 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   // Large sorts of two or more passes: the emission only counts, and the
   // first pass regenerates the pairs (one write of them instead of a
   // write, a read and a write).
-  const EmitGen gen{w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect,
-                    n, num_pairs, f.gx, vbits};
+  EmitGen gen{w.part_t, w.part_r, w.tiles, w.order, w.sort_flag, w.rect,
+              n, num_pairs, f.gx, vbits, TagSrc{}};
   if (first_fused && first.regenerate && radix_passes(end_bit) >= 2) first.gen = &gen;
+  // Pair tags for the forward (wide keys whose first pass regenerates the
+  // pairs, with a spare word bit after it): the emission-scatter tests each
+  // (tile, gaussian) pair as the forward's visibility cull would and the
+  // last pass writes the result beside point_list (into the values buffer,
+  // free by then), so the forward skips the culled entries of its lists
+  // without gathering their records.
+  uint8_t* pair_tags = nullptr;
+  if (end_bit + vbits > 32 && first.gen && diff_ranges && num_pairs > 1 &&
+      narrowed_sort_fits(end_bit, vbits, 1)) {
+    gen.tags = TagSrc{w.rec, rec_stride(g->channels), g->plane_probs, g->planes};
+    pair_tags = reinterpret_cast<uint8_t*>(b.vals_s);
+  }
   if (end_bit + vbits <= 32) {
     // Tile and gaussian fit one word: sort 4-byte words on the tile bits.
     {
@@ -659,7 +678,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
       HRF_STAGE("tile_sort", s);
       HRF_TRY(radix_sort_pairs_narrowed(b.keys_a, b.vals_s, b.keys_b, num_pairs, end_bit, vbits,
                                         b.radix, s, reinterpret_cast<uint32_t*>(point_list),
-                                        first_fused ? &first : nullptr));
+                                        first_fused ? &first : nullptr, pair_tags));
     }
   } else {
     const bool odd = (radix_passes(end_bit) % 2) == 1;
@@ -696,6 +715,7 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
   rp.ranges = diff_ranges ? w.ranges : ranges;
   rp.ranges_out = diff_ranges ? ranges : nullptr;
   rp.plist = point_list;
+  rp.ptag = pair_tags;
   rp.pmask = w.pmask;
   rp.rec = w.rec;
   rp.pprobs = g->plane_probs;

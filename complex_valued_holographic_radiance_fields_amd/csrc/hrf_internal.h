@@ -238,8 +238,18 @@ size_t radix_scratch_elems(int64_t n);
 // blocks, block b's pairs being [bounds[b], bounds[b + 1]), their counts
 // already in the sort scratch (digit-major, np columns).  The pass's
 // scatter partitions are `group` consecutive emission blocks each.
+// Inputs of the pair tags (render_cull.h): the render records, their stride
+// and the plane weights (n x P).  rec == nullptr: no tags.
+struct TagSrc {
+  const float* rec;
+  int rec_stride;
+  const float* pprobs;
+  int P;
+};
 // What the fused emission-scatter needs to regenerate the emission's pairs
-// (the emission launch's own inputs).
+// (the emission launch's own inputs), and with tags.rec set (wide keys
+// only), what it needs to tag each pair in value bit 31 with the forward's
+// visibility test (pair_visible).
 struct EmitGen {
   const uint64_t* part_t;
   const uint64_t* part_r;
@@ -251,6 +261,7 @@ struct EmitGen {
   int64_t k;
   int gx;
   int vbits;
+  TagSrc tags;
 };
 // regenerate (set by emit_first_pass): the sort is large enough (8192-key
 // tiles, one emission block per partition) for the emission to store no
@@ -276,27 +287,33 @@ int radix_passes(int end_bit);
 // passes sort those words on bits [vbits, vbits + end_bit - d0) as
 // radix_sort_keys, the last writing the values into final_out.  Four bytes
 // move per pair in the later passes instead of eight.  ka and kb are
-// overwritten; first: as for radix_sort_pairs.
+// overwritten; first: as for radix_sort_pairs.  tags != nullptr: the
+// fused emission-scatter tags the pairs (first->gen->tags set; needs
+// end_bit - d0 + vbits <= 31, the tag riding in word bit 31 through the
+// later passes) and the last pass writes each pair's tag (0 or 1) into
+// tags[i] beside final_out[i].
 int radix_sort_pairs_narrowed(uint32_t* ka, const uint32_t* va, uint32_t* kb, int64_t n,
                               int end_bit, int vbits, uint32_t* scratch, hipStream_t s,
-                              uint32_t* final_out, const SortFirstPass* first = nullptr);
+                              uint32_t* final_out, const SortFirstPass* first = nullptr,
+                              uint8_t* tags = nullptr);
 // Whether radix_sort_pairs_narrowed applies to end_bit key bits and vbits
-// value bits.
-inline bool narrowed_sort_fits(int end_bit, int vbits) {
+// value bits (spare = 1: with a tag bit beside them).
+inline bool narrowed_sort_fits(int end_bit, int vbits, int spare = 0) {
   const int passes = radix_passes(end_bit);
   if (passes < 2 || end_bit > 32) return false;
   const int d0 = end_bit / passes;  // the first pass's digit (the narrowest)
-  return end_bit - d0 + vbits <= 32;
+  return end_bit - d0 + vbits + spare <= 32;
 }
 // Stable LSD radix sort of u32 words on bits [lo_bit, lo_bit + nbits) only
 // (the other bits ride along unsorted), in ceil(nbits/8) passes with the
 // digit widths of radix_sort_pairs; same scratch and ping-pong convention.
 // final_out != nullptr (needs n > 1, nbits > 0): the last pass writes
-// word & final_mask there instead of into the ping-pong buffers.
+// word & final_mask there instead of into the ping-pong buffers, and with
+// final_tags, word >> 31 into final_tags (one byte per word).
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s,
                     uint32_t* final_out = nullptr, uint32_t final_mask = 0xFFFFFFFFu,
-                    const SortFirstPass* first = nullptr);
+                    const SortFirstPass* first = nullptr, uint8_t* final_tags = nullptr);
 // Whether the pair emission of n Gaussians and k pairs takes the first
 // tile-sort pass's histogram (of `bits` digit bits): only when groups of
 // consecutive emission blocks hold several sort tiles of pairs each while
@@ -374,6 +391,10 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
 struct RenderParams {
   const int32_t* ranges;
   const int32_t* plist;
+  // Optional pair tags beside plist (large wide-key sorts): 0 marks an entry
+  // the forward culls in every plane (render_cull.h, pair_visible), which
+  // the forward then skips without gathering its plane mask or record.
+  const uint8_t* ptag;
   const uint32_t* pmask;
   const float* rec;
   const float* pprobs;

@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "hrf_internal.h"
+#include "render_cull.h"
 #include "render_member.h"
 #include "wave_reduce.h"
 
@@ -113,88 +114,6 @@ constexpr int kWtSubShift = 16;
 constexpr int kSubPosBits = 28;
 constexpr uint32_t kSubPosMask = (1u << kSubPosBits) - 1u;
 
-// Culling of backward work.  A Gaussian can reach alpha >= 1/255 at a pixel
-// only where q = d^T A d <= 2 ln(255 o w) (power = -q/2, A the conic,
-// d = mean - pixel).  alpha_threshold returns that bound widened by 0.1% +
-// 0.01, far beyond the rounding of the exp/power evaluation, or -1 when no
-// pixel can qualify (o*w below 1/255).
-__device__ __forceinline__ float alpha_threshold(float ow) {
-  if (ow * 255.0f < 0.999f) return -1.0f;
-  return 2.0f * __logf(ow * 255.0f) * 1.001f + 0.01f;
-}
-
-// Cull tests.  q(d) = cxx dx^2 + 2 cxy dx dy + czz dy^2 with d = mean -
-// pixel centre: a convex quadratic when the conic is positive definite.
-// CullShape holds the conic with 2 cxy and the two 1-D minimiser slopes
-// -cxy/cxx and -cxy/czz (hardware reciprocals).  pd = false (not positive
-// definite, or NaN): never culled.
-struct CullShape {
-  float cxx, czz, t12, nx, nz;
-  bool pd;
-};
-
-__device__ __forceinline__ CullShape cull_shape(float cxx, float cxy, float czz) {
-  CullShape c;
-  c.cxx = cxx;
-  c.czz = czz;
-  c.t12 = 2.0f * cxy;
-  c.pd = cxx > 0.0f && czz > 0.0f && cxx * czz - cxy * cxy > 0.0f;
-  c.nx = -cxy * __builtin_amdgcn_rcpf(cxx);
-  c.nz = -cxy * __builtin_amdgcn_rcpf(czz);
-  return c;
-}
-
-// min of q(u, v) = a u^2 + t u v + b v^2 over u in [lo, hi] at a fixed v:
-// the 1-D minimiser n v (n = -t / 2a), clamped to the interval.  q at any
-// point of the interval bounds the minimum from above, and the minimiser's
-// rounding moves q by a (du)^2, far inside the thresholds' margins.
-__device__ __forceinline__ float seg_min(float a, float b, float t, float n, float v, float lo,
-                                         float hi) {
-  const float u = fminf(fmaxf(n * v, lo), hi);
-  return fmaf(u, fmaf(a, u, t * v), (b * v) * v);
-}
-
-// Minimum of q over the box of pixel centres [x0, x0+ext] x [y0, y0+ext]
-// (0 when the mean lies in it).  A convex function's minimum over a box is
-// reached on the faces the mean lies beyond: the segment from the mean (q's
-// minimum) to any point of the box enters the box through one of them, and
-// q along it never exceeds its value at that point.  So it is the smaller
-// of the minima over the face x = clamp(mx, x0, x1) (over the box's dy
-// range) and the face y = clamp(my, y0, y1) (over its dx range); when the
-// mean lies within the box's range of a coordinate, that "face" is a line
-// through the box, whose minimum only bounds the box's from above.
-__device__ __forceinline__ float box_min(float mx, float my, const CullShape& c, float x0,
-                                         float y0, float ext) {
-  const float dxl = mx - (x0 + ext), dxh = mx - x0;
-  const float dyl = my - (y0 + ext), dyh = my - y0;
-  const float dxn = fminf(fmaxf(0.0f, dxl), dxh);  // mx - clamp(mx, x0, x1)
-  const float dyn = fminf(fmaxf(0.0f, dyl), dyh);
-  const float mv = seg_min(c.czz, c.cxx, c.t12, c.nz, dxn, dyl, dyh);
-  const float mh = seg_min(c.cxx, c.czz, c.t12, c.nx, dyn, dxl, dxh);
-  return fminf(mv, mh);
-}
-
-// Exact test: does q(d) <= thr hold at some point of that box?
-__device__ __forceinline__ bool box_reaches(float mx, float my, const CullShape& c, float thr,
-                                            float x0, float y0, float ext) {
-  return !c.pd || box_min(mx, my, c, x0, y0, ext) <= thr;
-}
-
-// Forward members without effect.  A Gaussian whose alpha stays below 2^-26
-// at every pixel of the tile (q > 2 ln(o w 2^26) over the tile's pixel
-// centres, widened as above) cannot change T there: alpha T is below half
-// an ulp of T, so T (1 - alpha) rounds back to T (1 - alpha rounds to 1), and
-// the termination test and
-// final_T are exactly as if it had been composited.  Its field contribution
-// is below 2^-25 T |amplitude|.  Such members are not staged; the tile's
-// largest such list position still counts as the last contributor for
-// pixels that never terminate (every culled member has power <= 0 there, as
-// a composited one would).  Non-positive-definite conics are never culled.
-__device__ __forceinline__ float invisible_threshold(float ow) {
-  const float thr = 2.0f * __logf(ow * 67108864.0f);  // alpha < 2^-26
-  return fmaxf(thr, 0.0f) * 1.001f + 0.01f;
-}
-
 // A conic the fast member loops may evaluate in their own form: positive
 // definite with |correlation| below 0.99 (b b2 < 0.98 a c).  The exponent
 // dx (A dx + B dy) + C dy^2 is a sum of terms at most (1 + r) / (1 - r) = 199
@@ -255,8 +174,12 @@ __device__ __forceinline__ void fwd_member_ref(const float4 a, const float4 b, c
   lastj = (ok && real) ? j : lastj;
 }
 
-template <int C>
-__global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderParams p) {
+// kTag: the list has pair tags (p.ptag): untagged entries are culled in
+// every plane, so they are skipped without loading their plane mask or
+// record; a block that ends with a pixel still live then looks for the
+// last culled member among them from the list's end (for n_contrib).
+template <int C, bool kTag>
+__device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
   constexpr int NQ = fwd_quads(C);
   constexpr int NQX = fwd_quads_exact(C);
   constexpr int RS = rec_stride(C);
@@ -296,10 +219,12 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
   // Each batch's list entries and their plane masks are loaded during the
   // previous batch: they depend only on the list, and two dependent loads
   // per batch (entry, then mask) would otherwise precede the record loads.
+  // (kTag: an untagged entry's index becomes -1, which no test admits.)
   int g_next = 0;
   uint32_t m_next = 0;
   if (static_cast<int>(threadIdx.x) < n) {
     g_next = p.plist[r0 + static_cast<int>(threadIdx.x)];
+    if (kTag && p.ptag[r0 + static_cast<int>(threadIdx.x)] == 0) g_next = -1;
     if (static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
       m_next = p.pmask[g_next];
   }
@@ -317,6 +242,7 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     {
       const int kn = k + kBlock;
       g_next = kn < n ? p.plist[r0 + kn] : 0;
+      if (kTag && kn < n && p.ptag[r0 + kn] == 0) g_next = -1;
       m_next = 0;
     }
     if (mem) {
@@ -484,6 +410,23 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     if (live0 && lastj >= 0) last = s_pos[lastj];
   }
 
+  if (kTag && __syncthreads_or(!(T < kTermT))) {
+    // Some pixel composited the whole list, the skipped (untagged) members
+    // of this plane included: the last of them, if past s_kcull, is its
+    // last contributor.  Scanned from the list's end, one batch at a time,
+    // until a batch holds one.
+    for (int top = n; top > 0; top -= kBlock) {
+      const int k = top - 1 - static_cast<int>(threadIdx.x);
+      bool cand = false;
+      if (k >= 0 && p.ptag[r0 + k] == 0) {
+        const int g = p.plist[r0 + k];
+        cand = static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+               ((p.pmask[g] >> plane) & 1u);
+      }
+      if (cand) atomicMax(&s_kcull, k + 1);
+      if (__syncthreads_or(cand)) break;
+    }
+  }
   if (sub_out && threadIdx.x == 0) p.sub_cnt_out[tile * p.P + plane] = listed;
   __syncthreads();
   // A pixel that never terminated composited every member, culled ones too.
@@ -497,6 +440,15 @@ __global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderPar
     p.final_T[plane * HW + pix] = T;
     p.n_contrib[plane * HW + pix] = last;
   }
+}
+
+template <int C>
+__global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd(RenderParams p) {
+  render_fwd_block<C, false>(p);
+}
+template <int C>
+__global__ __launch_bounds__(kBlock, C == 2 ? 7 : 8) void k_render_fwd_tagged(RenderParams p) {
+  render_fwd_block<C, true>(p);
 }
 
 // Backward staged record: the global record's quad count, one more at C = 2
@@ -1033,15 +985,19 @@ __global__ void k_render_empty(float2* field, float* final_T, int32_t* n_contrib
 int launch_render_forward(const RenderParams& p, hipStream_t s) {
   const int nblocks = p.gx * p.gy * p.P;
   if (nblocks <= 0) return HRF_OK;
+  const bool tag = p.ptag != nullptr;
   switch (p.C) {
     case 1:
-      hipLaunchKernelGGL(k_render_fwd<1>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (tag) hipLaunchKernelGGL(k_render_fwd_tagged<1>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL(k_render_fwd<1>, dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     case 2:
-      hipLaunchKernelGGL(k_render_fwd<2>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (tag) hipLaunchKernelGGL(k_render_fwd_tagged<2>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL(k_render_fwd<2>, dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     case 3:
-      hipLaunchKernelGGL(k_render_fwd<3>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      if (tag) hipLaunchKernelGGL(k_render_fwd_tagged<3>, dim3(nblocks), dim3(kBlock), 0, s, p);
+      else hipLaunchKernelGGL(k_render_fwd<3>, dim3(nblocks), dim3(kBlock), 0, s, p);
       break;
     default:
       set_error("render: channels must be 1..3 (got %d)", p.C);

@@ -12,6 +12,7 @@
 #include <type_traits>
 
 #include "hrf_internal.h"
+#include "render_cull.h"
 
 namespace hrf {
 namespace {
@@ -291,13 +292,15 @@ __device__ __forceinline__ uint32_t digit_run_start(const uint32_t* __restrict__
 // first tile; this clears it again for the next.  narrow >= 0 (with
 // values): one word per element into kout, (key >> nshift) << narrow | value
 // — the key bits the later passes sort on, above the value's narrow bits.
+// tag_out (key writes): word bit 31 of each element as a byte beside it.
 template <int RB, bool VALS, int TH, bool FULL>
 __device__ __forceinline__ void scatter_tile(
     const uint32_t (&key)[kRadixItems], const uint32_t (&val)[kRadixItems], int64_t bbase,
     int64_t pend, int wave, int lane, uint64_t lt_mask, int shift, uint32_t mask,
     uint32_t (*s_cnt)[1 << RB], uint32_t* s_delta, uint32_t* s_wsum, uint32_t* s_key,
     uint32_t* s_val, uint32_t& run, bool write_keys, uint32_t* __restrict__ kout,
-    uint32_t* __restrict__ vout, uint32_t out_mask, int narrow = -1, int nshift = 0) {
+    uint32_t* __restrict__ vout, uint32_t out_mask, int narrow = -1, int nshift = 0,
+    uint8_t* __restrict__ tag_out = nullptr) {
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
   const int64_t wbase = bbase + static_cast<int64_t>(wave) * (kRadixItems * 64);
@@ -370,6 +373,7 @@ __device__ __forceinline__ void scatter_tile(
         const uint32_t pos = s_delta[(k >> shift) & mask] + static_cast<uint32_t>(i);
         kout[pos] = k & out_mask;
         if (VALS) vout[pos] = s_val[i];
+        if (tag_out) tag_out[pos] = static_cast<uint8_t>(k >> 31);
       }
     }
   } else {
@@ -398,7 +402,7 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
     uint32_t mask, const uint32_t* __restrict__ hist_scan,
     const uint32_t* __restrict__ digit_totals, int nparts, int sub,
     const uint32_t* __restrict__ run_flag, uint32_t out_mask,
-    const int64_t* __restrict__ bounds, int narrow, int nshift) {
+    const int64_t* __restrict__ bounds, int narrow, int nshift, uint8_t* __restrict__ tag_out) {
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
   static_assert(kBins <= TH, "one thread per digit");
@@ -457,12 +461,12 @@ __global__ __launch_bounds__(TH) void k_radix_scatter(
       load_tile<VALS>(kin, vin, bbase + kTile + woff, pend, lane, nkey, nval);
     scatter_tile<RB, VALS, TH, true>(key, val, bbase, pend, wave, lane, lt_mask, shift, mask,
                                      s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
-                                     kout, vout, out_mask, narrow, nshift);
+                                     kout, vout, out_mask, narrow, nshift, tag_out);
   }
   if (bbase < pend)
     scatter_tile<RB, VALS, TH, false>(nkey, nval, bbase, pend, wave, lane, lt_mask, shift, mask,
                                       s_cnt, s_delta, s_wsum, s_key, s_val, run, write_keys,
-                                      kout, vout, out_mask, narrow, nshift);
+                                      kout, vout, out_mask, narrow, nshift, tag_out);
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t n) {
@@ -704,7 +708,8 @@ __global__ __launch_bounds__(kScanThreads) void k_offsets_scan(
 
 // Pairs [a, a + cnt) of an emission block, whose pair offsets are
 // s_off[0..nr] and whose Gaussians and packed rectangles are s_g and s_rect
-// (rank order), handed to store(j, tile id, gaussian) for j = 0..cnt-1: one
+// (rank order), handed to store(j, tile id, gaussian, the gaussian's index
+// in the block, tile x, tile y) for j = 0..cnt-1: one
 // binary search finds the first pair's Gaussian and tile (one division by
 // the rectangle width), then a walk goes on (next tile of the rectangle, y
 // outer and x inner as rasterizer_splat.cu:162-173 emits them; next
@@ -742,7 +747,7 @@ __device__ __forceinline__ void walk_pairs(uint64_t a, int cnt, const uint64_t* 
       ty = rc.x >> 16;
       gb = s_g[lo];
     }
-    store(j, ty * ugx + tx, gb);
+    store(j, ty * ugx + tx, gb, lo, tx, ty);
     if (++tx == maxx) {
       tx = minx;
       ++ty;
@@ -898,7 +903,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
     const int j0 = static_cast<int>(threadIdx.x) * kEmitPer;
     if (j0 < clen) {
       const int cnt = clen - j0 < kEmitPer ? clen - j0 : kEmitPer;
-      walk_pairs(c0 + j0, cnt, s_off, nr, s_rect, s_g, ugx, [&](int j, uint32_t tile, uint32_t gb) {
+      walk_pairs(c0 + j0, cnt, s_off, nr, s_rect, s_g, ugx,
+                 [&](int j, uint32_t tile, uint32_t gb, int, uint32_t, uint32_t) {
         if (kWide) {
           s_words[emit_pad(j0 + j)] = tile;
           s_vals[emit_pad(j0 + j)] = gb;
@@ -947,6 +953,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_packed(
 // distinct banks across the wave (lane t writes 8t + (j ^ (t >> 3))), and
 // the scatter's reads (64 consecutive items per wave) stay one contiguous
 // run, so the tile needs no padding.
+// Wide keys with ts.rec set: each pair's value carries in bit 31 whether
+// the forward keeps the gaussian in that tile in some plane (pair_visible;
+// the gaussians' cull keys staged in LDS), and the last sort pass writes
+// that bit beside point_list for the forward.
 template <bool kWide, int RB, int TH>
 __global__ __launch_bounds__(TH) void k_emit_scatter(
     const uint64_t* __restrict__ part_t, const uint64_t* __restrict__ part_r,
@@ -954,7 +964,7 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     const uint32_t* __restrict__ sorted_flag, const uint2* __restrict__ rect, int64_t n,
     int64_t k, int gx, int vbits, uint32_t* __restrict__ kout, uint32_t* __restrict__ vout,
     int shift, uint32_t mask, const uint32_t* __restrict__ hist_scan,
-    const uint32_t* __restrict__ digit_totals, int nparts, int narrow, int nshift) {
+    const uint32_t* __restrict__ digit_totals, int nparts, int narrow, int nshift, TagSrc ts) {
   constexpr bool VALS = kWide;
   constexpr int kBins = 1 << RB;
   constexpr int kWaves = TH / 64, kTile = TH * kRadixItems;
@@ -969,10 +979,12 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
   __shared__ uint32_t s_g[kEmitThreads];
   __shared__ uint2 s_rect[kEmitThreads];
   __shared__ uint64_t s_wave[kWaves];
+  __shared__ CullKey s_ck[kWide ? kEmitThreads : 1];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   uint32_t run = digit_run_start<RB>(digit_totals, hist_scan, nparts,
                                      static_cast<int>(blockIdx.x), wave, lane, s_wsum);
+  const bool tagged = kWide && ts.rec != nullptr;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kEmitThreads;
@@ -982,6 +994,12 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     const uint32_t g = ordered(order, sorted_flag, rb + threadIdx.x);
     s_g[threadIdx.x] = g;
     s_rect[threadIdx.x] = rect[g];
+    if (tagged) {
+      const float4* r4 = reinterpret_cast<const float4*>(
+          ts.rec + static_cast<int64_t>(g) * ts.rec_stride);
+      s_ck[kWide ? threadIdx.x : 0] =
+          cull_key(r4[0], r4[1], ts.pprobs + static_cast<int64_t>(g) * ts.P, ts.P);
+    }
   }
   for (int e = threadIdx.x; e < kWaves * kBins; e += TH) s_cnt[e / kBins][e % kBins] = 0;
   __syncthreads();
@@ -995,11 +1013,18 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     if (j0 < clen) {
       const int cnt = clen - j0 < kRadixItems ? clen - j0 : kRadixItems;
       walk_pairs(static_cast<uint64_t>(c0 + j0), cnt, s_off, nr, s_rect, s_g, ugx,
-                 [&](int j, uint32_t tile, uint32_t gb) {
+                 [&](int j, uint32_t tile, uint32_t gb, int lo, uint32_t tx, uint32_t ty) {
                    const int i = j0 + j;
                    const int sw = i ^ ((i >> 6) & 7);
                    s_key[sw] = kWide ? tile : ((tile << vbits) | gb);
-                   if (VALS) s_val[sw] = gb;
+                   if (VALS) {
+                     uint32_t v = gb;
+                     if (tagged &&
+                         pair_visible(s_ck[kWide ? lo : 0], static_cast<float>(tx * hrf::kTile),
+                                      static_cast<float>(ty * hrf::kTile)))
+                       v |= 0x80000000u;
+                     s_val[sw] = v;
+                   }
                  });
     }
     __syncthreads();
@@ -1204,11 +1229,12 @@ template <int RB, bool VALS>
 int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, uint32_t* dst_v,
                int64_t n, const RadixParts& rp, int shift, uint32_t mask, uint32_t* scratch,
                const uint32_t* run_flag, hipStream_t s, uint32_t out_mask = 0xFFFFFFFFu,
-               const SortFirstPass* fp = nullptr, int narrow = -1) {
+               const SortFirstPass* fp = nullptr, int narrow = -1, uint8_t* tag_out = nullptr) {
   // fp: the histogram is in the scratch already (taken by the pair
   // emission over its blocks, which are this pass's partitions).  narrow
   // >= 0: the pass writes one word per pair into dst_k, the key bits above
   // this digit shifted over the value's `narrow` bits (VALS only).
+  // tag_out: each written key's bit 31 as a byte beside it.
   const int nshift = shift + __builtin_popcount(mask);
   const int np = fp ? fp->np : rp.np;
   const int64_t hist_n = static_cast<int64_t>(np) << RB;
@@ -1249,23 +1275,24 @@ int radix_pass(const uint32_t* src_k, const uint32_t* src_v, uint32_t* dst_k, ui
       hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreadsLarge>), dim3(np),
                          dim3(kRadixThreadsLarge), 0, s, g.part_t, g.part_r, g.tiles, g.order,
                          g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
-                         mask, hist, totals, np, narrow, nshift);
+                         mask, hist, totals, np, narrow, nshift, g.tags);
     else
       hipLaunchKernelGGL((k_emit_scatter<VALS, RB, kRadixThreads>), dim3(np),
                          dim3(kRadixThreads), 0, s, g.part_t, g.part_r, g.tiles, g.order,
                          g.sorted_flag, g.rect, g.n, g.k, g.gx, g.vbits, dst_k, dst_v, shift,
-                         mask, hist, totals, np, narrow, nshift);
+                         mask, hist, totals, np, narrow, nshift, g.tags);
     HRF_LAUNCH_CHECK();
     return HRF_OK;
   }
   if (large)
     hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreadsLarge>), dim3(nblk),
                        dim3(kRadixThreadsLarge), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask,
-                       hist, totals, np, sub, run_flag, out_mask, bounds, narrow, nshift);
+                       hist, totals, np, sub, run_flag, out_mask, bounds, narrow, nshift,
+                       tag_out);
   else
     hipLaunchKernelGGL((k_radix_scatter<RB, VALS, kRadixThreads>), dim3(nblk),
                        dim3(kRadixThreads), 0, s, src_k, src_v, dst_k, dst_v, n, shift, mask, hist,
-                       totals, np, sub, run_flag, out_mask, bounds, narrow, nshift);
+                       totals, np, sub, run_flag, out_mask, bounds, narrow, nshift, tag_out);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1286,24 +1313,24 @@ int radix_pass_bits(int bits, const uint32_t* src_k, const uint32_t* src_v, uint
                     uint32_t* dst_v, int64_t n, const RadixParts& rp, int shift,
                     uint32_t* scratch, const uint32_t* run_flag, hipStream_t s,
                     uint32_t out_mask = 0xFFFFFFFFu, const SortFirstPass* fp = nullptr,
-                    int narrow = -1) {
+                    int narrow = -1, uint8_t* tag_out = nullptr) {
   const uint32_t mask = (1u << bits) - 1u;
   switch (bits) {
     case 1: case 2: case 3: case 4:
       return radix_pass<4, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp, narrow);
+                                 run_flag, s, out_mask, fp, narrow, tag_out);
     case 5:
       return radix_pass<5, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp, narrow);
+                                 run_flag, s, out_mask, fp, narrow, tag_out);
     case 6:
       return radix_pass<6, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp, narrow);
+                                 run_flag, s, out_mask, fp, narrow, tag_out);
     case 7:
       return radix_pass<7, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp, narrow);
+                                 run_flag, s, out_mask, fp, narrow, tag_out);
     case 8:
       return radix_pass<8, VALS>(src_k, src_v, dst_k, dst_v, n, rp, shift, mask, scratch,
-                                 run_flag, s, out_mask, fp, narrow);
+                                 run_flag, s, out_mask, fp, narrow, tag_out);
     default:
       set_error("internal: radix digit of %d bits", bits);
       return HRF_ERR_INVALID;
@@ -1347,12 +1374,17 @@ int radix_sort_pairs(uint32_t* ka, uint32_t* va, uint32_t* kb, uint32_t* vb, int
 
 int radix_sort_pairs_narrowed(uint32_t* ka, const uint32_t* va, uint32_t* kb, int64_t n,
                               int end_bit, int vbits, uint32_t* scratch, hipStream_t s,
-                              uint32_t* final_out, const SortFirstPass* first) {
+                              uint32_t* final_out, const SortFirstPass* first,
+                              uint8_t* tags) {
   const int passes = radix_passes(end_bit);
   const int bits0 = passes >= 2 ? digit_bits(end_bit, passes, 0) : 0;
-  if (n <= 1 || passes < 2 || end_bit > 32 || vbits < 1 || end_bit - bits0 + vbits > 32 ||
-      !final_out) {
+  if (n <= 1 || passes < 2 || end_bit > 32 || vbits < 1 ||
+      end_bit - bits0 + vbits > (tags ? 31 : 32) || !final_out) {
     set_error("internal: narrowed pair sort of %d key bits over %d value bits", end_bit, vbits);
+    return HRF_ERR_INVALID;
+  }
+  if (tags && !(first && first->gen && first->gen->tags.rec)) {
+    set_error("internal: pair tags need the tagging emission-scatter");
     return HRF_ERR_INVALID;
   }
   RadixParts rp{};
@@ -1364,12 +1396,12 @@ int radix_sort_pairs_narrowed(uint32_t* ka, const uint32_t* va, uint32_t* kb, in
   // words: a key sort whose last pass writes the values into final_out.
   bool in_b = false;
   return radix_sort_keys(kb, ka, n, vbits, end_bit - bits0, scratch, &in_b, s, final_out,
-                         (1u << vbits) - 1u, nullptr);
+                         (1u << vbits) - 1u, nullptr, tags);
 }
 
 int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits,
                     uint32_t* scratch, bool* result_in_b, hipStream_t s, uint32_t* final_out,
-                    uint32_t final_mask, const SortFirstPass* first) {
+                    uint32_t final_mask, const SortFirstPass* first, uint8_t* final_tags) {
   *result_in_b = false;
   if (n <= 1 || nbits <= 0) {
     if (final_out) {
@@ -1389,7 +1421,8 @@ int radix_sort_keys(uint32_t* ka, uint32_t* kb, int64_t n, int lo_bit, int nbits
     uint32_t* out = last ? final_out : dst;
     const uint32_t om = last ? final_mask : 0xFFFFFFFFu;
     HRF_TRY(radix_pass_bits<false>(bits, src, nullptr, out, nullptr, n, rp, lo_bit + done,
-                                   scratch, nullptr, s, om, pass == 0 ? first : nullptr));
+                                   scratch, nullptr, s, om, pass == 0 ? first : nullptr, -1,
+                                   last ? final_tags : nullptr));
     done += bits;
     uint32_t* t = src;
     src = dst;

@@ -902,3 +902,115 @@ def test_backward_prologue_on_a_second_stream(hrf):
     errs = [rel_l2(a.cpu().numpy(), b.cpu().numpy()) for a, b in zip(other, ref)]
     print(f"mismatched preparation: rel-L2 per gradient {['%.1e' % e for e in errs]}", flush=True)
     assert max(errs) < 1e-6
+
+
+def _tag_scene(case):
+    """Scenes for the pair-tag path: needle-like Gaussians (one axis e^-2.5,
+    the others e^-6) whose 3-sigma tile rectangles hold many tiles they never
+    reach, soft plane weights (several planes per Gaussian, some below the
+    cutoff), or opaque ones where most pixels terminate."""
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    P, C = (1, 1) if case == "p1c1" else (3, 3)
+    spec = scenes.SceneSpec("tags", 12, 20_000, 384, 320, P, [639e-9, 515e-9, 473e-9][:C],
+                            [-1e-3, 0.0, 1e-3][:P], "uniform", log_scale_mean=-6.0,
+                            log_scale_std=0.5)
+    sc = scenes.generate(spec)
+    rng = np.random.default_rng(5)
+    m = sc.scales.shape[0]
+    sc.scales[:, 0] = np.exp(rng.normal(-2.5, 0.5, size=m)).astype(np.float32)
+    if case == "soft":
+        w = rng.uniform(0, 1, size=sc.pprobs.shape).astype(np.float32)
+        w[rng.uniform(size=w.shape) < 0.4] = 0.0
+        w[rng.uniform(size=w.shape) < 0.05] = 5e-7
+        sc.pprobs[:] = w
+    if case == "dense":
+        sc.scales[:, 1:] *= np.float32(np.exp(1.5))
+        sc.opac[:] = 0.97
+    return sc
+
+
+@pytest.mark.parametrize("case", ["needles", "soft", "dense", "p1c1"])
+def test_tagged_pair_lists(hrf, oracle_mod, monkeypatch, case):
+    """Pair tags (wide keys whose first sort pass regenerates the pairs: the
+    emission tests each (tile, gaussian) pair as the forward's visibility cull
+    would, the last pass writes the result beside point_list, and the
+    forward skips the untagged entries unseen).  Forced here at small sizes
+    (HRF_SORT_VBITS widens the gaussian field past one word,
+    HRF_SORT_REGENERATE takes the regenerating first pass).  Binning against
+    the oracle bit for bit; field, final_T, n_contrib and the plane member
+    lists identical to the untagged path's (the tags only skip what that path
+    culls); field and the 8 gradients (backward on the tagged forward's plane
+    lists) against the oracle."""
+    import torch
+    from complex_valued_holographic_radiance_fields_amd import rasterizer
+
+    sc = _tag_scene(case)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    W, H = sc.spec.width, sc.spec.height
+    t = scenes_torch(sc)
+    args = (t["cam_means"], t["z"], t["quats"], t["scales"], t["colours"], t["phase"], t["opac"],
+            t["pprobs"], sc.fx, sc.fy, sc.px, sc.py, t["view"])
+
+    def run():
+        out = rasterizer.forward(*args, (W, H), (16, 16), 1.0, 1000.0, keep_geometry=True)
+        torch.cuda.synchronize()
+        return out
+
+    plain_field, plain_info, plain_geom = run()
+    monkeypatch.setenv("HRF_SORT_VBITS", "24")
+    monkeypatch.setenv("HRF_SORT_REGENERATE", "1")
+    field, info, geom = run()
+    monkeypatch.delenv("HRF_SORT_VBITS")
+    monkeypatch.delenv("HRF_SORT_REGENERATE")
+    fT, nc, pl, ranges, vis = info
+    K = int(pl.numel())
+    done = float((fT < 1e-4).float().mean())
+    print(f"tags {case}: N={g.n} K={K} terminated={done:.3f}", flush=True)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+    assert torch.equal(field, plain_field)
+    for a, b in zip(info[:2], plain_info[:2]):
+        assert torch.equal(a, b)
+    # plane member lists: the counts, and each (tile, plane) list's entries
+    # up to its count (the buffer past them is scratch)
+    P = g.P
+    ntiles = ranges.shape[0]
+    c0 = (P * K * 8 + 255) // 256 * 256
+    lists = []
+    for gm in (geom, plain_geom):
+        buf = gm.plane_lists.cpu().numpy()
+        ent = buf[:P * K * 8].view(np.int64).reshape(P, K)
+        cnt = buf[c0:c0 + ntiles * P * 4].view(np.int32).reshape(ntiles, P)
+        lists.append((ent, cnt))
+    np.testing.assert_array_equal(lists[0][1], lists[1][1])
+    r_np = ranges.cpu().numpy()
+    for tile in range(ntiles):
+        for p in range(P):
+            a, c = r_np[tile, 0], lists[0][1][tile, p]
+            np.testing.assert_array_equal(lists[0][0][p, a:a + c], lists[1][0][p, a:a + c])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+    assert rel_l2(fT.cpu().numpy(), ref["final_T"]) < TOL
+    assert np.mean(nc.cpu().numpy() != ref["n_contrib"]) < 1e-3
+    if case == "dense":
+        assert done > 0.2
+    else:
+        assert done < 0.9
+
+    rng = np.random.default_rng(6)
+    gf = ((rng.normal(size=field.shape) + 1j * rng.normal(size=field.shape)) *
+          np.sqrt(0.5)).astype(np.complex64)
+    grads = rasterizer.backward(torch.from_numpy(gf).cuda(), *args, (W, H), (16, 16), fT, nc, pl,
+                                ranges, 1.0, 1000.0, geometry=geom)
+    torch.cuda.synchronize()
+    state = dict(ref, final_T=fT.cpu().numpy(), n_contrib=nc.cpu().numpy())
+    rb = oracle_mod.rasterize_backward(g, cam, state, gf)
+    names = ["cam", "z", "quats", "scales", "colours", "phase", "opac", "plane"]
+    for name, a in zip(names, grads):
+        if name == "z":
+            continue
+        err = rel_l2(a.cpu().numpy(), rb[name])
+        print(f"tags {case} grad_{name}: rel_l2={err:.3e}", flush=True)
+        assert err < TOL, (name, err)
