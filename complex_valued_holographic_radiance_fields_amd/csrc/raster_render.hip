@@ -106,6 +106,10 @@ constexpr int kWtClamp = 0x400;
 constexpr float kNoClampOw = 0.98f;
 constexpr int kWtSubShift = 16;
 
+// List entries per window of the tagged forward walk (tag bytes scanned per
+// compaction; positions within a window fit 16 bits).
+constexpr int kTagWin = 1024;
+
 // Plane member list entries: (gaussian, list position | quadrant mask << 28).
 // The mask has bit w set when the member's alpha >= 1/255 region meets the
 // 8x8 quadrant w of the tile (the backward's box test, made once in the
@@ -219,32 +223,28 @@ __device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
   // Each batch's list entries and their plane masks are loaded during the
   // previous batch: they depend only on the list, and two dependent loads
   // per batch (entry, then mask) would otherwise precede the record loads.
-  // (kTag: an untagged entry's index becomes -1, which no test admits.)
   int g_next = 0;
   uint32_t m_next = 0;
-  if (static_cast<int>(threadIdx.x) < n) {
+  if (!kTag && static_cast<int>(threadIdx.x) < n) {
     g_next = p.plist[r0 + static_cast<int>(threadIdx.x)];
-    if (kTag && p.ptag[r0 + static_cast<int>(threadIdx.x)] == 0) g_next = -1;
     if (static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
       m_next = p.pmask[g_next];
   }
   __syncthreads();  // s_kcull's initialisation before the batches' culls
-  for (int base = 0; base < n; base += kBlock) {
-    const int k = base + static_cast<int>(threadIdx.x);
-    const int g = g_next;
-    bool mem = k < n && static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
-               ((m_next >> plane) & 1u);
+  // One batch: this thread's entry (list position k, gaussian g; mem: a
+  // member of this plane) is culled, the block's members are staged and
+  // composited.  Returns true, having staged nothing, once every pixel of
+  // the block is done.  load_next / mask_next: the untagged walk's loads of
+  // the next batch's entries and plane masks, issued before and after the
+  // record loads.
+  auto batch = [&](const int k, const int g, bool mem, auto&& load_next,
+                   auto&& mask_next) -> bool {
     // geometry quads; the amplitude quads load at the LDS write
     float4 rq[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
     float w = 0.0f;
     unsigned qm4 = 0;  // quadrants the member reaches at alpha >= 1/255
     const float4* src = nullptr;
-    {
-      const int kn = k + kBlock;
-      g_next = kn < n ? p.plist[r0 + kn] : 0;
-      if (kTag && kn < n && p.ptag[r0 + kn] == 0) g_next = -1;
-      m_next = 0;
-    }
+    load_next();
     if (mem) {
       src = reinterpret_cast<const float4*>(p.rec + static_cast<int64_t>(g) * RS);
       rq[0] = src[0];
@@ -269,9 +269,7 @@ __device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
         }
       }
     }
-    if (base + kBlock + static_cast<int>(threadIdx.x) < n &&
-        static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
-      m_next = p.pmask[g_next];
+    mask_next();
     // One barrier publishes each wave's member count (the compaction), whether
     // it stages a conic that is not safe (then the batch runs the exact
     // loop) and whether all its pixels are done (then the block is).  The
@@ -306,7 +304,7 @@ __device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
         clamp = clamp || (t & kWtClamp) != 0;
         all_done = all_done && (t & kWtDone) != 0;
       }
-      if (all_done) break;
+      if (all_done) return true;
       pos = off + bits_below_lane(bal);
       spos = soff + bits_below_lane(bsub);
     }
@@ -408,6 +406,88 @@ __device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
       }
     }
     if (live0 && lastj >= 0) last = s_pos[lastj];
+    return false;
+  };
+
+  if constexpr (!kTag) {
+    for (int base = 0; base < n; base += kBlock) {
+      const int k = base + static_cast<int>(threadIdx.x);
+      const int g = g_next;
+      const bool mem = k < n &&
+                       static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n) &&
+                       ((m_next >> plane) & 1u);
+      const bool done = batch(
+          k, g, mem,
+          [&] {
+            const int kn = k + kBlock;
+            g_next = kn < n ? p.plist[r0 + kn] : 0;
+            m_next = 0;
+          },
+          [&] {
+            if (k + kBlock < n &&
+                static_cast<uint64_t>(static_cast<uint32_t>(g_next)) < static_cast<uint64_t>(p.n))
+              m_next = p.pmask[g_next];
+          });
+      if (done) break;
+    }
+  } else {
+    // Tagged lists: windows of kTagWin entries; the tagged positions of a
+    // window (tag bytes only, in list order) are compacted into s_cand and
+    // staged in batches of kBlock, so a block walks its list in a fraction
+    // of the batches (config 4 tags ~5% of its entries).  Candidate order:
+    // (i, wave, lane) for entry wb + i kBlock + threadIdx.x, which is list
+    // order.
+    constexpr int kPer = kTagWin / kBlock;
+    __shared__ unsigned short s_cand[kTagWin];
+    __shared__ int s_wc[kBlock / 64][kPer];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int wb = 0; wb < n; wb += kTagWin) {
+      uint64_t bal[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int k = wb + i * kBlock + static_cast<int>(threadIdx.x);
+        bal[i] = __ballot(k < n && p.ptag[r0 + k] != 0);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) s_wc[wave][i] = __popcll(bal[i]);
+      }
+      // (the block leaves once every pixel is done)
+      if (!__syncthreads_or(!(T < kTermT))) break;
+      int ncand = 0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        int off = ncand;
+#pragma unroll
+        for (int wv = 0; wv < kBlock / 64; ++wv) {
+          const int c = s_wc[wv][i];
+          off += (wv < wave) ? c : 0;
+          ncand += c;
+        }
+        if ((bal[i] >> lane) & 1ull)
+          s_cand[off + bits_below_lane(bal[i])] =
+              static_cast<unsigned short>(i * kBlock + static_cast<int>(threadIdx.x));
+      }
+      __syncthreads();
+      bool done = false;
+      for (int cb = 0; cb < ncand; cb += kBlock) {
+        const int ci = cb + static_cast<int>(threadIdx.x);
+        int k = 0, g = -1;
+        uint32_t m = 0;
+        if (ci < ncand) {
+          k = wb + static_cast<int>(s_cand[ci]);
+          g = p.plist[r0 + k];
+          if (static_cast<uint64_t>(static_cast<uint32_t>(g)) < static_cast<uint64_t>(p.n))
+            m = p.pmask[g];
+        }
+        const bool mem = ci < ncand && ((m >> plane) & 1u);
+        if (batch(k, g, mem, [] {}, [] {})) {
+          done = true;
+          break;
+        }
+      }
+      if (done) break;
+    }
   }
 
   if (kTag && __syncthreads_or(!(T < kTermT))) {

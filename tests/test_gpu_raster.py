@@ -939,9 +939,9 @@ def test_tagged_pair_lists(hrf, oracle_mod, monkeypatch, case):
     (HRF_SORT_VBITS widens the gaussian field past one word,
     HRF_SORT_REGENERATE takes the regenerating first pass).  Binning against
     the oracle bit for bit; field, final_T, n_contrib and the plane member
-    lists identical to the untagged path's (the tags only skip what that path
-    culls); field and the 8 gradients (backward on the tagged forward's plane
-    lists) against the oracle."""
+    lists as the untagged path's (the tags only skip what that path culls; the
+    batches differ, so to rounding); field and the 8 gradients (backward on
+    the tagged forward's plane lists) against the oracle."""
     import torch
     from complex_valued_holographic_radiance_fields_amd import rasterizer
 
@@ -971,11 +971,15 @@ def test_tagged_pair_lists(hrf, oracle_mod, monkeypatch, case):
     np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
     np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
     np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
-    assert torch.equal(field, plain_field)
-    for a, b in zip(info[:2], plain_info[:2]):
-        assert torch.equal(a, b)
-    # plane member lists: the counts, and each (tile, plane) list's entries
-    # up to its count (the buffer past them is scratch)
+    # Against the untagged path: the tagged walk stages its candidates in
+    # other batches (so a batch's choice of the reference-order or the fast
+    # exponent may differ: rounding only), and may stop one window later.
+    assert rel_l2(field.cpu().numpy(), plain_field.cpu().numpy()) < 1e-6
+    assert rel_l2(fT.cpu().numpy(), plain_info[0].cpu().numpy()) < 1e-6
+    assert np.mean(nc.cpu().numpy() != plain_info[1].cpu().numpy()) < 1e-3
+    # plane member lists: per (tile, plane) the same entries in the same
+    # order up to the shorter list's count (the buffer past a count is
+    # scratch)
     P = g.P
     ntiles = ranges.shape[0]
     c0 = (P * K * 8 + 255) // 256 * 256
@@ -985,11 +989,11 @@ def test_tagged_pair_lists(hrf, oracle_mod, monkeypatch, case):
         ent = buf[:P * K * 8].view(np.int64).reshape(P, K)
         cnt = buf[c0:c0 + ntiles * P * 4].view(np.int32).reshape(ntiles, P)
         lists.append((ent, cnt))
-    np.testing.assert_array_equal(lists[0][1], lists[1][1])
     r_np = ranges.cpu().numpy()
     for tile in range(ntiles):
         for p in range(P):
-            a, c = r_np[tile, 0], lists[0][1][tile, p]
+            a = r_np[tile, 0]
+            c = min(lists[0][1][tile, p], lists[1][1][tile, p])
             np.testing.assert_array_equal(lists[0][0][p, a:a + c], lists[1][0][p, a:a + c])
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
     assert rel_l2(fT.cpu().numpy(), ref["final_T"]) < TOL
