@@ -1012,6 +1012,10 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
     const int clen = static_cast<int>(e1 - c0 < kTile ? e1 - c0 : kTile);
     if (j0 < clen) {
       const int cnt = clen - j0 < kRadixItems ? clen - j0 : kRadixItems;
+      // The cull key of the gaussian being walked, reloaded only when the
+      // walk moves on to the next one.
+      int ck_lo = -1;
+      CullKey ck{};
       walk_pairs(static_cast<uint64_t>(c0 + j0), cnt, s_off, nr, s_rect, s_g, ugx,
                  [&](int j, uint32_t tile, uint32_t gb, int lo, uint32_t tx, uint32_t ty) {
                    const int i = j0 + j;
@@ -1019,10 +1023,15 @@ __global__ __launch_bounds__(TH) void k_emit_scatter(
                    s_key[sw] = kWide ? tile : ((tile << vbits) | gb);
                    if (VALS) {
                      uint32_t v = gb;
-                     if (tagged &&
-                         pair_visible(s_ck[kWide ? lo : 0], static_cast<float>(tx * hrf::kTile),
-                                      static_cast<float>(ty * hrf::kTile)))
-                       v |= 0x80000000u;
+                     if (tagged) {
+                       if (lo != ck_lo) {
+                         ck = s_ck[kWide ? lo : 0];
+                         ck_lo = lo;
+                       }
+                       if (pair_visible(ck, static_cast<float>(tx * hrf::kTile),
+                                        static_cast<float>(ty * hrf::kTile)))
+                         v |= 0x80000000u;
+                     }
                      s_val[sw] = v;
                    }
                  });
