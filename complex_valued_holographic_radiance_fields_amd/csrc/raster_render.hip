@@ -108,7 +108,7 @@ constexpr int kWtSubShift = 16;
 
 // List entries per window of the tagged forward walk (tag bytes scanned per
 // compaction; positions within a window fit 16 bits).
-constexpr int kTagWin = 1024;
+constexpr int kTagWin = 2048;
 
 // Plane member list entries: (gaussian, list position | quadrant mask << 28).
 // The mask has bit w set when the member's alpha >= 1/255 region meets the
