@@ -249,6 +249,7 @@ struct GeomWs {
   // array fits kMaxTileDiff (the render call then reads them here).
   int32_t* diff;
   int32_t* ranges;
+  int32_t* tile_order;  // tile ids, longest list first (the forward's block order)
 };
 
 GeomWs carve_geom(Carver& cv, int64_t n, int C) {
@@ -271,6 +272,7 @@ GeomWs carve_geom(Carver& cv, int64_t n, int C) {
   w.sort_flag = cv.take<uint32_t>(4);
   w.diff = cv.take<int32_t>(kMaxTileDiff);
   w.ranges = cv.take<int32_t>(2 * kMaxTileDiff);
+  w.tile_order = cv.take<int32_t>(kMaxTileDiff);
   return w;
 }
 
@@ -509,7 +511,8 @@ int hrf_raster_forward_prepare(const hrf_gaussians* g, const hrf_camera* cam, vo
   // for the counts (and the render call reads them from the workspace).
   if (diff_ranges) {
     HRF_STAGE("ranges", s);
-    HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s));
+    HRF_TRY(launch_tile_ranges_from_rects(w.tiles, w.rect, n, f.gx, f.gy, w.diff, w.ranges, s,
+                                          w.tile_order));
   }
   HRF_TRY(readback_wait(slot.r, tag, s));
   slot.pending = false;
@@ -714,6 +717,9 @@ int hrf_raster_forward_render(const hrf_gaussians* g, const hrf_camera* cam, voi
 
   rp.ranges = diff_ranges ? w.ranges : ranges;
   rp.ranges_out = diff_ranges ? ranges : nullptr;
+  // Longest tile lists first (formed with the ranges in the prepare call).
+  rp.tile_order = diff_ranges ? w.tile_order : nullptr;
+  rp.tile_order_n = f.ntiles;
   rp.plist = point_list;
   rp.ptag = pair_tags;
   rp.pmask = w.pmask;

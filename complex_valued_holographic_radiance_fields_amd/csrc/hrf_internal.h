@@ -331,10 +331,19 @@ int radix_first_bits(int nbits);
 // projection of the same call clears it), integrated in one block.
 // Only for tile grids whose difference array fits kMaxTileDiff entries.
 constexpr int64_t kMaxTileDiff = 16000;  // 64000 B of LDS
+// Cost bucket of a list length: 8 buckets per octave of (c + 1), 256 in
+// all (the render kernels' longest-first block orders).
+__device__ __forceinline__ int cost_bucket(int c) {
+  const unsigned v = static_cast<unsigned>(c < 0 ? 0 : c) + 1u;
+  const int e = 31 - __clz(v);
+  const unsigned mant = e >= 3 ? (v >> (e - 3)) & 7u : (v << (3 - e)) & 7u;
+  return e * 8 + static_cast<int>(mant);
+}
 int64_t tile_diff_elems(int gx, int gy);
 bool tile_diff_fits(int gx, int gy);
 int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int64_t n, int gx,
-                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s);
+                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s,
+                                  int32_t* tile_order = nullptr);
 
 // Exclusive pair offsets off[0..n] (off[n] = K) of the tile counts taken in
 // depth-rank order (tiles[order[i]]; order == nullptr: index order) and
@@ -391,6 +400,11 @@ int launch_fill_f32(float* p, float v, int64_t n, hipStream_t s);
 struct RenderParams {
   const int32_t* ranges;
   const int32_t* plist;
+  // Forward, optional: tile ids longest list first (tile_order_n of them);
+  // the blocks then take the tiles in that order, a tile's planes on one
+  // XCD.
+  const int32_t* tile_order;
+  int tile_order_n;
   // Optional pair tags beside plist (large wide-key sorts): 0 marks an entry
   // the forward culls in every plane (render_cull.h, pair_visible), which
   // the forward then skips without gathering its plane mask or record.

@@ -194,7 +194,27 @@ __device__ __forceinline__ void render_fwd_block(const RenderParams& p) {
   __shared__ int s_kcull;  // 1 + the largest list position culled as invisible
 
   int tile, plane;
-  map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
+  if (p.tile_order) {
+    // Tiles longest list first; hardware block b runs on XCD b % 8, and in
+    // each group of 8 P consecutive blocks XCD x takes the P planes of the
+    // group's x-th tile (a tile's planes share its list in one L2).  The
+    // last, partial group is taken in plain order.
+    const int b = blockIdx.x, P = p.P, nt = p.tile_order_n;
+    const int full = (nt / 8) * 8 * P;
+    int rank;
+    if (b < full) {
+      const int grp = b / (8 * P), r = b - grp * 8 * P;
+      rank = grp * 8 + (r & 7);
+      plane = r >> 3;
+    } else {
+      const int r = b - full;
+      rank = (nt / 8) * 8 + r / P;
+      plane = r - (r / P) * P;
+    }
+    tile = p.tile_order[rank];
+  } else {
+    map_block(blockIdx.x, gridDim.x, p.P, &tile, &plane);
+  }
   const int tx = tile % p.gx, ty = tile / p.gx;
   const int pxi = tx * kTile + (threadIdx.x & 15);
   const int pyi = ty * kTile + (threadIdx.x >> 4);
@@ -980,14 +1000,6 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
     else
       walk(std::false_type{}, std::false_type{});
   }
-}
-
-// Cost bucket of a member count: 8 buckets per octave of (c + 1).
-__device__ __forceinline__ int cost_bucket(int c) {
-  const unsigned v = static_cast<unsigned>(c < 0 ? 0 : c) + 1u;
-  const int e = 31 - __clz(v);
-  const unsigned mant = e >= 3 ? (v >> (e - 3)) & 7u : (v << (3 - e)) & 7u;
-  return e * 8 + static_cast<int>(mant);
 }
 
 constexpr int kOrderThreads = 1024;

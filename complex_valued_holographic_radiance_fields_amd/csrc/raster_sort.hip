@@ -1154,9 +1154,13 @@ __device__ __forceinline__ void wave_prefix_lds(int32_t* p, int len, int step) {
 // per line), then an exclusive scan of the counts in tile order; empty
 // tiles get (0, 0), as a zero-filled ranges buffer has for tiles without
 // pairs.
+// With tile_order: also the tile ids by list length, longest first (256
+// logarithmic buckets, cost_bucket; arbitrary order within a bucket), for
+// the forward render's block order.
 __global__ __launch_bounds__(kDiffThreads) void k_ranges_from_diff(const int32_t* __restrict__ diff,
                                                                   int gx, int gy,
-                                                                  int32_t* __restrict__ ranges) {
+                                                                  int32_t* __restrict__ ranges,
+                                                                  int32_t* __restrict__ tile_order) {
   extern __shared__ int32_t s_d[];
   __shared__ int32_t s_wave[kDiffThreads / 64];
   constexpr int kWaves = kDiffThreads / 64;
@@ -1181,6 +1185,40 @@ __global__ __launch_bounds__(kDiffThreads) void k_ranges_from_diff(const int32_t
     ranges[2 * t + 1] = c > 0 ? start + c : 0;
     start += c;
   }
+  if (!tile_order) return;
+  constexpr int kBins = 256;
+  __shared__ int32_t s_bin[kBins];
+  for (int i = threadIdx.x; i < kBins; i += kDiffThreads) s_bin[i] = 0;
+  __syncthreads();
+  for (int t = t0; t < t0 + per && t < nt; ++t)
+    atomicAdd(&s_bin[cost_bucket(s_d[(t / gx) * gw + t % gx])], 1);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    // exclusive scan over the bins from the highest bucket down: lane l
+    // owns bins 255-4l .. 252-4l
+    const int lane = threadIdx.x;
+    int v[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = s_bin[kBins - 1 - 4 * lane - j];
+      sum += v[j];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const int y = __shfl_up(inc, dd, 64);
+      if (lane >= dd) inc += y;
+    }
+    int run = inc - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s_bin[kBins - 1 - 4 * lane - j] = run;
+      run += v[j];
+    }
+  }
+  __syncthreads();
+  for (int t = t0; t < t0 + per && t < nt; ++t)
+    tile_order[atomicAdd(&s_bin[cost_bucket(s_d[(t / gx) * gw + t % gx])], 1)] = t;
 }
 
 }  // namespace
@@ -1586,7 +1624,8 @@ int64_t tile_diff_elems(int gx, int gy) {
 bool tile_diff_fits(int gx, int gy) { return tile_diff_elems(gx, gy) <= kMaxTileDiff; }
 
 int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int64_t n, int gx,
-                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s) {
+                                  int gy, int32_t* diff, int32_t* ranges, hipStream_t s,
+                                  int32_t* tile_order) {
   if (!tile_diff_fits(gx, gy)) {
     set_error("internal: tile grid %dx%d too large for the LDS difference array", gx, gy);
     return HRF_ERR_INVALID;
@@ -1601,7 +1640,7 @@ int launch_tile_ranges_from_rects(const uint32_t* tiles, const uint2* rect, int6
     HRF_LAUNCH_CHECK();
   }
   hipLaunchKernelGGL(k_ranges_from_diff, dim3(1), dim3(kDiffThreads), lds, s, diff, gx, gy,
-                     ranges);
+                     ranges, tile_order);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
