@@ -63,7 +63,9 @@ def profiled_valu(config, stage, C, M):
     transcendental counts per dispatch, the issue peak (the published FP32
     vector peak in wave64 instructions/s), the extra issue slots a
     transcendental takes, and the measured rate of the forward's own member
-    loop (a calibration kernel with no memory traffic or barriers)."""
+    loop (a calibration kernel with no memory traffic or barriers; its rate
+    per shader cycle at the forward kernel's clock in the same counter
+    run)."""
     path = os.path.join(REPO, "profiles", f"valu_{config}.txt")
     name = STAGE_KERNEL.get(stage, "").format(C=C, M=M)
     if not name or not os.path.exists(path):
