@@ -33,7 +33,7 @@ STAGES = ["project", "depth_sort", "scan", "emit", "tile_sort", "ranges", "rende
 STAGE_KERNEL = {"render_bwd": "k_render_bwd<{C}, true>", "render_fwd": "k_render_fwd<{C}>",
                 "project": "k_project", "geom_bwd": "k_geom_backward",
                 # the headline's variants: zero-padded inputs at most half the grid
-                "asm_col_fwd": "k_col_fwd<{M}, true, true>", "asm_col_adj": "k_col_adj<{M}, true, true>",
+                "asm_col_fwd": "k_col_fwd<{M}, true>", "asm_col_adj": "k_col_adj<{M}, true>",
                 "asm_rows_in": "k_rows_in<{M}, true>", "asm_rows_out": "k_rows_out<{M}>",
                 "emit": "k_emit_packed<false, false>", "ranges": "k_tile_diff"}
 

@@ -712,7 +712,7 @@ __device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb
 // adds them to what Z holds (accumulate != 0).
 // HALF: the field rows lie in [N/4, 3N/4); only that half is staged and the
 // forward transforms' first stage is pruned.
-template <int N, bool HALF, bool SYM>
+template <int N, bool HALF>
 __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int H, int r_pad, int S,
     int s_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw,
@@ -721,7 +721,6 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   constexpr int TB = kFftBatch;    // columns of an intermediate tile
   constexpr int T = kColThreads<N>;
   constexpr int ncb = N / TB;
-  constexpr int EPT = (B * N + T - 1) / T;
   __shared__ float2 lds[lds_elems<N, B, PlanCol<N>::template kPad<B>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
@@ -730,30 +729,38 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   const int cb = hb / (TB / B), col0 = (hb % (TB / B)) * B;  // tile, first column in it
   const int k0 = hb * B;
 
-  // kz of each owned element, or -1 where the aperture or the evanescent
-  // cut zeroes the transfer function for every plane.  SYM (no aperture):
-  // the transfer function depends on the row frequency only through its
-  // square, and rows i and N - i hold frequencies f and -f exactly, so a
-  // slot q = i B + b with i in [0, N/2] owns element q and, for 0 < i <
-  // N/2, its mirror (N - i) B + b, both with one kz and one sine and cosine
-  // per plane (the same values the per-element evaluation gives each).
-  constexpr int NS = SYM ? (N / 2 + 1) * B : B * N;  // slots
-  constexpr int SPT = SYM ? (NS + T - 1) / T : EPT;
+  // Row mirrors: the transfer function depends on the row frequency only
+  // through its square, and rows i and N - i hold frequencies f and -f
+  // exactly, so a slot q = i B + b with i in [0, N/2] owns element q and,
+  // for 0 < i < N/2, its mirror (N - i) B + b, both with one kz and one
+  // sine and cosine per plane (the values the per-element evaluation gives
+  // each).  The aperture (centred between samples) is tested per element:
+  // bits 2u and 2u + 1 of amask.  kz is -1 where the evanescent cut or the
+  // aperture zeroes the transfer function of both elements for every plane.
+  constexpr int NS = (N / 2 + 1) * B;  // slots
+  constexpr int SPT = (NS + T - 1) / T;
+  static_assert(2 * SPT <= 32, "two aperture bits per slot in one word");
   float kz[SPT];
-  float2 acc[SPT], acc2[SYM ? SPT : 1];
+  float2 acc[SPT], acc2[SPT];
+  uint32_t amask = 0;
 #pragma unroll
   for (int u = 0; u < SPT; ++u) {
     const int q = threadIdx.x + u * T;
     acc[u] = make_float2(0.0f, 0.0f);
-    if (SYM) acc2[SYM ? u : 0] = make_float2(0.0f, 0.0f);
+    acc2[u] = make_float2(0.0f, 0.0f);
     kz[u] = -1.0f;
     if (q < NS) {
       const int i = q / B, b = q % B;
       float fxv, fyv;
-      bool inap, prop;
-      coords(i, k0 + b, N, sfreq, SYM ? -1.0f : ap, &fxv, &fyv, &inap);
+      bool in1, in2 = false, prop;
+      coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &in1);
       const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
-      if (inap && prop) kz[u] = kk;
+      if (i != 0 && i != N / 2) {
+        float fx2, fy2;
+        coords(N - i, k0 + b, N, sfreq, ap, &fx2, &fy2, &in2);
+      }
+      if (prop && (in1 || in2)) kz[u] = kk;
+      amask |= (in1 ? 1u : 0u) << (2 * u) | (in2 ? 1u : 0u) << (2 * u + 1);
     }
   }
   for (int p = 0; p < P; ++p) {
@@ -807,17 +814,16 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
         if (within) {
           float sn, cs;
           sincos_big_ff(d * kz[u], &sn, &cs);
-          const float2 x = lds[pad<PlanCol<N>::template kPad<B>>(q)];
-          acc[u].x += x.x * cs - x.y * sn;
-          acc[u].y += x.x * sn + x.y * cs;
-          if (SYM) {
-            const int i = q / B;
-            if (i != 0 && i != N / 2) {
-              const float2 x2 = lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + q % B)];
-              float2& a2 = acc2[SYM ? u : 0];
-              a2.x += x2.x * cs - x2.y * sn;
-              a2.y += x2.x * sn + x2.y * cs;
-            }
+          if ((amask >> (2 * u)) & 1u) {
+            const float2 x = lds[pad<PlanCol<N>::template kPad<B>>(q)];
+            acc[u].x += x.x * cs - x.y * sn;
+            acc[u].y += x.x * sn + x.y * cs;
+          }
+          if ((amask >> (2 * u + 1)) & 1u) {
+            const float2 x2 =
+                lds[pad<PlanCol<N>::template kPad<B>>((N - q / B) * B + q % B)];
+            acc2[u].x += x2.x * cs - x2.y * sn;
+            acc2[u].y += x2.x * sn + x2.y * cs;
           }
         }
       }
@@ -829,11 +835,8 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     const int q = threadIdx.x + u * T;
     if (q < NS) {
       lds[pad<PlanCol<N>::template kPad<B>>(q)] = acc[u];
-      if (SYM) {
-        const int i = q / B;
-        if (i != 0 && i != N / 2)
-          lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + q % B)] = acc2[SYM ? u : 0];
-      }
+      const int i = q / B;
+      if (i != 0 && i != N / 2) lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + q % B)] = acc2[u];
     }
   }
   __syncthreads();
@@ -854,7 +857,7 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
 // receives rows [r_crop, r_crop+H) of iFFTcol(FFTcol(X[c]) conj(T[p,c]) A).
 // HALF: the S gradient rows lie in [N/4, 3N/4) (always, with N = 2S); only
 // that half is staged and the forward transform's first stage is pruned.
-template <int N, bool HALF, bool SYM>
+template <int N, bool HALF>
 __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
     const float2* __restrict__ X, float2* __restrict__ Z, int P, int C, int S, int s_pad, int H,
     int r_crop, float sfreq, float ap, AsmFftConsts mc, const float2* __restrict__ tw) {
@@ -862,7 +865,6 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
   constexpr int TB = kFftBatch;
   constexpr int T = kColThreads<N>;
   constexpr int ncb = N / TB;
-  constexpr int EPT = (B * N + T - 1) / T;
   __shared__ float2 lds[lds_elems<N, B, PlanCol<N>::template kPad<B>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
@@ -892,27 +894,33 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
   }
   __syncthreads();
   PlanCol<N>::template run<false, T, HALF, B>(lds, twp);
-  // SYM: slots own an element and its row mirror, as in k_col_fwd.
-  constexpr int NS = SYM ? (N / 2 + 1) * B : B * N;
-  constexpr int SPT = SYM ? (NS + T - 1) / T : EPT;
+  // Slots own an element and its row mirror, as in k_col_fwd.
+  constexpr int NS = (N / 2 + 1) * B;
+  constexpr int SPT = (NS + T - 1) / T;
+  static_assert(2 * SPT <= 32, "two aperture bits per slot in one word");
   float kz[SPT];
-  float2 gs[SPT], gs2[SYM ? SPT : 1];
+  float2 gs[SPT], gs2[SPT];
+  uint32_t amask = 0;
 #pragma unroll
   for (int u = 0; u < SPT; ++u) {
     const int q = threadIdx.x + u * T;
     kz[u] = -1.0f;
     gs[u] = make_float2(0.0f, 0.0f);
-    if (SYM) gs2[SYM ? u : 0] = make_float2(0.0f, 0.0f);
+    gs2[u] = make_float2(0.0f, 0.0f);
     if (q < NS) {
       const int i = q / B, b = q % B;
       float fxv, fyv;
-      bool inap, prop;
-      coords(i, k0 + b, N, sfreq, SYM ? -1.0f : ap, &fxv, &fyv, &inap);
+      bool in1, in2 = false, prop;
+      coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &in1);
       const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
-      if (inap && prop) kz[u] = kk;
       gs[u] = lds[pad<PlanCol<N>::template kPad<B>>(q)];
-      if (SYM && i != 0 && i != N / 2)
-        gs2[SYM ? u : 0] = lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + b)];
+      if (i != 0 && i != N / 2) {
+        float fx2, fy2;
+        coords(N - i, k0 + b, N, sfreq, ap, &fx2, &fy2, &in2);
+        gs2[u] = lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + b)];
+      }
+      if (prop && (in1 || in2)) kz[u] = kk;
+      amask |= (in1 ? 1u : 0u) << (2 * u) | (in2 ? 1u : 0u) << (2 * u + 1);
     }
   }
   for (int p = 0; p < P; ++p) {
@@ -937,18 +945,15 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
           if (within) {
             float sn, cs;
             sincos_big_ff(nd * kz[u], &sn, &cs);
-            r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
-            if (SYM) {
-              const float2 g2 = gs2[SYM ? u : 0];
-              r2 = make_float2(g2.x * cs - g2.y * sn, g2.x * sn + g2.y * cs);
-            }
+            if ((amask >> (2 * u)) & 1u)
+              r = make_float2(gs[u].x * cs - gs[u].y * sn, gs[u].x * sn + gs[u].y * cs);
+            if ((amask >> (2 * u + 1)) & 1u)
+              r2 = make_float2(gs2[u].x * cs - gs2[u].y * sn, gs2[u].x * sn + gs2[u].y * cs);
           }
         }
         lds[pad<PlanCol<N>::template kPad<B>>(q)] = r;
-        if (SYM) {
-          const int i = q / B;
-          if (i != 0 && i != N / 2) lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + q % B)] = r2;
-        }
+        const int i = q / B;
+        if (i != 0 && i != N / 2) lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + q % B)] = r2;
       }
     }
     __syncthreads();
@@ -1061,20 +1066,14 @@ int pass_col_fwd(const float2* X, float2* Z, int P, int C, int h_in, int h_out, 
   const float2* tw = nullptr;
   HRF_TRY(twiddles(N, &tw, true));
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
-  // Without an aperture the row mirrors share their transfer values.
-  const bool sym = !(ap > 0.0f);
-#define HRF_COL_FWD(HALF_, SYM_)                                                         \
-  hipLaunchKernelGGL((k_col_fwd<N, HALF_, SYM_>), grid, block, 0, s, X, Z, P, C, h_in, \
-                     N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,     \
-                     accumulate ? 1 : 0)
-  if (2 * h_in <= N) {
-    if (sym) HRF_COL_FWD(true, true);
-    else HRF_COL_FWD(true, false);
-  } else {
-    if (sym) HRF_COL_FWD(false, true);
-    else HRF_COL_FWD(false, false);
-  }
-#undef HRF_COL_FWD
+  if (2 * h_in <= N)
+    hipLaunchKernelGGL((k_col_fwd<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,
+                       accumulate ? 1 : 0);
+  else
+    hipLaunchKernelGGL((k_col_fwd<N, false>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw,
+                       accumulate ? 1 : 0);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
@@ -1087,18 +1086,12 @@ int pass_col_adj(const float2* X, float2* Z, int P, int C, int h_in, int h_out, 
   const float2* tw = nullptr;
   HRF_TRY(twiddles(N, &tw, true));
   const dim3 grid(C * (N / kColBatch<N>)), block(kColThreads<N>);
-  const bool sym = !(ap > 0.0f);
-#define HRF_COL_ADJ(HALF_, SYM_)                                                         \
-  hipLaunchKernelGGL((k_col_adj<N, HALF_, SYM_>), grid, block, 0, s, X, Z, P, C, h_in, \
-                     N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw)
-  if (2 * h_in <= N) {
-    if (sym) HRF_COL_ADJ(true, true);
-    else HRF_COL_ADJ(true, false);
-  } else {
-    if (sym) HRF_COL_ADJ(false, true);
-    else HRF_COL_ADJ(false, false);
-  }
-#undef HRF_COL_ADJ
+  if (2 * h_in <= N)
+    hipLaunchKernelGGL((k_col_adj<N, true>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw);
+  else
+    hipLaunchKernelGGL((k_col_adj<N, false>), grid, block, 0, s, X, Z, P, C, h_in,
+                       N / 2 - h_in / 2, h_out, N / 2 - h_out / 2, sfreq, ap, mc, tw);
   HRF_LAUNCH_CHECK();
   return HRF_OK;
 }
