@@ -35,6 +35,11 @@ constexpr int kRadixBins = 256;
 // Partitioning of the radix passes: one tile per block up to
 // kRadixTargetParts tiles, beyond that up to kRadixMaxSub tiles per block.
 constexpr int kRadixTargetParts = 4096;
+// The same for sorts of 2048-key tiles (256-thread blocks): longer
+// partitions there (a block walks its next tile's keys in while it ranks
+// the current one) measured faster (headline tile sort 94 -> 90 us with
+// 1024 against 4096).
+constexpr int kRadixTargetPartsSmall = 1024;
 constexpr int kRadixMaxSub = 64;
 
 constexpr int kDiffThreads = 1024;
@@ -1259,7 +1264,8 @@ int radix_parts(int64_t n, RadixParts* p) {
   p->threads = n >= kRadixLargeMinKeys ? kRadixThreadsLarge : kRadixThreads;
   const int64_t tile = static_cast<int64_t>(p->threads) * kRadixItems;
   const int64_t tiles = (n + tile - 1) / tile;
-  int64_t sub = tiles / kRadixTargetParts;
+  int64_t sub =
+      tiles / (p->threads == kRadixThreadsLarge ? kRadixTargetParts : kRadixTargetPartsSmall);
   if (sub < 1) sub = 1;
   if (sub > kRadixMaxSub) sub = kRadixMaxSub;
   const int64_t np = (tiles + sub - 1) / sub;
