@@ -570,7 +570,7 @@ __device__ __forceinline__ float bwd_det_inv(const float4 c0, const float4 c1) {
 // transpose_reduce64.  Skipping a member for a whole wave is exact: every
 // lane of that wave would skip it (alpha < 1/255 or position >= n_contrib).
 template <int C, bool kSub>
-__global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderParams p) {
+__global__ __launch_bounds__(kBlock, C == 3 ? (kSub ? 5 : 4) : 2) void k_render_bwd(RenderParams p) {
   // Staged record: quads 0-1 as below, then the amplitude quads of the
   // global record, with 1/det of the member's cov2D in the first free slot
   // after the amplitudes (an extra quad at C = 2).  Fast batches: quad 0
@@ -583,14 +583,16 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
   constexpr int NVP = (NV + 3) / 4 * 4;  // padded for row_sum16
   static_assert(NVP <= 16, "one 16-lane row holds a member's sums");
   constexpr int G = kBwdChunk;
-  // Slot kBlock of s_rec is a dummy member that no pixel can use (list
-  // position beyond every n_contrib): the per-wave lists are padded with it
-  // to a multiple of G, so the member loop needs no bounds.  It is written
-  // per batch.
-  constexpr int kDummy = kBlock;
-  __shared__ float4 s_rec[(kBlock + 1) * NQ];
-  __shared__ int s_g[kBlock];
-  __shared__ unsigned short s_wl[4][kBlock + G];
+  // A batch stages kStage = 255 list entries, so that a slot index fits a
+  // byte (the per-wave lists are bytes and the Gaussian index rides in the
+  // staged record's last word: 32 KB of LDS, 5 blocks per CU).  Slot kStage
+  // of s_rec is a dummy member that no pixel can use (list position beyond
+  // every n_contrib): the per-wave lists are padded with it to a multiple
+  // of G, so the member loop needs no bounds.  It is written per batch.
+  constexpr int kStage = kBlock - 1;
+  constexpr int kDummy = kStage;
+  __shared__ float4 s_rec[(kStage + 1) * NQ];
+  __shared__ unsigned char s_wl[4][kBlock + G];
   __shared__ int s_cnt[4][5];
   __shared__ int s_wmax[4];
   // Per wave: the chunk's (Q, dcol) per (member, pixel), written by the
@@ -674,8 +676,8 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
     lim = c < 0 ? 0 : (c > n ? n : c);
     sub = p.sub + static_cast<int64_t>(plane) * p.num_pairs + r0;
   }
-  for (int end = lim; end > 0; end -= kBlock) {
-    const int start = end > kBlock ? end - kBlock : 0;
+  for (int end = lim; end > 0; end -= kStage) {
+    const int start = end > kStage ? end - kStage : 0;
     // No barrier here: until the count barrier below, a batch writes only
     // s_cnt, which the previous batch last read before its member loop; the
     // staging writes that the previous flush's reads must precede come after
@@ -790,28 +792,29 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
       }
       const float4 am0 = src[2];
       const float4 am1 = rec_quads(C) > 3 ? src[rec_quads(C) > 3 ? 3 : 2] : am0;
+      // The last quad's last word: the Gaussian index (int bits).
+      const float gb = __int_as_float(g);
       if (C == 1) {
-        s_rec[slot * NQ + 2] = make_float4(am0.x, am0.y, rq[1].w, 0.0f);
+        s_rec[slot * NQ + 2] = make_float4(am0.x, am0.y, rq[1].w, gb);
       } else if (C == 2) {
         s_rec[slot * NQ + 2] = am0;
-        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(rq[1].w, 0.0f, 0.0f, 0.0f);
+        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(rq[1].w, 0.0f, 0.0f, gb);
       } else {
         s_rec[slot * NQ + 2] = am0;
-        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(am1.x, am1.y, rq[1].w, 0.0f);
+        s_rec[slot * NQ + (NQ > 3 ? 3 : 2)] = make_float4(am1.x, am1.y, rq[1].w, gb);
       }
-      s_g[slot] = g;
       // Each wave's list is stored after its padding, so it ends at a
       // multiple of G.
 #pragma unroll
       for (int w = 0; w < 4; ++w)
         if ((qm >> w) & 1u)
-          s_wl[w][(G - tot[1 + w] % G) % G + off[1 + w]] = static_cast<unsigned short>(slot);
+          s_wl[w][(G - tot[1 + w] % G) % G + off[1 + w]] = static_cast<unsigned char>(slot);
     }
     if (static_cast<int>(threadIdx.x) < 4 * G) {
       const int w = threadIdx.x / G, j = threadIdx.x - w * G;
       // tot[1 + w] by selects: a runtime index would put tot[] in scratch
       const int tw = w == 0 ? tot[1] : (w == 1 ? tot[2] : (w == 2 ? tot[3] : tot[4]));
-      if (j < (G - tw % G) % G) s_wl[w][j] = static_cast<unsigned short>(kDummy);
+      if (j < (G - tw % G) % G) s_wl[w][j] = static_cast<unsigned char>(kDummy);
     }
     __syncthreads();
 
@@ -988,7 +991,8 @@ __global__ __launch_bounds__(kBlock, C == 3 ? 4 : 2) void k_render_bwd(RenderPar
                    : (vi < 5 ? -0.5f : 1.0f);
         const float scale = vi == 5 ? __builtin_amdgcn_rcpf(b2.w) : scale_l;
         if (q < NVP / 4 && vi < NV && slot2 != kDummy && tv != 0.0f)
-          unsafeAtomicAdd(p.acc + static_cast<int64_t>(s_g[slot2]) * AS + aslot, tv * scale);
+          unsafeAtomicAdd(p.acc + static_cast<int64_t>(__float_as_int(c12.w)) * AS + aslot,
+                          tv * scale);
         // The next chunk's phase-1 writes after this chunk's reads.
         __builtin_amdgcn_wave_barrier();
       }
