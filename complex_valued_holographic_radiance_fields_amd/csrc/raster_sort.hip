@@ -800,7 +800,9 @@ __device__ __forceinline__ void compact_visible_block(const VisibleOut& vo, int6
 // (tile and gaussian bits do not fit one word).  kStore == false (with
 // kHist): the pairs are only counted for the first sort pass's histogram;
 // k_emit_scatter regenerates and scatters them.
-constexpr int kEmitPer = 16;
+// (8 pairs per thread: 18.5 KB of LDS per block, 8 blocks per CU; 16
+// measured slower for config 2, 26 against 21.5 us, with 26.7 KB and 6.)
+constexpr int kEmitPer = 8;
 constexpr int kEmitChunk = kEmitThreads * kEmitPer;
 __device__ __forceinline__ int emit_pad(int i) { return i + i / kEmitPer; }
 
