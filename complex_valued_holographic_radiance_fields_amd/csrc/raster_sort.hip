@@ -1560,6 +1560,10 @@ bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirs
   // any size: one emission block per partition.
   const char* force = std::getenv("HRF_SORT_REGENERATE");
   const bool forced = force && force[0] == '1';
+  // Below the large sorts the first pass takes tile-aligned partitions of
+  // several tiles and its own histogram (headline: emission + first pass
+  // 2.8 us faster than with the emission's histogram over its blocks).
+  if (!forced && k < kRadixLargeMinKeys) return false;
   const int64_t avg = k / np > 0 ? k / np : 1;  // pairs per emission block
   int64_t group = (kFirstPassTargetPairs + avg - 1) / avg;
   if (np / group < kFirstPassMinParts) group = np / kFirstPassMinParts;
