@@ -1557,18 +1557,21 @@ bool emit_first_pass(int64_t n, int64_t k, int bits, uint32_t* scratch, SortFirs
   const int64_t np = blocks_for(n, kEmitThreads);
   if (np > 0x7FFFFFFF) return false;
   // HRF_SORT_REGENERATE=1 (for tests) takes the fused emission-scatter at
-  // any size: one emission block per partition.
+  // any size: one emission block per partition; =2 takes the emission's
+  // histogram over groups of its blocks (the stored pairs then scattered by
+  // the first pass) at any size.
   const char* force = std::getenv("HRF_SORT_REGENERATE");
   const bool forced = force && force[0] == '1';
+  const bool forced_hist = force && force[0] == '2';
   // Below the large sorts the first pass takes tile-aligned partitions of
   // several tiles and its own histogram (headline: emission + first pass
   // 2.8 us faster than with the emission's histogram over its blocks).
-  if (!forced && k < kRadixLargeMinKeys) return false;
+  if (!forced && !forced_hist && k < kRadixLargeMinKeys) return false;
   const int64_t avg = k / np > 0 ? k / np : 1;  // pairs per emission block
   int64_t group = (kFirstPassTargetPairs + avg - 1) / avg;
   if (np / group < kFirstPassMinParts) group = np / kFirstPassMinParts;
   if (group < 1 || forced) group = 1;
-  if (!forced && avg * group < kFirstPassTargetPairs / 2) return false;
+  if (!forced && !forced_hist && avg * group < kFirstPassTargetPairs / 2) return false;
   const int64_t need = first_bounds_off(np, bits) + 2 * (np + 1);
   if (need > static_cast<int64_t>(radix_scratch_elems(k))) return false;
   first->np = static_cast<int>(np);

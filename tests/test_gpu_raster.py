@@ -466,6 +466,31 @@ def test_forward_parity_regenerated_first_pass(hrf, oracle_mod, monkeypatch, cas
     assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
 
 
+@pytest.mark.parametrize("case", ["grid", "mid"])
+def test_forward_parity_emission_histogram(hrf, oracle_mod, monkeypatch, case):
+    """The pair emission taking the first sort pass's histogram over groups
+    of its blocks (the pass's partitions, partial tiles at their edges) and
+    storing the pairs for that pass: chosen by itself only for sorts of 2^26
+    pairs or more whose emission blocks hold few pairs;
+    HRF_SORT_REGENERATE=2 takes it at these sizes.  Binning bit-exact."""
+    from complex_valued_holographic_radiance_fields_amd import scenes
+
+    a = REGEN_SCENES[case]
+    spec = scenes.SceneSpec(a["name"], a["seed"], a["n"], a["W"], a["H"], a["P"], a["wl"],
+                            a["d"], a["layout"], log_scale_mean=a["log_scale_mean"],
+                            log_scale_std=a["log_scale_std"])
+    sc = scenes.generate(spec)
+    g, cam = oracle_inputs(sc)
+    ref = oracle_mod.rasterize_forward(g, cam)
+    print(f"emission histogram, {case}: N={g.n} K={ref['K']}", flush=True)
+    monkeypatch.setenv("HRF_SORT_REGENERATE", "2")
+    t, field, (fT, nc, pl, ranges, vis) = _run_gpu_forward(sc)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ref["ranges"])
+    np.testing.assert_array_equal(pl.cpu().numpy(), ref["point_list"])
+    np.testing.assert_array_equal(vis.cpu().numpy(), ref["visible"])
+    assert rel_l2(field.cpu().numpy(), ref["field"]) < TOL
+
+
 def _plane_list_scene(case):
     import dataclasses
 
