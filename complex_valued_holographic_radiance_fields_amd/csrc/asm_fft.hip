@@ -456,6 +456,69 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
   if constexpr (sizeof...(Rest) > 0)
     run_stages<T, B, K, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
+
+// Last stage of a transform with its outputs handed to out(pos, b, value)
+// (pos: the output's index within transform b of the batch) instead of
+// stored back: the crop a caller keeps goes straight to memory, with no
+// LDS store, no barriers and no LDS read-back.  In the last stage j < NS,
+// so butterfly j's outputs are pos = j + t NS: for each t a wave's lanes
+// (B consecutive transforms per butterfly) hand over 64 / B consecutive
+// positions of each transform.  The caller synchronises before it reuses
+// the batch.
+template <int N, int R, int NS, bool INV, int OFF, int T, int B, int K, class Out>
+__device__ __forceinline__ void fft_stage_out(const float2* lds, const float2* __restrict__ tw,
+                                              Out& out) {
+  static_assert(NS * R == N, "the last stage of the plan");
+  constexpr int NB = B * NS;
+  constexpr int BPT = (NB + T - 1) / T;
+  constexpr int LS = B * NS;
+  constexpr bool lin_load = LS % 32 == 0;
+  constexpr int LSP = LS / 32 * (32 + K);
+  unsigned tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  int twoff = 0;
+  asm volatile("" : "+s"(twoff));
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    const unsigned q = tid + u * T;
+    if (BPT * T == NB || q < static_cast<unsigned>(NB)) {
+      const unsigned j = q / B;
+      const int b = static_cast<int>(q % B);
+      float2 x[R];
+      if (lin_load) {
+        const int base = pad<K>(static_cast<int>(q));
+#pragma unroll
+        for (int t = 0; t < R; ++t) x[t] = lds[base + t * LSP];
+      } else {
+#pragma unroll
+        for (int t = 0; t < R; ++t) x[t] = lds[pad<K>(static_cast<int>(q + t * LS))];
+      }
+      if (NS > 1) {
+        const float2* wk = tw + (twoff + OFF + static_cast<int>(j) * (R - 1) - 1);
+#pragma unroll
+        for (int t = 1; t < R; ++t) {
+          float2 w = wk[t];
+          if (INV) w.y = -w.y;
+          x[t] = cmulf(x[t], w);
+        }
+      }
+      Dft<R, INV>::run(x);
+#pragma unroll
+      for (int t = 0; t < R; ++t) out(static_cast<int>(j) + t * NS, b, x[t]);
+    }
+  }
+}
+
+template <int T, int B, int K, int N, bool INV, int NS, int OFF, class Out, int R, int... Rest>
+__device__ __forceinline__ void run_stages_out(float2* lds, const float2* __restrict__ tw,
+                                               Out& out) {
+  if constexpr (sizeof...(Rest) > 0) {
+    fft_stage<N, R, NS, INV, OFF, T, false, B, K>(lds, tw);
+    run_stages_out<T, B, K, N, INV, NS * R, OFF + NS * (R - 1), Out, Rest...>(lds, tw, out);
+  } else {
+    fft_stage_out<N, R, NS, INV, OFF, T, B, K>(lds, tw, out);
+  }
+}
 template <typename... A>
 constexpr int first_radix(int r, A...) {
   return r;
@@ -486,6 +549,11 @@ struct Plan;
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
       run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
     }                                                                               \
+    template <bool INV, int T, int B, class Out>                                    \
+    __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
+                                                   Out& out) {                      \
+      run_stages_out<T, B, kPad<B>, NN, INV, 1, 0, Out, __VA_ARGS__>(lds, tw, out); \
+    }                                                                               \
   };
 HRF_FFT_PLANS(HRF_FFT_PLAN)
 #undef HRF_FFT_PLAN
@@ -505,6 +573,11 @@ struct PlanCol : Plan<N> {};
     template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
       run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
+    }                                                                               \
+    template <bool INV, int T, int B, class Out>                                    \
+    __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
+                                                   Out& out) {                      \
+      run_stages_out<T, B, kPad<B>, NN, INV, 1, 0, Out, __VA_ARGS__>(lds, tw, out); \
     }                                                                               \
   };
 HRF_FFT_COL_PLANS(HRF_FFT_PLAN)
@@ -684,15 +757,15 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
     }
   }
   __syncthreads();
-  Plan<N>::template run<true, T, false, RB>(lds, twp);
-  for (int e = threadIdx.x; e < RB * w_out; e += T) {
-    const int rr = e % RB, i = e / RB;
+  // The last stage stores the kept columns [c_out, c_out + w_out) itself.
+  float2* drow = dst + static_cast<int64_t>(img) * h * w_out;
+  auto out = [&](int pos, int rr, float2 v) {
+    const unsigned i = static_cast<unsigned>(pos - c_out);
     const int r = r0 + rr;
-    if (r < h) {
-      const float2 v = lds[pad<Plan<N>::template kPad<RB>>(RB * (c_out + i) + rr)];
-      dst[(static_cast<int64_t>(img) * h + r) * w_out + i] = cscale(v, scale);
-    }
-  }
+    if (i < static_cast<unsigned>(w_out) && r < h)
+      drow[static_cast<int64_t>(r) * w_out + i] = cscale(v, scale);
+  };
+  Plan<N>::template run_out<true, T, RB>(lds, twp, out);
 }
 
 __device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb, int ncb) {
@@ -840,16 +913,17 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     }
   }
   __syncthreads();
-  PlanCol<N>::template run<true, T, false, B>(lds, twp);
+  // The inverse transform's last stage stores the kept rows
+  // [s_crop, s_crop + S) itself.
   float2* dst = Z + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
-  if (accumulate) {
-    for (int e = threadIdx.x; e < B * S; e += T) {
-      const int o = (e / B) * TB + e % B;
-      dst[o] = cadd(dst[o], lds[pad<PlanCol<N>::template kPad<B>>(e + s_crop * B)]);
+  auto out = [&](int pos, int b, float2 v) {
+    const unsigned r = static_cast<unsigned>(pos - s_crop);
+    if (r < static_cast<unsigned>(S)) {
+      float2* o = dst + r * TB + b;
+      *o = accumulate ? cadd(*o, v) : v;
     }
-  } else {
-    for (int e = threadIdx.x; e < B * S; e += T) dst[(e / B) * TB + e % B] = lds[pad<PlanCol<N>::template kPad<B>>(e + s_crop * B)];
-  }
+  };
+  PlanCol<N>::template run_out<true, T, B>(lds, twp, out);
 }
 
 // B': adjoint column pass.  X tiled (C, S, N) row spectra of the padded
@@ -957,9 +1031,14 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
       }
     }
     __syncthreads();
-    PlanCol<N>::template run<true, T, false, B>(lds, twp);
+    // The last stage stores the kept rows [r_crop, r_crop + H) itself; the
+    // next plane's barrier orders its LDS reads before the batch is rewritten.
     float2* dst = Z + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
-    for (int e = threadIdx.x; e < B * H; e += T) dst[(e / B) * TB + e % B] = lds[pad<PlanCol<N>::template kPad<B>>(e + r_crop * B)];
+    auto out = [&](int pos, int b, float2 v) {
+      const unsigned r = static_cast<unsigned>(pos - r_crop);
+      if (r < static_cast<unsigned>(H)) dst[r * TB + b] = v;
+    };
+    PlanCol<N>::template run_out<true, T, B>(lds, twp, out);
   }
 }
 
