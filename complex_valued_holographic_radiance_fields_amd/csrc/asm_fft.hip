@@ -457,6 +457,62 @@ __device__ __forceinline__ void run_stages(float2* lds, const float2* __restrict
     run_stages<T, B, K, N, INV, false, NS * R, OFF + NS * (R - 1), Rest...>(lds, tw);
 }
 
+// First stage of a transform with its inputs taken from in(pos, b) (pos:
+// the input's index within transform b of the batch) instead of a staged
+// batch: butterfly j reads pos = j + t N/R, so for each t a wave's lanes
+// fetch 64 / B consecutive positions of each of the B transforms, straight
+// into the registers the butterfly uses (no LDS store, barrier or LDS read
+// of a staged copy).  HALF: as in fft_stage, the inputs at t < R/4 and
+// t >= 3R/4 are zero and are not fetched.  The caller guarantees that no
+// thread still reads the batch from an earlier phase.
+template <int N, int R, bool INV, int T, bool HALF, int B, int K, class In>
+__device__ __forceinline__ void fft_stage_in(float2* lds, In& in) {
+  static_assert(!HALF || R == 8 || R == 16, "pruned first stage is radix 8 or 16");
+  constexpr int NR = N / R;
+  constexpr int NB = B * NR;
+  constexpr int BPT = (NB + T - 1) / T;
+  constexpr bool lin_store = B % 32 == 0 || (B * R) % 32 == 0;
+  constexpr int SSP = B % 32 == 0 ? B / 32 * (32 + K) : B;
+  unsigned tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    const unsigned q = tid + u * T;
+    if (BPT * T == NB || q < static_cast<unsigned>(NB)) {
+      const unsigned j = q / B;
+      const int b = static_cast<int>(q % B);
+      float2 x[R];
+#pragma unroll
+      for (int t = 0; t < R; ++t)
+        if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = in(static_cast<int>(j) + t * NR, b);
+      if constexpr (HALF && R == 8)
+        dft8_half<INV>(x);
+      else if constexpr (HALF)
+        dft16<INV, true>(x);
+      else
+        Dft<R, INV>::run(x);
+      // Stockham output position j R + t, interleaved (NS = 1).
+      const int a0 = static_cast<int>(q + B * j * (R - 1));
+      if (lin_store) {
+        const int ob = pad<K>(a0);
+#pragma unroll
+        for (int t = 0; t < R; ++t) lds[ob + (B % 32 == 0 ? t * SSP : pad<K>(t * B))] = x[t];
+      } else {
+#pragma unroll
+        for (int t = 0; t < R; ++t) lds[pad<K>(a0 + t * B)] = x[t];
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <int T, int B, int K, int N, bool INV, bool HALF, class In, int R, int... Rest>
+__device__ __forceinline__ void run_stages_in(float2* lds, const float2* __restrict__ tw, In& in) {
+  fft_stage_in<N, R, INV, T, HALF, B, K>(lds, in);
+  if constexpr (sizeof...(Rest) > 0)
+    run_stages<T, B, K, N, INV, false, R, R - 1, Rest...>(lds, tw);
+}
+
 // Last stage of a transform with its outputs handed to out(pos, b, value)
 // (pos: the output's index within transform b of the batch) instead of
 // stored back: the crop a caller keeps goes straight to memory, with no
@@ -549,6 +605,11 @@ struct Plan;
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
       run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
     }                                                                               \
+    template <bool INV, int T, bool HALF, int B, class In>                          \
+    __device__ __forceinline__ static void run_in(float2* lds, const float2* tw,    \
+                                                  In& in) {                         \
+      run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
+    }                                                                               \
     template <bool INV, int T, int B, class Out>                                    \
     __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
                                                    Out& out) {                      \
@@ -573,6 +634,11 @@ struct PlanCol : Plan<N> {};
     template <bool INV, int T = kFftThreads, bool HALF = false, int B = kFftBatch>  \
     __device__ __forceinline__ static void run(float2* lds, const float2* tw) {     \
       run_stages<T, B, kPad<B>, NN, INV, HALF, 1, 0, __VA_ARGS__>(lds, tw);         \
+    }                                                                               \
+    template <bool INV, int T, bool HALF, int B, class In>                          \
+    __device__ __forceinline__ static void run_in(float2* lds, const float2* tw,    \
+                                                  In& in) {                         \
+      run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
     }                                                                               \
     template <bool INV, int T, int B, class Out>                                    \
     __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
@@ -687,30 +753,17 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __rest
   const int blocks_per_img = (h + RB - 1) / RB;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * RB;
-  {
-    // All of a thread's loads are issued before the first LDS write.
-    constexpr int E0 = HALF ? RB * N / 4 : 0;
-    constexpr int EN = HALF ? RB * N / 2 : RB * N;
-    constexpr int IT = (EN + T - 1) / T;
-    float2 v[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      const int rr = e % RB, i = e / RB;  // 64/RB lanes per row: 512/RB-byte runs
-      const int r = r0 + rr;
-      const int col = i - c_in;
-      v[it] = make_float2(0.0f, 0.0f);
-      if (e < E0 + EN && r < h && col >= 0 && col < w_in)
-        v[it] = src[(static_cast<int64_t>(img) * h + r) * w_in + col];
-    }
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      if (e < E0 + EN) lds[pad<Plan<N>::template kPad<RB>>(e)] = v[it];
-    }
-  }
-  __syncthreads();
-  Plan<N>::template run<false, T, HALF, RB>(lds, twp);
+  // The first stage reads the rows straight from memory: position pos of
+  // row rr is column pos - c_in of the image (zero outside [0, w_in)).
+  const float2* srow = src + static_cast<int64_t>(img) * h * w_in;
+  auto in = [&](int pos, int rr) -> float2 {
+    const unsigned col = static_cast<unsigned>(pos - c_in);
+    const int r = r0 + rr;
+    return (r < h && col < static_cast<unsigned>(w_in))
+               ? srow[static_cast<int64_t>(r) * w_in + col]
+               : make_float2(0.0f, 0.0f);
+  };
+  Plan<N>::template run_in<false, T, HALF, RB>(lds, twp, in);
   // Tile cb's rows r0 .. r0 + RB - 1 are RB * TB consecutive words.
   for (int e = threadIdx.x; e < RB * N; e += T) {
     const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
@@ -837,31 +890,16 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
     }
   }
   for (int p = 0; p < P; ++p) {
+    // The previous plane's reads of the batch end here; the transform's
+    // first stage then reads the plane's column tile straight from memory
+    // (rows outside [r_pad, r_pad + H) are zero).
     __syncthreads();
     const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
-    constexpr int E0 = HALF ? B * N / 4 : 0;
-    constexpr int E1 = HALF ? 3 * B * N / 4 : B * N;
-    // kz and acc are live here, so the copy keeps only kPlaneLoads loads in
-    // flight per thread (a whole-tile register buffer would not fit).
-    constexpr int kPlaneLoads = 4;
-    for (int e0 = E0 + static_cast<int>(threadIdx.x); e0 < E1;
-         e0 += kPlaneLoads * T) {
-      float2 v[kPlaneLoads];
-#pragma unroll
-      for (int u = 0; u < kPlaneLoads; ++u) {
-        const int e = e0 + u * T;
-        const int r = e / B - r_pad;
-        v[u] = make_float2(0.0f, 0.0f);
-        if (e < E1 && r >= 0 && r < H) v[u] = src[r * TB + e % B];
-      }
-#pragma unroll
-      for (int u = 0; u < kPlaneLoads; ++u) {
-        const int e = e0 + u * T;
-        if (e < E1) lds[pad<PlanCol<N>::template kPad<B>>(e)] = v[u];
-      }
-    }
-    __syncthreads();
-    PlanCol<N>::template run<false, T, HALF, B>(lds, twp);
+    auto in = [&](int pos, int b) -> float2 {
+      const unsigned r = static_cast<unsigned>(pos - r_pad);
+      return r < static_cast<unsigned>(H) ? src[r * TB + b] : make_float2(0.0f, 0.0f);
+    };
+    PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -947,27 +985,14 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
   const int cb = hb / (TB / B), col0 = (hb % (TB / B)) * B;
   const int k0 = hb * B;
 
+  // The forward transform's first stage reads the column tile straight
+  // from memory (rows outside [s_pad, s_pad + S) are zero).
   const float2* src = X + tile_off(c, ncb, cb, S, 0, 0, TB) + col0;
-  {
-    constexpr int E0 = HALF ? B * N / 4 : 0;
-    constexpr int EN = HALF ? B * N / 2 : B * N;
-    constexpr int IT = (EN + T - 1) / T;
-    float2 v[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      const int r = e / B - s_pad;
-      v[it] = make_float2(0.0f, 0.0f);
-      if (e < E0 + EN && r >= 0 && r < S) v[it] = src[r * TB + e % B];
-    }
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = E0 + static_cast<int>(threadIdx.x) + it * T;
-      if (e < E0 + EN) lds[pad<PlanCol<N>::template kPad<B>>(e)] = v[it];
-    }
-  }
-  __syncthreads();
-  PlanCol<N>::template run<false, T, HALF, B>(lds, twp);
+  auto in = [&](int pos, int b) -> float2 {
+    const unsigned r = static_cast<unsigned>(pos - s_pad);
+    return r < static_cast<unsigned>(S) ? src[r * TB + b] : make_float2(0.0f, 0.0f);
+  };
+  PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
   // Slots own an element and its row mirror, as in k_col_fwd.
   constexpr int NS = (N / 2 + 1) * B;
   constexpr int SPT = (NS + T - 1) / T;
