@@ -350,9 +350,6 @@ template <int N, int B = kFftBatch, int K = 4>
 constexpr int lds_elems() {
   return pad<K>(B * N - 1) + 1;
 }
-// Elements per thread when a block copies its B x N batch.
-template <int N, int T = kFftThreads, int B = kFftBatch>
-constexpr int kCopyIters = (B * N + T - 1) / T;
 
 // Twiddles are stored per stage, in the order the butterflies use them:
 // the stage with radix R after NS points have been combined holds
@@ -575,6 +572,15 @@ __device__ __forceinline__ void run_stages_out(float2* lds, const float2* __rest
     fft_stage_out<N, R, NS, INV, OFF, T, B, K>(lds, tw, out);
   }
 }
+// First stage from in(), last stage to out() (plans of two or more stages).
+template <int T, int B, int K, int N, bool INV, bool HALF, class In, class Out, int R,
+          int... Rest>
+__device__ __forceinline__ void run_stages_in_out(float2* lds, const float2* __restrict__ tw,
+                                                  In& in, Out& out) {
+  static_assert(sizeof...(Rest) > 0, "a plan of two or more stages");
+  fft_stage_in<N, R, INV, T, HALF, B, K>(lds, in);
+  run_stages_out<T, B, K, N, INV, R, R - 1, Out, Rest...>(lds, tw, out);
+}
 template <typename... A>
 constexpr int first_radix(int r, A...) {
   return r;
@@ -610,6 +616,12 @@ struct Plan;
                                                   In& in) {                         \
       run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
     }                                                                               \
+    template <bool INV, int T, bool HALF, int B, class In, class Out>               \
+    __device__ __forceinline__ static void run_in_out(float2* lds, const float2* tw,\
+                                                      In& in, Out& out) {           \
+      run_stages_in_out<T, B, kPad<B>, NN, INV, HALF, In, Out, __VA_ARGS__>(lds, tw,\
+                                                                 in, out);          \
+    }                                                                               \
     template <bool INV, int T, int B, class Out>                                    \
     __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
                                                    Out& out) {                      \
@@ -639,6 +651,12 @@ struct PlanCol : Plan<N> {};
     __device__ __forceinline__ static void run_in(float2* lds, const float2* tw,    \
                                                   In& in) {                         \
       run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
+    }                                                                               \
+    template <bool INV, int T, bool HALF, int B, class In, class Out>               \
+    __device__ __forceinline__ static void run_in_out(float2* lds, const float2* tw,\
+                                                      In& in, Out& out) {           \
+      run_stages_in_out<T, B, kPad<B>, NN, INV, HALF, In, Out, __VA_ARGS__>(lds, tw,\
+                                                                 in, out);          \
     }                                                                               \
     template <bool INV, int T, int B, class Out>                                    \
     __device__ __forceinline__ static void run_out(float2* lds, const float2* tw,   \
@@ -763,13 +781,14 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_in(const float2* __rest
                ? srow[static_cast<int64_t>(r) * w_in + col]
                : make_float2(0.0f, 0.0f);
   };
-  Plan<N>::template run_in<false, T, HALF, RB>(lds, twp, in);
-  // Tile cb's rows r0 .. r0 + RB - 1 are RB * TB consecutive words.
-  for (int e = threadIdx.x; e < RB * N; e += T) {
-    const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
+  // The last stage stores the spectrum rows tile-major itself (for each
+  // output index a wave covers 64 / RB columns of the RB rows: runs of
+  // RB TB words, tile cb's rows r0 .. r0 + RB - 1).
+  auto out = [&](int pos, int rr, float2 v) {
     const int r = r0 + rr;
-    if (r < h) dst[tile_off(img, ncb, cb, h, r, bc, TB)] = lds[pad<Plan<N>::template kPad<RB>>(RB * (TB * cb + bc) + rr)];
-  }
+    if (r < h) dst[tile_off(img, ncb, pos / TB, h, r, pos % TB, TB)] = v;
+  };
+  Plan<N>::template run_in_out<false, T, HALF, RB>(lds, twp, in, out);
 }
 
 // C / C': inverse FFT of kRowBatch rows of a tiled (nimg, h, N) spectrum;
@@ -785,32 +804,19 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
   constexpr int T = kRowThreads<N>;
   constexpr int TB = kFftBatch;
   constexpr int ncb = N / TB;
-  constexpr int IT = kCopyIters<N, T, RB>;
   __shared__ float2 lds[lds_elems<N, RB, Plan<N>::template kPad<RB>>()];
   __shared__ float2 s_tw[kTwLdsElems<N>];
   const float2* twp = stage_twiddles<N, T>(s_tw, tw);
   const int blocks_per_img = (h + RB - 1) / RB;
   const int img = blockIdx.x / blocks_per_img;
   const int r0 = (blockIdx.x - img * blocks_per_img) * RB;
-  {
-    float2 v[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * T;
-      const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
-      const int r = r0 + rr;
-      v[it] = make_float2(0.0f, 0.0f);
-      if (e < RB * N && r < h) v[it] = src[tile_off(img, ncb, cb, h, r, bc, TB)];
-    }
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-      const int e = static_cast<int>(threadIdx.x) + it * T;
-      const int cb = e / (RB * TB), rr = (e / TB) % RB, bc = e % TB;
-      if (e < RB * N) lds[pad<Plan<N>::template kPad<RB>>(RB * (TB * cb + bc) + rr)] = v[it];
-    }
-  }
-  __syncthreads();
-  // The last stage stores the kept columns [c_out, c_out + w_out) itself.
+  // The first stage reads the tile-major spectrum rows straight from
+  // memory, the last stores the kept columns [c_out, c_out + w_out).
+  auto in = [&](int pos, int rr) -> float2 {
+    const int r = r0 + rr;
+    return r < h ? src[tile_off(img, ncb, pos / TB, h, r, pos % TB, TB)]
+                 : make_float2(0.0f, 0.0f);
+  };
   float2* drow = dst + static_cast<int64_t>(img) * h * w_out;
   auto out = [&](int pos, int rr, float2 v) {
     const unsigned i = static_cast<unsigned>(pos - c_out);
@@ -818,7 +824,7 @@ __global__ __launch_bounds__(kRowThreads<N>) void k_rows_out(const float2* __res
     if (i < static_cast<unsigned>(w_out) && r < h)
       drow[static_cast<int64_t>(r) * w_out + i] = cscale(v, scale);
   };
-  Plan<N>::template run_out<true, T, RB>(lds, twp, out);
+  Plan<N>::template run_in_out<true, T, false, RB>(lds, twp, in, out);
 }
 
 __device__ __forceinline__ void map_cblock(int bid, int nblk, int* chan, int* cb, int ncb) {
