@@ -503,6 +503,59 @@ __device__ __forceinline__ void fft_stage_in(float2* lds, In& in) {
   __syncthreads();
 }
 
+// The first stage split in two for a caller that overlaps the loads with
+// other work (one butterfly per thread): first_stage_load fetches thread
+// q's inputs (the q < B N/R that own a butterfly) into x, first_stage_finish
+// transforms and stores them as fft_stage_in does.
+template <int N, int R, int T, bool HALF, int B, class In>
+__device__ __forceinline__ void first_stage_load(In& in, float2 (&x)[R]) {
+  constexpr int NR = N / R;
+  static_assert(B * NR <= T, "one butterfly per thread");
+  const unsigned q = threadIdx.x;
+  if (q < static_cast<unsigned>(B * NR)) {
+    const int j = static_cast<int>(q / B), b = static_cast<int>(q % B);
+#pragma unroll
+    for (int t = 0; t < R; ++t)
+      if (!HALF || (t >= R / 4 && t < 3 * R / 4)) x[t] = in(j + t * NR, b);
+  }
+}
+template <int N, int R, bool INV, int T, bool HALF, int B, int K>
+__device__ __forceinline__ void first_stage_finish(float2* lds, float2 (&x)[R]) {
+  static_assert(!HALF || R == 8 || R == 16, "pruned first stage is radix 8 or 16");
+  constexpr int NB = B * (N / R);
+  static_assert(NB <= T, "one butterfly per thread");
+  constexpr bool lin_store = B % 32 == 0 || (B * R) % 32 == 0;
+  constexpr int SSP = B % 32 == 0 ? B / 32 * (32 + K) : B;
+  unsigned q = threadIdx.x;
+  asm volatile("" : "+v"(q));
+  if (q < static_cast<unsigned>(NB)) {
+    const unsigned j = q / B;
+    if constexpr (HALF && R == 8)
+      dft8_half<INV>(x);
+    else if constexpr (HALF)
+      dft16<INV, true>(x);
+    else
+      Dft<R, INV>::run(x);
+    const int a0 = static_cast<int>(q + B * j * (R - 1));
+    if (lin_store) {
+      const int ob = pad<K>(a0);
+#pragma unroll
+      for (int t = 0; t < R; ++t) lds[ob + (B % 32 == 0 ? t * SSP : pad<K>(t * B))] = x[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < R; ++t) lds[pad<K>(a0 + t * B)] = x[t];
+    }
+  }
+  __syncthreads();
+}
+template <int T, int B, int K, int N, bool INV, bool HALF, int R, int... Rest>
+__device__ __forceinline__ void run_stages_from(float2* lds, const float2* __restrict__ tw,
+                                                float2 (&x)[R]) {
+  first_stage_finish<N, R, INV, T, HALF, B, K>(lds, x);
+  if constexpr (sizeof...(Rest) > 0)
+    run_stages<T, B, K, N, INV, false, R, R - 1, Rest...>(lds, tw);
+}
+
 template <int T, int B, int K, int N, bool INV, bool HALF, class In, int R, int... Rest>
 __device__ __forceinline__ void run_stages_in(float2* lds, const float2* __restrict__ tw, In& in) {
   fft_stage_in<N, R, INV, T, HALF, B, K>(lds, in);
@@ -616,6 +669,16 @@ struct Plan;
                                                   In& in) {                         \
       run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
     }                                                                               \
+    static constexpr int kR1 = first_radix(__VA_ARGS__);                            \
+    template <int T, bool HALF, int B, class In>                                    \
+    __device__ __forceinline__ static void load_first(In& in, float2 (&x)[kR1]) {   \
+      first_stage_load<NN, kR1, T, HALF, B>(in, x);                                 \
+    }                                                                               \
+    template <bool INV, int T, bool HALF, int B>                                    \
+    __device__ __forceinline__ static void run_from(float2* lds, const float2* tw,  \
+                                                    float2 (&x)[kR1]) {             \
+      run_stages_from<T, B, kPad<B>, NN, INV, HALF, __VA_ARGS__>(lds, tw, x);       \
+    }                                                                               \
     template <bool INV, int T, bool HALF, int B, class In, class Out>               \
     __device__ __forceinline__ static void run_in_out(float2* lds, const float2* tw,\
                                                       In& in, Out& out) {           \
@@ -651,6 +714,16 @@ struct PlanCol : Plan<N> {};
     __device__ __forceinline__ static void run_in(float2* lds, const float2* tw,    \
                                                   In& in) {                         \
       run_stages_in<T, B, kPad<B>, NN, INV, HALF, In, __VA_ARGS__>(lds, tw, in);    \
+    }                                                                               \
+    static constexpr int kR1 = first_radix(__VA_ARGS__);                            \
+    template <int T, bool HALF, int B, class In>                                    \
+    __device__ __forceinline__ static void load_first(In& in, float2 (&x)[kR1]) {   \
+      first_stage_load<NN, kR1, T, HALF, B>(in, x);                                 \
+    }                                                                               \
+    template <bool INV, int T, bool HALF, int B>                                    \
+    __device__ __forceinline__ static void run_from(float2* lds, const float2* tw,  \
+                                                    float2 (&x)[kR1]) {             \
+      run_stages_from<T, B, kPad<B>, NN, INV, HALF, __VA_ARGS__>(lds, tw, x);       \
     }                                                                               \
     template <bool INV, int T, bool HALF, int B, class In, class Out>               \
     __device__ __forceinline__ static void run_in_out(float2* lds, const float2* tw,\
@@ -869,6 +942,17 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   // each).  The aperture (centred between samples) is tested per element:
   // bits 2u and 2u + 1 of amask.  kz is -1 where the evanescent cut or the
   // aperture zeroes the transfer function of both elements for every plane.
+  // kSplit: the first plane's first-stage loads are issued before the kz
+  // prologue, so its arithmetic overlaps their latency (half-grid inputs at
+  // the lengths where the registers the loads hold cost no occupancy).
+  constexpr bool kSplit = HALF && (N == 1600 || N == 3840 || N == 4096);
+  const float2* src = X + tile_off(c, ncb, cb, H, 0, 0, TB) + col0;
+  auto in = [&](int pos, int b) -> float2 {
+    const unsigned r = static_cast<unsigned>(pos - r_pad);
+    return r < static_cast<unsigned>(H) ? src[r * TB + b] : make_float2(0.0f, 0.0f);
+  };
+  float2 xin[PlanCol<N>::kR1];
+  if constexpr (kSplit) PlanCol<N>::template load_first<T, HALF, B>(in, xin);
   constexpr int NS = (N / 2 + 1) * B;  // slots
   constexpr int SPT = (NS + T - 1) / T;
   static_assert(2 * SPT <= 32, "two aperture bits per slot in one word");
@@ -898,14 +982,14 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_fwd(
   for (int p = 0; p < P; ++p) {
     // The previous plane's reads of the batch end here; the transform's
     // first stage then reads the plane's column tile straight from memory
-    // (rows outside [r_pad, r_pad + H) are zero).
+    // (rows outside [r_pad, r_pad + H) are zero); with kSplit the first
+    // plane's loads were issued before the kz prologue.
     __syncthreads();
-    const float2* src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
-    auto in = [&](int pos, int b) -> float2 {
-      const unsigned r = static_cast<unsigned>(pos - r_pad);
-      return r < static_cast<unsigned>(H) ? src[r * TB + b] : make_float2(0.0f, 0.0f);
-    };
-    PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
+    src = X + tile_off(p * C + c, ncb, cb, H, 0, 0, TB) + col0;
+    if (kSplit && p == 0)
+      PlanCol<N>::template run_from<false, T, HALF, B>(lds, twp, xin);
+    else
+      PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
     const float fxm = mc.fxmax[p * kMaxChannels + c], fym = mc.fymax[p * kMaxChannels + c];
     const bool band_all = mc.band_all[p * kMaxChannels + c] != 0;
     const float d = mc.d[p];
@@ -998,7 +1082,15 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
     const unsigned r = static_cast<unsigned>(pos - s_pad);
     return r < static_cast<unsigned>(S) ? src[r * TB + b] : make_float2(0.0f, 0.0f);
   };
-  PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
+  // kSplit: the first stage's loads are issued before the kz prologue, so
+  // its arithmetic overlaps their latency (half-grid inputs at the lengths
+  // where the registers the loads hold cost no occupancy).
+  constexpr bool kSplit = HALF && (N == 1600 || N == 3840 || N == 4096);
+  float2 xin[PlanCol<N>::kR1];
+  if constexpr (kSplit)
+    PlanCol<N>::template load_first<T, HALF, B>(in, xin);
+  else
+    PlanCol<N>::template run_in<false, T, HALF, B>(lds, twp, in);
   // Slots own an element and its row mirror, as in k_col_fwd.
   constexpr int NS = (N / 2 + 1) * B;
   constexpr int SPT = (NS + T - 1) / T;
@@ -1010,22 +1102,30 @@ __global__ __launch_bounds__(kColThreads<N>, kColMinBlocks<N>) void k_col_adj(
   for (int u = 0; u < SPT; ++u) {
     const int q = threadIdx.x + u * T;
     kz[u] = -1.0f;
-    gs[u] = make_float2(0.0f, 0.0f);
-    gs2[u] = make_float2(0.0f, 0.0f);
     if (q < NS) {
       const int i = q / B, b = q % B;
       float fxv, fyv;
       bool in1, in2 = false, prop;
       coords(i, k0 + b, N, sfreq, ap, &fxv, &fyv, &in1);
       const float kk = kz_of(mc.k[c], fxv, fyv, &prop);
-      gs[u] = lds[pad<PlanCol<N>::template kPad<B>>(q)];
       if (i != 0 && i != N / 2) {
         float fx2, fy2;
         coords(N - i, k0 + b, N, sfreq, ap, &fx2, &fy2, &in2);
-        gs2[u] = lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + b)];
       }
       if (prop && (in1 || in2)) kz[u] = kk;
       amask |= (in1 ? 1u : 0u) << (2 * u) | (in2 ? 1u : 0u) << (2 * u + 1);
+    }
+  }
+  if constexpr (kSplit) PlanCol<N>::template run_from<false, T, HALF, B>(lds, twp, xin);
+#pragma unroll
+  for (int u = 0; u < SPT; ++u) {
+    const int q = threadIdx.x + u * T;
+    gs[u] = make_float2(0.0f, 0.0f);
+    gs2[u] = make_float2(0.0f, 0.0f);
+    if (q < NS) {
+      const int i = q / B, b = q % B;
+      gs[u] = lds[pad<PlanCol<N>::template kPad<B>>(q)];
+      if (i != 0 && i != N / 2) gs2[u] = lds[pad<PlanCol<N>::template kPad<B>>((N - i) * B + b)];
     }
   }
   for (int p = 0; p < P; ++p) {
